@@ -1,0 +1,232 @@
+"""ctypes front-end of the test oracle (oracle/build/liboracle.so) and of the
+reference harness (oracle/_ref/libpicolm_ref.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, the smoke entry and the bench's
+CPU-baseline leg, as the checker.  The product package never imports it.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "build", "liboracle.so")
+REF_PATH = os.path.join(HERE, "_ref", "libpicolm_ref.so")
+REF_SRC = "/root/reference/picolm"
+
+ROPE_LLAMA = 0
+ROPE_QWEN = 1
+
+_f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+_u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
+_i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+
+
+def build(ref: bool | None = None) -> None:
+    """Compile the oracle (and the reference harness when its sources exist)."""
+    subprocess.run(["make", "-s", "-C", HERE, "all"], check=True)
+    if ref is None:
+        ref = os.path.isdir(REF_SRC)
+    if ref:
+        subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
+
+
+_lib = None
+_ref = None
+
+
+def lib() -> C.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build(ref=False)
+        L = C.CDLL(LIB_PATH)
+        L.orc_f16_to_f32.argtypes = [C.c_uint16]
+        L.orc_f16_to_f32.restype = C.c_float
+        L.orc_f32_to_f16.argtypes = [C.c_float]
+        L.orc_f32_to_f16.restype = C.c_uint16
+        L.orc_f32_to_f16_array.argtypes = [_f32p, _u16p, C.c_size_t]
+        L.orc_f32_to_f16_array.restype = None
+        L.orc_f16_to_f32_array.argtypes = [_u16p, _f32p, C.c_size_t]
+        L.orc_f16_to_f32_array.restype = None
+        L.orc_f16_checksum.argtypes = [C.c_uint64, C.c_uint64, C.c_int]
+        L.orc_f16_checksum.restype = C.c_uint64
+        L.orc_rope_tables.argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_float]
+        L.orc_rope_tables.restype = None
+        L.orc_rope.argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_int, _f32p, _f32p, C.c_int]
+        L.orc_rope.restype = None
+        dims = [C.c_int] * 8
+        L.orc_attn_decode.argtypes = dims + [_f32p, _f32p, _f32p, _u16p, _u16p, _f32p, _f32p, _f32p]
+        L.orc_attn_decode.restype = C.c_int
+        L.orc_attn_prefill.argtypes = dims + [C.c_int, _f32p, _f32p, _f32p, _u16p, _u16p,
+                                              _f32p, _f32p, _f32p, C.c_int]
+        L.orc_attn_prefill.restype = C.c_int
+        L.orc_attn_core.argtypes = [C.c_int] * 6 + [_f32p, _u16p, _u16p, _f32p]
+        L.orc_attn_core.restype = C.c_int
+        _lib = L
+    return _lib
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_PATH)
+
+
+def ref() -> C.CDLL:
+    global _ref
+    if _ref is None:
+        R = C.CDLL(REF_PATH)
+        R.fp32_to_fp16.argtypes = [C.c_float]
+        R.fp32_to_fp16.restype = C.c_uint16
+        R.fp16_to_fp32.argtypes = [C.c_uint16]
+        R.fp16_to_fp32.restype = C.c_float
+        R.rope.argtypes = [_f32p, _f32p, C.c_int, C.c_int, C.c_int, _f32p, _f32p, C.c_int]
+        R.rope.restype = None
+        R.ref_model_new.argtypes = [C.c_int] * 5 + [C.c_float, C.c_int, C.c_int, C.c_ulonglong, C.c_float]
+        R.ref_model_new.restype = C.c_void_p
+        R.ref_model_free.argtypes = [C.c_void_p]
+        R.ref_model_free.restype = None
+        R.ref_cache_ptrs.argtypes = [C.c_void_p] + [C.POINTER(C.c_void_p)] * 4
+        R.ref_cache_ptrs.restype = None
+        R.ref_set_decode_qkv.argtypes = [C.c_void_p, C.c_int, _f32p, _f32p, _f32p]
+        R.ref_set_decode_qkv.restype = None
+        R.ref_decode.argtypes = [C.c_void_p, C.c_int, C.c_int, _f32p]
+        R.ref_decode.restype = None
+        R.ref_prefill.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_int, _f32p]
+        R.ref_prefill.restype = None
+        R.ref_embed.argtypes = [C.c_void_p, _i32p, C.c_int, _f32p]
+        R.ref_embed.restype = None
+        R.ref_layer_inputs.argtypes = [C.c_void_p, C.c_int, _f32p, C.c_int, _f32p, _f32p, _f32p]
+        R.ref_layer_inputs.restype = None
+        R.ref_final_norm.argtypes = [C.c_void_p, _f32p, _f32p]
+        R.ref_final_norm.restype = None
+        _ref = R
+    return _ref
+
+
+# ---------------------------------------------------------------------------
+# numpy conveniences
+# ---------------------------------------------------------------------------
+
+def f32_to_f16(x: np.ndarray) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.empty(x.shape, dtype=np.uint16)
+    lib().orc_f32_to_f16_array(x.reshape(-1), out.reshape(-1), x.size)
+    return out
+
+
+def f16_to_f32(h: np.ndarray) -> np.ndarray:
+    h = np.ascontiguousarray(h, dtype=np.uint16)
+    out = np.empty(h.shape, dtype=np.float32)
+    lib().orc_f16_to_f32_array(h.reshape(-1), out.reshape(-1), h.size)
+    return out
+
+
+def rope_tables(max_seq_len: int, head_dim: int, base: float):
+    half = head_dim // 2
+    c = np.empty((max_seq_len, half), dtype=np.float32)
+    s = np.empty((max_seq_len, half), dtype=np.float32)
+    lib().orc_rope_tables(c.reshape(-1), s.reshape(-1), max_seq_len, head_dim, base)
+    return c, s
+
+
+def rope(q, k, head_dim, n_heads, n_kv_heads, cos_row, sin_row, rope_type):
+    """In-place RoPE of one token's q [n_heads*D] and k [n_kv_heads*D]."""
+    lib().orc_rope(q, k, head_dim, n_heads, n_kv_heads,
+                   np.ascontiguousarray(cos_row, np.float32),
+                   np.ascontiguousarray(sin_row, np.float32), rope_type)
+
+
+class Shape:
+    """Attention shape: n_layers, n_heads, n_kv_heads, head_dim, max_seq_len."""
+
+    def __init__(self, n_layers, n_heads, n_kv_heads, head_dim, max_seq_len,
+                 rope_base=10000.0, rope_type=ROPE_LLAMA):
+        self.n_layers = n_layers
+        self.n_heads = n_heads
+        self.n_kv_heads = n_kv_heads
+        self.head_dim = head_dim
+        self.max_seq_len = max_seq_len
+        self.rope_base = rope_base
+        self.rope_type = rope_type
+
+    @property
+    def q_dim(self):
+        return self.n_heads * self.head_dim
+
+    @property
+    def kv_dim(self):
+        return self.n_kv_heads * self.head_dim
+
+    def cache_elems(self):
+        return self.n_layers * self.max_seq_len * self.kv_dim
+
+    def dims(self):
+        return (self.n_layers, self.n_heads, self.n_kv_heads, self.head_dim,
+                self.max_seq_len, self.rope_type)
+
+
+def attn_decode(shp: Shape, layer, pos, q, k, v, kc, vc, cos_t, sin_t):
+    """Oracle decode step; q, k rotated in place, caches appended in place."""
+    out = np.empty(shp.q_dim, dtype=np.float32)
+    rc = lib().orc_attn_decode(*shp.dims(), layer, pos, q, k, v, kc, vc,
+                               cos_t.reshape(-1), sin_t.reshape(-1), out)
+    if rc != 0:
+        raise ValueError("orc_attn_decode rejected its arguments")
+    return out
+
+
+def attn_prefill(shp: Shape, layer, start_pos, n_tokens, q, k, v, kc, vc,
+                 cos_t, sin_t, out_stride=None):
+    stride = shp.q_dim if out_stride is None else out_stride
+    out = np.zeros(max(n_tokens, 1) * stride, dtype=np.float32)
+    rc = lib().orc_attn_prefill(*shp.dims(), layer, start_pos, n_tokens,
+                                q.reshape(-1), k.reshape(-1), v.reshape(-1),
+                                kc, vc, cos_t.reshape(-1), sin_t.reshape(-1),
+                                out, stride)
+    if rc != 0:
+        raise ValueError("orc_attn_prefill rejected its arguments")
+    return out[: n_tokens * stride].reshape(n_tokens, stride)
+
+
+def attn_core(shp: Shape, layer, pos, q, kc, vc):
+    out = np.empty(shp.q_dim, dtype=np.float32)
+    rc = lib().orc_attn_core(shp.n_heads, shp.n_kv_heads, shp.head_dim,
+                             shp.max_seq_len, layer, pos,
+                             np.ascontiguousarray(q, np.float32), kc, vc, out)
+    if rc != 0:
+        raise ValueError("orc_attn_core rejected its arguments")
+    return out
+
+
+class RefModel:
+    """The reference's own forward pass on a tiny model (oracle/ref_harness.c)."""
+
+    def __init__(self, shp: Shape, mode: int, seed: int = 1, w_scale: float = 0.25):
+        R = ref()
+        self.shp = shp
+        self.h = R.ref_model_new(shp.n_layers, shp.n_heads, shp.n_kv_heads,
+                                 shp.head_dim, shp.max_seq_len, shp.rope_base,
+                                 shp.rope_type, mode, seed, w_scale)
+        if not self.h:
+            raise MemoryError("ref_model_new failed")
+        ptrs = [C.c_void_p() for _ in range(4)]
+        R.ref_cache_ptrs(self.h, *[C.byref(p) for p in ptrs])
+        n = shp.cache_elems()
+        half = shp.head_dim // 2
+        self.kc = np.ctypeslib.as_array(C.cast(ptrs[0], C.POINTER(C.c_uint16)), (n,))
+        self.vc = np.ctypeslib.as_array(C.cast(ptrs[1], C.POINTER(C.c_uint16)), (n,))
+        self.cos = np.ctypeslib.as_array(C.cast(ptrs[2], C.POINTER(C.c_float)),
+                                         (shp.max_seq_len, half))
+        self.sin = np.ctypeslib.as_array(C.cast(ptrs[3], C.POINTER(C.c_float)),
+                                         (shp.max_seq_len, half))
+
+    def close(self):
+        if self.h:
+            ref().ref_model_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
