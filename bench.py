@@ -1,0 +1,240 @@
+"""Benchmark of picolm's attention block on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+
+A step is one token's decode attention over all layers of the model (one
+launch of plh_attn_decode covering every layer), with inputs resident in HBM.
+The default workload is TinyLlama-1.1B-shaped decode at position 2047
+(22 layers, 32 q heads, 4 kv heads, head_dim 64, FP16 cache of 2048 rows).
+
+Method:
+  * the FP16 caches are rotated over enough copies (>= 512 MiB in total) that
+    the 256 MiB Infinity Cache cannot serve a step from the previous one;
+  * the K timed steps are captured into one HIP graph (no host launch cost
+    between steps); the graph is replayed once untimed and once timed,
+    bracketed by device synchronisation.  ms_per_step is the wall clock of the
+    timed replay / K; roofline.achieved uses hipEvents recorded on the library
+    stream around the timed replay (mean duration per launch);
+  * algorithmic bytes per token (all layers):
+      L * [ (pos+1)*2*Hkv*D*2  (K+V rows read)
+            + Hq*D*4 + 2*Hkv*D*4 (q, k, v in) + 2*Hkv*D*2 (row written)
+            + Hq*D*4 (out) ]
+  * cpu_baseline: the oracle (the reference's attention restated in C, same
+    op order, out-of-line fp16 widening as in the reference build) timed on
+    one host thread over a bounded sample of the same workload.
+Prints one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "attn µs/token + KV GB/s (% HBM peak) decode; prefill TFLOP/s (% MFMA)"
+HBM_PEAK_GBS = 8000.0
+MALL_DEFEAT_BYTES = 512 << 20
+
+WORKLOADS = {
+    "tinyllama_decode_pos2047": dict(L=22, Hq=32, Hkv=4, D=64, S=2048, theta=1e4, pos=2047),
+    "tinyllama_decode_pos256": dict(L=22, Hq=32, Hkv=4, D=64, S=2048, theta=1e4, pos=256),
+    "llama32_decode_pos8191": dict(L=16, Hq=32, Hkv=8, D=64, S=8192, theta=5e5, pos=8191),
+    "llama2_decode_pos4095": dict(L=32, Hq=32, Hkv=32, D=128, S=4096, theta=1e4, pos=4095),
+}
+
+
+def decode_bytes(w) -> int:
+    L, Hq, Hkv, D, pos = w["L"], w["Hq"], w["Hkv"], w["D"], w["pos"]
+    per_layer = ((pos + 1) * 2 * Hkv * D * 2 + Hq * D * 4 + 2 * Hkv * D * 4
+                 + 2 * Hkv * D * 2 + Hq * D * 4)
+    return L * per_layer
+
+
+def traffic_from_profiles(name: str):
+    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
+    WRITE_SIZE, calibrated against a copy kernel), if a summary exists."""
+    path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes")
+    except (OSError, ValueError):
+        return None
+
+
+def run_decode(P, w, steps, warmup, name):
+    cfg = P.AttnConfig(w["L"], w["Hq"], w["Hkv"], w["D"], w["S"], w["theta"], 0)
+    cache_bytes = cfg.cache_elems * 2
+    n_copies = max(1, math.ceil(MALL_DEFEAT_BYTES / (2 * cache_bytes)))
+    rng = np.random.default_rng(2047)
+    pos = w["pos"]
+
+    # copy 0: rows 0..pos-1 of every layer hold N(0,1) rounded to fp16 on the
+    # device with the reference's rounding; other rows are zero
+    L, S, kv = cfg.n_layers, cfg.max_seq_len, cfg.kv_dim
+    cos_t, sin_t = P.rope_tables(S, cfg.head_dim, cfg.rope_freq_base)
+    d_cos, d_sin = P.DeviceBuffer.from_numpy(cos_t), P.DeviceBuffer.from_numpy(sin_t)
+    staging = P.DeviceBuffer(L * S * kv * 4)
+    keys, vals = [], []
+    for which in range(2):
+        host = np.zeros((L, S, kv), np.float32)
+        host[:, :pos] = rng.standard_normal((L, pos, kv), dtype=np.float32)
+        staging.upload(host)
+        buf = P.DeviceBuffer(cache_bytes)
+        P.f32_to_f16(staging.ptr, buf.ptr, L * S * kv)
+        (keys if which == 0 else vals).append(buf)
+        del host
+    staging.free()
+    for c in range(1, n_copies):
+        for lst in (keys, vals):
+            b = P.DeviceBuffer(cache_bytes)
+            b.copy_from(lst[0])
+            lst.append(b)
+    qkv = []
+    for c in range(n_copies):
+        q = P.DeviceBuffer.from_numpy(rng.standard_normal((L, cfg.q_dim), dtype=np.float32))
+        k = P.DeviceBuffer.from_numpy(rng.standard_normal((L, kv), dtype=np.float32))
+        v = P.DeviceBuffer.from_numpy(rng.standard_normal((L, kv), dtype=np.float32))
+        o = P.DeviceBuffer(L * cfg.q_dim * 4)
+        qkv.append((q, k, v, o))
+    P.synchronize()
+
+    def launch(i):
+        c = i % n_copies
+        q, k, v, o = qkv[c]
+        P.check(P.lib.plh_attn_decode(L, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, S, 0, 0, L,
+                                      pos, q.ptr, k.ptr, v.ptr, keys[c].ptr, vals[c].ptr,
+                                      d_cos.ptr, d_sin.ptr, o.ptr), "plh_attn_decode")
+
+    for i in range(max(1, warmup)):   # also sizes the split-K workspace
+        launch(i)
+    P.synchronize()
+
+    with P.Graph() as g:
+        for i in range(steps):
+            launch(i)
+    g.launch()                     # untimed replay
+    P.synchronize()
+    e0, e1 = P.Event(), P.Event()
+    t0 = time.perf_counter()
+    e0.record()
+    g.launch()
+    e1.record()
+    P.synchronize()
+    wall = time.perf_counter() - t0
+    k_mean = e0.elapsed_ms(e1) / steps
+
+    algo = decode_bytes(w)
+    ms_step = wall * 1e3 / steps
+    achieved = algo / (k_mean * 1e-3) / 1e9
+    result = {
+        "value": algo / (ms_step * 1e-3) / 1e9,
+        "unit": "GB/s",
+        "ms_per_step": ms_step,
+        "us_per_token": ms_step * 1e3,
+        "kernel_us_mean": k_mean * 1e3,
+        "algorithmic_bytes_per_step": algo,
+        "cache_copies_rotated": n_copies,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
+                     "traffic": traffic_from_profiles(name)},
+    }
+    # keep what the CPU baseline needs (copy 0 before further appends)
+    result["_cpu_inputs"] = (cfg, keys[0], vals[0], qkv[0], cos_t, sin_t)
+    return result
+
+
+def cpu_baseline(P, w, res, budget_s=12.0):
+    """The oracle on one host thread over a bounded sample of the workload, and
+    a parity spot check of the GPU output of the same step."""
+    from oracle import oracle as O
+    cfg, dkey, dval, (dq, dk, dv, dout), cos_t, sin_t = res.pop("_cpu_inputs")
+    L, pos = cfg.n_layers, w["pos"]
+    kc = dkey.download(np.uint16, (cfg.cache_elems,))
+    vc = dval.download(np.uint16, (cfg.cache_elems,))
+    q = dq.download(np.float32, (L, cfg.q_dim))
+    k = dk.download(np.float32, (L, cfg.kv_dim))
+    v = dv.download(np.float32, (L, cfg.kv_dim))
+    gpu_out = dout.download(np.float32, (L, cfg.q_dim))
+    shp = O.Shape(L, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.max_seq_len,
+                  cfg.rope_freq_base, 0)
+    tokens, t_total, worst = 0, 0.0, 0.0
+    layers_done = 0
+    while t_total < budget_s and tokens < 50:
+        for l in range(L):
+            qi, ki = q[l].copy(), k[l].copy()
+            t0 = time.perf_counter()
+            ref = O.attn_decode(shp, l, pos, qi, ki, v[l], kc, vc, cos_t, sin_t)
+            t_total += time.perf_counter() - t0
+            layers_done += 1
+            if tokens == 0:
+                err = np.abs(gpu_out[l] - ref).reshape(-1, cfg.head_dim).max(1)
+                den = np.abs(ref).reshape(-1, cfg.head_dim).max(1)
+                worst = max(worst, float((err / den).max()))
+            if t_total >= budget_s:
+                break
+        tokens += 1
+    token_s = t_total / layers_done * L
+    algo = decode_bytes(w)
+    return {
+        "cpu_baseline": {"value": algo / token_s / 1e9, "unit": "GB/s", "cores": 1,
+                         "kind": "port", "us_per_token": token_s * 1e6,
+                         "sample": f"{layers_done} layer-steps ({layers_done / L:.2f} tokens) of "
+                                   f"{w['L']}-layer decode at pos {pos}, oracle on 1 thread"},
+        "parity_normwise_max": worst,
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="tinyllama_decode_pos2047", choices=sorted(WORKLOADS))
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU; the attention block needs no "
+                                   "collectives (see DESIGN.md for how it would shard)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import picolm_amd as P
+    P.init(0)
+    w = WORKLOADS[args.workload]
+    res = run_decode(P, w, args.steps, args.warmup, args.workload)
+    extra = {}
+    if not args.no_cpu:
+        extra = cpu_baseline(P, w, res)
+    else:
+        res.pop("_cpu_inputs", None)
+    line = {
+        "metric": METRIC,
+        "value": res.pop("value"),
+        "unit": res.pop("unit"),
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": res.pop("ms_per_step"),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic",
+        "config": {"workload": args.workload, "n_layers": w["L"], "n_heads": w["Hq"],
+                   "n_kv_heads": w["Hkv"], "head_dim": w["D"], "max_seq_len": w["S"],
+                   "pos": w["pos"], "rope_theta": w["theta"], "batch": 1},
+    }
+    line["hbm_frac"] = res["roofline"]["frac"]
+    line.update(res)
+    line.update(extra)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

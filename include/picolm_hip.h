@@ -1,0 +1,106 @@
+/*
+ * picolm_hip.h -- device-level C ABI of libpicolm_hip.so (gfx950 / MI355X).
+ *
+ * Plain pointers and sizes only.  Every pointer named "device" is HBM memory
+ * obtained from plh_malloc (or any hipMalloc allocation on the current
+ * device).  All work is queued on the library's single stream; calls return
+ * once the work is queued unless stated otherwise.
+ *
+ * Return convention (gpu.h:23-26 of the reference): 0 = done, -1 = not
+ * handled / failed; plh_last_error() then holds a message.
+ *
+ * KV-cache layout (model.h:98-100, model.c:802-805, bit-exact with the
+ * reference): uint16 fp16 bit patterns,
+ *     cache[((layer * max_seq_len + t) * n_kv_heads + kv_head) * head_dim + d]
+ * with key_cache and val_cache as two such blocks.  RoPE tables are
+ * [max_seq_len][head_dim/2] fp32, cos and sin (model.c:545-556).
+ */
+#ifndef PICOLM_HIP_H
+#define PICOLM_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PLH_ROPE_LLAMA 0 /* pairs (2i, 2i+1), model.h:15-18 */
+#define PLH_ROPE_QWEN 1  /* pairs (i, i + head_dim/2)        */
+
+/* ---- lifecycle (the device half of gpu_init / gpu_shutdown, gpu.h:12-29) -- */
+int plh_init(int device);
+void plh_shutdown(void);
+int plh_available(void);
+const char *plh_last_error(void);
+int plh_device_count(void);
+
+/* ---- device memory and synchronisation ---------------------------------- */
+void *plh_malloc(size_t bytes);
+int plh_free(void *dptr);
+int plh_memcpy_htod(void *dst, const void *src, size_t bytes);
+int plh_memcpy_dtoh(void *dst, const void *src, size_t bytes);
+int plh_memcpy_dtod(void *dst, const void *src, size_t bytes);
+int plh_memset(void *dst, int value, size_t bytes);
+int plh_synchronize(void);
+
+/* ---- timing on the library stream (hipEvents) -------------------------- */
+void *plh_event_create(void);
+int plh_event_record(void *ev);
+float plh_event_elapsed_ms(void *start, void *stop); /* waits for stop */
+void plh_event_destroy(void *ev);
+
+/* ---- HIP graphs of the library stream ------------------------------------ */
+/* Everything queued between begin and end (decode launches, event records) is
+ * captured instead of run; plh_graph_launch replays it.  Decode launches need
+ * no memset and allocate nothing once the workspace has been sized by one
+ * eager call of the same shape, so they can be captured. */
+int plh_capture_begin(void);
+void *plh_capture_end(void); /* instantiated graph, or NULL */
+int plh_graph_launch(void *graph);
+void plh_graph_destroy(void *graph);
+
+/* ---- host-side RoPE tables ---------------------------------------------- */
+/* Replaces model.c:545-556 (init_rope_tables) with the same libm calls in the
+ * same order, so the tables are bit-identical to the reference's on the same
+ * host.  cos_tab/sin_tab are HOST arrays [max_seq_len][head_dim/2]. */
+void plh_rope_tables_host(float *cos_tab, float *sin_tab, int max_seq_len,
+                          int head_dim, float freq_base);
+
+/* ---- fp16 conversion (quant.c:41-78 semantics) --------------------------- */
+/* dst[i] = fp32_to_fp16(src[i]) with round-half-away-from-zero, on device. */
+int plh_f32_to_f16(const float *src, uint16_t *dst, size_t n);
+/* Order-independent checksum of the conversion over the fp32 bit patterns
+ * [first, first+count): sum of (f16(x)+1) * (mix64(x)|1) mod 2^64.  Blocking;
+ * result written to *checksum (host).  Used to sweep all 2^32 inputs. */
+int plh_f16_checksum(uint64_t first, uint64_t count, uint64_t *checksum);
+
+/* ---- decode attention ---------------------------------------------------- */
+/* Replaces model.c:819-892 (rope, FP16 append, online-softmax GQA attention)
+ * for one token at position `pos`, for `n_launch_layers` consecutive layers
+ * starting at `layer0` in ONE launch (n_launch_layers = 1 is the per-layer
+ * call of model_forward_ex; more layers is the bench's all-layers step, not a
+ * reference call).  Per launched layer li (all device pointers):
+ *   q   + li*n_heads*head_dim     fp32 q (not rotated; left unmodified)
+ *   k,v + li*n_kv_heads*head_dim  fp32 k (not rotated), v
+ *   out + li*n_heads*head_dim     fp32 attention output
+ * The kernel rotates q and k with table row `pos`, writes f16(k_rot), f16(v)
+ * into row `pos` of layer layer0+li of the caches, and attends over rows
+ * 0..pos.  Supported: head_dim 64 or 128, n_heads % n_kv_heads == 0,
+ * |q| < 65504. */
+int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                    int max_seq_len, int rope_type, int layer0,
+                    int n_launch_layers, int pos, const float *q,
+                    const float *k, const float *v, uint16_t *key_cache,
+                    uint16_t *val_cache, const float *rope_cos,
+                    const float *rope_sin, float *out);
+
+/* Tuning knobs (bench sweeps).  key 1: decode target workgroups per launch
+ * (0 = default); key 2: decode minimum positions per split (multiple of 128). */
+int plh_set_tuning(int key, int value);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PICOLM_HIP_H */

@@ -1,0 +1,80 @@
+"""Loads the product library lib/libpicolm_hip.so and declares its C ABI
+(include/picolm_hip.h, include/gpu_hip.h).
+
+There is no fallback: if the library is missing this import fails loudly.
+Build it with `python -c "import __graft_entry__ as g; g.build()"` or
+`make -C picolm_amd`.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "lib", "libpicolm_hip.so")
+
+
+class PicolmHipError(RuntimeError):
+    """A call into libpicolm_hip returned -1 (not handled / failed)."""
+
+
+def _load() -> C.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is not built; run `make -C {HERE}` (hipcc, gfx950)")
+    return C.CDLL(LIB_PATH, mode=C.RTLD_GLOBAL)
+
+
+lib = _load()
+
+_vp = C.c_void_p
+_i = C.c_int
+_sz = C.c_size_t
+
+_SIGS = {
+    # lifecycle
+    "plh_init": (_i, [_i]),
+    "plh_shutdown": (None, []),
+    "plh_available": (_i, []),
+    "plh_last_error": (C.c_char_p, []),
+    "plh_device_count": (_i, []),
+    # memory
+    "plh_malloc": (_vp, [_sz]),
+    "plh_free": (_i, [_vp]),
+    "plh_memcpy_htod": (_i, [_vp, _vp, _sz]),
+    "plh_memcpy_dtoh": (_i, [_vp, _vp, _sz]),
+    "plh_memcpy_dtod": (_i, [_vp, _vp, _sz]),
+    "plh_memset": (_i, [_vp, _i, _sz]),
+    "plh_synchronize": (_i, []),
+    # events
+    "plh_event_create": (_vp, []),
+    "plh_event_record": (_i, [_vp]),
+    "plh_event_elapsed_ms": (C.c_float, [_vp, _vp]),
+    "plh_event_destroy": (None, [_vp]),
+    # graphs
+    "plh_capture_begin": (_i, []),
+    "plh_capture_end": (_vp, []),
+    "plh_graph_launch": (_i, [_vp]),
+    "plh_graph_destroy": (None, [_vp]),
+    # tables, conversion
+    "plh_rope_tables_host": (None, [_vp, _vp, _i, _i, C.c_float]),
+    "plh_f32_to_f16": (_i, [_vp, _vp, _sz]),
+    "plh_f16_checksum": (_i, [C.c_uint64, C.c_uint64, C.POINTER(C.c_uint64)]),
+    # attention
+    "plh_attn_decode": (_i, [_i] * 9 + [_vp] * 8),
+    "plh_set_tuning": (_i, [_i, _i]),
+}
+
+for _name, (_res, _args) in _SIGS.items():
+    _f = getattr(lib, _name)
+    _f.restype = _res
+    _f.argtypes = _args
+
+
+def last_error() -> str:
+    msg = lib.plh_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        raise PicolmHipError(f"{what} failed: {last_error()}")

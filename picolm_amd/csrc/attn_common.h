@@ -1,0 +1,81 @@
+// attn_common.h -- device helpers shared by the decode and prefill kernels.
+//
+// All HIP sources are compiled with -ffp-contract=off: the reference's
+// arithmetic (picolm/Makefile:2, -std=c11) never fuses a multiply into an
+// add, and the RoPE rotation and the fp16 rounding of the KV cache must be
+// bit-identical to it.  Where a fused multiply-add is harmless it is written
+// explicitly with __builtin_fmaf.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+namespace plh {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kNegBig = -1e30f;  // finite "minus infinity" of the online softmax
+
+// fp32 -> fp16 bits with the reference's rounding (quant.c:41-78): half an
+// fp16 ulp is added to the magnitude and the result truncated, i.e. round half
+// AWAY from zero; fp32 subnormals become signed zero; magnitudes below 2^-25
+// become signed zero; overflow gives +-inf; NaN gives sign|0x7E00.  The
+// hardware conversion rounds to nearest even and would differ on exact ties.
+__device__ __forceinline__ uint16_t f16_bits_rha(float f) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t sgn = (u >> 16) & 0x8000u;
+  uint32_t mag = u & 0x7FFFFFFFu;
+  uint32_t e32 = mag >> 23;
+  if (e32 == 0u) return (uint16_t)sgn;
+  if (e32 == 0xFFu) return (uint16_t)(sgn | 0x7C00u | ((mag & 0x7FFFFFu) ? 0x0200u : 0u));
+  int e16 = (int)e32 - 112;
+  if (e16 >= 31) return (uint16_t)(sgn | 0x7C00u);
+  if (e16 >= 1) return (uint16_t)(sgn | (((mag - (112u << 23)) + 0x1000u) >> 13));
+  if (e16 < -10) return (uint16_t)sgn;
+  uint32_t sig = (mag & 0x7FFFFFu) | 0x800000u;
+  uint32_t sh = (uint32_t)(14 - e16);
+  return (uint16_t)(sgn | ((sig + (1u << (sh - 1u))) >> sh));
+}
+
+// fp16 bits -> fp32.  The hardware widening is exact for every non-NaN input,
+// which is all the reference's fp16_to_fp32 (quant.c:11-39) does.
+__device__ __forceinline__ float f16_bits_to_f32(uint16_t h) {
+  _Float16 x = __builtin_bit_cast(_Float16, h);
+  return (float)x;
+}
+
+// One RoPE rotation as the reference writes it (tensor.c:583-601):
+// a' = a*c - b*s, b' = a*s + b*c, each product and sum rounded separately
+// (the translation unit is built with -ffp-contract=off).
+__device__ __forceinline__ void rope_rotate(float& a, float& b, float c, float s) {
+  float t0 = a * c;
+  float t1 = b * s;
+  float t2 = a * s;
+  float t3 = b * c;
+  a = t0 - t1;
+  b = t2 + t3;
+}
+
+// Splits an fp32 value into fp16 hi + lo so that an fp16 MFMA over both parts
+// reproduces the fp32 operand to ~2^-22 relative (hi keeps 11 bits, lo the
+// next 11).  Values must be below 65504 in magnitude.
+__device__ __forceinline__ void split_hi_lo(float x, _Float16& hi, _Float16& lo) {
+  hi = (_Float16)x;
+  lo = (_Float16)(x - (float)hi);
+}
+
+__device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+__device__ __forceinline__ float shfl_xor_f(float v, int mask) {
+  return __shfl_xor(v, mask, 64);
+}
+
+}  // namespace plh

@@ -1,0 +1,489 @@
+// attn_decode.hip -- single-token decode attention for gfx950.
+//
+// Replaces model.c:819-892: RoPE of q and k with table row `pos`, append of
+// f16(k_rot), f16(v) at cache row `pos`, and the online-softmax GQA attention
+// over rows 0..pos.  One launch may cover several layers (each layer is an
+// independent problem; the bench's all-layers step uses this).
+//
+// Work decomposition.  A "group" is (layer, kv head, block of <=16 q heads of
+// that kv head's GQA group); the group's positions are cut into `n_split`
+// splits of `split_len` rows; a workgroup (4 wavefronts) owns one (group,
+// split) unit and its waves take 32-row tiles of the split in turn.  Every
+// K/V byte of the group is read from HBM exactly once, whatever the GQA
+// factor, because all q heads of the group ride in the same MFMA.
+//
+// Per 32-row tile, per wave:
+//   S^T[t][h] = K[t][:] . q[h][:]   two v_mfma_f32_16x16x32_f16 row blocks,
+//                                   q split into fp16 hi+lo (two MFMAs each)
+//                                   so the product keeps ~fp32 precision;
+//   online softmax in the log2 domain (one max/exp2 per score);
+//   O^T[d][h] += V^T[d][t] P^T[t][h] with P split hi+lo; V is transposed
+//                                   through a per-wave LDS tile.
+// The S^T accumulator layout (lane = 16*g + h holds rows 4g..4g+3 of each
+// 16-row block) is used directly as the B operand of the PV product: the
+// K slots (g, j) of that product map to tile rows 4g+j (j<4) and 16+4g+j-4
+// (j>=4), and the LDS read of V^T uses the same map.
+//
+// Row `pos` itself is never read back from the cache: the workgroup owning
+// the last split computes k_rot/v for that row, writes the fp16 row, and
+// folds it into its result as one extra softmax partial.  No workgroup reads
+// memory another one writes until the split combine.
+//
+// Split combine: each workgroup merges its 4 waves (and the new row) through
+// LDS.  With one split it writes the normalised output; otherwise it stores
+// (max, sum, acc[D]) per head to the workspace and a second, small kernel
+// merges the splits of each group.  The two launches are ordered by the
+// stream; no workgroup waits on another, so there are no atomics, counters
+// or device-scope fences (on gfx950 each agent-scope fence writes back and
+// invalidates the XCD's whole L2).
+#include <math.h>
+
+#include "attn_common.h"
+#include "picolm_hip.h"
+#include "plh_internal.h"
+
+using namespace plh;
+
+namespace {
+
+constexpr int kWaves = 4;
+constexpr int kThreads = 64 * kWaves;
+constexpr int kTile = 32;
+
+// Loads q rows of this lane's head (zero for lanes beyond the group) and
+// rotates them with table row pos.  Lane (col, grp) gets
+// q[h][32*db + 8*grp + j] for db < D/32, j < 8.
+template <int D>
+__device__ __forceinline__ void load_q_rot(const DecodeArgs& a, int li, int kvh, int G, int h0,
+                                           int nh, int col, int grp, float (&qf)[D / 32][8]) {
+  constexpr int ND = D / 32;
+  const bool valid = col < nh;
+  const float* qrow = a.q + (size_t)li * a.n_heads * D + (size_t)(kvh * G + h0 + (valid ? col : 0)) * D;
+#pragma unroll
+  for (int db = 0; db < ND; ++db) {
+    float4 x0 = *(const float4*)(qrow + 32 * db + 8 * grp);
+    float4 x1 = *(const float4*)(qrow + 32 * db + 8 * grp + 4);
+    qf[db][0] = valid ? x0.x : 0.f;
+    qf[db][1] = valid ? x0.y : 0.f;
+    qf[db][2] = valid ? x0.z : 0.f;
+    qf[db][3] = valid ? x0.w : 0.f;
+    qf[db][4] = valid ? x1.x : 0.f;
+    qf[db][5] = valid ? x1.y : 0.f;
+    qf[db][6] = valid ? x1.z : 0.f;
+    qf[db][7] = valid ? x1.w : 0.f;
+  }
+  const float* cr = a.cos_t + (size_t)a.pos * (D / 2);
+  const float* sr = a.sin_t + (size_t)a.pos * (D / 2);
+  if (a.rope_type == PLH_ROPE_QWEN) {
+    // pairs (i, i + D/2): d and d + D/2 sit in blocks db and db + ND/2
+#pragma unroll
+    for (int db = 0; db < ND / 2; ++db) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        int i = 32 * db + 8 * grp + j;
+        rope_rotate(qf[db][j], qf[db + ND / 2][j], cr[i], sr[i]);
+      }
+    }
+  } else {
+    // pairs (2i, 2i+1) inside the lane's 8 consecutive elements
+#pragma unroll
+    for (int db = 0; db < ND; ++db) {
+      float4 c4 = *(const float4*)(cr + 16 * db + 4 * grp);
+      float4 s4 = *(const float4*)(sr + 16 * db + 4 * grp);
+      rope_rotate(qf[db][0], qf[db][1], c4.x, s4.x);
+      rope_rotate(qf[db][2], qf[db][3], c4.y, s4.y);
+      rope_rotate(qf[db][4], qf[db][5], c4.z, s4.z);
+      rope_rotate(qf[db][6], qf[db][7], c4.w, s4.w);
+    }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
+  constexpr int ND = D / 32;          // 32-wide d blocks of QK
+  constexpr int NO = D / 16;          // 16-wide d blocks of PV
+  constexpr int VP = D + 8;           // LDS pitch of a V tile row (halves)
+  constexpr int VCH = D / 8;          // 16-byte chunks per V row
+  constexpr int VROWS = 64 / VCH;     // V rows per wave-wide load
+  constexpr int VLOADS = kTile / VROWS;
+  constexpr int kVtileHalves = kWaves * kTile * VP;
+  constexpr int kCombFloats = (kWaves + 1) * 16 * (D + 2) + 2 * D;
+  constexpr int kSmemBytes =
+      (kVtileHalves * 2 > kCombFloats * 4) ? kVtileHalves * 2 : kCombFloats * 4;
+  __shared__ __align__(16) unsigned char smem[kSmemBytes];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+
+  // XCD-aware unit order: consecutive workgroup ids go to different XCDs, so
+  // each XCD takes a contiguous range of units (whole groups: per_xcd is a
+  // multiple of n_split) and a group's splits share one L2.
+  const int unit = (int)(blockIdx.x & 7) * a.per_xcd + (int)(blockIdx.x >> 3);
+  if (unit >= a.n_units) return;
+  const int split = unit % a.n_split;
+  const int group = unit / a.n_split;
+  const int hblk = group % a.n_hblk;
+  const int kvh = (group / a.n_hblk) % a.n_kv_heads;
+  const int li = group / (a.n_hblk * a.n_kv_heads);
+  const int layer = a.layer0 + li;
+  const int G = a.n_heads / a.n_kv_heads;
+  const int h0 = hblk * 16;
+  const int nh = min(16, G - h0);
+  const int kv_dim = a.n_kv_heads * D;
+  const int pos = a.pos;
+  const bool owner = split == a.n_split - 1;
+
+  // ---- q operands: rotated, split into fp16 hi + lo ------------------------
+  half8_t qhi[ND], qlo[ND];
+  {
+    float qf[ND][8];
+    load_q_rot<D>(a, li, kvh, G, h0, nh, col, grp, qf);
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        _Float16 hi, lo;
+        split_hi_lo(qf[db][j], hi, lo);
+        qhi[db][j] = hi;
+        qlo[db][j] = lo;
+      }
+  }
+
+  // ---- stream the split's cached rows [tb, te) ------------------------------
+  const int tb = split * a.split_len;
+  const int te = min(tb + a.split_len, pos);
+  const size_t row0 = (size_t)layer * a.max_seq_len;
+  const uint16_t* kbase = a.kc + (size_t)kvh * D;
+  const uint16_t* vbase = a.vc + (size_t)kvh * D;
+  _Float16* vt = reinterpret_cast<_Float16*>(smem) + wave * (kTile * VP);
+  const float sscale = a.score_scale;
+
+  float m = kNegBig, l = 0.f;
+  float4_t o[NO];
+#pragma unroll
+  for (int ob = 0; ob < NO; ++ob) o[ob] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int t0 = tb + wave * kTile; t0 < te; t0 += kWaves * kTile) {
+    const int tlast = te - 1;  // rows past the split are clamped here and masked
+    half8_t ka[2][ND];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int row = min(t0 + 16 * rb + col, tlast);
+      const uint16_t* p = kbase + (row0 + row) * kv_dim + 8 * grp;
+#pragma unroll
+      for (int db = 0; db < ND; ++db) ka[rb][db] = *(const half8_t*)(p + 32 * db);
+    }
+    half8_t vr[VLOADS];
+#pragma unroll
+    for (int i = 0; i < VLOADS; ++i) {
+      const int row = min(t0 + i * VROWS + lane / VCH, tlast);
+      vr[i] = *(const half8_t*)(vbase + (row0 + row) * kv_dim + 8 * (lane % VCH));
+    }
+
+    float4_t s[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      s[rb] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int db = 0; db < ND; ++db) {
+        s[rb] = mfma16x16x32(ka[rb][db], qhi[db], s[rb]);
+        s[rb] = mfma16x16x32(ka[rb][db], qlo[db], s[rb]);
+      }
+    }
+
+#pragma unroll
+    for (int i = 0; i < VLOADS; ++i)
+      *(half8_t*)(vt + (i * VROWS + lane / VCH) * VP + 8 * (lane % VCH)) = vr[i];
+
+    // online softmax over this tile (log2 domain)
+    float u[2][4];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = t0 + 16 * rb + 4 * grp + r;
+        float x = s[rb][r] * sscale;
+        x = (t <= tlast) ? x : -INFINITY;
+        u[rb][r] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
+    tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
+    const float mnew = fmaxf(m, tmax);
+    const float alpha = fast_exp2(m - mnew);
+    m = mnew;
+    half8_t ph, pl;
+    float psum = 0.f;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float p = fast_exp2(u[rb][r] - mnew);
+        psum += p;
+        _Float16 hi, lo;
+        split_hi_lo(p, hi, lo);
+        ph[4 * rb + r] = hi;
+        pl[4 * rb + r] = lo;
+      }
+    l = l * alpha + psum;
+#pragma unroll
+    for (int ob = 0; ob < NO; ++ob) o[ob] *= alpha;
+
+#pragma unroll
+    for (int ob = 0; ob < NO; ++ob) {
+      half8_t va;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int t = (j < 4) ? 4 * grp + j : 16 + 4 * grp + (j - 4);
+        va[j] = vt[t * VP + 16 * ob + col];
+      }
+      o[ob] = mfma16x16x32(va, ph, o[ob]);
+      o[ob] = mfma16x16x32(va, pl, o[ob]);
+    }
+  }
+
+  // per-head sum over the 4 lane groups
+  l += shfl_xor_f(l, 16);
+  l += shfl_xor_f(l, 32);
+
+  __syncthreads();  // V tiles are dead; the LDS now holds the combine slots
+  float* cm = reinterpret_cast<float*>(smem);          // [kWaves+1][16]
+  float* cl = cm + (kWaves + 1) * 16;                  // [kWaves+1][16]
+  float* co = cl + (kWaves + 1) * 16;                  // [kWaves][16][D]
+  float* cvn = co + kWaves * 16 * D;                   // [D] new V row (fp32)
+  float* ckn = cvn + D;                                // [D] new K row (fp32)
+  if (grp == 0) {
+    cm[wave * 16 + col] = m;
+    cl[wave * 16 + col] = l;
+  }
+#pragma unroll
+  for (int ob = 0; ob < NO; ++ob)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) co[(wave * 16 + col) * D + 16 * ob + 4 * grp + r] = o[ob][r];
+
+  // ---- row pos: rotate, round, store, and score it (owner, wave 0) ----------
+  if (owner && wave == 0) {
+    const float* kin = a.k + (size_t)li * kv_dim + (size_t)kvh * D;
+    const float* vin = a.v + (size_t)li * kv_dim + (size_t)kvh * D;
+    uint16_t* krow = a.kc + (row0 + pos) * kv_dim + (size_t)kvh * D;
+    uint16_t* vrow = a.vc + (row0 + pos) * kv_dim + (size_t)kvh * D;
+    const float* cr = a.cos_t + (size_t)pos * (D / 2);
+    const float* sr = a.sin_t + (size_t)pos * (D / 2);
+    for (int i = lane; i < D / 2; i += 64) {
+      const int i0 = (a.rope_type == PLH_ROPE_QWEN) ? i : 2 * i;
+      const int i1 = (a.rope_type == PLH_ROPE_QWEN) ? i + D / 2 : 2 * i + 1;
+      float k0 = kin[i0], k1 = kin[i1];
+      rope_rotate(k0, k1, cr[i], sr[i]);
+      const uint16_t b0 = f16_bits_rha(k0), b1 = f16_bits_rha(k1);
+      krow[i0] = b0;
+      krow[i1] = b1;
+      ckn[i0] = f16_bits_to_f32(b0);
+      ckn[i1] = f16_bits_to_f32(b1);
+    }
+    for (int d = lane; d < D; d += 64) {
+      const uint16_t b = f16_bits_rha(vin[d]);
+      vrow[d] = b;
+      cvn[d] = f16_bits_to_f32(b);
+    }
+    // ckn is written and read by the same wave; order the LDS accesses
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    float qf[ND][8];
+    load_q_rot<D>(a, li, kvh, G, h0, nh, col, grp, qf);
+    float sc = 0.f;
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) sc = __builtin_fmaf(qf[db][j], ckn[32 * db + 8 * grp + j], sc);
+    sc += shfl_xor_f(sc, 16);
+    sc += shfl_xor_f(sc, 32);
+    if (grp == 0) {
+      cm[kWaves * 16 + col] = sc * sscale;
+      cl[kWaves * 16 + col] = 1.0f;
+    }
+  }
+  __syncthreads();
+
+  // ---- merge the waves (and the new row) of this workgroup -------------------
+  const int q_dim = a.n_heads * D;
+  float* out_base = a.out + (size_t)li * q_dim + (size_t)(kvh * G + h0) * D;
+  for (int idx = tid; idx < nh * D; idx += kThreads) {
+    const int h = idx / D, d = idx - (idx / D) * D;
+    float M = kNegBig;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, cm[w * 16 + h]);
+    if (owner) M = fmaxf(M, cm[kWaves * 16 + h]);
+    float L = 0.f, O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float wt = fast_exp2(cm[w * 16 + h] - M);
+      L = __builtin_fmaf(cl[w * 16 + h], wt, L);
+      O = __builtin_fmaf(co[(w * 16 + h) * D + d], wt, O);
+    }
+    if (owner) {
+      const float wt = fast_exp2(cm[kWaves * 16 + h] - M);
+      L += wt;
+      O = __builtin_fmaf(cvn[d], wt, O);
+    }
+    if (a.n_split == 1) {
+      out_base[(size_t)h * D + d] = O * (1.0f / L);
+    } else {
+      a.part_o[((size_t)unit * 16 + h) * D + d] = O;
+      if (d == 0) {
+        a.part_m[(size_t)unit * 16 + h] = M;
+        a.part_l[(size_t)unit * 16 + h] = L;
+      }
+    }
+  }
+}
+
+// Merges the n_split partials of one group: out = sum_s O_s 2^(m_s-M) /
+// sum_s l_s 2^(m_s-M) with M the largest m_s.
+template <int D>
+__global__ __launch_bounds__(kThreads) void attn_decode_combine_kernel(DecodeArgs a) {
+  const int group = blockIdx.x;
+  const int hblk = group % a.n_hblk;
+  const int kvh = (group / a.n_hblk) % a.n_kv_heads;
+  const int li = group / (a.n_hblk * a.n_kv_heads);
+  const int G = a.n_heads / a.n_kv_heads;
+  const int h0 = hblk * 16;
+  const int nh = min(16, G - h0);
+  float* out_base = a.out + (size_t)li * a.n_heads * D + (size_t)(kvh * G + h0) * D;
+  const int u0 = group * a.n_split;
+  for (int idx = threadIdx.x; idx < nh * D; idx += kThreads) {
+    const int h = idx / D, d = idx - (idx / D) * D;
+    float M = kNegBig;
+    for (int sp = 0; sp < a.n_split; ++sp) M = fmaxf(M, a.part_m[(size_t)(u0 + sp) * 16 + h]);
+    float L = 0.f, O = 0.f;
+    for (int sp = 0; sp < a.n_split; ++sp) {
+      const float wt = fast_exp2(a.part_m[(size_t)(u0 + sp) * 16 + h] - M);
+      L = __builtin_fmaf(a.part_l[(size_t)(u0 + sp) * 16 + h], wt, L);
+      O = __builtin_fmaf(a.part_o[((size_t)(u0 + sp) * 16 + h) * D + d], wt, O);
+    }
+    out_base[(size_t)h * D + d] = O * (1.0f / L);
+  }
+}
+
+int g_target_units = 0;   // 0: 8 workgroups per CU
+int g_min_split = 128;
+
+}  // namespace
+
+extern "C" int plh_set_tuning(int key, int value) {
+  if (key == 1) {
+    g_target_units = value < 0 ? 0 : value;
+    return 0;
+  }
+  if (key == 2) {
+    if (value < 128 || value % 128) {
+      set_error("plh_set_tuning: minimum split must be a positive multiple of 128");
+      return -1;
+    }
+    g_min_split = value;
+    return 0;
+  }
+  set_error("plh_set_tuning: unknown key %d", key);
+  return -1;
+}
+
+extern "C" int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                               int max_seq_len, int rope_type, int layer0, int n_launch_layers,
+                               int pos, const float* q, const float* k, const float* v,
+                               uint16_t* key_cache, uint16_t* val_cache, const float* rope_cos,
+                               const float* rope_sin, float* out) {
+  Context& c = ctx();
+  if (!c.stream) {
+    set_error("plh_attn_decode: library not initialised");
+    return -1;
+  }
+  if (head_dim != 64 && head_dim != 128) {
+    set_error("plh_attn_decode: head_dim %d not supported (64, 128)", head_dim);
+    return -1;
+  }
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads) {
+    set_error("plh_attn_decode: n_heads %d must be a multiple of n_kv_heads %d", n_heads,
+              n_kv_heads);
+    return -1;
+  }
+  if (rope_type != PLH_ROPE_LLAMA && rope_type != PLH_ROPE_QWEN) {
+    set_error("plh_attn_decode: unknown rope_type %d", rope_type);
+    return -1;
+  }
+  if (max_seq_len <= 0 || pos < 0 || pos >= max_seq_len) {
+    set_error("plh_attn_decode: pos %d outside [0, %d)", pos, max_seq_len);
+    return -1;
+  }
+  if (layer0 < 0 || n_launch_layers <= 0 || layer0 + n_launch_layers > n_layers) {
+    set_error("plh_attn_decode: layers [%d, %d) outside [0, %d)", layer0,
+              layer0 + n_launch_layers, n_layers);
+    return -1;
+  }
+  if (!q || !k || !v || !key_cache || !val_cache || !rope_cos || !rope_sin || !out) {
+    set_error("plh_attn_decode: null pointer");
+    return -1;
+  }
+
+  const int G = n_heads / n_kv_heads;
+  const int n_hblk = (G + 15) / 16;
+  const int n_groups = n_launch_layers * n_kv_heads * n_hblk;
+  const int npos = pos + 1;
+  // Split plan: enough workgroups to fill the chip, each split at least
+  // g_min_split rows, split length a multiple of 4 waves x 32 rows.
+  const int target = g_target_units > 0 ? g_target_units : 8 * (c.num_cus > 0 ? c.num_cus : 256);
+  long want_split = ((long)npos * n_groups + target - 1) / target;
+  if (want_split < g_min_split) want_split = g_min_split;
+  want_split = (want_split + 127) / 128 * 128;
+  const int split_len = (int)want_split;
+  const int n_split = (npos + split_len - 1) / split_len;
+  const int n_units = n_groups * n_split;
+  const int groups_per_xcd = (n_groups + 7) / 8;
+  const int per_xcd = groups_per_xcd * n_split;
+
+  DecodeArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.kc = key_cache;
+  a.vc = val_cache;
+  a.cos_t = rope_cos;
+  a.sin_t = rope_sin;
+  a.out = out;
+  a.part_o = a.part_m = a.part_l = nullptr;
+  if (n_split > 1) {
+    const size_t po = (size_t)n_units * 16 * head_dim * sizeof(float);
+    const size_t pm = (size_t)n_units * 16 * sizeof(float);
+    if (ensure_workspace(po + 2 * pm)) return -1;
+    a.part_o = (float*)c.ws;
+    a.part_m = (float*)((char*)c.ws + po);
+    a.part_l = (float*)((char*)c.ws + po + pm);
+  }
+  a.layer0 = layer0;
+  a.n_launch_layers = n_launch_layers;
+  a.n_heads = n_heads;
+  a.n_kv_heads = n_kv_heads;
+  a.max_seq_len = max_seq_len;
+  a.pos = pos;
+  a.rope_type = rope_type;
+  a.n_hblk = n_hblk;
+  a.n_split = n_split;
+  a.split_len = split_len;
+  a.n_units = n_units;
+  a.per_xcd = per_xcd;
+  a.score_scale = kLog2e / sqrtf((float)head_dim);
+
+  const dim3 grid((unsigned)(8 * per_xcd)), block(kThreads);
+  if (head_dim == 64)
+    hipLaunchKernelGGL(attn_decode_kernel<64>, grid, block, 0, c.stream, a);
+  else
+    hipLaunchKernelGGL(attn_decode_kernel<128>, grid, block, 0, c.stream, a);
+  if (check_hip(hipGetLastError(), "attn_decode_kernel")) return -1;
+  if (n_split == 1) return 0;
+  if (head_dim == 64)
+    hipLaunchKernelGGL(attn_decode_combine_kernel<64>, dim3((unsigned)n_groups), block, 0,
+                       c.stream, a);
+  else
+    hipLaunchKernelGGL(attn_decode_combine_kernel<128>, dim3((unsigned)n_groups), block, 0,
+                       c.stream, a);
+  return check_hip(hipGetLastError(), "attn_decode_combine_kernel");
+}

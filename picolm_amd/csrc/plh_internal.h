@@ -1,0 +1,50 @@
+// plh_internal.h -- library-internal state and kernel argument blocks.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace plh {
+
+// One device, one stream, one growable workspace: the library follows the
+// reference backend's single global state (gpu.c:34-83); it is not
+// re-entrant and is driven from one host thread.
+struct Context {
+  int device = -1;
+  hipStream_t stream = nullptr;
+  void* ws = nullptr;          // split-K partials
+  size_t ws_bytes = 0;
+  int num_cus = 0;
+};
+
+Context& ctx();
+void set_error(const char* fmt, ...);
+int check_hip(hipError_t e, const char* what);
+
+// Makes sure the workspace holds at least `bytes`.  Growing it waits for the
+// queued work (which may still read the old one).  Returns 0 or -1.
+int ensure_workspace(size_t bytes);
+
+// Decode kernel arguments (all device pointers).
+struct DecodeArgs {
+  const float* q;          // [n_launch_layers][n_heads*D]
+  const float* k;          // [n_launch_layers][kv_dim]
+  const float* v;          // [n_launch_layers][kv_dim]
+  uint16_t* kc;            // [n_layers][S][kv_dim] fp16 bits
+  uint16_t* vc;
+  const float* cos_t;      // [S][D/2]
+  const float* sin_t;
+  float* out;              // [n_launch_layers][n_heads*D]
+  float* part_o;           // [n_units][16][D]
+  float* part_m;           // [n_units][16]
+  float* part_l;           // [n_units][16]
+  int layer0, n_launch_layers, n_heads, n_kv_heads, max_seq_len, pos, rope_type;
+  int n_hblk;              // ceil(G / 16): q-head blocks per kv head
+  int n_split, split_len;  // position splits per (layer, kv head, head block)
+  int n_units;             // n_groups * n_split
+  int per_xcd;             // units per XCD slice of the grid
+  float score_scale;       // log2(e) / sqrt(D)
+};
+
+}  // namespace plh

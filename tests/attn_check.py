@@ -1,0 +1,56 @@
+"""Tolerance and input helpers shared by the parity tests.
+
+Tolerance (written here once, used by every attention parity test):
+  per q head, normwise   max_d |gpu - ref| / max_d |ref|          <= tol
+  elementwise            |gpu - ref| <= tol * (|ref| + rms(ref_head))
+with tol = 1e-3, or 1e-2 for softmax-sensitive long contexts (more than 4096
+cached rows), following the attention-output bound of the build's target.
+The fp16 KV cache is compared bit for bit.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+TOL = 1e-3
+TOL_LONG = 1e-2
+
+
+def tol_for(n_rows: int) -> float:
+    return TOL_LONG if n_rows > 4096 else TOL
+
+
+def attn_errors(gpu: np.ndarray, ref: np.ndarray, head_dim: int):
+    g = gpu.reshape(-1, head_dim).astype(np.float64)
+    r = ref.reshape(-1, head_dim).astype(np.float64)
+    err = np.abs(g - r)
+    normwise = err.max(axis=1) / np.maximum(np.abs(r).max(axis=1), 1e-30)
+    rms = np.sqrt((r ** 2).mean(axis=1, keepdims=True))
+    elem = err / (np.abs(r) + rms + 1e-30)
+    return float(normwise.max()), float(elem.max())
+
+
+def assert_attn_close(gpu, ref, head_dim, tol=TOL, what=""):
+    assert np.all(np.isfinite(gpu)), f"{what}: non-finite output"
+    nw, el = attn_errors(gpu, ref, head_dim)
+    print(f"[parity] {what}: normwise {nw:.3e} elementwise {el:.3e} (tol {tol:g})", flush=True)
+    assert nw <= tol and el <= tol, f"{what}: normwise {nw:.3e} elementwise {el:.3e} > {tol:g}"
+    return nw, el
+
+
+def normal_f32(rng, shape, scale=1.0):
+    return (rng.standard_normal(shape) * scale).astype(np.float32)
+
+
+def filled_cache(O, cfg, rows: int, rng, poison_after=False):
+    """K and V caches [L][S][kv_dim] with rows 0..rows-1 holding N(0,1)
+    rounded by the reference's fp32_to_fp16; other rows zero (or NaN)."""
+    L, S, kv = cfg.n_layers, cfg.max_seq_len, cfg.kv_dim
+    kc = np.zeros((L, S, kv), np.uint16)
+    vc = np.zeros((L, S, kv), np.uint16)
+    if rows:
+        kc[:, :rows] = O.f32_to_f16(normal_f32(rng, (L, rows, kv)))
+        vc[:, :rows] = O.f32_to_f16(normal_f32(rng, (L, rows, kv)))
+    if poison_after:
+        kc[:, rows:] = 0x7E00
+        vc[:, rows:] = 0x7E00
+    return kc.reshape(-1), vc.reshape(-1)

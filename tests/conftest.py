@@ -24,3 +24,13 @@ def oracle_mod():
 REF_LIB = os.path.join(ROOT, "oracle", "_ref", "libpicolm_ref.so")
 needs_ref = pytest.mark.skipif(not os.path.exists(REF_LIB),
                                reason="reference harness not built (make -C oracle ref)")
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """The product library on device 0 (tests marked gpu only)."""
+    import picolm_amd as P
+    if P.lib.plh_device_count() < 1:
+        pytest.fail("no HIP device visible: gpu tests need an MI355X")
+    P.init(0)
+    return P
