@@ -11,7 +11,8 @@ import ctypes as C
 import os
 
 HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(HERE, "lib", "libpicolm_hip.so")
+# PICOLM_HIP_LIB points at a libpicolm_hip.so built elsewhere (same ABI).
+LIB_PATH = os.environ.get("PICOLM_HIP_LIB") or os.path.join(HERE, "lib", "libpicolm_hip.so")
 
 
 class PicolmHipError(RuntimeError):

@@ -8,9 +8,10 @@
 // Work decomposition.  A "group" is (layer, kv head, block of <=16 q heads of
 // that kv head's GQA group); the group's positions are cut into `n_split`
 // splits of `split_len` rows; a workgroup (4 wavefronts) owns one (group,
-// split) unit and its waves take 32-row tiles of the split in turn.  Every
-// K/V byte of the group is read from HBM exactly once, whatever the GQA
-// factor, because all q heads of the group ride in the same MFMA.
+// split) unit and its waves take 32-row tiles of the split in turn, keeping
+// the loads of the next 2-4 tiles in flight while one tile is computed.  Every K/V
+// byte of the group is read from HBM exactly once, whatever the GQA factor,
+// because all q heads of the group ride in the same MFMA.
 //
 // Per 32-row tile, per wave:
 //   S^T[t][h] = K[t][:] . q[h][:]   two v_mfma_f32_16x16x32_f16 row blocks,
@@ -27,15 +28,15 @@
 // Row `pos` itself is never read back from the cache: the workgroup owning
 // the last split computes k_rot/v for that row, writes the fp16 row, and
 // folds it into its result as one extra softmax partial.  No workgroup reads
-// memory another one writes until the split combine.
+// memory another one writes, except the split partials below.
 //
 // Split combine: each workgroup merges its 4 waves (and the new row) through
-// LDS.  With one split it writes the normalised output; otherwise it stores
-// (max, sum, acc[D]) per head to the workspace and a second, small kernel
-// merges the splits of each group.  The two launches are ordered by the
-// stream; no workgroup waits on another, so there are no atomics, counters
-// or device-scope fences (on gfx950 each agent-scope fence writes back and
-// invalidates the XCD's whole L2).
+// LDS.  With one split it writes the normalised output.  Otherwise it stores
+// (max, sum, acc[D]) per head to the workspace and a second, small kernel on
+// the same stream merges the splits of each group.  No workgroup waits on
+// another: on gfx950 an agent-scope release fence writes back the XCD's whole
+// L2, and a last-arriving-workgroup merge (one such fence per workgroup)
+// measured several times slower than the second launch.
 #include <math.h>
 
 #include "attn_common.h"
@@ -50,51 +51,219 @@ constexpr int kWaves = 4;
 constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 32;
 
-// Loads q rows of this lane's head (zero for lanes beyond the group) and
-// rotates them with table row pos.  Lane (col, grp) gets
-// q[h][32*db + 8*grp + j] for db < D/32, j < 8.
+// Tiles in flight per wave: head_dim 64 keeps 4 tiles (32 KB) of loads in
+// registers, head_dim 128 keeps 2 (also 32 KB).
 template <int D>
-__device__ __forceinline__ void load_q_rot(const DecodeArgs& a, int li, int kvh, int G, int h0,
-                                           int nh, int col, int grp, float (&qf)[D / 32][8]) {
+struct Prefetch {
+  static constexpr int depth = D == 64 ? 4 : 2;
+};
+
+template <int D>
+struct Tile {
+  static constexpr int ND = D / 32;       // 32-wide d blocks of QK
+  static constexpr int VCH = D / 8;       // 16-byte chunks per V row
+  static constexpr int VROWS = 64 / VCH;  // V rows per wave-wide load
+  static constexpr int VLOADS = kTile / VROWS;
+  half8_t k[2][ND];
+  half8_t v[VLOADS];
+};
+
+// q rows of this lane's head and their RoPE table entries, loaded before the
+// first K/V tiles so that waiting for them (the vector-memory counter is
+// in-order) does not wait for the tiles.  Lane (col, grp) holds
+// q[h][32*db + 8*grp + j] for db < D/32, j < 8 (zero for lanes beyond the
+// group), and the D/8 table entries its pairs need.
+template <int D>
+struct QRaw {
+  float q[D / 32][8];
+  float c[D / 8], s[D / 8];
+};
+
+template <int D>
+__device__ __forceinline__ void load_q_raw(const DecodeArgs& a, int li, int kvh, int G, int h0,
+                                           int nh, int col, int grp, QRaw<D>& r) {
   constexpr int ND = D / 32;
-  const bool valid = col < nh;
-  const float* qrow = a.q + (size_t)li * a.n_heads * D + (size_t)(kvh * G + h0 + (valid ? col : 0)) * D;
+  const bool valid = col < nh;  // lanes past the group load head h0's row; rope_q zeroes them
+  const float* qrow =
+      a.q + (size_t)li * a.n_heads * D + (size_t)(kvh * G + h0 + (valid ? col : 0)) * D;
 #pragma unroll
   for (int db = 0; db < ND; ++db) {
     float4 x0 = *(const float4*)(qrow + 32 * db + 8 * grp);
     float4 x1 = *(const float4*)(qrow + 32 * db + 8 * grp + 4);
-    qf[db][0] = valid ? x0.x : 0.f;
-    qf[db][1] = valid ? x0.y : 0.f;
-    qf[db][2] = valid ? x0.z : 0.f;
-    qf[db][3] = valid ? x0.w : 0.f;
-    qf[db][4] = valid ? x1.x : 0.f;
-    qf[db][5] = valid ? x1.y : 0.f;
-    qf[db][6] = valid ? x1.z : 0.f;
-    qf[db][7] = valid ? x1.w : 0.f;
+    r.q[db][0] = x0.x, r.q[db][1] = x0.y, r.q[db][2] = x0.z, r.q[db][3] = x0.w;
+    r.q[db][4] = x1.x, r.q[db][5] = x1.y, r.q[db][6] = x1.z, r.q[db][7] = x1.w;
   }
   const float* cr = a.cos_t + (size_t)a.pos * (D / 2);
   const float* sr = a.sin_t + (size_t)a.pos * (D / 2);
   if (a.rope_type == PLH_ROPE_QWEN) {
-    // pairs (i, i + D/2): d and d + D/2 sit in blocks db and db + ND/2
+    // pairs (i, i + D/2), i = 32*db + 8*grp + j for db < ND/2
 #pragma unroll
-    for (int db = 0; db < ND / 2; ++db) {
+    for (int db = 0; db < ND / 2; ++db)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        int i = 32 * db + 8 * grp + j;
-        rope_rotate(qf[db][j], qf[db + ND / 2][j], cr[i], sr[i]);
+      for (int hh = 0; hh < 2; ++hh) {
+        float4 c4 = *(const float4*)(cr + 32 * db + 8 * grp + 4 * hh);
+        float4 s4 = *(const float4*)(sr + 32 * db + 8 * grp + 4 * hh);
+        const int o = db * 8 + 4 * hh;
+        r.c[o] = c4.x, r.c[o + 1] = c4.y, r.c[o + 2] = c4.z, r.c[o + 3] = c4.w;
+        r.s[o] = s4.x, r.s[o + 1] = s4.y, r.s[o + 2] = s4.z, r.s[o + 3] = s4.w;
       }
-    }
   } else {
-    // pairs (2i, 2i+1) inside the lane's 8 consecutive elements
+    // pairs (2i, 2i+1), i = 16*db + 4*grp + jj
 #pragma unroll
     for (int db = 0; db < ND; ++db) {
       float4 c4 = *(const float4*)(cr + 16 * db + 4 * grp);
       float4 s4 = *(const float4*)(sr + 16 * db + 4 * grp);
-      rope_rotate(qf[db][0], qf[db][1], c4.x, s4.x);
-      rope_rotate(qf[db][2], qf[db][3], c4.y, s4.y);
-      rope_rotate(qf[db][4], qf[db][5], c4.z, s4.z);
-      rope_rotate(qf[db][6], qf[db][7], c4.w, s4.w);
+      const int o = db * 4;
+      r.c[o] = c4.x, r.c[o + 1] = c4.y, r.c[o + 2] = c4.z, r.c[o + 3] = c4.w;
+      r.s[o] = s4.x, r.s[o + 1] = s4.y, r.s[o + 2] = s4.z, r.s[o + 3] = s4.w;
     }
+  }
+}
+
+// Rotates the loaded q rows in place with the reference's pairing; lanes
+// beyond the group (valid false) get zero rows.
+template <int D>
+__device__ __forceinline__ void rope_q(int rope_type, bool valid, QRaw<D>& r) {
+  constexpr int ND = D / 32;
+#pragma unroll
+  for (int db = 0; db < ND; ++db)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) r.q[db][j] = valid ? r.q[db][j] : 0.f;
+  if (rope_type == PLH_ROPE_QWEN) {
+#pragma unroll
+    for (int db = 0; db < ND / 2; ++db)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        rope_rotate(r.q[db][j], r.q[db + ND / 2][j], r.c[db * 8 + j], r.s[db * 8 + j]);
+  } else {
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj)
+        rope_rotate(r.q[db][2 * jj], r.q[db][2 * jj + 1], r.c[db * 4 + jj], r.s[db * 4 + jj]);
+  }
+}
+
+// Inputs of the appended row pos that lane `lane` of the owner's wave 0 needs:
+// rope pairs i = lane (+64) of k, and v elements lane (+64).
+template <int D>
+struct RowRaw {
+  static constexpr int NP = (D / 2 + 63) / 64;
+  static constexpr int NV = (D + 63) / 64;
+  float k0[NP], k1[NP], c[NP], s[NP];
+  float v[NV];
+};
+
+template <int D>
+__device__ __forceinline__ void load_row_raw(const DecodeArgs& a, int li, int kvh, int lane,
+                                             RowRaw<D>& r) {
+  const int kv_dim = a.n_kv_heads * D;
+  const float* kin = a.k + (size_t)li * kv_dim + (size_t)kvh * D;
+  const float* vin = a.v + (size_t)li * kv_dim + (size_t)kvh * D;
+  const float* cr = a.cos_t + (size_t)a.pos * (D / 2);
+  const float* sr = a.sin_t + (size_t)a.pos * (D / 2);
+#pragma unroll
+  for (int u = 0; u < RowRaw<D>::NP; ++u) {
+    const int i = min(lane + 64 * u, D / 2 - 1);
+    const int i0 = (a.rope_type == PLH_ROPE_QWEN) ? i : 2 * i;
+    const int i1 = (a.rope_type == PLH_ROPE_QWEN) ? i + D / 2 : 2 * i + 1;
+    r.k0[u] = kin[i0];
+    r.k1[u] = kin[i1];
+    r.c[u] = cr[i];
+    r.s[u] = sr[i];
+  }
+#pragma unroll
+  for (int u = 0; u < RowRaw<D>::NV; ++u) r.v[u] = vin[min(lane + 64 * u, D - 1)];
+}
+
+// Issues the loads of the 32-row tile starting at t0; rows past tlast are
+// clamped to tlast (always a valid cached row) and masked out of the softmax.
+template <int D>
+__device__ __forceinline__ void load_tile(Tile<D>& T, const uint16_t* kbase,
+                                          const uint16_t* vbase, int kv_dim, int t0, int tlast,
+                                          int lane, int col, int grp) {
+  using TT = Tile<D>;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    const int row = min(t0 + 16 * rb + col, tlast);
+    const uint16_t* p = kbase + (size_t)row * kv_dim + 8 * grp;
+#pragma unroll
+    for (int db = 0; db < TT::ND; ++db) T.k[rb][db] = *(const half8_t*)(p + 32 * db);
+  }
+#pragma unroll
+  for (int i = 0; i < TT::VLOADS; ++i) {
+    const int row = min(t0 + i * TT::VROWS + lane / TT::VCH, tlast);
+    T.v[i] = *(const half8_t*)(vbase + (size_t)row * kv_dim + 8 * (lane % TT::VCH));
+  }
+}
+
+template <int D>
+__device__ __forceinline__ void process_tile(const Tile<D>& T, const half8_t (&qhi)[D / 32],
+                                             const half8_t (&qlo)[D / 32], _Float16* vt, int t0,
+                                             int tlast, int lane, int col, int grp, float sscale,
+                                             float& m, float& l, float4_t (&o)[D / 16]) {
+  using TT = Tile<D>;
+  constexpr int NO = D / 16;
+  constexpr int VP = D + 8;
+  float4_t s[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) {
+    s[rb] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int db = 0; db < TT::ND; ++db) {
+      s[rb] = mfma16x16x32(T.k[rb][db], qhi[db], s[rb]);
+      s[rb] = mfma16x16x32(T.k[rb][db], qlo[db], s[rb]);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < TT::VLOADS; ++i)
+    *(half8_t*)(vt + (i * TT::VROWS + lane / TT::VCH) * VP + 8 * (lane % TT::VCH)) = T.v[i];
+
+  // online softmax over this tile (log2 domain)
+  float u[2][4];
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int t = t0 + 16 * rb + 4 * grp + r;
+      float x = s[rb][r] * sscale;
+      x = (t <= tlast) ? x : -INFINITY;
+      u[rb][r] = x;
+      tmax = fmaxf(tmax, x);
+    }
+  tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
+  tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
+  const float mnew = fmaxf(m, tmax);
+  const float alpha = fast_exp2(m - mnew);
+  m = mnew;
+  half8_t ph, pl;
+  float psum = 0.f;
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const float p = fast_exp2(u[rb][r] - mnew);
+      psum += p;
+      _Float16 hi, lo;
+      split_hi_lo(p, hi, lo);
+      ph[4 * rb + r] = hi;
+      pl[4 * rb + r] = lo;
+    }
+  l = l * alpha + psum;
+#pragma unroll
+  for (int ob = 0; ob < NO; ++ob) o[ob] *= alpha;
+
+#pragma unroll
+  for (int ob = 0; ob < NO; ++ob) {
+    half8_t va;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int t = (j < 4) ? 4 * grp + j : 16 + 4 * grp + (j - 4);
+      va[j] = vt[t * VP + 16 * ob + col];
+    }
+    o[ob] = mfma16x16x32(va, ph, o[ob]);
+    o[ob] = mfma16x16x32(va, pl, o[ob]);
   }
 }
 
@@ -103,11 +272,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
   constexpr int ND = D / 32;          // 32-wide d blocks of QK
   constexpr int NO = D / 16;          // 16-wide d blocks of PV
   constexpr int VP = D + 8;           // LDS pitch of a V tile row (halves)
-  constexpr int VCH = D / 8;          // 16-byte chunks per V row
-  constexpr int VROWS = 64 / VCH;     // V rows per wave-wide load
-  constexpr int VLOADS = kTile / VROWS;
   constexpr int kVtileHalves = kWaves * kTile * VP;
-  constexpr int kCombFloats = (kWaves + 1) * 16 * (D + 2) + 2 * D;
+  constexpr int kCombFloats = kWaves * 16 * (D + 2);
   constexpr int kSmemBytes =
       (kVtileHalves * 2 > kCombFloats * 4) ? kVtileHalves * 2 : kCombFloats * 4;
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
@@ -134,113 +300,111 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
   const int pos = a.pos;
   const bool owner = split == a.n_split - 1;
 
+  // ---- loads: q (and the owner's new-row inputs) first, then the first tiles
+  const int tb = split * a.split_len;
+  const int te = min(tb + a.split_len, pos);   // cached rows [tb, te); row pos is new
+  const int tlast = te - 1;
+  const size_t row0 = (size_t)layer * a.max_seq_len;
+  const uint16_t* kbase = a.kc + row0 * kv_dim + (size_t)kvh * D;
+  const uint16_t* vbase = a.vc + row0 * kv_dim + (size_t)kvh * D;
+  constexpr int kStride = kWaves * kTile;
+  const int tw = tb + wave * kTile;  // this wave's first row; its tiles are kStride apart
+  const bool new_row = owner && wave == 0;
+
+  QRaw<D> qr;
+  load_q_raw<D>(a, li, kvh, G, h0, nh, col, grp, qr);
+  RowRaw<D> rr;
+  if (new_row) load_row_raw<D>(a, li, kvh, lane, rr);
+
+  // Rolling prefetch of depth PF: tile i of the wave lives in buffer i % PF,
+  // and refilling a buffer with tile i + PF starts as soon as tile i is done.
+  // Every load is issued unconditionally (tiles past the range re-read row
+  // tlast and are masked), so the compiler's wait counts stay exact and the
+  // prefetch is never drained early.  A split with no cached rows (te <= tb)
+  // skips the stream as a whole.
+  constexpr int PF = Prefetch<D>::depth;
+  const bool has_rows = te > tb;
+  Tile<D> buf[PF];
+  if (has_rows) {
+#pragma unroll
+    for (int j = 0; j < PF; ++j)
+      load_tile<D>(buf[j], kbase, vbase, kv_dim, tw + j * kStride, tlast, lane, col, grp);
+  }
+
   // ---- q operands: rotated, split into fp16 hi + lo ------------------------
+  // The owner's wave 0 also appends row pos (k rotated, both rows rounded)
+  // and scores it against the fp32 q rows.
+  __shared__ float s_knew[D], s_vnew[D], s_mnew[16];
   half8_t qhi[ND], qlo[ND];
-  {
-    float qf[ND][8];
-    load_q_rot<D>(a, li, kvh, G, h0, nh, col, grp, qf);
+  // keep the scheduler from hoisting q's uses (and their waits) above the tiles
+  __builtin_amdgcn_sched_barrier(0);
+  rope_q<D>(a.rope_type, col < nh, qr);
+#pragma unroll
+  for (int db = 0; db < ND; ++db)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      _Float16 hi, lo;
+      split_hi_lo(qr.q[db][j], hi, lo);
+      qhi[db][j] = hi;
+      qlo[db][j] = lo;
+    }
+  if (new_row) {
+    uint16_t* krow = a.kc + (row0 + pos) * kv_dim + (size_t)kvh * D;
+    uint16_t* vrow = a.vc + (row0 + pos) * kv_dim + (size_t)kvh * D;
+#pragma unroll
+    for (int u = 0; u < RowRaw<D>::NP; ++u) {
+      const int i = lane + 64 * u;
+      if (i < D / 2) {
+        const int i0 = (a.rope_type == PLH_ROPE_QWEN) ? i : 2 * i;
+        const int i1 = (a.rope_type == PLH_ROPE_QWEN) ? i + D / 2 : 2 * i + 1;
+        float k0 = rr.k0[u], k1 = rr.k1[u];
+        rope_rotate(k0, k1, rr.c[u], rr.s[u]);
+        const uint16_t b0 = f16_bits_rha(k0), b1 = f16_bits_rha(k1);
+        krow[i0] = b0;
+        krow[i1] = b1;
+        s_knew[i0] = f16_bits_to_f32(b0);
+        s_knew[i1] = f16_bits_to_f32(b1);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < RowRaw<D>::NV; ++u) {
+      const int d = lane + 64 * u;
+      if (d < D) {
+        const uint16_t b = f16_bits_rha(rr.v[u]);
+        vrow[d] = b;
+        s_vnew[d] = f16_bits_to_f32(b);
+      }
+    }
+    // s_knew is written and read by this wave only; order the LDS accesses
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+    float sc = 0.f;
 #pragma unroll
     for (int db = 0; db < ND; ++db)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        _Float16 hi, lo;
-        split_hi_lo(qf[db][j], hi, lo);
-        qhi[db][j] = hi;
-        qlo[db][j] = lo;
-      }
+      for (int j = 0; j < 8; ++j)
+        sc = __builtin_fmaf(qr.q[db][j], s_knew[32 * db + 8 * grp + j], sc);
+    sc += shfl_xor_f(sc, 16);
+    sc += shfl_xor_f(sc, 32);
+    if (grp == 0) s_mnew[col] = sc * a.score_scale;
   }
 
-  // ---- stream the split's cached rows [tb, te) ------------------------------
-  const int tb = split * a.split_len;
-  const int te = min(tb + a.split_len, pos);
-  const size_t row0 = (size_t)layer * a.max_seq_len;
-  const uint16_t* kbase = a.kc + (size_t)kvh * D;
-  const uint16_t* vbase = a.vc + (size_t)kvh * D;
+  // ---- stream the split's cached rows, one tile ahead ----------------------
   _Float16* vt = reinterpret_cast<_Float16*>(smem) + wave * (kTile * VP);
   const float sscale = a.score_scale;
-
   float m = kNegBig, l = 0.f;
   float4_t o[NO];
 #pragma unroll
   for (int ob = 0; ob < NO; ++ob) o[ob] = float4_t{0.f, 0.f, 0.f, 0.f};
 
-  for (int t0 = tb + wave * kTile; t0 < te; t0 += kWaves * kTile) {
-    const int tlast = te - 1;  // rows past the split are clamped here and masked
-    half8_t ka[2][ND];
+  if (has_rows) {
+    for (int base = tw; base < te; base += PF * kStride) {
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      const int row = min(t0 + 16 * rb + col, tlast);
-      const uint16_t* p = kbase + (row0 + row) * kv_dim + 8 * grp;
-#pragma unroll
-      for (int db = 0; db < ND; ++db) ka[rb][db] = *(const half8_t*)(p + 32 * db);
-    }
-    half8_t vr[VLOADS];
-#pragma unroll
-    for (int i = 0; i < VLOADS; ++i) {
-      const int row = min(t0 + i * VROWS + lane / VCH, tlast);
-      vr[i] = *(const half8_t*)(vbase + (row0 + row) * kv_dim + 8 * (lane % VCH));
-    }
-
-    float4_t s[2];
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      s[rb] = float4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int db = 0; db < ND; ++db) {
-        s[rb] = mfma16x16x32(ka[rb][db], qhi[db], s[rb]);
-        s[rb] = mfma16x16x32(ka[rb][db], qlo[db], s[rb]);
+      for (int j = 0; j < PF; ++j) {
+        const int t0 = base + j * kStride;
+        if (t0 < te)
+          process_tile<D>(buf[j], qhi, qlo, vt, t0, tlast, lane, col, grp, sscale, m, l, o);
+        load_tile<D>(buf[j], kbase, vbase, kv_dim, t0 + PF * kStride, tlast, lane, col, grp);
       }
-    }
-
-#pragma unroll
-    for (int i = 0; i < VLOADS; ++i)
-      *(half8_t*)(vt + (i * VROWS + lane / VCH) * VP + 8 * (lane % VCH)) = vr[i];
-
-    // online softmax over this tile (log2 domain)
-    float u[2][4];
-    float tmax = -INFINITY;
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = t0 + 16 * rb + 4 * grp + r;
-        float x = s[rb][r] * sscale;
-        x = (t <= tlast) ? x : -INFINITY;
-        u[rb][r] = x;
-        tmax = fmaxf(tmax, x);
-      }
-    tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
-    tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
-    const float mnew = fmaxf(m, tmax);
-    const float alpha = fast_exp2(m - mnew);
-    m = mnew;
-    half8_t ph, pl;
-    float psum = 0.f;
-#pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = fast_exp2(u[rb][r] - mnew);
-        psum += p;
-        _Float16 hi, lo;
-        split_hi_lo(p, hi, lo);
-        ph[4 * rb + r] = hi;
-        pl[4 * rb + r] = lo;
-      }
-    l = l * alpha + psum;
-#pragma unroll
-    for (int ob = 0; ob < NO; ++ob) o[ob] *= alpha;
-
-#pragma unroll
-    for (int ob = 0; ob < NO; ++ob) {
-      half8_t va;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int t = (j < 4) ? 4 * grp + j : 16 + 4 * grp + (j - 4);
-        va[j] = vt[t * VP + 16 * ob + col];
-      }
-      o[ob] = mfma16x16x32(va, ph, o[ob]);
-      o[ob] = mfma16x16x32(va, pl, o[ob]);
     }
   }
 
@@ -249,11 +413,9 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
   l += shfl_xor_f(l, 32);
 
   __syncthreads();  // V tiles are dead; the LDS now holds the combine slots
-  float* cm = reinterpret_cast<float*>(smem);          // [kWaves+1][16]
-  float* cl = cm + (kWaves + 1) * 16;                  // [kWaves+1][16]
-  float* co = cl + (kWaves + 1) * 16;                  // [kWaves][16][D]
-  float* cvn = co + kWaves * 16 * D;                   // [D] new V row (fp32)
-  float* ckn = cvn + D;                                // [D] new K row (fp32)
+  float* cm = reinterpret_cast<float*>(smem);          // [kWaves][16]
+  float* cl = cm + kWaves * 16;                        // [kWaves][16]
+  float* co = cl + kWaves * 16;                        // [kWaves][16][D]
   if (grp == 0) {
     cm[wave * 16 + col] = m;
     cl[wave * 16 + col] = l;
@@ -263,46 +425,6 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) co[(wave * 16 + col) * D + 16 * ob + 4 * grp + r] = o[ob][r];
 
-  // ---- row pos: rotate, round, store, and score it (owner, wave 0) ----------
-  if (owner && wave == 0) {
-    const float* kin = a.k + (size_t)li * kv_dim + (size_t)kvh * D;
-    const float* vin = a.v + (size_t)li * kv_dim + (size_t)kvh * D;
-    uint16_t* krow = a.kc + (row0 + pos) * kv_dim + (size_t)kvh * D;
-    uint16_t* vrow = a.vc + (row0 + pos) * kv_dim + (size_t)kvh * D;
-    const float* cr = a.cos_t + (size_t)pos * (D / 2);
-    const float* sr = a.sin_t + (size_t)pos * (D / 2);
-    for (int i = lane; i < D / 2; i += 64) {
-      const int i0 = (a.rope_type == PLH_ROPE_QWEN) ? i : 2 * i;
-      const int i1 = (a.rope_type == PLH_ROPE_QWEN) ? i + D / 2 : 2 * i + 1;
-      float k0 = kin[i0], k1 = kin[i1];
-      rope_rotate(k0, k1, cr[i], sr[i]);
-      const uint16_t b0 = f16_bits_rha(k0), b1 = f16_bits_rha(k1);
-      krow[i0] = b0;
-      krow[i1] = b1;
-      ckn[i0] = f16_bits_to_f32(b0);
-      ckn[i1] = f16_bits_to_f32(b1);
-    }
-    for (int d = lane; d < D; d += 64) {
-      const uint16_t b = f16_bits_rha(vin[d]);
-      vrow[d] = b;
-      cvn[d] = f16_bits_to_f32(b);
-    }
-    // ckn is written and read by the same wave; order the LDS accesses
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-    float qf[ND][8];
-    load_q_rot<D>(a, li, kvh, G, h0, nh, col, grp, qf);
-    float sc = 0.f;
-#pragma unroll
-    for (int db = 0; db < ND; ++db)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) sc = __builtin_fmaf(qf[db][j], ckn[32 * db + 8 * grp + j], sc);
-    sc += shfl_xor_f(sc, 16);
-    sc += shfl_xor_f(sc, 32);
-    if (grp == 0) {
-      cm[kWaves * 16 + col] = sc * sscale;
-      cl[kWaves * 16 + col] = 1.0f;
-    }
-  }
   __syncthreads();
 
   // ---- merge the waves (and the new row) of this workgroup -------------------
@@ -313,7 +435,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
     float M = kNegBig;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) M = fmaxf(M, cm[w * 16 + h]);
-    if (owner) M = fmaxf(M, cm[kWaves * 16 + h]);
+    if (owner) M = fmaxf(M, s_mnew[h]);
     float L = 0.f, O = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
@@ -322,9 +444,9 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
       O = __builtin_fmaf(co[(w * 16 + h) * D + d], wt, O);
     }
     if (owner) {
-      const float wt = fast_exp2(cm[kWaves * 16 + h] - M);
+      const float wt = fast_exp2(s_mnew[h] - M);
       L += wt;
-      O = __builtin_fmaf(cvn[d], wt, O);
+      O = __builtin_fmaf(s_vnew[d], wt, O);
     }
     if (a.n_split == 1) {
       out_base[(size_t)h * D + d] = O * (1.0f / L);
@@ -353,20 +475,28 @@ __global__ __launch_bounds__(kThreads) void attn_decode_combine_kernel(DecodeArg
   const int u0 = group * a.n_split;
   for (int idx = threadIdx.x; idx < nh * D; idx += kThreads) {
     const int h = idx / D, d = idx - (idx / D) * D;
-    float M = kNegBig;
-    for (int sp = 0; sp < a.n_split; ++sp) M = fmaxf(M, a.part_m[(size_t)(u0 + sp) * 16 + h]);
-    float L = 0.f, O = 0.f;
+    // one online pass: the loads of several splits are independent and issue
+    // together
+    float M = kNegBig, L = 0.f, O = 0.f;
+#pragma unroll 4
     for (int sp = 0; sp < a.n_split; ++sp) {
-      const float wt = fast_exp2(a.part_m[(size_t)(u0 + sp) * 16 + h] - M);
-      L = __builtin_fmaf(a.part_l[(size_t)(u0 + sp) * 16 + h], wt, L);
-      O = __builtin_fmaf(a.part_o[((size_t)(u0 + sp) * 16 + h) * D + d], wt, O);
+      const size_t u = (size_t)(u0 + sp) * 16 + h;
+      const float mi = a.part_m[u], li = a.part_l[u], oi = a.part_o[u * D + d];
+      const float Mn = fmaxf(M, mi);
+      const float ra = fast_exp2(M - Mn), rb = fast_exp2(mi - Mn);
+      L = L * ra + li * rb;
+      O = O * ra + oi * rb;
+      M = Mn;
     }
     out_base[(size_t)h * D + d] = O * (1.0f / L);
   }
 }
 
-int g_target_units = 0;   // 0: 8 workgroups per CU
-int g_min_split = 128;
+// Split plan defaults, from sweeps on MI355X (TinyLlama pos 2047, Llama-3.2
+// pos 8191, Llama-2 pos 4095): splits of >= 1024 rows and about four
+// workgroups per CU.
+int g_target_units = 0;   // 0: 4 workgroups per CU
+int g_min_split = 1024;
 
 }  // namespace
 
@@ -428,9 +558,10 @@ extern "C" int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int he
   const int n_hblk = (G + 15) / 16;
   const int n_groups = n_launch_layers * n_kv_heads * n_hblk;
   const int npos = pos + 1;
-  // Split plan: enough workgroups to fill the chip, each split at least
-  // g_min_split rows, split length a multiple of 4 waves x 32 rows.
-  const int target = g_target_units > 0 ? g_target_units : 8 * (c.num_cus > 0 ? c.num_cus : 256);
+  // Split plan: about `target` workgroups in all, each split at least
+  // g_min_split rows (fewer splits, fewer partials to merge), split length a
+  // multiple of 4 waves x 32 rows.
+  const int target = g_target_units > 0 ? g_target_units : 4 * (c.num_cus > 0 ? c.num_cus : 256);
   long want_split = ((long)npos * n_groups + target - 1) / target;
   if (want_split < g_min_split) want_split = g_min_split;
   want_split = (want_split + 127) / 128 * 128;

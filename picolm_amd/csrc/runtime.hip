@@ -32,6 +32,7 @@ int ensure_workspace(size_t bytes) {
   Context& c = g_ctx;
   if (c.ws && c.ws_bytes >= bytes) return 0;
   if (c.ws) {
+    // the old workspace may still be read by queued work
     if (check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize")) return -1;
     if (check_hip(hipFree(c.ws), "hipFree(workspace)")) return -1;
     c.ws = nullptr;

@@ -248,3 +248,18 @@ def test_decode_graph_replays_match_eager(gpu, oracle_mod):
     gk, gv = cache.fetch()
     assert np.array_equal(gk.reshape(3, -1, cfg.kv_dim)[:, :pos],
                           kc.reshape(3, -1, cfg.kv_dim)[:, :pos])
+
+
+@pytest.mark.parametrize("min_split", [128, 512, 1024, 2048])
+def test_decode_split_lengths(gpu, oracle_mod, min_split):
+    """Several split plans (one split, no combine launch, included) give
+    oracle-exact results."""
+    try:
+        gpu.check(gpu.lib.plh_set_tuning(2, min_split), "tuning")
+        cfg = gpu.AttnConfig(4, 32, 4, 64, 2048, 1e4, 0)
+        for pos in (2047, 700, 129):
+            run_decode(gpu, oracle_mod, cfg, pos, seed=pos + min_split, check_layers=[0, 3])
+        cfg = gpu.AttnConfig(2, 32, 32, 128, 1024, 1e4, 0)
+        run_decode(gpu, oracle_mod, cfg, 1000, seed=5 + min_split)
+    finally:
+        gpu.lib.plh_set_tuning(2, 1024)
