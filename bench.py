@@ -3,9 +3,13 @@
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
 
 A step is one token's decode attention over all layers of the model (one
-launch of plh_attn_decode covering every layer), with inputs resident in HBM.
+plh_attn_decode call covering every layer), with inputs resident in HBM.
 The default workload is TinyLlama-1.1B-shaped decode at position 2047
-(22 layers, 32 q heads, 4 kv heads, head_dim 64, FP16 cache of 2048 rows).
+(22 layers, 32 q heads, 4 kv heads, head_dim 64, FP16 cache of 2048 rows);
+the same line carries, under "prefill", the TinyLlama-shaped 512-token causal
+prefill (all 22 layers per step) in TFLOP/s of causal-pair flops
+(L * Hq * 4D * sum_i (i+1)) against the fp16 MFMA peak, with the HBM-bound
+roof of its fp32 q/k/v/out traffic.
 
 Method:
   * the FP16 caches are rotated over enough copies (>= 512 MiB in total) that
@@ -42,11 +46,15 @@ METRIC = "attn µs/token + KV GB/s (% HBM peak) decode; prefill TFLOP/s (% MFMA)
 HBM_PEAK_GBS = 8000.0
 MALL_DEFEAT_BYTES = 512 << 20
 
+MFMA_F16_PEAK_TFS = 2516.6
+
 WORKLOADS = {
     "tinyllama_decode_pos2047": dict(L=22, Hq=32, Hkv=4, D=64, S=2048, theta=1e4, pos=2047),
     "tinyllama_decode_pos256": dict(L=22, Hq=32, Hkv=4, D=64, S=2048, theta=1e4, pos=256),
     "llama32_decode_pos8191": dict(L=16, Hq=32, Hkv=8, D=64, S=8192, theta=5e5, pos=8191),
     "llama2_decode_pos4095": dict(L=32, Hq=32, Hkv=32, D=128, S=4096, theta=1e4, pos=4095),
+    "tinyllama_prefill_512": dict(L=22, Hq=32, Hkv=4, D=64, S=2048, theta=1e4, start=0, n=512),
+    "llama2_prefill_1024": dict(L=32, Hq=32, Hkv=32, D=128, S=4096, theta=1e4, start=0, n=1024),
 }
 
 
@@ -55,6 +63,19 @@ def decode_bytes(w) -> int:
     per_layer = ((pos + 1) * 2 * Hkv * D * 2 + Hq * D * 4 + 2 * Hkv * D * 4
                  + 2 * Hkv * D * 2 + Hq * D * 4)
     return L * per_layer
+
+
+def prefill_flops(w) -> int:
+    """Causal pairs only: L * Hq * 4D * sum_{i<N} (start + i + 1)."""
+    n, st = w["n"], w["start"]
+    pairs = n * st + n * (n + 1) // 2
+    return w["L"] * w["Hq"] * 4 * w["D"] * pairs
+
+
+def prefill_bytes(w) -> int:
+    """fp32 q, k, v in and out, fp16 rows appended, per launch (all layers)."""
+    L, n, Hq, Hkv, D = w["L"], w["n"], w["Hq"], w["Hkv"], w["D"]
+    return L * n * (Hq * D * 4 * 2 + 2 * Hkv * D * 4 + 2 * Hkv * D * 2)
 
 
 def traffic_from_profiles(name: str):
@@ -150,6 +171,96 @@ def run_decode(P, w, steps, warmup, name):
     return result
 
 
+def run_prefill(P, w, steps, warmup):
+    """One step = prefill of n prompt tokens over all layers (append kernel +
+    causal attention kernel), inputs rotated over enough copies to defeat the
+    Infinity Cache."""
+    cfg = P.AttnConfig(w["L"], w["Hq"], w["Hkv"], w["D"], w["S"], w["theta"], 0)
+    L, n, st = cfg.n_layers, w["n"], w["start"]
+    per_copy = prefill_bytes(w) + 2 * L * n * cfg.kv_dim * 2
+    n_copies = max(2, math.ceil(MALL_DEFEAT_BYTES / per_copy))
+    rng = np.random.default_rng(512)
+    copies = []
+    for c in range(n_copies):
+        cache = P.KVCache(cfg)
+        q = P.DeviceBuffer.from_numpy(rng.standard_normal((L, n, cfg.q_dim), dtype=np.float32))
+        k = P.DeviceBuffer.from_numpy(rng.standard_normal((L, n, cfg.kv_dim), dtype=np.float32))
+        v = P.DeviceBuffer.from_numpy(rng.standard_normal((L, n, cfg.kv_dim), dtype=np.float32))
+        o = P.DeviceBuffer(L * n * cfg.q_dim * 4)
+        copies.append((cache, q, k, v, o))
+    P.synchronize()
+
+    def launch(i):
+        cache, q, k, v, o = copies[i % n_copies]
+        P.prefill(cache, 0, st, n, q.ptr, k.ptr, v.ptr, o.ptr, None, L)
+
+    for i in range(max(1, warmup)):
+        launch(i)
+    P.synchronize()
+    with P.Graph() as g:
+        for i in range(steps):
+            launch(i)
+    g.launch()
+    P.synchronize()
+    e0, e1 = P.Event(), P.Event()
+    t0 = time.perf_counter()
+    e0.record()
+    g.launch()
+    e1.record()
+    P.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_ms(e1) / steps
+    flops = prefill_flops(w)
+    algo_bytes = prefill_bytes(w)
+    tfs = flops / (ms * 1e-3) / 1e12
+    roof = min(MFMA_F16_PEAK_TFS, flops / algo_bytes * HBM_PEAK_GBS / 1e3)
+    return {
+        "us_per_step": wall * 1e6 / steps,
+        "us_per_token": wall * 1e6 / steps / n,
+        "tflops": tfs,
+        "roofline": {"bound": "mfma", "achieved": tfs, "peak": MFMA_F16_PEAK_TFS,
+                     "unit": "TFLOP/s", "frac": tfs / MFMA_F16_PEAK_TFS,
+                     "hbm_roof_tflops": roof, "frac_of_binding_roof": tfs / roof},
+        "algorithmic_flops_per_step": flops,
+        "algorithmic_bytes_per_step": algo_bytes,
+        "copies_rotated": n_copies,
+        "_copies": copies,
+    }
+
+
+def cpu_baseline_prefill(P, w, res, budget_s=8.0):
+    """The oracle's prefill on one host thread over a bounded number of layers
+    of the same step, extrapolated to all layers."""
+    from oracle import oracle as O
+    cache, dq, dk, dv, dout = res.pop("_copies")[0]
+    cfg = cache.cfg
+    L, n, st = cfg.n_layers, w["n"], w["start"]
+    kc, vc = cache.fetch()
+    shp = O.Shape(L, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.max_seq_len,
+                  cfg.rope_freq_base, 0)
+    cos_t, sin_t = O.rope_tables(cfg.max_seq_len, cfg.head_dim, cfg.rope_freq_base)
+    q = dq.download(np.float32, (L, n, cfg.q_dim))
+    k = dk.download(np.float32, (L, n, cfg.kv_dim))
+    v = dv.download(np.float32, (L, n, cfg.kv_dim))
+    gpu_out = dout.download(np.float32, (L, n, cfg.q_dim))
+    t_total, layers, worst = 0.0, 0, 0.0
+    while t_total < budget_s and layers < L:
+        t0 = time.perf_counter()
+        ref = O.attn_prefill(shp, layers, st, n, q[layers].copy(), k[layers].copy(), v[layers],
+                             kc, vc, cos_t, sin_t)
+        t_total += time.perf_counter() - t0
+        err = np.abs(gpu_out[layers] - ref).reshape(-1, cfg.head_dim).max(1)
+        den = np.abs(ref).reshape(-1, cfg.head_dim).max(1)
+        worst = max(worst, float((err / den).max()))
+        layers += 1
+    step_s = t_total / layers * L
+    return {"cpu_baseline": {"value": prefill_flops(w) / step_s / 1e12, "unit": "TFLOP/s",
+                             "cores": 1, "kind": "port", "us_per_token": step_s * 1e6 / n,
+                             "sample": f"{layers} of {L} layers of the {n}-token prefill, oracle "
+                                       f"on 1 thread, extrapolated"},
+            "parity_normwise_max": worst}
+
+
 def cpu_baseline(P, w, res, budget_s=12.0):
     """The oracle on one host thread over a bounded sample of the workload, and
     a parity spot check of the GPU output of the same step."""
@@ -197,7 +308,9 @@ def main():
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="tinyllama_decode_pos2047", choices=sorted(WORKLOADS))
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
+    ap.add_argument("--no-prefill", action="store_true",
+                    help="skip the secondary prefill measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; the attention block needs no "
@@ -207,6 +320,22 @@ def main():
     import picolm_amd as P
     P.init(0)
     w = WORKLOADS[args.workload]
+    if "n" in w:   # a prefill workload as the headline
+        res = run_prefill(P, w, max(1, args.steps // 10), args.warmup)
+        extra = {} if args.no_cpu else cpu_baseline_prefill(P, w, res)
+        res.pop("_copies", None)
+        line = {"metric": METRIC, "value": res.pop("tflops"), "unit": "TFLOP/s", "n_gpus": 1,
+                "steps": max(1, args.steps // 10), "warmup": args.warmup,
+                "ms_per_step": res["us_per_step"] / 1e3, "higher_is_better": True,
+                "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
+                "config": {"workload": args.workload, "n_layers": w["L"], "n_heads": w["Hq"],
+                           "n_kv_heads": w["Hkv"], "head_dim": w["D"], "max_seq_len": w["S"],
+                           "start_pos": w["start"], "n_tokens": w["n"],
+                           "rope_theta": w["theta"], "batch": 1}}
+        line.update(res)
+        line.update(extra)
+        print(json.dumps(line), flush=True)
+        return
     res = run_decode(P, w, args.steps, args.warmup, args.workload)
     extra = {}
     if not args.no_cpu:
@@ -233,6 +362,15 @@ def main():
     line["hbm_frac"] = res["roofline"]["frac"]
     line.update(res)
     line.update(extra)
+    if not args.no_prefill:
+        # the metric's prefill half: TinyLlama-shaped 512-token causal prefill
+        pw = WORKLOADS["tinyllama_prefill_512"]
+        pres = run_prefill(P, pw, 20, 3)
+        pextra = {} if args.no_cpu else cpu_baseline_prefill(P, pw, pres, budget_s=4.0)
+        pres.pop("_copies", None)
+        pres["workload"] = "tinyllama_prefill_512"
+        pres.update(pextra)
+        line["prefill"] = pres
     print(json.dumps(line), flush=True)
 
 

@@ -95,6 +95,28 @@ int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int head_dim,
                     uint16_t *val_cache, const float *rope_cos,
                     const float *rope_sin, float *out);
 
+/* ---- prefill attention -------------------------------------------------- */
+/* Replaces model.c:1039-1089 (per prompt token: rope, FP16 append, online-
+ * softmax GQA attention) for n_tokens tokens at positions start_pos.. and
+ * n_launch_layers consecutive layers from layer0 (1 = the per-layer call of
+ * model_forward_prefill).  Per launched layer li (device pointers):
+ *   q   + li*n_tokens*n_heads*head_dim     [n_tokens][n_heads*head_dim] fp32
+ *   k,v + li*n_tokens*n_kv_heads*head_dim  [n_tokens][kv_dim] fp32
+ *   out + li*n_tokens*out_stride            row bi at out + bi*out_stride
+ * Rows start_pos..start_pos+n_tokens-1 of each layer's caches are written
+ * (f16 of rotated k, f16 of v, reference rounding); token bi attends over
+ * rows 0..start_pos+bi, the prefix rows coming from the cache as the
+ * reference's kvcache_load leaves them.  out_stride is a multiple of 4 and at
+ * least n_heads*head_dim (the reference uses n_embd).  n_tokens = 0 is a
+ * no-op. */
+int plh_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                     int max_seq_len, int rope_type, int layer0,
+                     int n_launch_layers, int start_pos, int n_tokens,
+                     const float *q, const float *k, const float *v,
+                     uint16_t *key_cache, uint16_t *val_cache,
+                     const float *rope_cos, const float *rope_sin, float *out,
+                     int out_stride);
+
 /* Tuning knobs (bench sweeps).  key 1: decode target workgroups per launch
  * (0 = default); key 2: decode minimum positions per split (multiple of 128). */
 int plh_set_tuning(int key, int value);

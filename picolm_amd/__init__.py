@@ -8,5 +8,5 @@ attention operator.
 """
 from ._native import LIB_PATH, PicolmHipError, check, lib  # noqa: F401
 from .attention import (ROPE_LLAMA, ROPE_QWEN, AttnConfig, KVCache, decode,  # noqa: F401
-                        f16_checksum, f32_to_f16, rope_tables)
+                        f16_checksum, f32_to_f16, prefill, rope_tables)
 from .device import DeviceBuffer, Event, Graph, init, synchronize  # noqa: F401

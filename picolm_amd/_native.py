@@ -62,6 +62,7 @@ _SIGS = {
     "plh_f16_checksum": (_i, [C.c_uint64, C.c_uint64, C.POINTER(C.c_uint64)]),
     # attention
     "plh_attn_decode": (_i, [_i] * 9 + [_vp] * 8),
+    "plh_attn_prefill": (_i, [_i] * 10 + [_vp] * 8 + [_i]),
     "plh_set_tuning": (_i, [_i, _i]),
 }
 

@@ -97,6 +97,19 @@ def decode(cache: KVCache, layer0: int, pos: int, q: int, k: int, v: int, out: i
           "plh_attn_decode")
 
 
+def prefill(cache: KVCache, layer0: int, start_pos: int, n_tokens: int, q: int, k: int, v: int,
+            out: int, out_stride: int | None = None, n_launch_layers: int = 1) -> None:
+    """Queues a causal prefill of n_tokens tokens at positions start_pos..
+    (device pointers q [L][N][q_dim], k/v [L][N][kv_dim], out [L][N][stride])."""
+    c = cache.cfg
+    stride = c.q_dim if out_stride is None else out_stride
+    check(lib.plh_attn_prefill(c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len,
+                               c.rope_type, layer0, n_launch_layers, start_pos, n_tokens, q, k, v,
+                               cache.key.ptr, cache.val.ptr, cache.cos.ptr, cache.sin.ptr, out,
+                               stride),
+          "plh_attn_prefill")
+
+
 def f32_to_f16(src: int, dst: int, n: int) -> None:
     """Device fp32 -> fp16 bits with the reference's rounding (quant.c:41-78)."""
     check(lib.plh_f32_to_f16(src, dst, n), "plh_f32_to_f16")

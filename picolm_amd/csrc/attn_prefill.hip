@@ -1,0 +1,372 @@
+// attn_prefill.hip -- causal prompt prefill for gfx950.
+//
+// Replaces model.c:1019-1090.  The reference walks the prompt serially: for
+// token bi (position start_pos+bi) it rotates q and k, appends f16(k_rot) and
+// f16(v) at cache row start_pos+bi, then attends over rows 0..start_pos+bi.
+// Because each token's row depends only on its own k/v, that is the same as
+// "append all rows, then causal attention", which is what the two kernels
+// here do:
+//
+//   prefill_append_kernel  rotates k (table row = its position), rounds k_rot
+//                          and v with the reference's fp16 rounding and writes
+//                          rows start_pos .. start_pos+n_tokens-1;
+//   prefill_attn_kernel    flash attention over the cache with fp16 MFMA and
+//                          an fp32 online softmax.
+//
+// Attention workgroup = (layer, kv head, block of bq prompt tokens).  Its 8
+// waves own 16 "columns" each; a column is one (token, q head) pair of the
+// block, so all q heads of the kv head's GQA group share every K/V tile.
+// K/V tiles of 32 rows are staged in LDS (double-buffered, loaded by the
+// whole workgroup): K row-major, V transposed (d-major), so that
+//   S^T[t][c] = K[t][:] . q_c      A = K rows (ds_read_b128), B = q_c hi/lo
+//   O^T[d][c] += V^T[d][t] P^T[t][c]  A = V^T (ds_read_b128), B = P hi/lo
+// The two 16-row MFMA blocks of S^T read K rows in the order
+// pi_rb(i) = 8*(i/4) + 4*rb + i%4, which leaves lane group g holding rows
+// 8g..8g+7 of the tile: exactly the K slots of the PV product, so P never
+// leaves registers and each V^T operand is one contiguous 16-byte LDS read.
+// q and P are split into fp16 hi + lo parts (two MFMAs each), keeping the
+// products at ~fp32 precision.
+#include <math.h>
+
+#include "attn_common.h"
+#include "picolm_hip.h"
+#include "plh_internal.h"
+
+using namespace plh;
+
+namespace {
+
+constexpr int kPW = 8;               // waves per attention workgroup
+constexpr int kPThreads = 64 * kPW;
+constexpr int kKT = 32;              // K/V rows per tile
+
+template <int D>
+__global__ __launch_bounds__(256) void prefill_append_kernel(PrefillArgs a) {
+  const int kv_dim = a.n_kv_heads * D;
+  const int pairs = kv_dim / 2;
+  const long total = (long)a.n_launch_layers * a.n_tokens * pairs;
+  for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < total;
+       idx += (long)gridDim.x * 256) {
+    const int pr = (int)(idx % pairs);
+    const long rest = idx / pairs;
+    const int tok = (int)(rest % a.n_tokens);
+    const int li = (int)(rest / a.n_tokens);
+    const int kvh = pr / (D / 2), i = pr % (D / 2);
+    const int i0 = (a.rope_type == PLH_ROPE_QWEN) ? i : 2 * i;
+    const int i1 = (a.rope_type == PLH_ROPE_QWEN) ? i + D / 2 : 2 * i + 1;
+    const int pos = a.start_pos + tok;
+    const size_t in_row = ((size_t)li * a.n_tokens + tok) * kv_dim + (size_t)kvh * D;
+    float k0 = a.k[in_row + i0], k1 = a.k[in_row + i1];
+    const float v0 = a.v[in_row + i0], v1 = a.v[in_row + i1];
+    rope_rotate(k0, k1, a.cos_t[(size_t)pos * (D / 2) + i], a.sin_t[(size_t)pos * (D / 2) + i]);
+    const size_t out_row =
+        ((size_t)(a.layer0 + li) * a.max_seq_len + pos) * kv_dim + (size_t)kvh * D;
+    a.kc[out_row + i0] = f16_bits_rha(k0);
+    a.kc[out_row + i1] = f16_bits_rha(k1);
+    a.vc[out_row + i0] = f16_bits_rha(v0);
+    a.vc[out_row + i1] = f16_bits_rha(v1);
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) {
+  constexpr int ND = D / 32;     // 32-wide d blocks of QK
+  constexpr int NO = D / 16;     // 16-wide d blocks of PV
+  constexpr int KP = D + 8;      // LDS pitch of a K row (halves)
+  constexpr int VP = kKT + 8;    // LDS pitch of a V^T row (halves)
+  constexpr int KCH = kKT * D / 8;  // 16-byte chunks of a K (or V) tile
+  __shared__ __align__(16) _Float16 ks[2][kKT * KP];
+  __shared__ __align__(16) _Float16 vs[2][D * VP];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int col = lane & 15, grp = lane >> 4;
+
+  // XCD-aware order: each XCD takes whole (layer, kv head) groups, so the
+  // group's K/V tiles, read by all its q blocks, stay in one L2; within a
+  // group the heavy (late) q blocks go first.
+  const int nq = a.n_qblk;
+  const int unit = (int)(blockIdx.x & 7) * a.per_xcd + (int)(blockIdx.x >> 3);
+  if (unit >= a.n_units) return;
+  const int qb = nq - 1 - unit % nq;
+  const int kvh = (unit / nq) % a.n_kv_heads;
+  const int li = (unit / nq) / a.n_kv_heads;
+  const int layer = a.layer0 + li;
+  const int G = a.n_heads / a.n_kv_heads;
+  const int kv_dim = a.n_kv_heads * D;
+  const int q_dim = a.n_heads * D;
+  const int i0 = qb * a.bq;
+  const int last_tok = min(i0 + a.bq, a.n_tokens) - 1;
+  const int n_rows = a.start_pos + last_tok + 1;          // rows [0, n_rows) are needed
+  const int n_tiles = (n_rows + kKT - 1) / kKT;
+
+  // this lane's column: token i0+tok, q head kvh*G+hh
+  const int c = wave * 16 + col;
+  const int tok = c / G, hh = c - (c / G) * G;
+  const bool cvalid = tok < a.bq && i0 + tok < a.n_tokens;
+  const int tok_c = cvalid ? i0 + tok : last_tok;          // clamped for addressing
+  const int p_col = a.start_pos + tok_c;                  // causal limit of the column
+
+  // ---- cooperative tile loads (issued early; stored to LDS after compute) --
+  const size_t row0 = (size_t)layer * a.max_seq_len;
+  const uint16_t* kbase = a.kc + row0 * kv_dim + (size_t)kvh * D;
+  const uint16_t* vbase = a.vc + row0 * kv_dim + (size_t)kvh * D;
+  constexpr int LPT = (2 * KCH + kPThreads - 1) / kPThreads;  // chunks per thread
+  half8_t ld[LPT];
+  auto issue_loads = [&](int t0) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int ch = tid + u * kPThreads;
+      const int cc = ch % KCH;                 // chunk within its tile
+      const int r = cc / (D / 8), q8 = cc % (D / 8);
+      const int row = min(t0 + r, n_rows - 1);
+      const uint16_t* src = (ch < KCH ? kbase : vbase) + (size_t)row * kv_dim + 8 * q8;
+      ld[u] = *(const half8_t*)src;
+    }
+  };
+  auto store_lds = [&](int b) {
+#pragma unroll
+    for (int u = 0; u < LPT; ++u) {
+      const int ch = tid + u * kPThreads;
+      if (ch < 2 * KCH) {
+        const int cc = ch % KCH;
+        const int r = cc / (D / 8), q8 = cc % (D / 8);
+        if (ch < KCH) {
+          *(half8_t*)&ks[b][r * KP + 8 * q8] = ld[u];
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) vs[b][(8 * q8 + e) * VP + r] = ld[u][e];
+        }
+      }
+    }
+  };
+  issue_loads(0);
+
+  // ---- q operands of this lane's column: rotated, zero if invalid ----------
+  half8_t qhi[ND], qlo[ND];
+  {
+    const float* qrow = a.q + ((size_t)li * a.n_tokens + tok_c) * q_dim +
+                        (size_t)(kvh * G + (cvalid ? hh : 0)) * D;
+    const float* cr = a.cos_t + (size_t)p_col * (D / 2);
+    const float* sr = a.sin_t + (size_t)p_col * (D / 2);
+    float qf[ND][8];
+#pragma unroll
+    for (int db = 0; db < ND; ++db) {
+      const float4 x0 = *(const float4*)(qrow + 32 * db + 8 * grp);
+      const float4 x1 = *(const float4*)(qrow + 32 * db + 8 * grp + 4);
+      qf[db][0] = x0.x, qf[db][1] = x0.y, qf[db][2] = x0.z, qf[db][3] = x0.w;
+      qf[db][4] = x1.x, qf[db][5] = x1.y, qf[db][6] = x1.z, qf[db][7] = x1.w;
+    }
+    if (a.rope_type == PLH_ROPE_QWEN) {
+#pragma unroll
+      for (int db = 0; db < ND / 2; ++db)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const int i = 32 * db + 8 * grp + j;
+          rope_rotate(qf[db][j], qf[db + ND / 2][j], cr[i], sr[i]);
+        }
+    } else {
+#pragma unroll
+      for (int db = 0; db < ND; ++db) {
+        const float4 c4 = *(const float4*)(cr + 16 * db + 4 * grp);
+        const float4 s4 = *(const float4*)(sr + 16 * db + 4 * grp);
+        rope_rotate(qf[db][0], qf[db][1], c4.x, s4.x);
+        rope_rotate(qf[db][2], qf[db][3], c4.y, s4.y);
+        rope_rotate(qf[db][4], qf[db][5], c4.z, s4.z);
+        rope_rotate(qf[db][6], qf[db][7], c4.w, s4.w);
+      }
+    }
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        _Float16 hi, lo;
+        split_hi_lo(cvalid ? qf[db][j] : 0.f, hi, lo);
+        qhi[db][j] = hi;
+        qlo[db][j] = lo;
+      }
+  }
+
+  store_lds(0);
+  __syncthreads();
+
+  const float sscale = a.score_scale;
+  float m = kNegBig, l = 0.f;
+  float4_t o[NO];
+#pragma unroll
+  for (int ob = 0; ob < NO; ++ob) o[ob] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+  for (int it = 0; it < n_tiles; ++it) {
+    const int b = it & 1;
+    const int t0 = it * kKT;
+    const bool more = it + 1 < n_tiles;
+    if (more) issue_loads(t0 + kKT);
+
+    // S^T for this wave's 16 columns
+    float4_t s[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int krow = 8 * (col >> 2) + 4 * rb + (col & 3);
+      s[rb] = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int db = 0; db < ND; ++db) {
+        const half8_t kk = *(const half8_t*)&ks[b][krow * KP + 32 * db + 8 * grp];
+        s[rb] = mfma16x16x32(kk, qhi[db], s[rb]);
+        s[rb] = mfma16x16x32(kk, qlo[db], s[rb]);
+      }
+    }
+    // online softmax: lane holds rows t0 + 8*grp + j, j = 4*rb + r
+    float u[8];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int t = t0 + 8 * grp + 4 * rb + r;
+        float x = s[rb][r] * sscale;
+        x = (t <= p_col) ? x : -INFINITY;
+        u[4 * rb + r] = x;
+        tmax = fmaxf(tmax, x);
+      }
+    tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
+    tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
+    const float mnew = fmaxf(m, tmax);
+    const float alpha = fast_exp2(m - mnew);
+    m = mnew;
+    half8_t ph, pl;
+    float psum = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float p = fast_exp2(u[j] - mnew);
+      psum += p;
+      _Float16 hi, lo;
+      split_hi_lo(p, hi, lo);
+      ph[j] = hi;
+      pl[j] = lo;
+    }
+    l = l * alpha + psum;
+#pragma unroll
+    for (int ob = 0; ob < NO; ++ob) {
+      const half8_t va = *(const half8_t*)&vs[b][(16 * ob + col) * VP + 8 * grp];
+      o[ob] *= alpha;
+      o[ob] = mfma16x16x32(va, ph, o[ob]);
+      o[ob] = mfma16x16x32(va, pl, o[ob]);
+    }
+
+    if (more) store_lds(b ^ 1);
+    __syncthreads();
+  }
+
+  // ---- normalise and write: lane holds d = 16*ob + 4*grp + r of its column ---
+  l += shfl_xor_f(l, 16);
+  l += shfl_xor_f(l, 32);
+  if (cvalid) {
+    const float inv = 1.0f / l;
+    float* orow = a.out + ((size_t)li * a.n_tokens + i0 + tok) * a.out_stride +
+                  (size_t)(kvh * G + hh) * D;
+#pragma unroll
+    for (int ob = 0; ob < NO; ++ob) {
+      float4 w;
+      w.x = o[ob][0] * inv;
+      w.y = o[ob][1] * inv;
+      w.z = o[ob][2] * inv;
+      w.w = o[ob][3] * inv;
+      *(float4*)(orow + 16 * ob + 4 * grp) = w;
+    }
+  }
+}
+
+}  // namespace
+
+extern "C" int plh_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                                int max_seq_len, int rope_type, int layer0, int n_launch_layers,
+                                int start_pos, int n_tokens, const float* q, const float* k,
+                                const float* v, uint16_t* key_cache, uint16_t* val_cache,
+                                const float* rope_cos, const float* rope_sin, float* out,
+                                int out_stride) {
+  Context& c = ctx();
+  if (!c.stream) {
+    set_error("plh_attn_prefill: library not initialised");
+    return -1;
+  }
+  if (head_dim != 64 && head_dim != 128) {
+    set_error("plh_attn_prefill: head_dim %d not supported (64, 128)", head_dim);
+    return -1;
+  }
+  if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads) {
+    set_error("plh_attn_prefill: n_heads %d must be a multiple of n_kv_heads %d", n_heads,
+              n_kv_heads);
+    return -1;
+  }
+  const int G = n_heads / n_kv_heads;
+  if (G > 16 * kPW) {
+    set_error("plh_attn_prefill: GQA group %d larger than %d", G, 16 * kPW);
+    return -1;
+  }
+  if (rope_type != PLH_ROPE_LLAMA && rope_type != PLH_ROPE_QWEN) {
+    set_error("plh_attn_prefill: unknown rope_type %d", rope_type);
+    return -1;
+  }
+  if (max_seq_len <= 0 || start_pos < 0 || n_tokens < 0 ||
+      (long)start_pos + (long)n_tokens > (long)max_seq_len) {
+    set_error("plh_attn_prefill: rows [%d, %ld) outside [0, %d)", start_pos,
+              (long)start_pos + n_tokens, max_seq_len);
+    return -1;
+  }
+  if (layer0 < 0 || n_launch_layers <= 0 || layer0 + n_launch_layers > n_layers) {
+    set_error("plh_attn_prefill: layers [%d, %d) outside [0, %d)", layer0,
+              layer0 + n_launch_layers, n_layers);
+    return -1;
+  }
+  if (out_stride < n_heads * head_dim || out_stride % 4) {
+    set_error("plh_attn_prefill: out_stride %d must be a multiple of 4 and >= n_heads*head_dim %d",
+              out_stride, n_heads * head_dim);
+    return -1;
+  }
+  if (n_tokens == 0) return 0;
+  if (!q || !k || !v || !key_cache || !val_cache || !rope_cos || !rope_sin || !out) {
+    set_error("plh_attn_prefill: null pointer");
+    return -1;
+  }
+
+  PrefillArgs a;
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.kc = key_cache;
+  a.vc = val_cache;
+  a.cos_t = rope_cos;
+  a.sin_t = rope_sin;
+  a.out = out;
+  a.layer0 = layer0;
+  a.n_launch_layers = n_launch_layers;
+  a.n_heads = n_heads;
+  a.n_kv_heads = n_kv_heads;
+  a.max_seq_len = max_seq_len;
+  a.rope_type = rope_type;
+  a.start_pos = start_pos;
+  a.n_tokens = n_tokens;
+  a.out_stride = out_stride;
+  a.bq = (16 * kPW) / G;
+  a.n_qblk = (n_tokens + a.bq - 1) / a.bq;
+  const int n_groups = n_launch_layers * n_kv_heads;
+  a.n_units = n_groups * a.n_qblk;
+  a.per_xcd = (n_groups + 7) / 8 * a.n_qblk;
+  a.score_scale = kLog2e / sqrtf((float)head_dim);
+
+  const long pairs = (long)n_launch_layers * n_tokens * (n_kv_heads * head_dim / 2);
+  long ab = (pairs + 255) / 256;
+  if (ab > 16384) ab = 16384;
+  const unsigned grid = (unsigned)(8 * a.per_xcd);
+  if (head_dim == 64) {
+    hipLaunchKernelGGL(prefill_append_kernel<64>, dim3((unsigned)ab), dim3(256), 0, c.stream, a);
+    if (check_hip(hipGetLastError(), "prefill_append_kernel")) return -1;
+    hipLaunchKernelGGL(prefill_attn_kernel<64>, dim3(grid), dim3(kPThreads), 0, c.stream, a);
+  } else {
+    hipLaunchKernelGGL(prefill_append_kernel<128>, dim3((unsigned)ab), dim3(256), 0, c.stream,
+                       a);
+    if (check_hip(hipGetLastError(), "prefill_append_kernel")) return -1;
+    hipLaunchKernelGGL(prefill_attn_kernel<128>, dim3(grid), dim3(kPThreads), 0, c.stream, a);
+  }
+  return check_hip(hipGetLastError(), "prefill_attn_kernel");
+}

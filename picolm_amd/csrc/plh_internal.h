@@ -48,3 +48,26 @@ struct DecodeArgs {
 };
 
 }  // namespace plh
+
+namespace plh {
+
+// Prefill kernel arguments (all device pointers).
+struct PrefillArgs {
+  const float* q;          // [n_launch_layers][n_tokens][n_heads*D]
+  const float* k;          // [n_launch_layers][n_tokens][kv_dim]
+  const float* v;          // [n_launch_layers][n_tokens][kv_dim]
+  uint16_t* kc;            // [n_layers][S][kv_dim] fp16 bits
+  uint16_t* vc;
+  const float* cos_t;      // [S][D/2]
+  const float* sin_t;
+  float* out;              // [n_launch_layers][n_tokens][out_stride]
+  int layer0, n_launch_layers, n_heads, n_kv_heads, max_seq_len, rope_type;
+  int start_pos, n_tokens, out_stride;
+  int bq;                  // tokens per q block
+  int n_qblk;              // q blocks per (layer, kv head)
+  int n_units;             // n_launch_layers * n_kv_heads * n_qblk
+  int per_xcd;             // units per XCD slice of the grid
+  float score_scale;       // log2(e) / sqrt(D)
+};
+
+}  // namespace plh
