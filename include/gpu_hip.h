@@ -1,0 +1,87 @@
+/*
+ * gpu_hip.h -- picolm's GPU backend interface (gpu.h) for the MI355X
+ * attention block.
+ *
+ * Same conventions as the reference's gpu.h (gpu.h:7-42): one global backend,
+ * lifecycle gpu_init -> gpu_upload_model -> ... -> gpu_shutdown, and every
+ * gpu_try_* returns 0 when it did the work or -1 when the caller must run its
+ * own CPU code (nothing half-applied).  Without USE_HIP the calls are inline
+ * stubs returning -1 / 0, as gpu.h:31-42 does without USE_VULKAN.
+ *
+ * Environment (gpu.c:143-150, 241-252 style):
+ *   PICOLM_HIP_DISABLE=1  gpu_init fails, everything stays on the CPU
+ *   PICOLM_HIP_DEVICE=N   device index (default 0)
+ *   PICOLM_GPU_LAYERS=N   only layers < N use the GPU; later layers get -1
+ *
+ * Host caches stay authoritative: every successful call copies the rows it
+ * appended back into m->state.key_cache / val_cache, so the CPU fallback and
+ * kvcache_save (model.c:1158-1197) see bit-identical data.
+ */
+#ifndef PICOLM_GPU_HIP_H
+#define PICOLM_GPU_HIP_H
+
+#include "model.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#ifdef USE_HIP
+
+/* gpu.h:12-15 -- select the device, create the stream.  0 or -1. */
+int gpu_init(const model_t *m);
+/* gpu.h:17-20 -- allocate the device FP16 KV cache [L][S][kv_dim] and RoPE
+ * tables, upload the host tables and cache.  0 or -1. */
+int gpu_upload_model(const model_t *m);
+/* gpu.h:22 -- 1 when initialised and uploaded. */
+int gpu_available(void);
+/* gpu.h:24-26 -- weight GEMV offload is not part of this backend: always -1,
+ * the caller's CPU matmul runs (tensor.c:202-205). */
+int gpu_try_matmul(float *out, const float *x, const void *W, int n, int d, int qtype);
+/* gpu.h:28 -- drain and release everything. */
+void gpu_shutdown(void);
+
+/* Replaces model.c:819-892 for layer `layer` at position `pos`: RoPE of q/k,
+ * FP16 append of row pos, online-softmax GQA attention over rows 0..pos.
+ * q [n_heads*head_dim], k and v [n_kv_heads*head_dim] are read (not rotated
+ * in place; nothing reads them afterwards), out [n_heads*head_dim] written. */
+int gpu_try_attention(model_t *m, int layer, int pos, float *q, float *k,
+                      const float *v, float *out);
+/* Replaces model.c:1039-1089 for n_tokens prompt rows at start_pos..:
+ * q [n_tokens][n_heads*head_dim], k/v [n_tokens][kv_dim]; out row bi at
+ * out + bi*n_embd (model.c:1057). */
+int gpu_try_attention_prefill(model_t *m, int layer, int start_pos, int n_tokens,
+                              float *q, float *k, const float *v, float *out);
+/* KV coherence for kvcache_save / kvcache_load (model.c:1146-1259): copy rows
+ * 0..n_pos-1 of every layer device -> host (download) or host -> device
+ * (upload). 0 or -1. */
+int gpu_kv_download(const model_t *m, int n_pos);
+int gpu_kv_upload(const model_t *m, int n_pos);
+
+#else /* !USE_HIP */
+
+static inline int gpu_init(const model_t *m) { (void)m; return -1; }
+static inline int gpu_upload_model(const model_t *m) { (void)m; return -1; }
+static inline int gpu_available(void) { return 0; }
+static inline int gpu_try_matmul(float *o, const float *x, const void *W, int n, int d, int qt) {
+    (void)o; (void)x; (void)W; (void)n; (void)d; (void)qt; return -1;
+}
+static inline void gpu_shutdown(void) {}
+static inline int gpu_try_attention(model_t *m, int l, int p, float *q, float *k,
+                                    const float *v, float *o) {
+    (void)m; (void)l; (void)p; (void)q; (void)k; (void)v; (void)o; return -1;
+}
+static inline int gpu_try_attention_prefill(model_t *m, int l, int s, int n, float *q,
+                                            float *k, const float *v, float *o) {
+    (void)m; (void)l; (void)s; (void)n; (void)q; (void)k; (void)v; (void)o; return -1;
+}
+static inline int gpu_kv_download(const model_t *m, int n) { (void)m; (void)n; return -1; }
+static inline int gpu_kv_upload(const model_t *m, int n) { (void)m; (void)n; return -1; }
+
+#endif /* USE_HIP */
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PICOLM_GPU_HIP_H */

@@ -1,0 +1,257 @@
+/*
+ * gpu_hip.c -- picolm's gpu.h backend surface over libpicolm_hip (C11).
+ *
+ * The reference's Vulkan backend (gpu.c) keeps one global state, uploads
+ * weights once and answers gpu_try_matmul synchronously with a staging copy,
+ * a dispatch and a fence wait (gpu.c:579-702).  This backend does the same
+ * for the attention block: one global state, the FP16 KV cache and RoPE
+ * tables resident in HBM, and synchronous gpu_try_attention /
+ * gpu_try_attention_prefill calls (copy in, one or two kernel launches, copy
+ * out).  After every call the rows it appended are copied back into the
+ * model's host cache, so the host cache stays authoritative and bit-equal to
+ * the device one; a HIP failure after device state may have changed marks the
+ * backend unavailable so that every later call falls back to the CPU.
+ *
+ * Built with USE_HIP; compiles against either this package's model.h or the
+ * reference's (it reads only config.{n_embd, n_heads, n_kv_heads, n_layers,
+ * max_seq_len, head_dim, rope_type} and state.{key_cache, val_cache,
+ * rope_cos, rope_sin}).
+ */
+#include "gpu_hip.h"
+
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "picolm_hip.h"
+
+static struct {
+    int inited;     /* plh_init succeeded */
+    int uploaded;   /* caches and tables resident */
+    int n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, n_embd;
+    int gpu_layers; /* layers < gpu_layers use the device */
+    uint16_t *d_key, *d_val;
+    float *d_cos, *d_sin;
+    float *d_q, *d_k, *d_v, *d_out; /* staging, sized for stage_tokens rows */
+    int stage_tokens;
+} gs;
+
+static int env_int(const char *name, int dflt) {
+    const char *s = getenv(name);
+    if (!s || !*s) return dflt;
+    return atoi(s);
+}
+
+static void backend_lost(const char *what) {
+    fprintf(stderr, "gpu_hip: %s failed (%s); attention stays on the CPU from now on\n", what,
+            plh_last_error());
+    gs.uploaded = 0;
+}
+
+int gpu_init(const model_t *m) {
+    if (gs.inited) return 0;
+    if (env_int("PICOLM_HIP_DISABLE", 0)) return -1;
+    const model_config_t *c = &m->config;
+    if (c->head_dim != 64 && c->head_dim != 128) {
+        fprintf(stderr, "gpu_hip: head_dim %d has no kernel, attention stays on the CPU\n",
+                c->head_dim);
+        return -1;
+    }
+    if (plh_init(env_int("PICOLM_HIP_DEVICE", 0)) != 0) {
+        fprintf(stderr, "gpu_hip: %s\n", plh_last_error());
+        return -1;
+    }
+    gs.inited = 1;
+    gs.n_layers = c->n_layers;
+    gs.n_heads = c->n_heads;
+    gs.n_kv_heads = c->n_kv_heads;
+    gs.head_dim = c->head_dim;
+    gs.max_seq_len = c->max_seq_len;
+    gs.rope_type = (int)c->rope_type;
+    gs.n_embd = c->n_embd;
+    gs.gpu_layers = env_int("PICOLM_GPU_LAYERS", c->n_layers);
+    return 0;
+}
+
+static size_t cache_bytes(void) {
+    return (size_t)gs.n_layers * (size_t)gs.max_seq_len * (size_t)gs.n_kv_heads *
+           (size_t)gs.head_dim * sizeof(uint16_t);
+}
+
+static int ensure_stage(int n_tokens) {
+    if (n_tokens <= gs.stage_tokens) return 0;
+    plh_free(gs.d_q);
+    plh_free(gs.d_k);
+    plh_free(gs.d_v);
+    plh_free(gs.d_out);
+    gs.d_q = gs.d_k = gs.d_v = gs.d_out = NULL;
+    gs.stage_tokens = 0;
+    size_t q_dim = (size_t)gs.n_heads * gs.head_dim;
+    size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
+    size_t stride = (size_t)gs.n_embd > q_dim ? (size_t)gs.n_embd : q_dim;
+    gs.d_q = (float *)plh_malloc((size_t)n_tokens * q_dim * sizeof(float));
+    gs.d_k = (float *)plh_malloc((size_t)n_tokens * kv_dim * sizeof(float));
+    gs.d_v = (float *)plh_malloc((size_t)n_tokens * kv_dim * sizeof(float));
+    gs.d_out = (float *)plh_malloc((size_t)n_tokens * stride * sizeof(float));
+    if (!gs.d_q || !gs.d_k || !gs.d_v || !gs.d_out) return -1;
+    gs.stage_tokens = n_tokens;
+    return 0;
+}
+
+int gpu_upload_model(const model_t *m) {
+    if (!gs.inited) return -1;
+    if (gs.uploaded) return 0;
+    size_t tab = (size_t)gs.max_seq_len * (size_t)(gs.head_dim / 2) * sizeof(float);
+    gs.d_key = (uint16_t *)plh_malloc(cache_bytes());
+    gs.d_val = (uint16_t *)plh_malloc(cache_bytes());
+    gs.d_cos = (float *)plh_malloc(tab);
+    gs.d_sin = (float *)plh_malloc(tab);
+    if (!gs.d_key || !gs.d_val || !gs.d_cos || !gs.d_sin || ensure_stage(1) != 0) {
+        fprintf(stderr, "gpu_hip: out of device memory: %s\n", plh_last_error());
+        return -1;
+    }
+    /* The tables are the host's own (model.c:545-556), so device RoPE is
+     * bit-identical; the cache mirrors whatever the host holds. */
+    if (plh_memcpy_htod(gs.d_cos, m->state.rope_cos, tab) != 0 ||
+        plh_memcpy_htod(gs.d_sin, m->state.rope_sin, tab) != 0 ||
+        plh_memcpy_htod(gs.d_key, m->state.key_cache, cache_bytes()) != 0 ||
+        plh_memcpy_htod(gs.d_val, m->state.val_cache, cache_bytes()) != 0) {
+        fprintf(stderr, "gpu_hip: upload failed: %s\n", plh_last_error());
+        return -1;
+    }
+    gs.uploaded = 1;
+    return 0;
+}
+
+int gpu_available(void) { return gs.inited && gs.uploaded; }
+
+int gpu_try_matmul(float *out, const float *x, const void *W, int n, int d, int qtype) {
+    (void)out; (void)x; (void)W; (void)n; (void)d; (void)qtype;
+    return -1;
+}
+
+void gpu_shutdown(void) {
+    if (gs.inited) {
+        plh_synchronize();
+        plh_free(gs.d_key);
+        plh_free(gs.d_val);
+        plh_free(gs.d_cos);
+        plh_free(gs.d_sin);
+        plh_free(gs.d_q);
+        plh_free(gs.d_k);
+        plh_free(gs.d_v);
+        plh_free(gs.d_out);
+        plh_shutdown();
+    }
+    memset(&gs, 0, sizeof gs);
+}
+
+static int same_shape(const model_t *m) {
+    const model_config_t *c = &m->config;
+    return c->n_layers == gs.n_layers && c->n_heads == gs.n_heads &&
+           c->n_kv_heads == gs.n_kv_heads && c->head_dim == gs.head_dim &&
+           c->max_seq_len == gs.max_seq_len && (int)c->rope_type == gs.rope_type &&
+           c->n_embd == gs.n_embd;
+}
+
+/* Copies rows [r0, r0+n) of layer `layer` from the device caches into the
+ * host caches. */
+static int rows_to_host(const model_t *m, int layer, int r0, int n) {
+    size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
+    size_t off = ((size_t)layer * gs.max_seq_len + (size_t)r0) * kv_dim;
+    size_t bytes = (size_t)n * kv_dim * sizeof(uint16_t);
+    if (plh_memcpy_dtoh(m->state.key_cache + off, gs.d_key + off, bytes) != 0) return -1;
+    if (plh_memcpy_dtoh(m->state.val_cache + off, gs.d_val + off, bytes) != 0) return -1;
+    return 0;
+}
+
+int gpu_try_attention(model_t *m, int layer, int pos, float *q, float *k, const float *v,
+                      float *out) {
+    if (!gpu_available() || !same_shape(m)) return -1;
+    if (layer < 0 || layer >= gs.n_layers || layer >= gs.gpu_layers) return -1;
+    if (pos < 0 || pos >= gs.max_seq_len) return -1;
+    size_t q_bytes = (size_t)gs.n_heads * gs.head_dim * sizeof(float);
+    size_t kv_bytes = (size_t)gs.n_kv_heads * gs.head_dim * sizeof(float);
+    if (plh_memcpy_htod(gs.d_q, q, q_bytes) != 0 || plh_memcpy_htod(gs.d_k, k, kv_bytes) != 0 ||
+        plh_memcpy_htod(gs.d_v, v, kv_bytes) != 0)
+        return -1; /* nothing on the device changed yet */
+    if (plh_attn_decode(gs.n_layers, gs.n_heads, gs.n_kv_heads, gs.head_dim, gs.max_seq_len,
+                        gs.rope_type, layer, 1, pos, gs.d_q, gs.d_k, gs.d_v, gs.d_key, gs.d_val,
+                        gs.d_cos, gs.d_sin, gs.d_out) != 0) {
+        backend_lost("plh_attn_decode");
+        return -1;
+    }
+    if (plh_memcpy_dtoh(out, gs.d_out, q_bytes) != 0 || rows_to_host(m, layer, pos, 1) != 0) {
+        backend_lost("copy back");
+        return -1;
+    }
+    return 0;
+}
+
+int gpu_try_attention_prefill(model_t *m, int layer, int start_pos, int n_tokens, float *q,
+                              float *k, const float *v, float *out) {
+    if (!gpu_available() || !same_shape(m)) return -1;
+    if (layer < 0 || layer >= gs.n_layers || layer >= gs.gpu_layers) return -1;
+    if (start_pos < 0 || n_tokens < 0 || (long)start_pos + n_tokens > (long)gs.max_seq_len)
+        return -1;
+    if (n_tokens == 0) return 0;
+    if (ensure_stage(n_tokens) != 0) {
+        backend_lost("staging allocation");
+        return -1;
+    }
+    size_t q_dim = (size_t)gs.n_heads * gs.head_dim;
+    size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
+    size_t stride = (size_t)gs.n_embd; /* out row bi at out + bi*n_embd (model.c:1057) */
+    if (stride < q_dim) return -1;
+    if (plh_memcpy_htod(gs.d_q, q, (size_t)n_tokens * q_dim * sizeof(float)) != 0 ||
+        plh_memcpy_htod(gs.d_k, k, (size_t)n_tokens * kv_dim * sizeof(float)) != 0 ||
+        plh_memcpy_htod(gs.d_v, v, (size_t)n_tokens * kv_dim * sizeof(float)) != 0)
+        return -1;
+    int dev_stride = (int)((q_dim + 3) & ~(size_t)3);
+    if (plh_attn_prefill(gs.n_layers, gs.n_heads, gs.n_kv_heads, gs.head_dim, gs.max_seq_len,
+                         gs.rope_type, layer, 1, start_pos, n_tokens, gs.d_q, gs.d_k, gs.d_v,
+                         gs.d_key, gs.d_val, gs.d_cos, gs.d_sin, gs.d_out, dev_stride) != 0) {
+        backend_lost("plh_attn_prefill");
+        return -1;
+    }
+    int rc = 0;
+    if ((size_t)dev_stride == stride) {
+        rc = plh_memcpy_dtoh(out, gs.d_out, (size_t)n_tokens * stride * sizeof(float));
+    } else {
+        for (int bi = 0; bi < n_tokens && rc == 0; bi++)
+            rc = plh_memcpy_dtoh(out + (size_t)bi * stride, gs.d_out + (size_t)bi * dev_stride,
+                                 q_dim * sizeof(float));
+    }
+    if (rc != 0 || rows_to_host(m, layer, start_pos, n_tokens) != 0) {
+        backend_lost("copy back");
+        return -1;
+    }
+    return 0;
+}
+
+static int kv_copy(const model_t *m, int n_pos, int to_host) {
+    if (!gpu_available() || !same_shape(m) || n_pos < 0 || n_pos > gs.max_seq_len) return -1;
+    size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
+    size_t bytes = (size_t)n_pos * kv_dim * sizeof(uint16_t);
+    for (int l = 0; l < gs.n_layers; l++) {
+        size_t off = (size_t)l * gs.max_seq_len * kv_dim;
+        int rc;
+        if (to_host) {
+            rc = plh_memcpy_dtoh(m->state.key_cache + off, gs.d_key + off, bytes) ||
+                 plh_memcpy_dtoh(m->state.val_cache + off, gs.d_val + off, bytes);
+        } else {
+            rc = plh_memcpy_htod(gs.d_key + off, m->state.key_cache + off, bytes) ||
+                 plh_memcpy_htod(gs.d_val + off, m->state.val_cache + off, bytes);
+        }
+        if (rc) {
+            backend_lost(to_host ? "kv download" : "kv upload");
+            return -1;
+        }
+    }
+    return 0;
+}
+
+int gpu_kv_download(const model_t *m, int n_pos) { return kv_copy(m, n_pos, 1); }
+
+int gpu_kv_upload(const model_t *m, int n_pos) { return kv_copy(m, n_pos, 0); }

@@ -1,0 +1,132 @@
+/*
+ * test_gpu_hip.c -- drives the gpu.h-style boundary (gpu_hip.c) the way
+ * picolm's forward passes would: per layer, gpu_try_attention_prefill at the
+ * point of model.c:1039 for the prompt, then gpu_try_attention at the point
+ * of model.c:819 for each generated token; a call returning -1 leaves the
+ * work to the caller's CPU block, which this harness records and skips.
+ *
+ * Usage: test_gpu_hip <input.bin> <output.bin>
+ * input : int32 [L, Hq, Hkv, D, S, rope_type, n_prompt, n_decode], float32
+ *         theta, then prompt q [L][P][q_dim], k, v [L][P][kv_dim], then
+ *         decode q [T][L][q_dim], k, v [T][L][kv_dim]
+ * output: int32 [rc_init, rc_upload, rc_download_roundtrip, rc_upload_roundtrip],
+ *         int32 rc_prefill[L], int32 rc_decode[T][L],
+ *         float32 prefill out [L][P][n_embd], decode out [T][L][q_dim],
+ *         uint16 host key cache, val cache.
+ */
+#include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "gpu_hip.h"
+#include "picolm_hip.h"
+
+static void *xread(FILE *f, size_t bytes) {
+    void *p = malloc(bytes ? bytes : 1);
+    if (!p || fread(p, 1, bytes, f) != bytes) {
+        fprintf(stderr, "short read\n");
+        exit(2);
+    }
+    return p;
+}
+
+int main(int argc, char **argv) {
+    if (argc != 3) return 2;
+    FILE *fi = fopen(argv[1], "rb");
+    if (!fi) return 2;
+    int32_t hdr[8];
+    float theta;
+    if (fread(hdr, 4, 8, fi) != 8 || fread(&theta, 4, 1, fi) != 1) return 2;
+    const int L = hdr[0], Hq = hdr[1], Hkv = hdr[2], D = hdr[3], S = hdr[4], rt = hdr[5];
+    const int P = hdr[6], T = hdr[7];
+    const size_t q_dim = (size_t)Hq * D, kv_dim = (size_t)Hkv * D;
+    float *pq = xread(fi, (size_t)L * P * q_dim * 4);
+    float *pk = xread(fi, (size_t)L * P * kv_dim * 4);
+    float *pv = xread(fi, (size_t)L * P * kv_dim * 4);
+    float *dq = xread(fi, (size_t)T * L * q_dim * 4);
+    float *dk = xread(fi, (size_t)T * L * kv_dim * 4);
+    float *dv = xread(fi, (size_t)T * L * kv_dim * 4);
+    fclose(fi);
+
+    model_t m;
+    memset(&m, 0, sizeof m);
+    m.config.n_embd = (int)q_dim;
+    m.config.n_heads = Hq;
+    m.config.n_kv_heads = Hkv;
+    m.config.n_layers = L;
+    m.config.max_seq_len = S;
+    m.config.head_dim = D;
+    m.config.rope_freq_base = theta;
+    m.config.rope_type = (rope_type_t)rt;
+    size_t cache_elems = (size_t)L * S * kv_dim;
+    m.state.key_cache = calloc(cache_elems, 2); /* zero-filled like model.c:612-619 */
+    m.state.val_cache = calloc(cache_elems, 2);
+    m.state.rope_cos = malloc((size_t)S * (D / 2) * 4);
+    m.state.rope_sin = malloc((size_t)S * (D / 2) * 4);
+    plh_rope_tables_host(m.state.rope_cos, m.state.rope_sin, S, D, theta);
+
+    int32_t rc[4] = {0, 0, 0, 0};
+    int32_t *rc_pre = calloc((size_t)L, 4);
+    int32_t *rc_dec = calloc((size_t)T * L, 4);
+    float *out_pre = calloc((size_t)L * P * q_dim, 4);
+    float *out_dec = calloc((size_t)T * L * q_dim, 4);
+
+    rc[0] = gpu_init(&m);
+    rc[1] = rc[0] == 0 ? gpu_upload_model(&m) : -1;
+
+    /* prompt: model_forward_prefill's layer loop, attention block per layer */
+    for (int l = 0; l < L; l++) {
+        rc_pre[l] = gpu_try_attention_prefill(&m, l, 0, P, pq + (size_t)l * P * q_dim,
+                                              pk + (size_t)l * P * kv_dim,
+                                              pv + (size_t)l * P * kv_dim,
+                                              out_pre + (size_t)l * P * q_dim);
+    }
+    /* generation: model_forward_ex's layer loop at pos P + t */
+    for (int t = 0; t < T; t++)
+        for (int l = 0; l < L; l++) {
+            size_t i = (size_t)t * L + l;
+            rc_dec[i] = gpu_try_attention(&m, l, P + t, dq + i * q_dim, dk + i * kv_dim,
+                                          dv + i * kv_dim, out_dec + i * q_dim);
+        }
+
+    /* kvcache_save / kvcache_load coherence: download into a cleared host
+     * cache must give back the same bytes; upload then download too */
+    int n_pos = P + T;
+    uint16_t *kcopy = malloc(cache_elems * 2), *vcopy = malloc(cache_elems * 2);
+    memcpy(kcopy, m.state.key_cache, cache_elems * 2);
+    memcpy(vcopy, m.state.val_cache, cache_elems * 2);
+    if (gpu_available()) {
+        memset(m.state.key_cache, 0, cache_elems * 2);
+        memset(m.state.val_cache, 0, cache_elems * 2);
+        rc[2] = gpu_kv_download(&m, n_pos);
+        if (rc[2] == 0 && (memcmp(kcopy, m.state.key_cache, cache_elems * 2) ||
+                           memcmp(vcopy, m.state.val_cache, cache_elems * 2)))
+            rc[2] = 1;
+        rc[3] = gpu_kv_upload(&m, n_pos);
+        if (rc[3] == 0) {
+            memset(m.state.key_cache, 0, cache_elems * 2);
+            memset(m.state.val_cache, 0, cache_elems * 2);
+            rc[3] = gpu_kv_download(&m, n_pos);
+            if (rc[3] == 0 && (memcmp(kcopy, m.state.key_cache, cache_elems * 2) ||
+                               memcmp(vcopy, m.state.val_cache, cache_elems * 2)))
+                rc[3] = 1;
+        }
+    } else {
+        rc[2] = gpu_kv_download(&m, n_pos);
+        rc[3] = gpu_kv_upload(&m, n_pos);
+    }
+    gpu_shutdown();
+
+    FILE *fo = fopen(argv[2], "wb");
+    if (!fo) return 2;
+    fwrite(rc, 4, 4, fo);
+    fwrite(rc_pre, 4, (size_t)L, fo);
+    fwrite(rc_dec, 4, (size_t)T * L, fo);
+    fwrite(out_pre, 4, (size_t)L * P * q_dim, fo);
+    fwrite(out_dec, 4, (size_t)T * L * q_dim, fo);
+    fwrite(kcopy, 2, cache_elems, fo);
+    fwrite(vcopy, 2, cache_elems, fo);
+    fclose(fo);
+    return 0;
+}

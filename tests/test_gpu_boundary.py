@@ -1,0 +1,133 @@
+"""The gpu.h-style boundary (gpu_hip.c) on the GPU, driven from C by
+tests/c/test_gpu_hip the way picolm's forward passes would call it.
+
+Checks: every call handled (0), prefill and decode outputs against the
+oracle, the host KV cache (kept authoritative by the boundary) bit-equal to
+the oracle's, download/upload round trips for kvcache_save/load, and the
+fallback switches: PICOLM_HIP_DISABLE=1 (all -1, nothing touched) and
+PICOLM_GPU_LAYERS=1 (later layers -1, their rows untouched).
+"""
+import os
+import subprocess
+
+import numpy as np
+import pytest
+
+from attn_check import assert_attn_close
+from conftest import ROOT
+
+pytestmark = pytest.mark.gpu
+
+EXE = os.path.join(ROOT, "tests", "c", "test_gpu_hip")
+
+
+def run_case(tmp_path, dims, theta, P, T, seed, env_extra=None):
+    L, Hq, Hkv, D, S, rt = dims
+    rng = np.random.default_rng(seed)
+    q_dim, kv_dim = Hq * D, Hkv * D
+    pq = rng.standard_normal((L, P, q_dim), dtype=np.float32)
+    pk = rng.standard_normal((L, P, kv_dim), dtype=np.float32)
+    pv = rng.standard_normal((L, P, kv_dim), dtype=np.float32)
+    dq = rng.standard_normal((T, L, q_dim), dtype=np.float32)
+    dk = rng.standard_normal((T, L, kv_dim), dtype=np.float32)
+    dv = rng.standard_normal((T, L, kv_dim), dtype=np.float32)
+    fin, fout = tmp_path / "in.bin", tmp_path / "out.bin"
+    with open(fin, "wb") as f:
+        np.array([L, Hq, Hkv, D, S, rt, P, T], np.int32).tofile(f)
+        np.array([theta], np.float32).tofile(f)
+        for a in (pq, pk, pv, dq, dk, dv):
+            a.tofile(f)
+    env = dict(os.environ)
+    env.update(env_extra or {})
+    print(f"[case] dims {dims} P {P} T {T} env {env_extra}", flush=True)
+    r = subprocess.run([EXE, str(fin), str(fout)], env=env, capture_output=True, text=True,
+                       timeout=240)
+    assert r.returncode == 0, r.stderr
+    buf = open(fout, "rb").read()
+    off = 0
+
+    def take(dtype, count):
+        nonlocal off
+        a = np.frombuffer(buf, dtype=dtype, count=count, offset=off)
+        off += a.nbytes
+        return a
+    rc = take(np.int32, 4)
+    rc_pre = take(np.int32, L)
+    rc_dec = take(np.int32, T * L).reshape(T, L)
+    out_pre = take(np.float32, L * P * q_dim).reshape(L, P, q_dim)
+    out_dec = take(np.float32, T * L * q_dim).reshape(T, L, q_dim)
+    n = L * S * kv_dim
+    kc = take(np.uint16, n)
+    vc = take(np.uint16, n)
+    return (rc, rc_pre, rc_dec, out_pre, out_dec, kc, vc), (pq, pk, pv, dq, dk, dv)
+
+
+def oracle_run(O, dims, theta, inputs, layers_gpu):
+    """Reference semantics for the layers that ran on the GPU; layers that fell
+    back are left untouched (the harness skips the CPU block)."""
+    L, Hq, Hkv, D, S, rt = dims
+    pq, pk, pv, dq, dk, dv = inputs
+    P, T = pq.shape[1], dq.shape[0]
+    shp = O.Shape(L, Hq, Hkv, D, S, theta, rt)
+    cos_t, sin_t = O.rope_tables(S, D, theta)
+    kc = np.zeros(L * S * Hkv * D, np.uint16)
+    vc = kc.copy()
+    pre = np.zeros((L, P, Hq * D), np.float32)
+    dec = np.zeros((T, L, Hq * D), np.float32)
+    for l in layers_gpu:
+        pre[l] = O.attn_prefill(shp, l, 0, P, pq[l].copy(), pk[l].copy(), pv[l], kc, vc,
+                                cos_t, sin_t)
+    for t in range(T):
+        for l in layers_gpu:
+            dec[t, l] = O.attn_decode(shp, l, P + t, dq[t, l].copy(), dk[t, l].copy(), dv[t, l],
+                                      kc, vc, cos_t, sin_t)
+    return pre, dec, kc, vc
+
+
+CASES = [
+    ((3, 32, 4, 64, 512, 0), 1e4, 200, 5),     # TinyLlama head layout
+    ((2, 32, 8, 64, 600, 0), 5e5, 257, 3),     # Llama-3.2 head layout
+    ((2, 32, 32, 128, 300, 0), 1e4, 90, 4),    # Llama-2 MHA
+    ((2, 16, 2, 64, 128, 1), 1e6, 60, 3),      # QWEN rotation
+]
+
+
+@pytest.mark.parametrize("dims,theta,P,T", CASES)
+def test_boundary_prefill_then_decode(tmp_path, oracle_mod, dims, theta, P, T):
+    (rc, rc_pre, rc_dec, out_pre, out_dec, kc, vc), inputs = run_case(tmp_path, dims, theta, P,
+                                                                        T, seed=P + T)
+    L, D = dims[0], dims[3]
+    assert list(rc) == [0, 0, 0, 0], rc
+    assert np.all(rc_pre == 0) and np.all(rc_dec == 0)
+    pre, dec, okc, ovc = oracle_run(oracle_mod, dims, theta, inputs, range(L))
+    for l in range(L):
+        assert_attn_close(out_pre[l], pre[l], D, 1e-3, f"prefill layer {l}")
+        for t in range(T):
+            assert_attn_close(out_dec[t, l], dec[t, l], D, 1e-3, f"decode t{t} layer {l}")
+    assert np.array_equal(kc, okc) and np.array_equal(vc, ovc)
+
+
+def test_boundary_disabled_falls_back_untouched(tmp_path, oracle_mod):
+    dims, theta, P, T = CASES[0]
+    (rc, rc_pre, rc_dec, out_pre, out_dec, kc, vc), _ = run_case(
+        tmp_path, dims, theta, 40, 2, seed=1, env_extra={"PICOLM_HIP_DISABLE": "1"})
+    assert rc[0] == -1 and rc[1] == -1 and rc[2] == -1 and rc[3] == -1
+    assert np.all(rc_pre == -1) and np.all(rc_dec == -1)
+    assert not out_pre.any() and not out_dec.any()
+    assert not kc.any() and not vc.any()
+
+
+def test_boundary_gpu_layers_limit(tmp_path, oracle_mod):
+    dims, theta, P, T = CASES[0]
+    L, D = dims[0], dims[3]
+    (rc, rc_pre, rc_dec, out_pre, out_dec, kc, vc), inputs = run_case(
+        tmp_path, dims, theta, 70, 3, seed=2, env_extra={"PICOLM_GPU_LAYERS": "1"})
+    assert rc[0] == 0 and rc[1] == 0
+    assert rc_pre[0] == 0 and np.all(rc_pre[1:] == -1)
+    assert np.all(rc_dec[:, 0] == 0) and np.all(rc_dec[:, 1:] == -1)
+    pre, dec, okc, ovc = oracle_run(oracle_mod, dims, theta, inputs, [0])
+    assert_attn_close(out_pre[0], pre[0], D, 1e-3, "prefill layer 0")
+    for t in range(3):
+        assert_attn_close(out_dec[t, 0], dec[t, 0], D, 1e-3, f"decode t{t} layer 0")
+    assert not out_pre[1:].any() and not out_dec[:, 1:].any()
+    assert np.array_equal(kc, okc) and np.array_equal(vc, ovc)
