@@ -12,6 +12,7 @@
 
 typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
@@ -68,11 +69,57 @@ __device__ __forceinline__ void split_hi_lo(float x, _Float16& hi, _Float16& lo)
   lo = (_Float16)(x - (float)hi);
 }
 
+// Same split for a pair of values, for softmax weights in [0, 2^8]:
+// hi = rtz(x) by the packed round-toward-zero conversion, lo = f16(x - hi) by
+// two mixed-precision FMAs (f16 first operand, f32 addend, f16 result written
+// into the low / high half of the register).  x - hi is exact, so hi + lo
+// keeps ~22 bits.  Three instructions per pair.
+__device__ __forceinline__ void split_pair_rtz(float x0, float x1, half2_t& hi, half2_t& lo) {
+  const uint32_t h = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_pkrtz(x0, x1));
+  uint32_t l;
+  asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(l) : "v"(h), "v"(x0));
+  asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+      : "+v"(l)
+      : "v"(h), "v"(x1));
+  hi = __builtin_bit_cast(half2_t, h);
+  lo = __builtin_bit_cast(half2_t, l);
+}
+
+// IEEE-754 maximum (NaN-propagating); lowers to v_maximum3_f32 on gfx950
+// without the NaN-quieting moves that fmaxf needs.
+__device__ __forceinline__ float vmax(float a, float b) {
+  return __builtin_elementwise_maximum(a, b);
+}
+
+// gfx950 transposing LDS read (ds_read_b64_tr_b16).  Within each 16-lane group,
+// lane i passes the address of 4 consecutive fp16 values: chunk i%4 of row
+// i/4 of a 4 x 16 block.  Lane i receives column i of that block, rows 0..3.
+__device__ __forceinline__ half4_t lds_read_tr4(const _Float16* p) {
+  typedef __fp16 fp16x4_t __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) fp16x4_t lds_fp16x4;
+  return __builtin_bit_cast(half4_t, __builtin_amdgcn_ds_read_tr16_b64_v4f16((lds_fp16x4*)p));
+}
+
 __device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Maximum over lanes l and l^16 (resp. l^32) with the gfx950 row-swap
+// permutes: permlane16_swap(x, x) returns rows {0,0,2,2} and {1,1,3,3} of x
+// (rows of 16 lanes), permlane32_swap(x, x) returns halves {0,0} and {1,1}, so
+// the larger of the two results is the pairwise maximum.  No LDS round trip.
+__device__ __forceinline__ float max_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float max_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
   return __shfl_xor(v, mask, 64);

@@ -17,15 +17,21 @@
 // waves own 16 "columns" each; a column is one (token, q head) pair of the
 // block, so all q heads of the kv head's GQA group share every K/V tile.
 // K/V tiles of 32 rows are staged in LDS (double-buffered, loaded by the
-// whole workgroup): K row-major, V transposed (d-major), so that
+// whole workgroup), both row-major:
 //   S^T[t][c] = K[t][:] . q_c      A = K rows (ds_read_b128), B = q_c hi/lo
-//   O^T[d][c] += V^T[d][t] P^T[t][c]  A = V^T (ds_read_b128), B = P hi/lo
+//   O^T[d][c] += V^T[d][t] P^T[t][c]  A = V^T (two ds_read_b64_tr_b16), B = P hi/lo
 // The two 16-row MFMA blocks of S^T read K rows in the order
 // pi_rb(i) = 8*(i/4) + 4*rb + i%4, which leaves lane group g holding rows
 // 8g..8g+7 of the tile: exactly the K slots of the PV product, so P never
-// leaves registers and each V^T operand is one contiguous 16-byte LDS read.
-// q and P are split into fp16 hi + lo parts (two MFMAs each), keeping the
-// products at ~fp32 precision.
+// leaves registers; the transposing LDS read turns row-major V into the
+// d-major A operand.  q and P are split into fp16 hi + lo parts (two MFMAs
+// each), keeping the products at ~fp32 precision.
+//
+// Softmax bookkeeping per tile is kept short: the maximum is taken over raw
+// scores and the 1/sqrt(D)*log2(e) scale is folded into the exp2 argument;
+// the causal mask is applied only on tiles that cross a column's last row;
+// the running maximum is raised (and O, l rescaled) only when a new score
+// exceeds it by more than 2^kLazy, so weights stay below 2^kLazy.
 #include <math.h>
 
 #include "attn_common.h"
@@ -39,6 +45,7 @@ namespace {
 constexpr int kPW = 8;               // waves per attention workgroup
 constexpr int kPThreads = 64 * kPW;
 constexpr int kKT = 32;              // K/V rows per tile
+constexpr float kLazy = 8.0f;        // rescale threshold (log2 units)
 
 template <int D>
 __global__ __launch_bounds__(256) void prefill_append_kernel(PrefillArgs a) {
@@ -73,13 +80,17 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   constexpr int ND = D / 32;     // 32-wide d blocks of QK
   constexpr int NO = D / 16;     // 16-wide d blocks of PV
   constexpr int KP = D + 8;      // LDS pitch of a K row (halves)
-  constexpr int VP = kKT + 8;    // LDS pitch of a V^T row (halves)
+  constexpr int VP = D + 16;     // LDS pitch of a V row (halves): the 4 rows of a
+                                 // transposing read land in disjoint banks
   constexpr int KCH = kKT * D / 8;  // 16-byte chunks of a K (or V) tile
-  __shared__ __align__(16) _Float16 ks[2][kKT * KP];
-  __shared__ __align__(16) _Float16 vs[2][D * VP];
+  constexpr int KBUF = kKT * KP;  // one K tile buffer (halves)
+  constexpr int VBUF = kKT * VP;  // one V tile buffer (halves)
+  constexpr int VOFF = 2 * KBUF;  // V buffers follow the two K buffers
+  __shared__ __align__(16) _Float16 smem[2 * KBUF + 2 * VBUF];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
 
   // XCD-aware order: each XCD takes whole (layer, kv head) groups, so the
@@ -106,6 +117,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   const bool cvalid = tok < a.bq && i0 + tok < a.n_tokens;
   const int tok_c = cvalid ? i0 + tok : last_tok;          // clamped for addressing
   const int p_col = a.start_pos + tok_c;                  // causal limit of the column
+  // smallest causal limit among the wave's columns (wave-uniform)
+  const int p_min = __builtin_amdgcn_readfirstlane(
+      a.start_pos + min(i0 + (wave * 16) / G, last_tok));
 
   // ---- cooperative tile loads (issued early; stored to LDS after compute) --
   const size_t row0 = (size_t)layer * a.max_seq_len;
@@ -124,21 +138,21 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
       ld[u] = *(const half8_t*)src;
     }
   };
+  // LDS destination of each loaded chunk in buffer 0, and the step to buffer 1
+  int st_off[LPT], st_step[LPT];
+#pragma unroll
+  for (int u = 0; u < LPT; ++u) {
+    const int ch = tid + u * kPThreads;
+    const int cc = ch % KCH;
+    const int r = cc / (D / 8), q8 = cc % (D / 8);
+    st_off[u] = ch < KCH ? r * KP + 8 * q8 : VOFF + r * VP + 8 * q8;
+    st_step[u] = ch < KCH ? KBUF : VBUF;
+  }
   auto store_lds = [&](int b) {
 #pragma unroll
-    for (int u = 0; u < LPT; ++u) {
-      const int ch = tid + u * kPThreads;
-      if (ch < 2 * KCH) {
-        const int cc = ch % KCH;
-        const int r = cc / (D / 8), q8 = cc % (D / 8);
-        if (ch < KCH) {
-          *(half8_t*)&ks[b][r * KP + 8 * q8] = ld[u];
-        } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) vs[b][(8 * q8 + e) * VP + r] = ld[u][e];
-        }
-      }
-    }
+    for (int u = 0; u < LPT; ++u)
+      if (tid + u * kPThreads < 2 * KCH)
+        *(half8_t*)&smem[st_off[u] + b * st_step[u]] = ld[u];
   };
   issue_loads(0);
 
@@ -191,10 +205,16 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   __syncthreads();
 
   const float sscale = a.score_scale;
-  float m = kNegBig, l = 0.f;
+  float ms = kNegBig;            // running max (scaled, log2 units)
+  float4_t lsum = float4_t{0.f, 0.f, 0.f, 0.f};  // running sum (all 4 entries equal)
+  half8_t ones;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones[j] = (_Float16)1.0f;
   float4_t o[NO];
 #pragma unroll
   for (int ob = 0; ob < NO; ++ob) o[ob] = float4_t{0.f, 0.f, 0.f, 0.f};
+  // transposing-read address of this lane: row 8*grp + col/4, chunk col%4
+  const int vofs = (8 * grp + (col >> 2)) * VP + 4 * (col & 3);
 
   for (int it = 0; it < n_tiles; ++it) {
     const int b = it & 1;
@@ -202,7 +222,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
     const bool more = it + 1 < n_tiles;
     if (more) issue_loads(t0 + kKT);
 
-    // S^T for this wave's 16 columns
+    // S^T for this wave's 16 columns (raw scores)
     float4_t s[2];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
@@ -210,45 +230,54 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
       s[rb] = float4_t{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int db = 0; db < ND; ++db) {
-        const half8_t kk = *(const half8_t*)&ks[b][krow * KP + 32 * db + 8 * grp];
+        const half8_t kk = *(const half8_t*)&smem[b * KBUF + krow * KP + 32 * db + 8 * grp];
         s[rb] = mfma16x16x32(kk, qhi[db], s[rb]);
         s[rb] = mfma16x16x32(kk, qlo[db], s[rb]);
       }
     }
-    // online softmax: lane holds rows t0 + 8*grp + j, j = 4*rb + r
+    // lane holds rows t0 + 8*grp + j, j = 4*rb + r
     float u[8];
-    float tmax = -INFINITY;
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int t = t0 + 8 * grp + 4 * rb + r;
-        float x = s[rb][r] * sscale;
-        x = (t <= p_col) ? x : -INFINITY;
-        u[4 * rb + r] = x;
-        tmax = fmaxf(tmax, x);
-      }
-    tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
-    tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
-    const float mnew = fmaxf(m, tmax);
-    const float alpha = fast_exp2(m - mnew);
-    m = mnew;
-    half8_t ph, pl;
-    float psum = 0.f;
+      for (int r = 0; r < 4; ++r) u[4 * rb + r] = s[rb][r];
+    if (t0 + kKT - 1 > p_min) {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const float p = fast_exp2(u[j] - mnew);
-      psum += p;
-      _Float16 hi, lo;
-      split_hi_lo(p, hi, lo);
-      ph[j] = hi;
-      pl[j] = lo;
+      for (int j = 0; j < 8; ++j)
+        if (t0 + 8 * grp + j > p_col) u[j] = -INFINITY;
     }
-    l = l * alpha + psum;
+    float tmax = u[0];
+#pragma unroll
+    for (int j = 1; j < 8; ++j) tmax = vmax(tmax, u[j]);
+    tmax = max_xor32(max_xor16(tmax));
+    const float tms = tmax * sscale;
+    if (__ballot(tms > ms + kLazy)) {
+      const float mnew = fmaxf(ms, tms);
+      const float alpha = fast_exp2(ms - mnew);
+      ms = mnew;
+      lsum *= alpha;
+#pragma unroll
+      for (int ob = 0; ob < NO; ++ob) o[ob] *= alpha;
+    }
+    half8_t ph, pl;
+#pragma unroll
+    for (int j = 0; j < 8; j += 2) {
+      const float p0 = fast_exp2(__builtin_fmaf(u[j], sscale, -ms));
+      const float p1 = fast_exp2(__builtin_fmaf(u[j + 1], sscale, -ms));
+      half2_t hi, lo;
+      split_pair_rtz(p0, p1, hi, lo);
+      ph[j] = hi[0], ph[j + 1] = hi[1];
+      pl[j] = lo[0], pl[j + 1] = lo[1];
+    }
+    // row sums on the matrix core: every row of ones . P^T is the column sum
+    lsum = mfma16x16x32(ones, ph, lsum);
+    lsum = mfma16x16x32(ones, pl, lsum);
 #pragma unroll
     for (int ob = 0; ob < NO; ++ob) {
-      const half8_t va = *(const half8_t*)&vs[b][(16 * ob + col) * VP + 8 * grp];
-      o[ob] *= alpha;
+      const _Float16* vp = &smem[VOFF + b * VBUF + vofs + 16 * ob];
+      const half4_t v0 = lds_read_tr4(vp);
+      const half4_t v1 = lds_read_tr4(vp + 4 * VP);
+      const half8_t va = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
       o[ob] = mfma16x16x32(va, ph, o[ob]);
       o[ob] = mfma16x16x32(va, pl, o[ob]);
     }
@@ -258,10 +287,8 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   }
 
   // ---- normalise and write: lane holds d = 16*ob + 4*grp + r of its column ---
-  l += shfl_xor_f(l, 16);
-  l += shfl_xor_f(l, 32);
   if (cvalid) {
-    const float inv = 1.0f / l;
+    const float inv = 1.0f / lsum[0];
     float* orow = a.out + ((size_t)li * a.n_tokens + i0 + tok) * a.out_stride +
                   (size_t)(kvh * G + hh) * D;
 #pragma unroll

@@ -6,6 +6,12 @@ Tolerance (written here once, used by every attention parity test):
 with tol = 1e-3, or 1e-2 for softmax-sensitive long contexts (more than 4096
 cached rows), following the attention-output bound of the build's target.
 The fp16 KV cache is compared bit for bit.
+
+Precision guard: the kernels split q and the softmax weights into fp16 hi + lo
+parts so that the MFMA products keep ~22 bits.  Dropping either lo part still
+passes 1e-3 (it costs ~2e-4 normwise on N(0,1) data), so the normwise error
+is also held to PREC = 5e-5, well above the ~1e-5 that fp32 summation-order
+differences reach on these inputs.
 """
 from __future__ import annotations
 
@@ -13,6 +19,7 @@ import numpy as np
 
 TOL = 1e-3
 TOL_LONG = 1e-2
+PREC = 5e-5
 
 
 def tol_for(n_rows: int) -> float:
@@ -29,11 +36,13 @@ def attn_errors(gpu: np.ndarray, ref: np.ndarray, head_dim: int):
     return float(normwise.max()), float(elem.max())
 
 
-def assert_attn_close(gpu, ref, head_dim, tol=TOL, what=""):
+def assert_attn_close(gpu, ref, head_dim, tol=TOL, what="", prec=PREC):
     assert np.all(np.isfinite(gpu)), f"{what}: non-finite output"
     nw, el = attn_errors(gpu, ref, head_dim)
     print(f"[parity] {what}: normwise {nw:.3e} elementwise {el:.3e} (tol {tol:g})", flush=True)
     assert nw <= tol and el <= tol, f"{what}: normwise {nw:.3e} elementwise {el:.3e} > {tol:g}"
+    if prec is not None:
+        assert nw <= prec, f"{what}: normwise {nw:.3e} above the hi/lo precision guard {prec:g}"
     return nw, el
 
 
