@@ -9,7 +9,12 @@
 // that kv head's GQA group); the group's positions are cut into `n_split`
 // splits of `split_len` rows; a workgroup (4 wavefronts) owns one (group,
 // split) unit and its waves take 32-row tiles of the split in turn, keeping
-// the loads of the next 2-4 tiles in flight while one tile is computed.  Every K/V
+// the loads of the next tile in flight while one tile is computed.
+// Splits are short (512-1024 rows) and numerous (several workgroups per CU):
+// on MI355X one CU streams only ~35 GB/s, so reaching HBM bandwidth needs
+// nearly every CU streaming, and small register-light workgroups keep several
+// per CU in flight to cover each one's q-load latency.  Deeper per-wave
+// prefetch measured slower.  Every K/V
 // byte of the group is read from HBM exactly once, whatever the GQA factor,
 // because all q heads of the group ride in the same MFMA.
 //
@@ -17,13 +22,18 @@
 //   S^T[t][h] = K[t][:] . q[h][:]   two v_mfma_f32_16x16x32_f16 row blocks,
 //                                   q split into fp16 hi+lo (two MFMAs each)
 //                                   so the product keeps ~fp32 precision;
-//   online softmax in the log2 domain (one max/exp2 per score);
-//   O^T[d][h] += V^T[d][t] P^T[t][h] with P split hi+lo; V is transposed
-//                                   through a per-wave LDS tile.
+//   online softmax in the log2 domain: maximum over raw scores, scale folded
+//                                   into the exp2 argument, rescale of O only
+//                                   when the maximum grows by more than 2^8;
+//   O^T[d][h] += V^T[d][t] P^T[t][h] with P split hi+lo; V goes row-major
+//                                   through a per-wave LDS tile and comes back
+//                                   transposed by ds_read_b64_tr_b16;
+//   the softmax denominators ride in the same MFMA pipe (ones . P^T).
 // The S^T accumulator layout (lane = 16*g + h holds rows 4g..4g+3 of each
 // 16-row block) is used directly as the B operand of the PV product: the
 // K slots (g, j) of that product map to tile rows 4g+j (j<4) and 16+4g+j-4
-// (j>=4), and the LDS read of V^T uses the same map.
+// (j>=4); the two transposing reads of a 16-column block fetch exactly those
+// rows.
 //
 // Row `pos` itself is never read back from the cache: the workgroup owning
 // the last split computes k_rot/v for that row, writes the fp16 row, and
@@ -47,16 +57,23 @@ using namespace plh;
 
 namespace {
 
-constexpr int kWaves = 4;
-constexpr int kThreads = 64 * kWaves;
 constexpr int kTile = 32;
+constexpr float kLazy = 8.0f;  // rescale threshold (log2 units)
+constexpr int kCombineThreads = 256;
 
-// Tiles in flight per wave: head_dim 64 keeps 4 tiles (32 KB) of loads in
-// registers, head_dim 128 keeps 2 (also 32 KB).
+// Workgroup shape: W waves, each keeping PF tiles of loads in registers
+// (32 VGPRs per tile at head_dim 64, 64 at 128).
 template <int D>
-struct Prefetch {
-  static constexpr int depth = D == 64 ? 4 : 2;
+struct DecodeShape;
+template <>
+struct DecodeShape<64> {
+  static constexpr int W = 4, PF = 1;
 };
+template <>
+struct DecodeShape<128> {
+  static constexpr int W = 4, PF = 1;
+};
+constexpr int kCombineChunk = 16;  // split partials loaded together by the combine
 
 template <int D>
 struct Tile {
@@ -201,10 +218,11 @@ template <int D>
 __device__ __forceinline__ void process_tile(const Tile<D>& T, const half8_t (&qhi)[D / 32],
                                              const half8_t (&qlo)[D / 32], _Float16* vt, int t0,
                                              int tlast, int lane, int col, int grp, float sscale,
-                                             float& m, float& l, float4_t (&o)[D / 16]) {
+                                             half8_t ones, float& ms, float4_t& lsum,
+                                             float4_t (&o)[D / 16]) {
   using TT = Tile<D>;
   constexpr int NO = D / 16;
-  constexpr int VP = D + 8;
+  constexpr int VP = D + 16;
   float4_t s[2];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb) {
@@ -215,63 +233,71 @@ __device__ __forceinline__ void process_tile(const Tile<D>& T, const half8_t (&q
       s[rb] = mfma16x16x32(T.k[rb][db], qlo[db], s[rb]);
     }
   }
+  // V rows into the wave's LDS tile, row-major
 #pragma unroll
   for (int i = 0; i < TT::VLOADS; ++i)
     *(half8_t*)(vt + (i * TT::VROWS + lane / TT::VCH) * VP + 8 * (lane % TT::VCH)) = T.v[i];
 
-  // online softmax over this tile (log2 domain)
-  float u[2][4];
-  float tmax = -INFINITY;
+  // online softmax over this tile (log2 domain); slot j holds tile row
+  // 4*grp + j (j < 4) or 16 + 4*grp + j - 4
+  float u[8];
 #pragma unroll
   for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int t = t0 + 16 * rb + 4 * grp + r;
-      float x = s[rb][r] * sscale;
-      x = (t <= tlast) ? x : -INFINITY;
-      u[rb][r] = x;
-      tmax = fmaxf(tmax, x);
-    }
-  tmax = fmaxf(tmax, shfl_xor_f(tmax, 16));
-  tmax = fmaxf(tmax, shfl_xor_f(tmax, 32));
-  const float mnew = fmaxf(m, tmax);
-  const float alpha = fast_exp2(m - mnew);
-  m = mnew;
-  half8_t ph, pl;
-  float psum = 0.f;
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb)
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const float p = fast_exp2(u[rb][r] - mnew);
-      psum += p;
-      _Float16 hi, lo;
-      split_hi_lo(p, hi, lo);
-      ph[4 * rb + r] = hi;
-      pl[4 * rb + r] = lo;
-    }
-  l = l * alpha + psum;
-#pragma unroll
-  for (int ob = 0; ob < NO; ++ob) o[ob] *= alpha;
-
-#pragma unroll
-  for (int ob = 0; ob < NO; ++ob) {
-    half8_t va;
+    for (int r = 0; r < 4; ++r) u[4 * rb + r] = s[rb][r];
+  if (t0 + kTile - 1 > tlast) {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const int t = (j < 4) ? 4 * grp + j : 16 + 4 * grp + (j - 4);
-      va[j] = vt[t * VP + 16 * ob + col];
+      const int t = t0 + (j < 4 ? 4 * grp + j : 12 + 4 * grp + j);
+      if (t > tlast) u[j] = -INFINITY;
     }
+  }
+  float tmax = u[0];
+#pragma unroll
+  for (int j = 1; j < 8; ++j) tmax = vmax(tmax, u[j]);
+  tmax = max_xor32(max_xor16(tmax));
+  const float tms = tmax * sscale;
+  if (__ballot(tms > ms + kLazy)) {
+    const float mnew = fmaxf(ms, tms);
+    const float alpha = fast_exp2(ms - mnew);
+    ms = mnew;
+    lsum *= alpha;
+#pragma unroll
+    for (int ob = 0; ob < NO; ++ob) o[ob] *= alpha;
+  }
+  half8_t ph, pl;
+#pragma unroll
+  for (int j = 0; j < 8; j += 2) {
+    const float p0 = fast_exp2(__builtin_fmaf(u[j], sscale, -ms));
+    const float p1 = fast_exp2(__builtin_fmaf(u[j + 1], sscale, -ms));
+    half2_t hi, lo;
+    split_pair_rtz(p0, p1, hi, lo);
+    ph[j] = hi[0], ph[j + 1] = hi[1];
+    pl[j] = lo[0], pl[j + 1] = lo[1];
+  }
+  lsum = mfma16x16x32(ones, ph, lsum);
+  lsum = mfma16x16x32(ones, pl, lsum);
+
+  // transposing reads: rows 4*grp + col/4 and 16 + 4*grp + col/4, chunk col%4
+  const _Float16* vr = vt + (4 * grp + (col >> 2)) * VP + 4 * (col & 3);
+#pragma unroll
+  for (int ob = 0; ob < NO; ++ob) {
+    const half4_t v0 = lds_read_tr4(vr + 16 * ob);
+    const half4_t v1 = lds_read_tr4(vr + 16 * VP + 16 * ob);
+    const half8_t va = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
     o[ob] = mfma16x16x32(va, ph, o[ob]);
     o[ob] = mfma16x16x32(va, pl, o[ob]);
   }
 }
 
 template <int D>
-__global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(DecodeArgs a) {
+  constexpr int kWaves = DecodeShape<D>::W;
+  constexpr int kThreads = 64 * kWaves;
   constexpr int ND = D / 32;          // 32-wide d blocks of QK
   constexpr int NO = D / 16;          // 16-wide d blocks of PV
-  constexpr int VP = D + 8;           // LDS pitch of a V tile row (halves)
+  constexpr int VP = D + 16;          // LDS pitch of a V tile row (halves): the 4 rows
+                                      // of a transposing read land in disjoint banks
   constexpr int kVtileHalves = kWaves * kTile * VP;
   constexpr int kCombFloats = kWaves * 16 * (D + 2);
   constexpr int kSmemBytes =
@@ -279,7 +305,8 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
 
   const int tid = threadIdx.x;
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
 
   // XCD-aware unit order: consecutive workgroup ids go to different XCDs, so
@@ -322,7 +349,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
   // tlast and are masked), so the compiler's wait counts stay exact and the
   // prefetch is never drained early.  A split with no cached rows (te <= tb)
   // skips the stream as a whole.
-  constexpr int PF = Prefetch<D>::depth;
+  constexpr int PF = DecodeShape<D>::PF;
   const bool has_rows = te > tb;
   Tile<D> buf[PF];
   if (has_rows) {
@@ -391,7 +418,11 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
   // ---- stream the split's cached rows, one tile ahead ----------------------
   _Float16* vt = reinterpret_cast<_Float16*>(smem) + wave * (kTile * VP);
   const float sscale = a.score_scale;
-  float m = kNegBig, l = 0.f;
+  float m = kNegBig;                              // running max (scaled, log2 units)
+  float4_t lsum = float4_t{0.f, 0.f, 0.f, 0.f};  // running sum (all entries equal)
+  half8_t ones;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ones[j] = (_Float16)1.0f;
   float4_t o[NO];
 #pragma unroll
   for (int ob = 0; ob < NO; ++ob) o[ob] = float4_t{0.f, 0.f, 0.f, 0.f};
@@ -402,15 +433,13 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
       for (int j = 0; j < PF; ++j) {
         const int t0 = base + j * kStride;
         if (t0 < te)
-          process_tile<D>(buf[j], qhi, qlo, vt, t0, tlast, lane, col, grp, sscale, m, l, o);
+          process_tile<D>(buf[j], qhi, qlo, vt, t0, tlast, lane, col, grp, sscale, ones, m, lsum,
+                          o);
         load_tile<D>(buf[j], kbase, vbase, kv_dim, t0 + PF * kStride, tlast, lane, col, grp);
       }
     }
   }
-
-  // per-head sum over the 4 lane groups
-  l += shfl_xor_f(l, 16);
-  l += shfl_xor_f(l, 32);
+  const float l = lsum[0];
 
   __syncthreads();  // V tiles are dead; the LDS now holds the combine slots
   float* cm = reinterpret_cast<float*>(smem);          // [kWaves][16]
@@ -463,7 +492,7 @@ __global__ __launch_bounds__(kThreads) void attn_decode_kernel(DecodeArgs a) {
 // Merges the n_split partials of one group: out = sum_s O_s 2^(m_s-M) /
 // sum_s l_s 2^(m_s-M) with M the largest m_s.
 template <int D>
-__global__ __launch_bounds__(kThreads) void attn_decode_combine_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kCombineThreads) void attn_decode_combine_kernel(DecodeArgs a) {
   const int group = blockIdx.x;
   const int hblk = group % a.n_hblk;
   const int kvh = (group / a.n_hblk) % a.n_kv_heads;
@@ -473,30 +502,45 @@ __global__ __launch_bounds__(kThreads) void attn_decode_combine_kernel(DecodeArg
   const int nh = min(16, G - h0);
   float* out_base = a.out + (size_t)li * a.n_heads * D + (size_t)(kvh * G + h0) * D;
   const int u0 = group * a.n_split;
-  for (int idx = threadIdx.x; idx < nh * D; idx += kThreads) {
+  for (int idx = threadIdx.x; idx < nh * D; idx += kCombineThreads) {
     const int h = idx / D, d = idx - (idx / D) * D;
-    // one online pass: the loads of several splits are independent and issue
-    // together
+    // the loads of a chunk of splits are issued together, then merged
     float M = kNegBig, L = 0.f, O = 0.f;
-#pragma unroll 4
-    for (int sp = 0; sp < a.n_split; ++sp) {
-      const size_t u = (size_t)(u0 + sp) * 16 + h;
-      const float mi = a.part_m[u], li = a.part_l[u], oi = a.part_o[u * D + d];
-      const float Mn = fmaxf(M, mi);
-      const float ra = fast_exp2(M - Mn), rb = fast_exp2(mi - Mn);
-      L = L * ra + li * rb;
-      O = O * ra + oi * rb;
-      M = Mn;
+    for (int s0 = 0; s0 < a.n_split; s0 += kCombineChunk) {
+      float mi[kCombineChunk], li[kCombineChunk], oi[kCombineChunk];
+#pragma unroll
+      for (int j = 0; j < kCombineChunk; ++j) {
+        const size_t u = (size_t)(u0 + min(s0 + j, a.n_split - 1)) * 16 + h;
+        mi[j] = a.part_m[u];
+        li[j] = a.part_l[u];
+        oi[j] = a.part_o[u * D + d];
+      }
+      float Mc = M;
+#pragma unroll
+      for (int j = 0; j < kCombineChunk; ++j)
+        if (s0 + j < a.n_split) Mc = fmaxf(Mc, mi[j]);
+      const float r = fast_exp2(M - Mc);
+      L *= r;
+      O *= r;
+#pragma unroll
+      for (int j = 0; j < kCombineChunk; ++j) {
+        if (s0 + j < a.n_split) {
+          const float w = fast_exp2(mi[j] - Mc);
+          L = __builtin_fmaf(li[j], w, L);
+          O = __builtin_fmaf(oi[j], w, O);
+        }
+      }
+      M = Mc;
     }
     out_base[(size_t)h * D + d] = O * (1.0f / L);
   }
 }
 
-// Split plan defaults, from sweeps on MI355X (TinyLlama pos 2047, Llama-3.2
-// pos 8191, Llama-2 pos 4095): splits of >= 1024 rows and about four
-// workgroups per CU.
-int g_target_units = 0;   // 0: 4 workgroups per CU
-int g_min_split = 1024;
+// Split plan defaults, from sweeps on MI355X (TinyLlama pos 256 and 2047,
+// Llama-3.2 pos 8191, Llama-2 pos 4095): about four workgroups per CU,
+// splits of >= 512 rows (shorter contexts then need no combine launch).
+int g_target_units = 0;   // 0: four workgroups per CU
+int g_min_split = 512;
 
 }  // namespace
 
@@ -560,7 +604,7 @@ extern "C" int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int he
   const int npos = pos + 1;
   // Split plan: about `target` workgroups in all, each split at least
   // g_min_split rows (fewer splits, fewer partials to merge), split length a
-  // multiple of 4 waves x 32 rows.
+  // multiple of 128 rows.
   const int target = g_target_units > 0 ? g_target_units : 4 * (c.num_cus > 0 ? c.num_cus : 256);
   long want_split = ((long)npos * n_groups + target - 1) / target;
   if (want_split < g_min_split) want_split = g_min_split;
@@ -603,18 +647,20 @@ extern "C" int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int he
   a.per_xcd = per_xcd;
   a.score_scale = kLog2e / sqrtf((float)head_dim);
 
-  const dim3 grid((unsigned)(8 * per_xcd)), block(kThreads);
+  const dim3 grid((unsigned)(8 * per_xcd)), cblock(kCombineThreads);
   if (head_dim == 64)
-    hipLaunchKernelGGL(attn_decode_kernel<64>, grid, block, 0, c.stream, a);
+    hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(64 * DecodeShape<64>::W), 0, c.stream,
+                       a);
   else
-    hipLaunchKernelGGL(attn_decode_kernel<128>, grid, block, 0, c.stream, a);
+    hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(64 * DecodeShape<128>::W), 0,
+                       c.stream, a);
   if (check_hip(hipGetLastError(), "attn_decode_kernel")) return -1;
   if (n_split == 1) return 0;
   if (head_dim == 64)
-    hipLaunchKernelGGL(attn_decode_combine_kernel<64>, dim3((unsigned)n_groups), block, 0,
+    hipLaunchKernelGGL(attn_decode_combine_kernel<64>, dim3((unsigned)n_groups), cblock, 0,
                        c.stream, a);
   else
-    hipLaunchKernelGGL(attn_decode_combine_kernel<128>, dim3((unsigned)n_groups), block, 0,
+    hipLaunchKernelGGL(attn_decode_combine_kernel<128>, dim3((unsigned)n_groups), cblock, 0,
                        c.stream, a);
   return check_hip(hipGetLastError(), "attn_decode_combine_kernel");
 }
