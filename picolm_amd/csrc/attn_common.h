@@ -61,6 +61,16 @@ __device__ __forceinline__ void rope_rotate(float& a, float& b, float c, float s
   b = t2 + t3;
 }
 
+// RoPE rotation of an operand that is only used in dot products (q): the
+// same pairing and table entries, with each output one product and one
+// fused multiply-add (within one fp32 rounding of the reference's
+// four-product form; the cached k rows keep that exact form).
+__device__ __forceinline__ void rope_rotate_fused(float& a, float& b, float c, float s) {
+  const float a0 = a;
+  a = __builtin_fmaf(a0, c, -(b * s));
+  b = __builtin_fmaf(a0, s, b * c);
+}
+
 // Splits an fp32 value into fp16 hi + lo so that an fp16 MFMA over both parts
 // reproduces the fp32 operand to ~2^-22 relative (hi keeps 11 bits, lo the
 // next 11).  Values must be below 65504 in magnitude.
@@ -69,7 +79,8 @@ __device__ __forceinline__ void split_hi_lo(float x, _Float16& hi, _Float16& lo)
   lo = (_Float16)(x - (float)hi);
 }
 
-// Same split for a pair of values, for softmax weights in [0, 2^8]:
+// Same split for a pair of values (|x| below 65504; used for q and for
+// softmax weights in [0, 2^8]):
 // hi = rtz(x) by the packed round-toward-zero conversion, lo = f16(x - hi) by
 // two mixed-precision FMAs (f16 first operand, f32 addend, f16 result written
 // into the low / high half of the register).  x - hi is exact, so hi + lo

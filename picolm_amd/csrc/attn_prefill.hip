@@ -76,7 +76,8 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(PrefillArgs a) {
 }
 
 template <int D>
-__global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) {
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? 6 : 4)))
+void prefill_attn_kernel(PrefillArgs a) {
   constexpr int ND = D / 32;     // 32-wide d blocks of QK
   constexpr int NO = D / 16;     // 16-wide d blocks of PV
   constexpr int KP = D + 8;      // LDS pitch of a K row (halves)
@@ -156,7 +157,9 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   };
   issue_loads(0);
 
-  // ---- q operands of this lane's column: rotated, zero if invalid ----------
+  // ---- q operands of this lane's column: rotated, split into fp16 hi + lo --
+  // Columns past the prompt (cvalid false) read the last token's row and are
+  // never stored; each column's softmax is independent, so they need no mask.
   half8_t qhi[ND], qlo[ND];
   {
     const float* qrow = a.q + ((size_t)li * a.n_tokens + tok_c) * q_dim +
@@ -177,27 +180,27 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
           const int i = 32 * db + 8 * grp + j;
-          rope_rotate(qf[db][j], qf[db + ND / 2][j], cr[i], sr[i]);
+          rope_rotate_fused(qf[db][j], qf[db + ND / 2][j], cr[i], sr[i]);
         }
     } else {
 #pragma unroll
       for (int db = 0; db < ND; ++db) {
         const float4 c4 = *(const float4*)(cr + 16 * db + 4 * grp);
         const float4 s4 = *(const float4*)(sr + 16 * db + 4 * grp);
-        rope_rotate(qf[db][0], qf[db][1], c4.x, s4.x);
-        rope_rotate(qf[db][2], qf[db][3], c4.y, s4.y);
-        rope_rotate(qf[db][4], qf[db][5], c4.z, s4.z);
-        rope_rotate(qf[db][6], qf[db][7], c4.w, s4.w);
+        rope_rotate_fused(qf[db][0], qf[db][1], c4.x, s4.x);
+        rope_rotate_fused(qf[db][2], qf[db][3], c4.y, s4.y);
+        rope_rotate_fused(qf[db][4], qf[db][5], c4.z, s4.z);
+        rope_rotate_fused(qf[db][6], qf[db][7], c4.w, s4.w);
       }
     }
 #pragma unroll
     for (int db = 0; db < ND; ++db)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        _Float16 hi, lo;
-        split_hi_lo(cvalid ? qf[db][j] : 0.f, hi, lo);
-        qhi[db][j] = hi;
-        qlo[db][j] = lo;
+      for (int j = 0; j < 8; j += 2) {
+        half2_t hi, lo;
+        split_pair_rtz(qf[db][j], qf[db][j + 1], hi, lo);
+        qhi[db][j] = hi[0], qhi[db][j + 1] = hi[1];
+        qlo[db][j] = lo[0], qlo[db][j + 1] = lo[1];
       }
   }
 
