@@ -47,31 +47,62 @@ constexpr int kPThreads = 64 * kPW;
 constexpr int kKT = 32;              // K/V rows per tile
 constexpr float kLazy = 8.0f;        // rescale threshold (log2 units)
 
+// One thread per (layer, token, kv head, 4 rope pairs): 16-byte loads of k
+// and v, and 8-byte fp16 stores.  LLAMA pairs (2i, 2i+1) for i = 4g..4g+3
+// cover elements 8g..8g+7; QWEN pairs (i, i + D/2) cover 4g..4g+3 and
+// D/2 + 4g..D/2 + 4g+3.
 template <int D>
 __global__ __launch_bounds__(256) void prefill_append_kernel(PrefillArgs a) {
+  constexpr int NG = D / 8;  // groups of 4 pairs per head
   const int kv_dim = a.n_kv_heads * D;
-  const int pairs = kv_dim / 2;
-  const long total = (long)a.n_launch_layers * a.n_tokens * pairs;
+  const long total = (long)a.n_launch_layers * a.n_tokens * a.n_kv_heads * NG;
+  const bool qwen = a.rope_type == PLH_ROPE_QWEN;
   for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < total;
        idx += (long)gridDim.x * 256) {
-    const int pr = (int)(idx % pairs);
-    const long rest = idx / pairs;
-    const int tok = (int)(rest % a.n_tokens);
-    const int li = (int)(rest / a.n_tokens);
-    const int kvh = pr / (D / 2), i = pr % (D / 2);
-    const int i0 = (a.rope_type == PLH_ROPE_QWEN) ? i : 2 * i;
-    const int i1 = (a.rope_type == PLH_ROPE_QWEN) ? i + D / 2 : 2 * i + 1;
+    const int g = (int)(idx % NG);
+    const long rest = idx / NG;
+    const int kvh = (int)(rest % a.n_kv_heads);
+    const long lt = rest / a.n_kv_heads;
+    const int tok = (int)(lt % a.n_tokens);
+    const int li = (int)(lt / a.n_tokens);
     const int pos = a.start_pos + tok;
-    const size_t in_row = ((size_t)li * a.n_tokens + tok) * kv_dim + (size_t)kvh * D;
-    float k0 = a.k[in_row + i0], k1 = a.k[in_row + i1];
-    const float v0 = a.v[in_row + i0], v1 = a.v[in_row + i1];
-    rope_rotate(k0, k1, a.cos_t[(size_t)pos * (D / 2) + i], a.sin_t[(size_t)pos * (D / 2) + i]);
+    const float* kin = a.k + (size_t)lt * kv_dim + (size_t)kvh * D;
+    const float* vin = a.v + (size_t)lt * kv_dim + (size_t)kvh * D;
     const size_t out_row =
         ((size_t)(a.layer0 + li) * a.max_seq_len + pos) * kv_dim + (size_t)kvh * D;
-    a.kc[out_row + i0] = f16_bits_rha(k0);
-    a.kc[out_row + i1] = f16_bits_rha(k1);
-    a.vc[out_row + i0] = f16_bits_rha(v0);
-    a.vc[out_row + i1] = f16_bits_rha(v1);
+    const float4 c4 = *(const float4*)(a.cos_t + (size_t)pos * (D / 2) + 4 * g);
+    const float4 s4 = *(const float4*)(a.sin_t + (size_t)pos * (D / 2) + 4 * g);
+    const float cc[4] = {c4.x, c4.y, c4.z, c4.w}, ss[4] = {s4.x, s4.y, s4.z, s4.w};
+    // element offsets of the two 4-wide pieces this thread owns
+    const int e0 = qwen ? 4 * g : 8 * g;
+    const int e1 = qwen ? D / 2 + 4 * g : 8 * g + 4;
+    const float4 ka = *(const float4*)(kin + e0), kb = *(const float4*)(kin + e1);
+    const float4 va = *(const float4*)(vin + e0), vb = *(const float4*)(vin + e1);
+    float k8[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
+    const float v8[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+    if (qwen) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rope_rotate(k8[j], k8[4 + j], cc[j], ss[j]);
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) rope_rotate(k8[2 * j], k8[2 * j + 1], cc[j], ss[j]);
+    }
+    uint16_t kh[8], vh[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      kh[j] = f16_bits_rha(k8[j]);
+      vh[j] = f16_bits_rha(v8[j]);
+    }
+    auto pack = [](const uint16_t* h) {
+      uint2 r;
+      r.x = (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+      r.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
+      return r;
+    };
+    *(uint2*)(a.kc + out_row + e0) = pack(kh);
+    *(uint2*)(a.kc + out_row + e1) = pack(kh + 4);
+    *(uint2*)(a.vc + out_row + e0) = pack(vh);
+    *(uint2*)(a.vc + out_row + e1) = pack(vh + 4);
   }
 }
 
@@ -384,8 +415,8 @@ extern "C" int plh_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int h
   a.per_xcd = (n_groups + 7) / 8 * a.n_qblk;
   a.score_scale = kLog2e / sqrtf((float)head_dim);
 
-  const long pairs = (long)n_launch_layers * n_tokens * (n_kv_heads * head_dim / 2);
-  long ab = (pairs + 255) / 256;
+  const long groups = (long)n_launch_layers * n_tokens * n_kv_heads * (head_dim / 8);
+  long ab = (groups + 255) / 256;
   if (ab > 16384) ab = 16384;
   const unsigned grid = (unsigned)(8 * a.per_xcd);
   if (head_dim == 64) {
