@@ -125,15 +125,25 @@ void prefill_attn_kernel(PrefillArgs a) {
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
 
-  // XCD-aware order: each XCD takes whole (layer, kv head) groups, so the
-  // group's K/V tiles, read by all its q blocks, stay in one L2; within a
-  // group the heavy (late) q blocks go first.
+  // XCD-aware order: each XCD takes whole (layer, kv head) groups, so a
+  // group's K/V tiles, read by all its q blocks, stay in one L2.  When the
+  // slice's K/V fits in L2 its units run heaviest q block first across all
+  // its groups (longest-first keeps the end of the launch even); otherwise
+  // group by group, heaviest first within a group, so that each group's
+  // tiles are reused while still cached.
   const int nq = a.n_qblk;
-  const int unit = (int)(blockIdx.x & 7) * a.per_xcd + (int)(blockIdx.x >> 3);
-  if (unit >= a.n_units) return;
-  const int qb = nq - 1 - unit % nq;
-  const int kvh = (unit / nq) % a.n_kv_heads;
-  const int li = (unit / nq) / a.n_kv_heads;
+  const int xcd = (int)(blockIdx.x & 7), l = (int)(blockIdx.x >> 3);
+  int group, qb;
+  if (a.qb_major) {
+    group = xcd * a.groups_per_xcd + l % a.groups_per_xcd;
+    qb = nq - 1 - l / a.groups_per_xcd;
+  } else {
+    group = xcd * a.groups_per_xcd + l / nq;
+    qb = nq - 1 - l % nq;
+  }
+  if (group >= a.n_launch_layers * a.n_kv_heads) return;
+  const int kvh = group % a.n_kv_heads;
+  const int li = group / a.n_kv_heads;
   const int layer = a.layer0 + li;
   const int G = a.n_heads / a.n_kv_heads;
   const int kv_dim = a.n_kv_heads * D;
@@ -412,7 +422,12 @@ extern "C" int plh_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int h
   a.n_qblk = (n_tokens + a.bq - 1) / a.bq;
   const int n_groups = n_launch_layers * n_kv_heads;
   a.n_units = n_groups * a.n_qblk;
-  a.per_xcd = (n_groups + 7) / 8 * a.n_qblk;
+  a.groups_per_xcd = (n_groups + 7) / 8;
+  a.per_xcd = a.groups_per_xcd * a.n_qblk;
+  // K/V bytes one XCD slice reads: by q-block order when they fit in a
+  // comfortable share of the XCD's 4 MB L2
+  const double slice_kv = (double)a.groups_per_xcd * (start_pos + n_tokens) * head_dim * 2 * 2;
+  a.qb_major = slice_kv <= 2.0 * 1024 * 1024 ? 1 : 0;
   a.score_scale = kLog2e / sqrtf((float)head_dim);
 
   const long groups = (long)n_launch_layers * n_tokens * n_kv_heads * (head_dim / 8);

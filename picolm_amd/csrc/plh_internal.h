@@ -44,6 +44,8 @@ struct DecodeArgs {
   int n_split, split_len;  // position splits per (layer, kv head, head block)
   int n_units;             // n_groups * n_split
   int per_xcd;             // units per XCD slice of the grid
+  int groups_per_xcd;      // (layer, kv head) groups per XCD slice
+  int qb_major;            // 1: order a slice's units by q block, heaviest first
   float score_scale;       // log2(e) / sqrt(D)
 };
 
@@ -67,6 +69,8 @@ struct PrefillArgs {
   int n_qblk;              // q blocks per (layer, kv head)
   int n_units;             // n_launch_layers * n_kv_heads * n_qblk
   int per_xcd;             // units per XCD slice of the grid
+  int groups_per_xcd;      // (layer, kv head) groups per XCD slice
+  int qb_major;            // 1: order a slice's units by q block, heaviest first
   float score_scale;       // log2(e) / sqrt(D)
 };
 
