@@ -539,8 +539,9 @@ __global__ __launch_bounds__(kCombineThreads) void attn_decode_combine_kernel(De
 // Split plan defaults, from sweeps on MI355X (TinyLlama pos 256 and 2047,
 // Llama-3.2 pos 8191, Llama-2 pos 4095): about four workgroups per CU,
 // splits of >= 512 rows (shorter contexts then need no combine launch).
+constexpr int kDefaultMinSplit = 512;
 int g_target_units = 0;   // 0: four workgroups per CU
-int g_min_split = 512;
+int g_min_split = kDefaultMinSplit;
 
 }  // namespace
 
@@ -550,6 +551,10 @@ extern "C" int plh_set_tuning(int key, int value) {
     return 0;
   }
   if (key == 2) {
+    if (value == 0) {
+      g_min_split = kDefaultMinSplit;
+      return 0;
+    }
     if (value < 128 || value % 128) {
       set_error("plh_set_tuning: minimum split must be a positive multiple of 128");
       return -1;

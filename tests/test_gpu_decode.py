@@ -262,4 +262,4 @@ def test_decode_split_lengths(gpu, oracle_mod, min_split):
         cfg = gpu.AttnConfig(2, 32, 32, 128, 1024, 1e4, 0)
         run_decode(gpu, oracle_mod, cfg, 1000, seed=5 + min_split)
     finally:
-        gpu.lib.plh_set_tuning(2, 1024)
+        gpu.lib.plh_set_tuning(2, 0)
