@@ -8,8 +8,8 @@ The default workload is TinyLlama-1.1B-shaped decode at position 2047
 (22 layers, 32 q heads, 4 kv heads, head_dim 64, FP16 cache of 2048 rows);
 the same line carries, under "prefill", the TinyLlama-shaped 512-token causal
 prefill (all 22 layers per step) in TFLOP/s of causal-pair flops
-(L * Hq * 4D * sum_i (i+1)) against the fp16 MFMA peak, with the HBM-bound
-roof of its fp32 q/k/v/out traffic.
+(L * Hq * 4D * sum_i (i+1)) against its binding roof (HBM, for the fp32
+q/k/v/out traffic at these sizes), with the fraction of the fp16 MFMA peak.
 
 Method:
   * the FP16 caches are rotated over enough copies (>= 512 MiB in total) that
@@ -23,9 +23,15 @@ Method:
       L * [ (pos+1)*2*Hkv*D*2  (K+V rows read)
             + Hq*D*4 + 2*Hkv*D*4 (q, k, v in) + 2*Hkv*D*2 (row written)
             + Hq*D*4 (out) ]
+  * per_layer_launches: the same token as L sequential one-layer calls (how
+    a per-layer forward pass uses the block), also graph-replayed;
   * cpu_baseline: the oracle (the reference's attention restated in C, same
     op order, out-of-line fp16 widening as in the reference build) timed on
-    one host thread over a bounded sample of the same workload.
+    one host thread over a bounded sample of the same workload -- the
+    reference runs its attention on one thread whatever its -j;
+    cpu_baseline_head_parallel: the same arithmetic with the q heads split
+    over up to 16 host threads, an upper bound only; "host" records nproc,
+    the CPU model and the C library.
 Prints one JSON line.
 """
 from __future__ import annotations
@@ -47,6 +53,8 @@ HBM_PEAK_GBS = 8000.0
 MALL_DEFEAT_BYTES = 512 << 20
 
 MFMA_F16_PEAK_TFS = 2516.6
+
+HOST_THREADS_MAX = 16   # the GPU box's host CPU share for one GPU
 
 WORKLOADS = {
     "tinyllama_decode_pos2047": dict(L=22, Hq=32, Hkv=4, D=64, S=2048, theta=1e4, pos=2047),
@@ -151,6 +159,31 @@ def run_decode(P, w, steps, warmup, name):
     wall = time.perf_counter() - t0
     k_mean = e0.elapsed_ms(e1) / steps
 
+    # the same token as L sequential one-layer launches (how a per-layer
+    # forward pass calls the block), timed the same way over fewer steps
+    pl_steps = max(1, steps // 10)
+    def launch_per_layer(i):
+        c = i % n_copies
+        q, k, v, o = qkv[c]
+        for l in range(L):
+            P.check(P.lib.plh_attn_decode(L, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, S, 0, l,
+                                          1, pos, q.ptr + l * cfg.q_dim * 4,
+                                          k.ptr + l * kv * 4, v.ptr + l * kv * 4, keys[c].ptr,
+                                          vals[c].ptr, d_cos.ptr, d_sin.ptr,
+                                          o.ptr + l * cfg.q_dim * 4), "plh_attn_decode")
+    launch_per_layer(0)
+    P.synchronize()
+    with P.Graph() as g2:
+        for i in range(pl_steps):
+            launch_per_layer(i)
+    g2.launch()
+    P.synchronize()
+    e0.record()
+    g2.launch()
+    e1.record()
+    P.synchronize()
+    pl_ms = e0.elapsed_ms(e1) / pl_steps
+
     algo = decode_bytes(w)
     ms_step = wall * 1e3 / steps
     achieved = algo / (k_mean * 1e-3) / 1e9
@@ -165,6 +198,9 @@ def run_decode(P, w, steps, warmup, name):
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": traffic_from_profiles(name)},
+        "per_layer_launches": {"us_per_token": pl_ms * 1e3,
+                               "gbs": algo / (pl_ms * 1e-3) / 1e9,
+                               "launches_per_token": L},
     }
     # keep what the CPU baseline needs (copy 0 before further appends)
     result["_cpu_inputs"] = (cfg, keys[0], vals[0], qkv[0], cos_t, sin_t)
@@ -297,13 +333,49 @@ def cpu_baseline(P, w, res, budget_s=12.0):
         tokens += 1
     token_s = t_total / layers_done * L
     algo = decode_bytes(w)
+    # head-parallel upper bound: the same per-head arithmetic over n host
+    # threads (the reference runs its attention on one thread whatever -j)
+    n_thr = min(os.cpu_count() or 1, HOST_THREADS_MAX)
+    t_mt, mt_layers = 0.0, 0
+    while t_mt < budget_s / 2 and mt_layers < 4 * L:
+        l = mt_layers % L
+        qi, ki = q[l].copy(), k[l].copy()
+        t0 = time.perf_counter()
+        O.attn_decode_mt(shp, l, pos, qi, ki, v[l], kc, vc, cos_t, sin_t, n_thr)
+        t_mt += time.perf_counter() - t0
+        mt_layers += 1
+    token_mt = t_mt / mt_layers * L
     return {
         "cpu_baseline": {"value": algo / token_s / 1e9, "unit": "GB/s", "cores": 1,
                          "kind": "port", "us_per_token": token_s * 1e6,
                          "sample": f"{layers_done} layer-steps ({layers_done / L:.2f} tokens) of "
                                    f"{w['L']}-layer decode at pos {pos}, oracle on 1 thread"},
+        "cpu_baseline_head_parallel": {
+            "value": algo / token_mt / 1e9, "unit": "GB/s", "cores": n_thr, "kind": "port",
+            "us_per_token": token_mt * 1e6,
+            "sample": f"{mt_layers} layer-steps of the same decode, q heads split over "
+                      f"{n_thr} threads: an upper bound, not the reference's own parallelism"},
+        "host": host_info(),
         "parity_normwise_max": worst,
     }
+
+
+def host_info():
+    """nproc, CPU model and C library of the machine the CPU legs ran on."""
+    model = None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        libc = os.confstr("CS_GNU_LIBC_VERSION")
+    except (ValueError, OSError):
+        libc = None
+    return {"nproc": os.cpu_count(), "cpu_model": model, "libc": libc}
 
 
 def main():

@@ -118,8 +118,8 @@ int plh_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int head_dim,
                      int out_stride);
 
 /* Tuning knobs (bench sweeps).  key 1: decode target workgroups per launch
- * (0 = default); key 2: decode minimum positions per split (multiple of 128,
- * 0 = default). */
+ * (0 = default); key 2: decode contexts of at most this many positions are
+ * not split (multiple of 128, 0 = default). */
 int plh_set_tuning(int key, int value);
 
 #ifdef __cplusplus

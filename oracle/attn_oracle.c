@@ -204,17 +204,17 @@ static int dims_ok(int n_heads, int n_kv_heads, int head_dim) {
  * online softmax keeps (max, sum, acc[D]) and branches exactly as the
  * reference does: a new maximum rescales by expf(old-new) and adds V with
  * weight 1, otherwise weight expf(score-max).  out = acc * (1/sum). */
-static void attend_one(int n_heads, int n_kv_heads, int head_dim,
-                       int seq_len, int layer, int pos, const float *q,
-                       const uint16_t *key_cache, const uint16_t *val_cache,
-                       float *out) {
+static void attend_heads(int n_heads, int n_kv_heads, int head_dim,
+                         int seq_len, int layer, int pos, const float *q,
+                         const uint16_t *key_cache, const uint16_t *val_cache,
+                         float *out, int h_begin, int h_end) {
     int kv_dim = n_kv_heads * head_dim;
     int group = n_heads / n_kv_heads;
     const uint16_t *kl = key_cache + (size_t)layer * (size_t)seq_len * (size_t)kv_dim;
     const uint16_t *vl = val_cache + (size_t)layer * (size_t)seq_len * (size_t)kv_dim;
     float scale_div = sqrtf((float)head_dim);
     float acc[256];
-    for (int h = 0; h < n_heads; h++) {
+    for (int h = h_begin; h < h_end; h++) {
         const float *qh = q + (size_t)h * (size_t)head_dim;
         int kvh = h / group;
         float m = -1e30f;
@@ -244,6 +244,60 @@ static void attend_one(int n_heads, int n_kv_heads, int head_dim,
         float *oh = out + (size_t)h * (size_t)head_dim;
         for (int d = 0; d < head_dim; d++) oh[d] = acc[d] * inv;
     }
+}
+
+static void attend_one(int n_heads, int n_kv_heads, int head_dim,
+                       int seq_len, int layer, int pos, const float *q,
+                       const uint16_t *key_cache, const uint16_t *val_cache,
+                       float *out) {
+    attend_heads(n_heads, n_kv_heads, head_dim, seq_len, layer, pos, q,
+                 key_cache, val_cache, out, 0, n_heads);
+}
+
+/* Head-parallel variant for the CPU baseline's upper bound: the q heads are
+ * split over pthreads, each head's arithmetic unchanged (so the results are
+ * bit-identical to attend_one).  The reference itself runs this loop on one
+ * thread whatever its -j (tensor.c:190-254 parallelises only the matmuls). */
+struct attend_job {
+    int n_heads, n_kv_heads, head_dim, seq_len, layer, pos;
+    const float *q;
+    const uint16_t *kc, *vc;
+    float *out;
+    int h_begin, h_end;
+};
+
+static void *attend_worker(void *arg) {
+    struct attend_job *j = (struct attend_job *)arg;
+    attend_heads(j->n_heads, j->n_kv_heads, j->head_dim, j->seq_len, j->layer,
+                 j->pos, j->q, j->kc, j->vc, j->out, j->h_begin, j->h_end);
+    return NULL;
+}
+
+static int attend_mt(int n_heads, int n_kv_heads, int head_dim, int seq_len,
+                     int layer, int pos, const float *q, const uint16_t *kc,
+                     const uint16_t *vc, float *out, int n_threads) {
+    if (n_threads > n_heads) n_threads = n_heads;
+    if (n_threads <= 1) {
+        attend_one(n_heads, n_kv_heads, head_dim, seq_len, layer, pos, q, kc, vc, out);
+        return 0;
+    }
+    if (n_threads > 256) n_threads = 256;
+    pthread_t tid[256];
+    struct attend_job job[256];
+    int started = 0;
+    for (int t = 0; t < n_threads; t++) {
+        job[t] = (struct attend_job){n_heads, n_kv_heads, head_dim, seq_len, layer, pos, q, kc,
+                                     vc, out, n_heads * t / n_threads,
+                                     n_heads * (t + 1) / n_threads};
+        if (t == 0) continue;
+        if (pthread_create(&tid[t], NULL, attend_worker, &job[t]) != 0) break;
+        started = t;
+    }
+    attend_worker(&job[0]);
+    for (int t = 1; t <= started; t++) pthread_join(tid[t], NULL);
+    /* heads of threads that failed to start run here */
+    for (int t = started + 1; t < n_threads; t++) attend_worker(&job[t]);
+    return 0;
 }
 
 /* model.c:802-805 + 822-826: row `pos` of layer `layer` gets f16(k), f16(v). */
@@ -285,6 +339,24 @@ int orc_attn_decode(int n_layers, int n_heads, int n_kv_heads, int head_dim,
     attend_one(n_heads, n_kv_heads, head_dim, max_seq_len, layer, pos, q,
                key_cache, val_cache, out);
     return 0;
+}
+
+int orc_attn_decode_mt(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                       int max_seq_len, int rope_type, int layer, int pos,
+                       float *q, float *k, const float *v,
+                       uint16_t *key_cache, uint16_t *val_cache,
+                       const float *cos_tab, const float *sin_tab, float *out,
+                       int n_threads) {
+    if (!dims_ok(n_heads, n_kv_heads, head_dim)) return -1;
+    if (layer < 0 || layer >= n_layers || pos < 0 || pos >= max_seq_len) return -1;
+    size_t half = (size_t)(head_dim / 2);
+    const float *c = cos_tab + (size_t)pos * half;
+    const float *s = sin_tab + (size_t)pos * half;
+    orc_rope(q, k, head_dim, n_heads, n_kv_heads, c, s, rope_type);
+    append_row(n_kv_heads, head_dim, max_seq_len, layer, pos, k, v, key_cache,
+               val_cache);
+    return attend_mt(n_heads, n_kv_heads, head_dim, max_seq_len, layer, pos, q,
+                     key_cache, val_cache, out, n_threads);
 }
 
 int orc_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int head_dim,

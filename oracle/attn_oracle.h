@@ -73,6 +73,17 @@ int orc_attn_decode(int n_layers, int n_heads, int n_kv_heads, int head_dim,
                     uint16_t *key_cache, uint16_t *val_cache,
                     const float *cos_tab, const float *sin_tab, float *out);
 
+/* orc_attn_decode with the q heads split over n_threads pthreads (each head's
+ * arithmetic unchanged, so the output is bit-identical).  For the CPU
+ * baseline's "head-parallel upper bound" only: the reference runs this loop
+ * on one thread. */
+int orc_attn_decode_mt(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                       int max_seq_len, int rope_type, int layer, int pos,
+                       float *q, float *k, const float *v,
+                       uint16_t *key_cache, uint16_t *val_cache,
+                       const float *cos_tab, const float *sin_tab, float *out,
+                       int n_threads);
+
 /* model.c:1019-1090 -- one layer, n_tokens prompt rows starting at start_pos,
  * processed serially: rope, append, attention over rows 0..start_pos+bi.
  * q [n_tokens][n_heads*head_dim] and k [n_tokens][kv_dim] rotated in place,

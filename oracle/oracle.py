@@ -61,6 +61,9 @@ def lib() -> C.CDLL:
         dims = [C.c_int] * 8
         L.orc_attn_decode.argtypes = dims + [_f32p, _f32p, _f32p, _u16p, _u16p, _f32p, _f32p, _f32p]
         L.orc_attn_decode.restype = C.c_int
+        L.orc_attn_decode_mt.argtypes = dims + [_f32p, _f32p, _f32p, _u16p, _u16p, _f32p, _f32p,
+                                                _f32p, C.c_int]
+        L.orc_attn_decode_mt.restype = C.c_int
         L.orc_attn_prefill.argtypes = dims + [C.c_int, _f32p, _f32p, _f32p, _u16p, _u16p,
                                               _f32p, _f32p, _f32p, C.c_int]
         L.orc_attn_prefill.restype = C.c_int
@@ -175,6 +178,17 @@ def attn_decode(shp: Shape, layer, pos, q, k, v, kc, vc, cos_t, sin_t):
                                cos_t.reshape(-1), sin_t.reshape(-1), out)
     if rc != 0:
         raise ValueError("orc_attn_decode rejected its arguments")
+    return out
+
+
+def attn_decode_mt(shp: Shape, layer, pos, q, k, v, kc, vc, cos_t, sin_t, n_threads):
+    """attn_decode with the q heads split over n_threads host threads
+    (bit-identical output); the CPU baseline's head-parallel upper bound."""
+    out = np.empty(shp.q_dim, dtype=np.float32)
+    rc = lib().orc_attn_decode_mt(*shp.dims(), layer, pos, q, k, v, kc, vc,
+                                  cos_t.reshape(-1), sin_t.reshape(-1), out, n_threads)
+    if rc != 0:
+        raise ValueError("orc_attn_decode_mt rejected its arguments")
     return out
 
 

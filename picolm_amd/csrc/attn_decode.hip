@@ -537,8 +537,8 @@ __global__ __launch_bounds__(kCombineThreads) void attn_decode_combine_kernel(De
 }
 
 // Split plan defaults, from sweeps on MI355X (TinyLlama pos 256 and 2047,
-// Llama-3.2 pos 8191, Llama-2 pos 4095): about four workgroups per CU,
-// splits of >= 512 rows (shorter contexts then need no combine launch).
+// Llama-3.2 pos 8191, Llama-2 pos 4095, one-layer launches): about four
+// workgroups per CU; contexts up to 512 positions are not split.
 constexpr int kDefaultMinSplit = 512;
 int g_target_units = 0;   // 0: four workgroups per CU
 int g_min_split = kDefaultMinSplit;
@@ -607,13 +607,15 @@ extern "C" int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int he
   const int n_hblk = (G + 15) / 16;
   const int n_groups = n_launch_layers * n_kv_heads * n_hblk;
   const int npos = pos + 1;
-  // Split plan: about `target` workgroups in all, each split at least
-  // g_min_split rows (fewer splits, fewer partials to merge), split length a
-  // multiple of 128 rows.
+  // Split plan: contexts of at most g_min_split positions are not split (the
+  // merge launch would cost more than it saves); longer ones are cut into
+  // splits of a multiple of 128 rows (one 32-row tile per wave at least),
+  // about `target` workgroups in all.
   const int target = g_target_units > 0 ? g_target_units : 4 * (c.num_cus > 0 ? c.num_cus : 256);
   long want_split = ((long)npos * n_groups + target - 1) / target;
-  if (want_split < g_min_split) want_split = g_min_split;
+  if (want_split < 128) want_split = 128;
   want_split = (want_split + 127) / 128 * 128;
+  if (npos <= g_min_split) want_split = npos;
   const int split_len = (int)want_split;
   const int n_split = (npos + split_len - 1) / split_len;
   const int n_units = n_groups * n_split;

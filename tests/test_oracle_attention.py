@@ -206,6 +206,27 @@ def test_prefill_equals_sequential_decode(oracle_mod):
     assert np.array_equal(kc1, kc2) and np.array_equal(vc1, vc2)
 
 
+@pytest.mark.parametrize("threads", [1, 3, 8, 40])
+def test_head_parallel_decode_is_bit_identical(oracle_mod, threads):
+    """The CPU baseline's head-parallel variant splits q heads over threads
+    without touching a head's arithmetic: outputs and caches equal the
+    single-thread oracle bit for bit (thread counts below, at and above the
+    head count)."""
+    O = oracle_mod
+    shp = O.Shape(2, 32, 4, 64, 256, rope_type=0)
+    rng = np.random.default_rng(9 + threads)
+    c, s = O.rope_tables(256, 64, 1e4)
+    kc1, vc1 = random_cache(O, shp, rng)
+    kc2, vc2 = kc1.copy(), vc1.copy()
+    q = rng.standard_normal(shp.q_dim).astype(np.float32)
+    k = rng.standard_normal(shp.kv_dim).astype(np.float32)
+    v = rng.standard_normal(shp.kv_dim).astype(np.float32)
+    a = O.attn_decode(shp, 1, 200, q.copy(), k.copy(), v, kc1, vc1, c, s)
+    b = O.attn_decode_mt(shp, 1, 200, q.copy(), k.copy(), v, kc2, vc2, c, s, threads)
+    assert np.array_equal(a, b)
+    assert np.array_equal(kc1, kc2) and np.array_equal(vc1, vc2)
+
+
 def test_out_of_range_is_rejected(oracle_mod):
     O = oracle_mod
     shp = O.Shape(1, 4, 2, 64, 16)
