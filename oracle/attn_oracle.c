@@ -189,6 +189,46 @@ void orc_rope(float *q, float *k, int head_dim, int n_heads, int n_kv_heads,
 }
 
 /* ------------------------------------------------------------------------ */
+/* QK-norm (Qwen3)                                                          */
+/* ------------------------------------------------------------------------ */
+
+/* tensor.c:425-492 as the reference builds on x86-64 with AVX2 (quant.h:33-46
+ * defines PICOLM_AVX2 from __AVX2__, which -march=native sets on any AVX2
+ * host): eight lane sums acc[j] += x[i]*x[i] over i = j mod 8 (product and
+ * sum rounded separately), folded as ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7))
+ * (hsum_avx2), a scalar tail for size % 8, then
+ * ss = 1/sqrtf(ss/size + eps) and out[i] = (x[i]*ss)*w[i]. */
+void orc_rmsnorm(float *out, const float *x, const float *w, int size, float eps) {
+    float acc[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+    int i = 0;
+    for (; i + 7 < size; i += 8)
+        for (int j = 0; j < 8; j++) {
+            float sq = x[i + j] * x[i + j];
+            acc[j] = acc[j] + sq;
+        }
+    float l0 = acc[0] + acc[4], l1 = acc[1] + acc[5];
+    float l2 = acc[2] + acc[6], l3 = acc[3] + acc[7];
+    float a02 = l0 + l2, a13 = l1 + l3;
+    float ss = a02 + a13;
+    for (; i < size; i++) ss += x[i] * x[i];
+    ss = 1.0f / sqrtf(ss / (float)size + eps);
+    for (int k = 0; k < size; k++) {
+        float t = x[k] * ss;
+        out[k] = t * w[k];
+    }
+}
+
+/* model.c:807-817 / 1029-1037: every q head and every k head normalised with
+ * the layer's q / k weights (head_dim floats each). */
+static void qk_norm(float *q, float *k, int n_heads, int n_kv_heads, int head_dim,
+                    const float *qnw, const float *knw, float eps) {
+    for (int h = 0; h < n_heads; h++)
+        orc_rmsnorm(q + (size_t)h * head_dim, q + (size_t)h * head_dim, qnw, head_dim, eps);
+    for (int h = 0; h < n_kv_heads; h++)
+        orc_rmsnorm(k + (size_t)h * head_dim, k + (size_t)h * head_dim, knw, head_dim, eps);
+}
+
+/* ------------------------------------------------------------------------ */
 /* Attention                                                                */
 /* ------------------------------------------------------------------------ */
 
@@ -328,8 +368,21 @@ int orc_attn_decode(int n_layers, int n_heads, int n_kv_heads, int head_dim,
                     float *q, float *k, const float *v,
                     uint16_t *key_cache, uint16_t *val_cache,
                     const float *cos_tab, const float *sin_tab, float *out) {
+    return orc_attn_decode_qkn(n_layers, n_heads, n_kv_heads, head_dim, max_seq_len,
+                               rope_type, layer, pos, q, k, v, key_cache, val_cache,
+                               cos_tab, sin_tab, out, NULL, NULL, 0.0f);
+}
+
+int orc_attn_decode_qkn(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                        int max_seq_len, int rope_type, int layer, int pos,
+                        float *q, float *k, const float *v,
+                        uint16_t *key_cache, uint16_t *val_cache,
+                        const float *cos_tab, const float *sin_tab, float *out,
+                        const float *q_norm, const float *k_norm, float eps) {
     if (!dims_ok(n_heads, n_kv_heads, head_dim)) return -1;
     if (layer < 0 || layer >= n_layers || pos < 0 || pos >= max_seq_len) return -1;
+    if ((q_norm == NULL) != (k_norm == NULL)) return -1;
+    if (q_norm) qk_norm(q, k, n_heads, n_kv_heads, head_dim, q_norm, k_norm, eps);
     size_t half = (size_t)(head_dim / 2);
     const float *c = cos_tab + (size_t)pos * half;
     const float *s = sin_tab + (size_t)pos * half;
@@ -365,8 +418,22 @@ int orc_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int head_dim,
                      uint16_t *key_cache, uint16_t *val_cache,
                      const float *cos_tab, const float *sin_tab,
                      float *out, int out_stride) {
+    return orc_attn_prefill_qkn(n_layers, n_heads, n_kv_heads, head_dim, max_seq_len,
+                                rope_type, layer, start_pos, n_tokens, q, k, v, key_cache,
+                                val_cache, cos_tab, sin_tab, out, out_stride, NULL, NULL,
+                                0.0f);
+}
+
+int orc_attn_prefill_qkn(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                         int max_seq_len, int rope_type, int layer, int start_pos,
+                         int n_tokens, float *q, float *k, const float *v,
+                         uint16_t *key_cache, uint16_t *val_cache,
+                         const float *cos_tab, const float *sin_tab,
+                         float *out, int out_stride,
+                         const float *q_norm, const float *k_norm, float eps) {
     if (!dims_ok(n_heads, n_kv_heads, head_dim)) return -1;
     if (layer < 0 || layer >= n_layers || start_pos < 0 || n_tokens < 0) return -1;
+    if ((q_norm == NULL) != (k_norm == NULL)) return -1;
     if ((long)start_pos + (long)n_tokens > (long)max_seq_len) return -1;
     size_t q_dim = (size_t)n_heads * (size_t)head_dim;
     size_t kv_dim = (size_t)n_kv_heads * (size_t)head_dim;
@@ -376,6 +443,7 @@ int orc_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int head_dim,
         float *qb = q + (size_t)bi * q_dim;
         float *kb = k + (size_t)bi * kv_dim;
         const float *vb = v + (size_t)bi * kv_dim;
+        if (q_norm) qk_norm(qb, kb, n_heads, n_kv_heads, head_dim, q_norm, k_norm, eps);
         orc_rope(qb, kb, head_dim, n_heads, n_kv_heads,
                  cos_tab + (size_t)pos * half, sin_tab + (size_t)pos * half,
                  rope_type);

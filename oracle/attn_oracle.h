@@ -95,6 +95,28 @@ int orc_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int head_dim,
                      const float *cos_tab, const float *sin_tab,
                      float *out, int out_stride);
 
+/* Qwen3 QK-norm variants (model.c:807-817 decode, 1029-1037 prefill): before
+ * the rotation every q head is RMS-normalised with q_norm[head_dim] and every
+ * k head with k_norm[head_dim] (epsilon eps).  q_norm = k_norm = NULL gives
+ * the plain functions above; only one of them NULL is an error. */
+int orc_attn_decode_qkn(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                        int max_seq_len, int rope_type, int layer, int pos,
+                        float *q, float *k, const float *v,
+                        uint16_t *key_cache, uint16_t *val_cache,
+                        const float *cos_tab, const float *sin_tab, float *out,
+                        const float *q_norm, const float *k_norm, float eps);
+int orc_attn_prefill_qkn(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                         int max_seq_len, int rope_type, int layer, int start_pos,
+                         int n_tokens, float *q, float *k, const float *v,
+                         uint16_t *key_cache, uint16_t *val_cache,
+                         const float *cos_tab, const float *sin_tab,
+                         float *out, int out_stride,
+                         const float *q_norm, const float *k_norm, float eps);
+
+/* tensor.c:425-492 rmsnorm in the reference's x86-64 AVX2 build order (see
+ * the definition).  out may alias x. */
+void orc_rmsnorm(float *out, const float *x, const float *w, int size, float eps);
+
 /* Attention only (model.c:848-892 for one token): no rope, no append.  Used
  * by tests that pin the softmax itself on hand-made caches. */
 int orc_attn_core(int n_heads, int n_kv_heads, int head_dim, int max_seq_len,

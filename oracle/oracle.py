@@ -69,6 +69,16 @@ def lib() -> C.CDLL:
         L.orc_attn_prefill.restype = C.c_int
         L.orc_attn_core.argtypes = [C.c_int] * 6 + [_f32p, _u16p, _u16p, _f32p]
         L.orc_attn_core.restype = C.c_int
+        _nf = C.POINTER(C.c_float)   # nullable
+        L.orc_attn_decode_qkn.argtypes = dims + [_f32p, _f32p, _f32p, _u16p, _u16p, _f32p, _f32p,
+                                                 _f32p, _nf, _nf, C.c_float]
+        L.orc_attn_decode_qkn.restype = C.c_int
+        L.orc_attn_prefill_qkn.argtypes = dims + [C.c_int, _f32p, _f32p, _f32p, _u16p, _u16p,
+                                                  _f32p, _f32p, _f32p, C.c_int, _nf, _nf,
+                                                  C.c_float]
+        L.orc_attn_prefill_qkn.restype = C.c_int
+        L.orc_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_float]
+        L.orc_rmsnorm.restype = None
         _lib = L
     return _lib
 
@@ -105,6 +115,10 @@ def ref() -> C.CDLL:
         R.ref_layer_inputs.restype = None
         R.ref_final_norm.argtypes = [C.c_void_p, _f32p, _f32p]
         R.ref_final_norm.restype = None
+        R.ref_set_qk_norm.argtypes = [C.c_void_p, C.c_int, _f32p, _f32p, C.c_float]
+        R.ref_set_qk_norm.restype = None
+        R.ref_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_float]
+        R.ref_rmsnorm.restype = None
         _ref = R
     return _ref
 
@@ -171,13 +185,37 @@ class Shape:
                 self.max_seq_len, self.rope_type)
 
 
-def attn_decode(shp: Shape, layer, pos, q, k, v, kc, vc, cos_t, sin_t):
-    """Oracle decode step; q, k rotated in place, caches appended in place."""
+def _nullable(a):
+    if a is None:
+        return None
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    return a.ctypes.data_as(C.POINTER(C.c_float))
+
+
+def attn_decode(shp: Shape, layer, pos, q, k, v, kc, vc, cos_t, sin_t,
+                q_norm=None, k_norm=None, eps=0.0):
+    """Oracle decode step; q, k rotated in place, caches appended in place.
+    q_norm / k_norm ([head_dim] each) apply Qwen3's QK-norm with epsilon eps."""
     out = np.empty(shp.q_dim, dtype=np.float32)
-    rc = lib().orc_attn_decode(*shp.dims(), layer, pos, q, k, v, kc, vc,
-                               cos_t.reshape(-1), sin_t.reshape(-1), out)
+    if q_norm is None and k_norm is None:
+        rc = lib().orc_attn_decode(*shp.dims(), layer, pos, q, k, v, kc, vc,
+                                   cos_t.reshape(-1), sin_t.reshape(-1), out)
+    else:
+        qn = None if q_norm is None else np.ascontiguousarray(q_norm, np.float32)
+        kn = None if k_norm is None else np.ascontiguousarray(k_norm, np.float32)
+        rc = lib().orc_attn_decode_qkn(*shp.dims(), layer, pos, q, k, v, kc, vc,
+                                       cos_t.reshape(-1), sin_t.reshape(-1), out,
+                                       _nullable(qn), _nullable(kn), eps)
     if rc != 0:
         raise ValueError("orc_attn_decode rejected its arguments")
+    return out
+
+
+def rmsnorm(x, w, eps):
+    """The reference's rmsnorm (x86-64 AVX2 build order) of one vector."""
+    x = np.ascontiguousarray(x, np.float32)
+    out = np.empty_like(x)
+    lib().orc_rmsnorm(out, x, np.ascontiguousarray(w, np.float32), x.size, eps)
     return out
 
 
@@ -193,13 +231,21 @@ def attn_decode_mt(shp: Shape, layer, pos, q, k, v, kc, vc, cos_t, sin_t, n_thre
 
 
 def attn_prefill(shp: Shape, layer, start_pos, n_tokens, q, k, v, kc, vc,
-                 cos_t, sin_t, out_stride=None):
+                 cos_t, sin_t, out_stride=None, q_norm=None, k_norm=None, eps=0.0):
     stride = shp.q_dim if out_stride is None else out_stride
     out = np.zeros(max(n_tokens, 1) * stride, dtype=np.float32)
-    rc = lib().orc_attn_prefill(*shp.dims(), layer, start_pos, n_tokens,
-                                q.reshape(-1), k.reshape(-1), v.reshape(-1),
-                                kc, vc, cos_t.reshape(-1), sin_t.reshape(-1),
-                                out, stride)
+    if q_norm is None and k_norm is None:
+        rc = lib().orc_attn_prefill(*shp.dims(), layer, start_pos, n_tokens,
+                                    q.reshape(-1), k.reshape(-1), v.reshape(-1),
+                                    kc, vc, cos_t.reshape(-1), sin_t.reshape(-1),
+                                    out, stride)
+    else:
+        qn = None if q_norm is None else np.ascontiguousarray(q_norm, np.float32)
+        kn = None if k_norm is None else np.ascontiguousarray(k_norm, np.float32)
+        rc = lib().orc_attn_prefill_qkn(*shp.dims(), layer, start_pos, n_tokens,
+                                        q.reshape(-1), k.reshape(-1), v.reshape(-1),
+                                        kc, vc, cos_t.reshape(-1), sin_t.reshape(-1),
+                                        out, stride, _nullable(qn), _nullable(kn), eps)
     if rc != 0:
         raise ValueError("orc_attn_prefill rejected its arguments")
     return out[: n_tokens * stride].reshape(n_tokens, stride)

@@ -280,3 +280,25 @@ uint64_t ref_f16_mismatches(uint64_t first, uint64_t count, f2h_fn other,
 void ref_f16_to_f32_array(const uint16_t *src, float *dst, size_t n) {
     for (size_t i = 0; i < n; i++) dst[i] = fp16_to_fp32(src[i]);
 }
+
+/* Qwen3 QK-norm for layer `layer` (model.c:807-817, 1029-1037): the layer's
+ * attn_q_norm / attn_k_norm tensors become non-null and the run state's
+ * dequantised per-head weights (model.c:657-670) take q_w / k_w; eps becomes
+ * the model's rms_norm_eps. */
+void ref_set_qk_norm(void *hv, int layer, const float *q_w, const float *k_w, float eps) {
+    ref_handle *h = (ref_handle *)hv;
+    model_t *m = &h->m;
+    int D = m->config.head_dim;
+    memcpy(m->state.attn_q_norm_w[layer], q_w, (size_t)D * sizeof(float));
+    memcpy(m->state.attn_k_norm_w[layer], k_w, (size_t)D * sizeof(float));
+    m->weights.layers[layer].attn_q_norm = m->state.attn_q_norm_w[layer];
+    m->weights.layers[layer].attn_k_norm = m->state.attn_k_norm_w[layer];
+    m->weights.layers[layer].type_attn_q_norm = GGUF_TYPE_F32;
+    m->weights.layers[layer].type_attn_k_norm = GGUF_TYPE_F32;
+    m->config.rms_norm_eps = eps;
+}
+
+/* The reference's rmsnorm (tensor.c:425-492) as this harness is built. */
+void ref_rmsnorm(float *out, const float *x, const float *w, int size, float eps) {
+    rmsnorm(out, x, w, size, eps);
+}
