@@ -117,6 +117,31 @@ int plh_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int head_dim,
                      const float *rope_cos, const float *rope_sin, float *out,
                      int out_stride);
 
+/* ---- Qwen3 QK-norm variants ----------------------------------------------- */
+/* The two calls above with the QK-norm of model.c:807-817 (decode) and
+ * 1029-1037 (prefill) in front of the rotation: every q head row is
+ * RMS-normalised with q_norm and every k head row with k_norm, epsilon
+ * norm_eps (the model's rms_norm_eps), as the reference's rmsnorm
+ * (tensor.c:425-492) computes it in its x86-64 AVX2 build -- the cached k
+ * rows stay bit-exact.  q_norm, k_norm: device pointers, [n_launch_layers]
+ * [head_dim] fp32 (layer li of the launch at + li*head_dim); both null gives
+ * the plain call, one null is an error. */
+int plh_attn_decode_qknorm(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                           int max_seq_len, int rope_type, int layer0,
+                           int n_launch_layers, int pos, const float *q,
+                           const float *k, const float *v, uint16_t *key_cache,
+                           uint16_t *val_cache, const float *rope_cos,
+                           const float *rope_sin, float *out, const float *q_norm,
+                           const float *k_norm, float norm_eps);
+int plh_attn_prefill_qknorm(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                            int max_seq_len, int rope_type, int layer0,
+                            int n_launch_layers, int start_pos, int n_tokens,
+                            const float *q, const float *k, const float *v,
+                            uint16_t *key_cache, uint16_t *val_cache,
+                            const float *rope_cos, const float *rope_sin, float *out,
+                            int out_stride, const float *q_norm, const float *k_norm,
+                            float norm_eps);
+
 /* Tuning knobs (bench sweeps).  key 1: decode target workgroups per launch
  * (0 = default); key 2: decode contexts of at most this many positions are
  * not split (multiple of 128, 0 = default). */

@@ -63,6 +63,8 @@ _SIGS = {
     # attention
     "plh_attn_decode": (_i, [_i] * 9 + [_vp] * 8),
     "plh_attn_prefill": (_i, [_i] * 10 + [_vp] * 8 + [_i]),
+    "plh_attn_decode_qknorm": (_i, [_i] * 9 + [_vp] * 10 + [C.c_float]),
+    "plh_attn_prefill_qknorm": (_i, [_i] * 10 + [_vp] * 8 + [_i, _vp, _vp, C.c_float]),
     "plh_set_tuning": (_i, [_i, _i]),
 }
 

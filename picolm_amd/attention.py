@@ -87,27 +87,49 @@ class KVCache:
 
 
 def decode(cache: KVCache, layer0: int, pos: int, q: int, k: int, v: int, out: int,
-           n_launch_layers: int = 1) -> None:
+           n_launch_layers: int = 1, q_norm: int | None = None, k_norm: int | None = None,
+           norm_eps: float = 0.0) -> None:
     """Queues one decode step (device pointers q, k, v, out) for
-    `n_launch_layers` layers starting at `layer0`."""
+    `n_launch_layers` layers starting at `layer0`.  q_norm / k_norm (device
+    pointers to [n_launch_layers][head_dim] fp32) add Qwen3's QK-norm."""
     c = cache.cfg
-    check(lib.plh_attn_decode(c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len,
-                              c.rope_type, layer0, n_launch_layers, pos, q, k, v,
-                              cache.key.ptr, cache.val.ptr, cache.cos.ptr, cache.sin.ptr, out),
-          "plh_attn_decode")
+    if q_norm is None and k_norm is None:
+        check(lib.plh_attn_decode(c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len,
+                                  c.rope_type, layer0, n_launch_layers, pos, q, k, v,
+                                  cache.key.ptr, cache.val.ptr, cache.cos.ptr, cache.sin.ptr,
+                                  out),
+              "plh_attn_decode")
+    else:
+        check(lib.plh_attn_decode_qknorm(c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim,
+                                         c.max_seq_len, c.rope_type, layer0, n_launch_layers,
+                                         pos, q, k, v, cache.key.ptr, cache.val.ptr,
+                                         cache.cos.ptr, cache.sin.ptr, out, q_norm, k_norm,
+                                         norm_eps),
+              "plh_attn_decode_qknorm")
 
 
 def prefill(cache: KVCache, layer0: int, start_pos: int, n_tokens: int, q: int, k: int, v: int,
-            out: int, out_stride: int | None = None, n_launch_layers: int = 1) -> None:
+            out: int, out_stride: int | None = None, n_launch_layers: int = 1,
+            q_norm: int | None = None, k_norm: int | None = None,
+            norm_eps: float = 0.0) -> None:
     """Queues a causal prefill of n_tokens tokens at positions start_pos..
-    (device pointers q [L][N][q_dim], k/v [L][N][kv_dim], out [L][N][stride])."""
+    (device pointers q [L][N][q_dim], k/v [L][N][kv_dim], out [L][N][stride]);
+    q_norm / k_norm as in decode."""
     c = cache.cfg
     stride = c.q_dim if out_stride is None else out_stride
-    check(lib.plh_attn_prefill(c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim, c.max_seq_len,
-                               c.rope_type, layer0, n_launch_layers, start_pos, n_tokens, q, k, v,
-                               cache.key.ptr, cache.val.ptr, cache.cos.ptr, cache.sin.ptr, out,
-                               stride),
-          "plh_attn_prefill")
+    if q_norm is None and k_norm is None:
+        check(lib.plh_attn_prefill(c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim,
+                                   c.max_seq_len, c.rope_type, layer0, n_launch_layers,
+                                   start_pos, n_tokens, q, k, v, cache.key.ptr, cache.val.ptr,
+                                   cache.cos.ptr, cache.sin.ptr, out, stride),
+              "plh_attn_prefill")
+    else:
+        check(lib.plh_attn_prefill_qknorm(c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim,
+                                          c.max_seq_len, c.rope_type, layer0, n_launch_layers,
+                                          start_pos, n_tokens, q, k, v, cache.key.ptr,
+                                          cache.val.ptr, cache.cos.ptr, cache.sin.ptr, out,
+                                          stride, q_norm, k_norm, norm_eps),
+              "plh_attn_prefill_qknorm")
 
 
 def f32_to_f16(src: int, dst: int, n: int) -> None:

@@ -132,6 +132,61 @@ __device__ __forceinline__ float max_xor32(float v) {
   return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
+// ---- QK-norm (Qwen3, model.c:807-817 / 1029-1037) ---------------------------
+// The reference's rmsnorm (tensor.c:425-492) as its x86-64 build runs it
+// (AVX2: quant.h:33-46): eight lane sums acc[j] += x[i]*x[i] over i = j mod 8
+// in increasing i (product and sum rounded separately), folded as
+// ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)), then 1/sqrtf(ss/size + eps); the
+// normalised value is (x*scale)*w.  Device division and square root are
+// correctly rounded (HIP's default), as on the host, so k rows normalised
+// here round to the same fp16 bits.
+__device__ __forceinline__ float rms_fold(const float (&acc)[8], int size, float eps) {
+  const float l0 = acc[0] + acc[4], l1 = acc[1] + acc[5];
+  const float l2 = acc[2] + acc[6], l3 = acc[3] + acc[7];
+  const float ss = (l0 + l2) + (l1 + l3);
+  return 1.0f / sqrtf(ss / (float)size + eps);
+}
+
+// Scale of a row of D floats in memory, summed by one thread.
+template <int D>
+__device__ __forceinline__ float rms_scale_row(const float* x, float eps) {
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll 2
+  for (int m = 0; m < D / 8; ++m) {
+    const float4 a = *(const float4*)(x + 8 * m);
+    const float4 b = *(const float4*)(x + 8 * m + 4);
+    acc[0] = acc[0] + a.x * a.x;
+    acc[1] = acc[1] + a.y * a.y;
+    acc[2] = acc[2] + a.z * a.z;
+    acc[3] = acc[3] + a.w * a.w;
+    acc[4] = acc[4] + b.x * b.x;
+    acc[5] = acc[5] + b.y * b.y;
+    acc[6] = acc[6] + b.z * b.z;
+    acc[7] = acc[7] + b.w * b.w;
+  }
+  return rms_fold(acc, D, eps);
+}
+
+// Scale of the head row of this lane's column when the row is spread over the
+// four lane groups as MFMA operands (lane (col, grp) holds element
+// 32*db + 8*grp + j in x[db][j]): every lane keeps the same eight running
+// sums and adds, in increasing element order, the square held by lane
+// (col, g), so the sums see exactly the reference's order.
+template <int D>
+__device__ __forceinline__ float rms_scale_cols(const float (&x)[D / 32][8], int col, float eps) {
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float sq = x[db][j] * x[db][j];
+        acc[j] = acc[j] + __shfl(sq, col + 16 * g, 64);
+      }
+  return rms_fold(acc, D, eps);
+}
+
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
   return __shfl_xor(v, mask, 64);
 }

@@ -89,14 +89,16 @@ struct Tile {
 // first K/V tiles so that waiting for them (the vector-memory counter is
 // in-order) does not wait for the tiles.  Lane (col, grp) holds
 // q[h][32*db + 8*grp + j] for db < D/32, j < 8 (zero for lanes beyond the
-// group), and the D/8 table entries its pairs need.
+// group), the D/8 table entries its pairs need and, with QK-norm, the q norm
+// weights of its elements.
 template <int D>
 struct QRaw {
   float q[D / 32][8];
   float c[D / 8], s[D / 8];
+  float w[D / 32][8];
 };
 
-template <int D>
+template <int D, bool QKN>
 __device__ __forceinline__ void load_q_raw(const DecodeArgs& a, int li, int kvh, int G, int h0,
                                            int nh, int col, int grp, QRaw<D>& r) {
   constexpr int ND = D / 32;
@@ -109,6 +111,16 @@ __device__ __forceinline__ void load_q_raw(const DecodeArgs& a, int li, int kvh,
     float4 x1 = *(const float4*)(qrow + 32 * db + 8 * grp + 4);
     r.q[db][0] = x0.x, r.q[db][1] = x0.y, r.q[db][2] = x0.z, r.q[db][3] = x0.w;
     r.q[db][4] = x1.x, r.q[db][5] = x1.y, r.q[db][6] = x1.z, r.q[db][7] = x1.w;
+  }
+  if (QKN) {
+    const float* wq = a.qn + (size_t)li * D;
+#pragma unroll
+    for (int db = 0; db < ND; ++db) {
+      const float4 w0 = *(const float4*)(wq + 32 * db + 8 * grp);
+      const float4 w1 = *(const float4*)(wq + 32 * db + 8 * grp + 4);
+      r.w[db][0] = w0.x, r.w[db][1] = w0.y, r.w[db][2] = w0.z, r.w[db][3] = w0.w;
+      r.w[db][4] = w1.x, r.w[db][5] = w1.y, r.w[db][6] = w1.z, r.w[db][7] = w1.w;
+    }
   }
   const float* cr = a.cos_t + (size_t)a.pos * (D / 2);
   const float* sr = a.sin_t + (size_t)a.pos * (D / 2);
@@ -137,11 +149,22 @@ __device__ __forceinline__ void load_q_raw(const DecodeArgs& a, int li, int kvh,
   }
 }
 
-// Rotates the loaded q rows in place with the reference's pairing; lanes
-// beyond the group (valid false) get zero rows.
-template <int D>
-__device__ __forceinline__ void rope_q(int rope_type, bool valid, QRaw<D>& r) {
+// Rotates the loaded q rows in place with the reference's pairing (after
+// QK-norm when enabled); lanes beyond the group (valid false) get zero rows.
+template <int D, bool QKN>
+__device__ __forceinline__ void rope_q(int rope_type, bool valid, int col, float eps,
+                                       QRaw<D>& r) {
   constexpr int ND = D / 32;
+  if (QKN) {
+    const float sc = rms_scale_cols<D>(r.q, col, eps);
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float t = r.q[db][j] * sc;
+        r.q[db][j] = t * r.w[db][j];
+      }
+  }
 #pragma unroll
   for (int db = 0; db < ND; ++db)
 #pragma unroll
@@ -166,12 +189,14 @@ __device__ __forceinline__ void rope_q(int rope_type, bool valid, QRaw<D>& r) {
 template <int D>
 struct RowRaw {
   static constexpr int NP = (D / 2 + 63) / 64;
+  static_assert(NP == 1, "one rope pair per lane");
   static constexpr int NV = (D + 63) / 64;
   float k0[NP], k1[NP], c[NP], s[NP];
+  float w0[NP], w1[NP];  // k norm weights of the pair (QK-norm)
   float v[NV];
 };
 
-template <int D>
+template <int D, bool QKN>
 __device__ __forceinline__ void load_row_raw(const DecodeArgs& a, int li, int kvh, int lane,
                                              RowRaw<D>& r) {
   const int kv_dim = a.n_kv_heads * D;
@@ -188,9 +213,36 @@ __device__ __forceinline__ void load_row_raw(const DecodeArgs& a, int li, int kv
     r.k1[u] = kin[i1];
     r.c[u] = cr[i];
     r.s[u] = sr[i];
+    if (QKN) {
+      r.w0[u] = a.kn[(size_t)li * D + i0];
+      r.w1[u] = a.kn[(size_t)li * D + i1];
+    }
   }
 #pragma unroll
   for (int u = 0; u < RowRaw<D>::NV; ++u) r.v[u] = vin[min(lane + 64 * u, D - 1)];
+}
+
+// QK-norm of the appended k row held as rope pairs by the wave (lane i holds
+// pair i: elements (2i, 2i+1), or (i, i + D/2) for the QWEN pairing): the
+// running sums take element 8m + j from the lane and slot that hold it, in
+// increasing element order, as rms_scale_cols does for q.
+template <int D>
+__device__ __forceinline__ void qk_norm_row(int rope_type, float eps, RowRaw<D>& r) {
+  const float sq0 = r.k0[0] * r.k0[0], sq1 = r.k1[0] * r.k1[0];
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (rope_type == PLH_ROPE_QWEN) {
+#pragma unroll
+    for (int e = 0; e < D; ++e)
+      acc[e & 7] = acc[e & 7] + __shfl(e < D / 2 ? sq0 : sq1, e < D / 2 ? e : e - D / 2, 64);
+  } else {
+#pragma unroll
+    for (int e = 0; e < D; ++e) acc[e & 7] = acc[e & 7] + __shfl((e & 1) ? sq1 : sq0, e >> 1, 64);
+  }
+  const float sc = rms_fold(acc, D, eps);
+  float t = r.k0[0] * sc;
+  r.k0[0] = t * r.w0[0];
+  t = r.k1[0] * sc;
+  r.k1[0] = t * r.w1[0];
 }
 
 // Issues the loads of the 32-row tile starting at t0; rows past tlast are
@@ -290,7 +342,7 @@ __device__ __forceinline__ void process_tile(const Tile<D>& T, const half8_t (&q
   }
 }
 
-template <int D>
+template <int D, bool QKN>
 __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(DecodeArgs a) {
   constexpr int kWaves = DecodeShape<D>::W;
   constexpr int kThreads = 64 * kWaves;
@@ -339,9 +391,9 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
   const bool new_row = owner && wave == 0;
 
   QRaw<D> qr;
-  load_q_raw<D>(a, li, kvh, G, h0, nh, col, grp, qr);
+  load_q_raw<D, QKN>(a, li, kvh, G, h0, nh, col, grp, qr);
   RowRaw<D> rr;
-  if (new_row) load_row_raw<D>(a, li, kvh, lane, rr);
+  if (new_row) load_row_raw<D, QKN>(a, li, kvh, lane, rr);
 
   // Rolling prefetch of depth PF: tile i of the wave lives in buffer i % PF,
   // and refilling a buffer with tile i + PF starts as soon as tile i is done.
@@ -365,7 +417,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
   half8_t qhi[ND], qlo[ND];
   // keep the scheduler from hoisting q's uses (and their waits) above the tiles
   __builtin_amdgcn_sched_barrier(0);
-  rope_q<D>(a.rope_type, col < nh, qr);
+  rope_q<D, QKN>(a.rope_type, col < nh, col, a.norm_eps, qr);
 #pragma unroll
   for (int db = 0; db < ND; ++db)
 #pragma unroll
@@ -376,6 +428,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
       qlo[db][j] = lo;
     }
   if (new_row) {
+    if (QKN) qk_norm_row<D>(a.rope_type, a.norm_eps, rr);
     uint16_t* krow = a.kc + (row0 + pos) * kv_dim + (size_t)kvh * D;
     uint16_t* vrow = a.vc + (row0 + pos) * kv_dim + (size_t)kvh * D;
 #pragma unroll
@@ -566,11 +619,12 @@ extern "C" int plh_set_tuning(int key, int value) {
   return -1;
 }
 
-extern "C" int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int head_dim,
-                               int max_seq_len, int rope_type, int layer0, int n_launch_layers,
-                               int pos, const float* q, const float* k, const float* v,
-                               uint16_t* key_cache, uint16_t* val_cache, const float* rope_cos,
-                               const float* rope_sin, float* out) {
+static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                            int max_seq_len, int rope_type, int layer0, int n_launch_layers,
+                            int pos, const float* q, const float* k, const float* v,
+                            uint16_t* key_cache, uint16_t* val_cache, const float* rope_cos,
+                            const float* rope_sin, float* out, const float* q_norm,
+                            const float* k_norm, float norm_eps) {
   Context& c = ctx();
   if (!c.stream) {
     set_error("plh_attn_decode: library not initialised");
@@ -602,6 +656,11 @@ extern "C" int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int he
     set_error("plh_attn_decode: null pointer");
     return -1;
   }
+  if ((q_norm == nullptr) != (k_norm == nullptr)) {
+    set_error("plh_attn_decode_qknorm: q_norm and k_norm must both be given or both be null");
+    return -1;
+  }
+  const bool qkn = q_norm != nullptr;
 
   const int G = n_heads / n_kv_heads;
   const int n_hblk = (G + 15) / 16;
@@ -652,15 +711,21 @@ extern "C" int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int he
   a.split_len = split_len;
   a.n_units = n_units;
   a.per_xcd = per_xcd;
+  a.qn = q_norm;
+  a.kn = k_norm;
+  a.norm_eps = norm_eps;
   a.score_scale = kLog2e / sqrtf((float)head_dim);
 
   const dim3 grid((unsigned)(8 * per_xcd)), cblock(kCombineThreads);
-  if (head_dim == 64)
-    hipLaunchKernelGGL(attn_decode_kernel<64>, grid, dim3(64 * DecodeShape<64>::W), 0, c.stream,
-                       a);
+  const dim3 b64(64 * DecodeShape<64>::W), b128(64 * DecodeShape<128>::W);
+  if (head_dim == 64 && !qkn)
+    hipLaunchKernelGGL((attn_decode_kernel<64, false>), grid, b64, 0, c.stream, a);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL((attn_decode_kernel<64, true>), grid, b64, 0, c.stream, a);
+  else if (!qkn)
+    hipLaunchKernelGGL((attn_decode_kernel<128, false>), grid, b128, 0, c.stream, a);
   else
-    hipLaunchKernelGGL(attn_decode_kernel<128>, grid, dim3(64 * DecodeShape<128>::W), 0,
-                       c.stream, a);
+    hipLaunchKernelGGL((attn_decode_kernel<128, true>), grid, b128, 0, c.stream, a);
   if (check_hip(hipGetLastError(), "attn_decode_kernel")) return -1;
   if (n_split == 1) return 0;
   if (head_dim == 64)
@@ -670,4 +735,26 @@ extern "C" int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int he
     hipLaunchKernelGGL(attn_decode_combine_kernel<128>, dim3((unsigned)n_groups), cblock, 0,
                        c.stream, a);
   return check_hip(hipGetLastError(), "attn_decode_combine_kernel");
+}
+
+extern "C" int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                               int max_seq_len, int rope_type, int layer0, int n_launch_layers,
+                               int pos, const float* q, const float* k, const float* v,
+                               uint16_t* key_cache, uint16_t* val_cache, const float* rope_cos,
+                               const float* rope_sin, float* out) {
+  return attn_decode_impl(n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, layer0,
+                          n_launch_layers, pos, q, k, v, key_cache, val_cache, rope_cos, rope_sin,
+                          out, nullptr, nullptr, 0.0f);
+}
+
+extern "C" int plh_attn_decode_qknorm(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                                      int max_seq_len, int rope_type, int layer0,
+                                      int n_launch_layers, int pos, const float* q,
+                                      const float* k, const float* v, uint16_t* key_cache,
+                                      uint16_t* val_cache, const float* rope_cos,
+                                      const float* rope_sin, float* out, const float* q_norm,
+                                      const float* k_norm, float norm_eps) {
+  return attn_decode_impl(n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, layer0,
+                          n_launch_layers, pos, q, k, v, key_cache, val_cache, rope_cos, rope_sin,
+                          out, q_norm, k_norm, norm_eps);
 }

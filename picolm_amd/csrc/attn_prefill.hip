@@ -51,7 +51,7 @@ constexpr float kLazy = 8.0f;        // rescale threshold (log2 units)
 // and v, and 8-byte fp16 stores.  LLAMA pairs (2i, 2i+1) for i = 4g..4g+3
 // cover elements 8g..8g+7; QWEN pairs (i, i + D/2) cover 4g..4g+3 and
 // D/2 + 4g..D/2 + 4g+3.
-template <int D>
+template <int D, bool QKN>
 __global__ __launch_bounds__(256) void prefill_append_kernel(PrefillArgs a) {
   constexpr int NG = D / 8;  // groups of 4 pairs per head
   const int kv_dim = a.n_kv_heads * D;
@@ -80,6 +80,19 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(PrefillArgs a) {
     const float4 va = *(const float4*)(vin + e0), vb = *(const float4*)(vin + e1);
     float k8[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
     const float v8[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
+    if (QKN) {
+      // QK-norm of the k head row before the rotation (this thread sums the
+      // whole row in the reference's order)
+      const float sc = rms_scale_row<D>(kin, a.norm_eps);
+      const float* wk = a.kn + (size_t)li * D;
+      const float4 wa = *(const float4*)(wk + e0), wb = *(const float4*)(wk + e1);
+      const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float t = k8[j] * sc;
+        k8[j] = t * w8[j];
+      }
+    }
     if (qwen) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) rope_rotate(k8[j], k8[4 + j], cc[j], ss[j]);
@@ -106,7 +119,7 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(PrefillArgs a) {
   }
 }
 
-template <int D>
+template <int D, bool QKN>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? 6 : 4)))
 void prefill_attn_kernel(PrefillArgs a) {
   constexpr int ND = D / 32;     // 32-wide d blocks of QK
@@ -214,6 +227,26 @@ void prefill_attn_kernel(PrefillArgs a) {
       const float4 x1 = *(const float4*)(qrow + 32 * db + 8 * grp + 4);
       qf[db][0] = x0.x, qf[db][1] = x0.y, qf[db][2] = x0.z, qf[db][3] = x0.w;
       qf[db][4] = x1.x, qf[db][5] = x1.y, qf[db][6] = x1.z, qf[db][7] = x1.w;
+    }
+    if (QKN) {
+      // QK-norm of the column's q head row before the rotation
+      const float* wq = a.qn + (size_t)li * D;
+      float w[ND][8];
+#pragma unroll
+      for (int db = 0; db < ND; ++db) {
+        const float4 w0 = *(const float4*)(wq + 32 * db + 8 * grp);
+        const float4 w1 = *(const float4*)(wq + 32 * db + 8 * grp + 4);
+        w[db][0] = w0.x, w[db][1] = w0.y, w[db][2] = w0.z, w[db][3] = w0.w;
+        w[db][4] = w1.x, w[db][5] = w1.y, w[db][6] = w1.z, w[db][7] = w1.w;
+      }
+      const float sc = rms_scale_cols<D>(qf, col, a.norm_eps);
+#pragma unroll
+      for (int db = 0; db < ND; ++db)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const float t = qf[db][j] * sc;
+          qf[db][j] = t * w[db][j];
+        }
     }
     if (a.rope_type == PLH_ROPE_QWEN) {
 #pragma unroll
@@ -349,12 +382,13 @@ void prefill_attn_kernel(PrefillArgs a) {
 
 }  // namespace
 
-extern "C" int plh_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int head_dim,
-                                int max_seq_len, int rope_type, int layer0, int n_launch_layers,
-                                int start_pos, int n_tokens, const float* q, const float* k,
-                                const float* v, uint16_t* key_cache, uint16_t* val_cache,
-                                const float* rope_cos, const float* rope_sin, float* out,
-                                int out_stride) {
+static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                             int max_seq_len, int rope_type, int layer0, int n_launch_layers,
+                             int start_pos, int n_tokens, const float* q, const float* k,
+                             const float* v, uint16_t* key_cache, uint16_t* val_cache,
+                             const float* rope_cos, const float* rope_sin, float* out,
+                             int out_stride, const float* q_norm, const float* k_norm,
+                             float norm_eps) {
   Context& c = ctx();
   if (!c.stream) {
     set_error("plh_attn_prefill: library not initialised");
@@ -394,11 +428,16 @@ extern "C" int plh_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int h
               out_stride, n_heads * head_dim);
     return -1;
   }
+  if ((q_norm == nullptr) != (k_norm == nullptr)) {
+    set_error("plh_attn_prefill_qknorm: q_norm and k_norm must both be given or both be null");
+    return -1;
+  }
   if (n_tokens == 0) return 0;
   if (!q || !k || !v || !key_cache || !val_cache || !rope_cos || !rope_sin || !out) {
     set_error("plh_attn_prefill: null pointer");
     return -1;
   }
+  const bool qkn = q_norm != nullptr;
 
   PrefillArgs a;
   a.q = q;
@@ -428,21 +467,57 @@ extern "C" int plh_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int h
   // comfortable share of the XCD's 4 MB L2
   const double slice_kv = (double)a.groups_per_xcd * (start_pos + n_tokens) * head_dim * 2 * 2;
   a.qb_major = slice_kv <= 2.0 * 1024 * 1024 ? 1 : 0;
+  a.qn = q_norm;
+  a.kn = k_norm;
+  a.norm_eps = norm_eps;
   a.score_scale = kLog2e / sqrtf((float)head_dim);
 
   const long groups = (long)n_launch_layers * n_tokens * n_kv_heads * (head_dim / 8);
   long ab = (groups + 255) / 256;
   if (ab > 16384) ab = 16384;
   const unsigned grid = (unsigned)(8 * a.per_xcd);
-  if (head_dim == 64) {
-    hipLaunchKernelGGL(prefill_append_kernel<64>, dim3((unsigned)ab), dim3(256), 0, c.stream, a);
+  const dim3 ag((unsigned)ab), ab256(256), pg(grid), pb(kPThreads);
+  if (head_dim == 64 && !qkn) {
+    hipLaunchKernelGGL((prefill_append_kernel<64, false>), ag, ab256, 0, c.stream, a);
     if (check_hip(hipGetLastError(), "prefill_append_kernel")) return -1;
-    hipLaunchKernelGGL(prefill_attn_kernel<64>, dim3(grid), dim3(kPThreads), 0, c.stream, a);
+    hipLaunchKernelGGL((prefill_attn_kernel<64, false>), pg, pb, 0, c.stream, a);
+  } else if (head_dim == 64) {
+    hipLaunchKernelGGL((prefill_append_kernel<64, true>), ag, ab256, 0, c.stream, a);
+    if (check_hip(hipGetLastError(), "prefill_append_kernel")) return -1;
+    hipLaunchKernelGGL((prefill_attn_kernel<64, true>), pg, pb, 0, c.stream, a);
+  } else if (!qkn) {
+    hipLaunchKernelGGL((prefill_append_kernel<128, false>), ag, ab256, 0, c.stream, a);
+    if (check_hip(hipGetLastError(), "prefill_append_kernel")) return -1;
+    hipLaunchKernelGGL((prefill_attn_kernel<128, false>), pg, pb, 0, c.stream, a);
   } else {
-    hipLaunchKernelGGL(prefill_append_kernel<128>, dim3((unsigned)ab), dim3(256), 0, c.stream,
-                       a);
+    hipLaunchKernelGGL((prefill_append_kernel<128, true>), ag, ab256, 0, c.stream, a);
     if (check_hip(hipGetLastError(), "prefill_append_kernel")) return -1;
-    hipLaunchKernelGGL(prefill_attn_kernel<128>, dim3(grid), dim3(kPThreads), 0, c.stream, a);
+    hipLaunchKernelGGL((prefill_attn_kernel<128, true>), pg, pb, 0, c.stream, a);
   }
   return check_hip(hipGetLastError(), "prefill_attn_kernel");
+}
+
+extern "C" int plh_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                                int max_seq_len, int rope_type, int layer0, int n_launch_layers,
+                                int start_pos, int n_tokens, const float* q, const float* k,
+                                const float* v, uint16_t* key_cache, uint16_t* val_cache,
+                                const float* rope_cos, const float* rope_sin, float* out,
+                                int out_stride) {
+  return attn_prefill_impl(n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, rope_type,
+                           layer0, n_launch_layers, start_pos, n_tokens, q, k, v, key_cache,
+                           val_cache, rope_cos, rope_sin, out, out_stride, nullptr, nullptr, 0.0f);
+}
+
+extern "C" int plh_attn_prefill_qknorm(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                                       int max_seq_len, int rope_type, int layer0,
+                                       int n_launch_layers, int start_pos, int n_tokens,
+                                       const float* q, const float* k, const float* v,
+                                       uint16_t* key_cache, uint16_t* val_cache,
+                                       const float* rope_cos, const float* rope_sin, float* out,
+                                       int out_stride, const float* q_norm, const float* k_norm,
+                                       float norm_eps) {
+  return attn_prefill_impl(n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, rope_type,
+                           layer0, n_launch_layers, start_pos, n_tokens, q, k, v, key_cache,
+                           val_cache, rope_cos, rope_sin, out, out_stride, q_norm, k_norm,
+                           norm_eps);
 }

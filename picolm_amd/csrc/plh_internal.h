@@ -44,8 +44,9 @@ struct DecodeArgs {
   int n_split, split_len;  // position splits per (layer, kv head, head block)
   int n_units;             // n_groups * n_split
   int per_xcd;             // units per XCD slice of the grid
-  int groups_per_xcd;      // (layer, kv head) groups per XCD slice
-  int qb_major;            // 1: order a slice's units by q block, heaviest first
+  const float* qn;         // QK-norm weights [n_launch_layers][D], or null
+  const float* kn;
+  float norm_eps;
   float score_scale;       // log2(e) / sqrt(D)
 };
 
@@ -71,6 +72,9 @@ struct PrefillArgs {
   int per_xcd;             // units per XCD slice of the grid
   int groups_per_xcd;      // (layer, kv head) groups per XCD slice
   int qb_major;            // 1: order a slice's units by q block, heaviest first
+  const float* qn;         // QK-norm weights [n_launch_layers][D], or null
+  const float* kn;
+  float norm_eps;
   float score_scale;       // log2(e) / sqrt(D)
 };
 
