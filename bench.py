@@ -63,14 +63,24 @@ WORKLOADS = {
     "llama2_decode_pos4095": dict(L=32, Hq=32, Hkv=32, D=128, S=4096, theta=1e4, pos=4095),
     "tinyllama_prefill_512": dict(L=22, Hq=32, Hkv=4, D=64, S=2048, theta=1e4, start=0, n=512),
     "llama2_prefill_1024": dict(L=32, Hq=32, Hkv=32, D=128, S=4096, theta=1e4, start=0, n=1024),
+    # Qwen3-0.6B-shaped: half-split rotation and per-head QK-norm (eps 1e-6)
+    "qwen3_decode_pos2047": dict(L=28, Hq=16, Hkv=8, D=128, S=2048, theta=1e6, pos=2047, rt=1,
+                                 qkn=1e-6),
+    "qwen3_prefill_512": dict(L=28, Hq=16, Hkv=8, D=128, S=2048, theta=1e6, start=0, n=512,
+                              rt=1, qkn=1e-6),
 }
+
+
+def qkn_bytes(w) -> int:
+    """The q and k norm weight rows read per launch (all layers), if any."""
+    return w["L"] * 2 * w["D"] * 4 if w.get("qkn") else 0
 
 
 def decode_bytes(w) -> int:
     L, Hq, Hkv, D, pos = w["L"], w["Hq"], w["Hkv"], w["D"], w["pos"]
     per_layer = ((pos + 1) * 2 * Hkv * D * 2 + Hq * D * 4 + 2 * Hkv * D * 4
                  + 2 * Hkv * D * 2 + Hq * D * 4)
-    return L * per_layer
+    return L * per_layer + qkn_bytes(w)
 
 
 def prefill_flops(w) -> int:
@@ -83,7 +93,7 @@ def prefill_flops(w) -> int:
 def prefill_bytes(w) -> int:
     """fp32 q, k, v in and out, fp16 rows appended, per launch (all layers)."""
     L, n, Hq, Hkv, D = w["L"], w["n"], w["Hq"], w["Hkv"], w["D"]
-    return L * n * (Hq * D * 4 * 2 + 2 * Hkv * D * 4 + 2 * Hkv * D * 2)
+    return L * n * (Hq * D * 4 * 2 + 2 * Hkv * D * 4 + 2 * Hkv * D * 2) + qkn_bytes(w)
 
 
 def traffic_from_profiles(name: str):
@@ -97,8 +107,19 @@ def traffic_from_profiles(name: str):
         return None
 
 
+def norm_weights(P, w, rng):
+    """Device [L][D] q and k norm weights for a QK-norm workload, else None."""
+    if not w.get("qkn"):
+        return None, None
+    shape = (w["L"], w["D"])
+    qn = (1.0 + 0.1 * rng.standard_normal(shape)).astype(np.float32)
+    kn = (1.0 + 0.1 * rng.standard_normal(shape)).astype(np.float32)
+    return P.DeviceBuffer.from_numpy(qn), P.DeviceBuffer.from_numpy(kn)
+
+
 def run_decode(P, w, steps, warmup, name):
-    cfg = P.AttnConfig(w["L"], w["Hq"], w["Hkv"], w["D"], w["S"], w["theta"], 0)
+    rt = w.get("rt", 0)
+    cfg = P.AttnConfig(w["L"], w["Hq"], w["Hkv"], w["D"], w["S"], w["theta"], rt)
     cache_bytes = cfg.cache_elems * 2
     n_copies = max(1, math.ceil(MALL_DEFEAT_BYTES / (2 * cache_bytes)))
     rng = np.random.default_rng(2047)
@@ -132,14 +153,25 @@ def run_decode(P, w, steps, warmup, name):
         v = P.DeviceBuffer.from_numpy(rng.standard_normal((L, kv), dtype=np.float32))
         o = P.DeviceBuffer(L * cfg.q_dim * 4)
         qkv.append((q, k, v, o))
+    d_qn, d_kn = norm_weights(P, w, rng)
     P.synchronize()
+
+    def call(layer0, n_layers, q, k, v, c, o):
+        """One plh_attn_decode(_qknorm) call over layers layer0.. (pointers
+        already offset to layer0)."""
+        common = (L, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, S, rt, layer0, n_layers, pos,
+                  q, k, v, keys[c].ptr, vals[c].ptr, d_cos.ptr, d_sin.ptr, o)
+        if d_qn is None:
+            P.check(P.lib.plh_attn_decode(*common), "plh_attn_decode")
+        else:
+            off = layer0 * cfg.head_dim * 4
+            P.check(P.lib.plh_attn_decode_qknorm(*common, d_qn.ptr + off, d_kn.ptr + off,
+                                                 w["qkn"]), "plh_attn_decode_qknorm")
 
     def launch(i):
         c = i % n_copies
         q, k, v, o = qkv[c]
-        P.check(P.lib.plh_attn_decode(L, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, S, 0, 0, L,
-                                      pos, q.ptr, k.ptr, v.ptr, keys[c].ptr, vals[c].ptr,
-                                      d_cos.ptr, d_sin.ptr, o.ptr), "plh_attn_decode")
+        call(0, L, q.ptr, k.ptr, v.ptr, c, o.ptr)
 
     for i in range(max(1, warmup)):   # also sizes the split-K workspace
         launch(i)
@@ -166,11 +198,8 @@ def run_decode(P, w, steps, warmup, name):
         c = i % n_copies
         q, k, v, o = qkv[c]
         for l in range(L):
-            P.check(P.lib.plh_attn_decode(L, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, S, 0, l,
-                                          1, pos, q.ptr + l * cfg.q_dim * 4,
-                                          k.ptr + l * kv * 4, v.ptr + l * kv * 4, keys[c].ptr,
-                                          vals[c].ptr, d_cos.ptr, d_sin.ptr,
-                                          o.ptr + l * cfg.q_dim * 4), "plh_attn_decode")
+            call(l, 1, q.ptr + l * cfg.q_dim * 4, k.ptr + l * kv * 4, v.ptr + l * kv * 4, c,
+                 o.ptr + l * cfg.q_dim * 4)
     launch_per_layer(0)
     P.synchronize()
     with P.Graph() as g2:
@@ -203,7 +232,7 @@ def run_decode(P, w, steps, warmup, name):
                                "launches_per_token": L},
     }
     # keep what the CPU baseline needs (copy 0 before further appends)
-    result["_cpu_inputs"] = (cfg, keys[0], vals[0], qkv[0], cos_t, sin_t)
+    result["_cpu_inputs"] = (cfg, keys[0], vals[0], qkv[0], cos_t, sin_t, d_qn, d_kn)
     return result
 
 
@@ -211,7 +240,7 @@ def run_prefill(P, w, steps, warmup):
     """One step = prefill of n prompt tokens over all layers (append kernel +
     causal attention kernel), inputs rotated over enough copies to defeat the
     Infinity Cache."""
-    cfg = P.AttnConfig(w["L"], w["Hq"], w["Hkv"], w["D"], w["S"], w["theta"], 0)
+    cfg = P.AttnConfig(w["L"], w["Hq"], w["Hkv"], w["D"], w["S"], w["theta"], w.get("rt", 0))
     L, n, st = cfg.n_layers, w["n"], w["start"]
     per_copy = prefill_bytes(w) + 2 * L * n * cfg.kv_dim * 2
     n_copies = max(2, math.ceil(MALL_DEFEAT_BYTES / per_copy))
@@ -224,11 +253,13 @@ def run_prefill(P, w, steps, warmup):
         v = P.DeviceBuffer.from_numpy(rng.standard_normal((L, n, cfg.kv_dim), dtype=np.float32))
         o = P.DeviceBuffer(L * n * cfg.q_dim * 4)
         copies.append((cache, q, k, v, o))
+    d_qn, d_kn = norm_weights(P, w, rng)
+    norms = {} if d_qn is None else dict(q_norm=d_qn.ptr, k_norm=d_kn.ptr, norm_eps=w["qkn"])
     P.synchronize()
 
     def launch(i):
         cache, q, k, v, o = copies[i % n_copies]
-        P.prefill(cache, 0, st, n, q.ptr, k.ptr, v.ptr, o.ptr, None, L)
+        P.prefill(cache, 0, st, n, q.ptr, k.ptr, v.ptr, o.ptr, None, L, **norms)
 
     for i in range(max(1, warmup)):
         launch(i)
@@ -265,6 +296,7 @@ def run_prefill(P, w, steps, warmup):
         "algorithmic_bytes_per_step": algo_bytes,
         "copies_rotated": n_copies,
         "_copies": copies,
+        "_norms": (d_qn, d_kn),
     }
 
 
@@ -277,7 +309,8 @@ def cpu_baseline_prefill(P, w, res, budget_s=8.0):
     L, n, st = cfg.n_layers, w["n"], w["start"]
     kc, vc = cache.fetch()
     shp = O.Shape(L, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.max_seq_len,
-                  cfg.rope_freq_base, 0)
+                  cfg.rope_freq_base, cfg.rope_type)
+    qn, kn = host_norms(res.pop("_norms"), L, cfg.head_dim)
     cos_t, sin_t = O.rope_tables(cfg.max_seq_len, cfg.head_dim, cfg.rope_freq_base)
     q = dq.download(np.float32, (L, n, cfg.q_dim))
     k = dk.download(np.float32, (L, n, cfg.kv_dim))
@@ -287,7 +320,7 @@ def cpu_baseline_prefill(P, w, res, budget_s=8.0):
     while t_total < budget_s and layers < L:
         t0 = time.perf_counter()
         ref = O.attn_prefill(shp, layers, st, n, q[layers].copy(), k[layers].copy(), v[layers],
-                             kc, vc, cos_t, sin_t)
+                             kc, vc, cos_t, sin_t, **norm_args(w, qn, kn, layers))
         t_total += time.perf_counter() - t0
         err = np.abs(gpu_out[layers] - ref).reshape(-1, cfg.head_dim).max(1)
         den = np.abs(ref).reshape(-1, cfg.head_dim).max(1)
@@ -301,11 +334,22 @@ def cpu_baseline_prefill(P, w, res, budget_s=8.0):
             "parity_normwise_max": worst}
 
 
+def host_norms(dev, L, D):
+    """Host copies of a QK-norm workload's [L][D] weights (None, None if none)."""
+    if dev[0] is None:
+        return None, None
+    return (dev[0].download(np.float32, (L, D)), dev[1].download(np.float32, (L, D)))
+
+
+def norm_args(w, qn, kn, layer):
+    return {} if qn is None else dict(q_norm=qn[layer], k_norm=kn[layer], eps=w["qkn"])
+
+
 def cpu_baseline(P, w, res, budget_s=12.0):
     """The oracle on one host thread over a bounded sample of the workload, and
     a parity spot check of the GPU output of the same step."""
     from oracle import oracle as O
-    cfg, dkey, dval, (dq, dk, dv, dout), cos_t, sin_t = res.pop("_cpu_inputs")
+    cfg, dkey, dval, (dq, dk, dv, dout), cos_t, sin_t, d_qn, d_kn = res.pop("_cpu_inputs")
     L, pos = cfg.n_layers, w["pos"]
     kc = dkey.download(np.uint16, (cfg.cache_elems,))
     vc = dval.download(np.uint16, (cfg.cache_elems,))
@@ -314,14 +358,16 @@ def cpu_baseline(P, w, res, budget_s=12.0):
     v = dv.download(np.float32, (L, cfg.kv_dim))
     gpu_out = dout.download(np.float32, (L, cfg.q_dim))
     shp = O.Shape(L, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.max_seq_len,
-                  cfg.rope_freq_base, 0)
+                  cfg.rope_freq_base, cfg.rope_type)
+    qn, kn = host_norms((d_qn, d_kn), L, cfg.head_dim)
     tokens, t_total, worst = 0, 0.0, 0.0
     layers_done = 0
     while t_total < budget_s and tokens < 50:
         for l in range(L):
             qi, ki = q[l].copy(), k[l].copy()
             t0 = time.perf_counter()
-            ref = O.attn_decode(shp, l, pos, qi, ki, v[l], kc, vc, cos_t, sin_t)
+            ref = O.attn_decode(shp, l, pos, qi, ki, v[l], kc, vc, cos_t, sin_t,
+                                **norm_args(w, qn, kn, l))
             t_total += time.perf_counter() - t0
             layers_done += 1
             if tokens == 0:
@@ -337,13 +383,23 @@ def cpu_baseline(P, w, res, budget_s=12.0):
     # threads (the reference runs its attention on one thread whatever -j)
     n_thr = min(os.cpu_count() or 1, HOST_THREADS_MAX)
     t_mt, mt_layers = 0.0, 0
-    while t_mt < budget_s / 2 and mt_layers < 4 * L:
+    while qn is None and t_mt < budget_s / 2 and mt_layers < 4 * L:
         l = mt_layers % L
         qi, ki = q[l].copy(), k[l].copy()
         t0 = time.perf_counter()
         O.attn_decode_mt(shp, l, pos, qi, ki, v[l], kc, vc, cos_t, sin_t, n_thr)
         t_mt += time.perf_counter() - t0
         mt_layers += 1
+    out = {
+        "cpu_baseline": {"value": algo / token_s / 1e9, "unit": "GB/s", "cores": 1,
+                         "kind": "port", "us_per_token": token_s * 1e6,
+                         "sample": f"{layers_done} layer-steps ({layers_done / L:.2f} tokens) of "
+                                   f"{w['L']}-layer decode at pos {pos}, oracle on 1 thread"},
+        "host": host_info(),
+        "parity_normwise_max": worst,
+    }
+    if mt_layers == 0:   # the head-parallel oracle has no QK-norm form
+        return out
     token_mt = t_mt / mt_layers * L
     return {
         "cpu_baseline": {"value": algo / token_s / 1e9, "unit": "GB/s", "cores": 1,
@@ -400,6 +456,7 @@ def main():
         res = run_prefill(P, w, max(1, args.steps // 10), args.warmup)
         extra = {} if args.no_cpu else cpu_baseline_prefill(P, w, res)
         res.pop("_copies", None)
+        res.pop("_norms", None)
         line = {"metric": METRIC, "value": res.pop("tflops"), "unit": "TFLOP/s", "n_gpus": 1,
                 "steps": max(1, args.steps // 10), "warmup": args.warmup,
                 "ms_per_step": res["us_per_step"] / 1e3, "higher_is_better": True,
@@ -407,7 +464,8 @@ def main():
                 "config": {"workload": args.workload, "n_layers": w["L"], "n_heads": w["Hq"],
                            "n_kv_heads": w["Hkv"], "head_dim": w["D"], "max_seq_len": w["S"],
                            "start_pos": w["start"], "n_tokens": w["n"],
-                           "rope_theta": w["theta"], "batch": 1}}
+                           "rope_theta": w["theta"], "rope_type": w.get("rt", 0),
+                           "qk_norm_eps": w.get("qkn"), "batch": 1}}
         line.update(res)
         line.update(extra)
         print(json.dumps(line), flush=True)
@@ -433,7 +491,8 @@ def main():
         "data": "synthetic",
         "config": {"workload": args.workload, "n_layers": w["L"], "n_heads": w["Hq"],
                    "n_kv_heads": w["Hkv"], "head_dim": w["D"], "max_seq_len": w["S"],
-                   "pos": w["pos"], "rope_theta": w["theta"], "batch": 1},
+                   "pos": w["pos"], "rope_theta": w["theta"], "rope_type": w.get("rt", 0),
+                   "qk_norm_eps": w.get("qkn"), "batch": 1},
     }
     line["hbm_frac"] = res["roofline"]["frac"]
     line.update(res)
@@ -444,6 +503,7 @@ def main():
         pres = run_prefill(P, pw, 20, 3)
         pextra = {} if args.no_cpu else cpu_baseline_prefill(P, pw, pres, budget_s=4.0)
         pres.pop("_copies", None)
+        pres.pop("_norms", None)
         pres["workload"] = "tinyllama_prefill_512"
         pres.update(pextra)
         line["prefill"] = pres

@@ -134,44 +134,44 @@ __device__ __forceinline__ float max_xor32(float v) {
 
 // ---- QK-norm (Qwen3, model.c:807-817 / 1029-1037) ---------------------------
 // The reference's rmsnorm (tensor.c:425-492) as its x86-64 build runs it
-// (AVX2: quant.h:33-46): eight lane sums acc[j] += x[i]*x[i] over i = j mod 8
+// (AVX2: quant.h:33-46): eight lane sums a[j] += x[i]*x[i] over i = j mod 8
 // in increasing i (product and sum rounded separately), folded as
 // ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)), then 1/sqrtf(ss/size + eps); the
 // normalised value is (x*scale)*w.  Device division and square root are
 // correctly rounded (HIP's default), as on the host, so k rows normalised
 // here round to the same fp16 bits.
-__device__ __forceinline__ float rms_fold(const float (&acc)[8], int size, float eps) {
-  const float l0 = acc[0] + acc[4], l1 = acc[1] + acc[5];
-  const float l2 = acc[2] + acc[6], l3 = acc[3] + acc[7];
-  const float ss = (l0 + l2) + (l1 + l3);
-  return 1.0f / sqrtf(ss / (float)size + eps);
-}
-
-// Scale of a row of D floats in memory, summed by one thread.
+//
+// Pair scheme: four lanes share a row; the lane with pair index p (0..3)
+// forms the sums a[2p] and a[2p+1] itself, in the reference's element order;
+// the fold then adds partner lanes' sums.  Floating addition is commutative,
+// so "own + partner" is the same value in both lanes and every lane ends with
+// the reference's exact scale.
 template <int D>
-__device__ __forceinline__ float rms_scale_row(const float* x, float eps) {
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-#pragma unroll 2
+__device__ __forceinline__ void rms_pair_sums(const float* x, int p, float& s0, float& s1) {
+  s0 = 0.f;
+  s1 = 0.f;
+#pragma unroll
   for (int m = 0; m < D / 8; ++m) {
-    const float4 a = *(const float4*)(x + 8 * m);
-    const float4 b = *(const float4*)(x + 8 * m + 4);
-    acc[0] = acc[0] + a.x * a.x;
-    acc[1] = acc[1] + a.y * a.y;
-    acc[2] = acc[2] + a.z * a.z;
-    acc[3] = acc[3] + a.w * a.w;
-    acc[4] = acc[4] + b.x * b.x;
-    acc[5] = acc[5] + b.y * b.y;
-    acc[6] = acc[6] + b.z * b.z;
-    acc[7] = acc[7] + b.w * b.w;
+    const float2 v = *(const float2*)(x + 8 * m + 2 * p);
+    s0 = s0 + v.x * v.x;
+    s1 = s1 + v.y * v.y;
   }
-  return rms_fold(acc, D, eps);
 }
 
-// Scale of the head row of this lane's column when the row is spread over the
-// four lane groups as MFMA operands (lane (col, grp) holds element
-// 32*db + 8*grp + j in x[db][j]): every lane keeps the same eight running
-// sums and adds, in increasing element order, the square held by lane
-// (col, g), so the sums see exactly the reference's order.
+// sum2(v) = v + (v of the lane with pair index p^2), sum1 likewise for p^1.
+template <class Sum2, class Sum1>
+__device__ __forceinline__ float rms_scale_pairs(float s0, float s1, int size, float eps,
+                                                 Sum2 sum2, Sum1 sum1) {
+  const float l0 = sum2(s0), l1 = sum2(s1);  // p even: a0+a4, a1+a5; p odd: a2+a6, a3+a7
+  const float h0 = sum1(l0), h1 = sum1(l1);  // (a0+a4)+(a2+a6), (a1+a5)+(a3+a7)
+  return 1.0f / sqrtf((h0 + h1) / (float)size + eps);
+}
+
+// Scale of the head row of this lane's column when the row is already in
+// registers as MFMA operands (lane (col, grp) holds element
+// 32*db + 8*grp + j in x[db][j]): every lane keeps the eight running sums
+// a[j] and adds, in increasing element order, the square held by lane
+// (col, g) -- no memory traffic, D/8 * 4 cross-lane reads per lane.
 template <int D>
 __device__ __forceinline__ float rms_scale_cols(const float (&x)[D / 32][8], int col, float eps) {
   float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
@@ -184,7 +184,32 @@ __device__ __forceinline__ float rms_scale_cols(const float (&x)[D / 32][8], int
         const float sq = x[db][j] * x[db][j];
         acc[j] = acc[j] + __shfl(sq, col + 16 * g, 64);
       }
-  return rms_fold(acc, D, eps);
+  const float l0 = acc[0] + acc[4], l1 = acc[1] + acc[5];
+  const float l2 = acc[2] + acc[6], l3 = acc[3] + acc[7];
+  return 1.0f / sqrtf(((l0 + l2) + (l1 + l3)) / (float)D + eps);
+}
+
+// Pair sums across the four 16-lane rows of a wave (p = lane / 16, the MFMA
+// operand layout): the gfx950 row-swap permutes return the values of both
+// rows of a pair, so their sum is own + partner.
+__device__ __forceinline__ float add_xor16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+__device__ __forceinline__ float add_xor32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false,
+                                                  false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Scale of row x for a lane in 16-lane row grp of the MFMA layout (all four
+// lanes of a column pass the same row).
+template <int D>
+__device__ __forceinline__ float rms_scale_grp(const float* x, int grp, float eps) {
+  float s0, s1;
+  rms_pair_sums<D>(x, grp, s0, s1);
+  return rms_scale_pairs(s0, s1, D, eps, add_xor32, add_xor16);
 }
 
 __device__ __forceinline__ float shfl_xor_f(float v, int mask) {

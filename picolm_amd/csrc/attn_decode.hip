@@ -96,6 +96,7 @@ struct QRaw {
   float q[D / 32][8];
   float c[D / 8], s[D / 8];
   float w[D / 32][8];
+  const float* row;  // this lane's q row
 };
 
 template <int D, bool QKN>
@@ -105,6 +106,7 @@ __device__ __forceinline__ void load_q_raw(const DecodeArgs& a, int li, int kvh,
   const bool valid = col < nh;  // lanes past the group load head h0's row; rope_q zeroes them
   const float* qrow =
       a.q + (size_t)li * a.n_heads * D + (size_t)(kvh * G + h0 + (valid ? col : 0)) * D;
+  r.row = qrow;
 #pragma unroll
   for (int db = 0; db < ND; ++db) {
     float4 x0 = *(const float4*)(qrow + 32 * db + 8 * grp);
@@ -152,11 +154,11 @@ __device__ __forceinline__ void load_q_raw(const DecodeArgs& a, int li, int kvh,
 // Rotates the loaded q rows in place with the reference's pairing (after
 // QK-norm when enabled); lanes beyond the group (valid false) get zero rows.
 template <int D, bool QKN>
-__device__ __forceinline__ void rope_q(int rope_type, bool valid, int col, float eps,
+__device__ __forceinline__ void rope_q(int rope_type, bool valid, int grp, float eps,
                                        QRaw<D>& r) {
   constexpr int ND = D / 32;
   if (QKN) {
-    const float sc = rms_scale_cols<D>(r.q, col, eps);
+    const float sc = rms_scale_grp<D>(r.row, grp, eps);
 #pragma unroll
     for (int db = 0; db < ND; ++db)
 #pragma unroll
@@ -194,6 +196,7 @@ struct RowRaw {
   float k0[NP], k1[NP], c[NP], s[NP];
   float w0[NP], w1[NP];  // k norm weights of the pair (QK-norm)
   float v[NV];
+  const float* kin;      // the k row (QK-norm sums)
 };
 
 template <int D, bool QKN>
@@ -204,6 +207,7 @@ __device__ __forceinline__ void load_row_raw(const DecodeArgs& a, int li, int kv
   const float* vin = a.v + (size_t)li * kv_dim + (size_t)kvh * D;
   const float* cr = a.cos_t + (size_t)a.pos * (D / 2);
   const float* sr = a.sin_t + (size_t)a.pos * (D / 2);
+  r.kin = kin;
 #pragma unroll
   for (int u = 0; u < RowRaw<D>::NP; ++u) {
     const int i = min(lane + 64 * u, D / 2 - 1);
@@ -223,22 +227,10 @@ __device__ __forceinline__ void load_row_raw(const DecodeArgs& a, int li, int kv
 }
 
 // QK-norm of the appended k row held as rope pairs by the wave (lane i holds
-// pair i: elements (2i, 2i+1), or (i, i + D/2) for the QWEN pairing): the
-// running sums take element 8m + j from the lane and slot that hold it, in
-// increasing element order, as rms_scale_cols does for q.
+// pair i); every lane forms the scale from the row in memory.
 template <int D>
-__device__ __forceinline__ void qk_norm_row(int rope_type, float eps, RowRaw<D>& r) {
-  const float sq0 = r.k0[0] * r.k0[0], sq1 = r.k1[0] * r.k1[0];
-  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  if (rope_type == PLH_ROPE_QWEN) {
-#pragma unroll
-    for (int e = 0; e < D; ++e)
-      acc[e & 7] = acc[e & 7] + __shfl(e < D / 2 ? sq0 : sq1, e < D / 2 ? e : e - D / 2, 64);
-  } else {
-#pragma unroll
-    for (int e = 0; e < D; ++e) acc[e & 7] = acc[e & 7] + __shfl((e & 1) ? sq1 : sq0, e >> 1, 64);
-  }
-  const float sc = rms_fold(acc, D, eps);
+__device__ __forceinline__ void qk_norm_row(int grp, float eps, RowRaw<D>& r) {
+  const float sc = rms_scale_grp<D>(r.kin, grp, eps);
   float t = r.k0[0] * sc;
   r.k0[0] = t * r.w0[0];
   t = r.k1[0] * sc;
@@ -417,7 +409,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
   half8_t qhi[ND], qlo[ND];
   // keep the scheduler from hoisting q's uses (and their waits) above the tiles
   __builtin_amdgcn_sched_barrier(0);
-  rope_q<D, QKN>(a.rope_type, col < nh, col, a.norm_eps, qr);
+  rope_q<D, QKN>(a.rope_type, col < nh, grp, a.norm_eps, qr);
 #pragma unroll
   for (int db = 0; db < ND; ++db)
 #pragma unroll
@@ -428,7 +420,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
       qlo[db][j] = lo;
     }
   if (new_row) {
-    if (QKN) qk_norm_row<D>(a.rope_type, a.norm_eps, rr);
+    if (QKN) qk_norm_row<D>(grp, a.norm_eps, rr);
     uint16_t* krow = a.kc + (row0 + pos) * kv_dim + (size_t)kvh * D;
     uint16_t* vrow = a.vc + (row0 + pos) * kv_dim + (size_t)kvh * D;
 #pragma unroll

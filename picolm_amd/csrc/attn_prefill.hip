@@ -57,6 +57,10 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(PrefillArgs a) {
   const int kv_dim = a.n_kv_heads * D;
   const long total = (long)a.n_launch_layers * a.n_tokens * a.n_kv_heads * NG;
   const bool qwen = a.rope_type == PLH_ROPE_QWEN;
+  // QK-norm: squares of each k row, for the row's own lanes (pitch D + 8
+  // keeps the four or eight rows of a wave in disjoint banks)
+  constexpr int kSqPitch = D + 8;
+  __shared__ __align__(16) float ksq[QKN ? (256 / NG) * kSqPitch : 1];
   for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < total;
        idx += (long)gridDim.x * 256) {
     const int g = (int)(idx % NG);
@@ -81,9 +85,29 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(PrefillArgs a) {
     float k8[8] = {ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w};
     const float v8[8] = {va.x, va.y, va.z, va.w, vb.x, vb.y, vb.z, vb.w};
     if (QKN) {
-      // QK-norm of the k head row before the rotation (this thread sums the
-      // whole row in the reference's order)
-      const float sc = rms_scale_row<D>(kin, a.norm_eps);
+      // QK-norm of the k head row before the rotation.  The row's NG lanes
+      // (consecutive, one wave) leave their squares in LDS; lane g then forms
+      // the running sums of classes 2(g&3) and 2(g&3)+1 in element order and
+      // the fold adds those of lanes g^2 and g^1.  LDS operations of a wave
+      // complete in order; the waits and clobbers keep the compiler's order.
+      float* sq = ksq + (threadIdx.x / NG) * kSqPitch;
+      *(float4*)(sq + e0) = make_float4(ka.x * ka.x, ka.y * ka.y, ka.z * ka.z, ka.w * ka.w);
+      *(float4*)(sq + e1) = make_float4(kb.x * kb.x, kb.y * kb.y, kb.z * kb.z, kb.w * kb.w);
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+      const int p = g & 3;
+      float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+      for (int m = 0; m < D / 8; ++m) {
+        const float2 t = *(const float2*)(sq + 8 * m + 2 * p);
+        s0 = s0 + t.x;
+        s1 = s1 + t.y;
+      }
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      __builtin_amdgcn_wave_barrier();
+      const float sc = rms_scale_pairs(
+          s0, s1, D, a.norm_eps, [](float v) { return v + __shfl_xor(v, 2, 64); },
+          [](float v) { return v + __shfl_xor(v, 1, 64); });
       const float* wk = a.kn + (size_t)li * D;
       const float4 wa = *(const float4*)(wk + e0), wb = *(const float4*)(wk + e1);
       const float w8[8] = {wa.x, wa.y, wa.z, wa.w, wb.x, wb.y, wb.z, wb.w};

@@ -12,10 +12,17 @@
  * the device one; a HIP failure after device state may have changed marks the
  * backend unavailable so that every later call falls back to the CPU.
  *
+ * Qwen3 layers (a non-null weights.layers[l].attn_q_norm, model.c:807-817
+ * and 1029-1037) run on the device too: their dequantized QK-norm weights
+ * (state.attn_q_norm_w[l] / attn_k_norm_w[l], model.c:657-670) are uploaded
+ * with the tables and the *_qknorm entry points normalise q and k before
+ * RoPE, with config.rms_norm_eps.
+ *
  * Built with USE_HIP; compiles against either this package's model.h or the
  * reference's (it reads only config.{n_embd, n_heads, n_kv_heads, n_layers,
- * max_seq_len, head_dim, rope_type} and state.{key_cache, val_cache,
- * rope_cos, rope_sin}).
+ * max_seq_len, head_dim, rope_type, rms_norm_eps},
+ * weights.layers[].attn_q_norm and state.{key_cache, val_cache, rope_cos,
+ * rope_sin, attn_q_norm_w, attn_k_norm_w}).
  */
 #include "gpu_hip.h"
 
@@ -30,9 +37,12 @@ static struct {
     int inited;     /* plh_init succeeded */
     int uploaded;   /* caches and tables resident */
     int n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, n_embd;
+    float norm_eps;
     int gpu_layers; /* layers < gpu_layers use the device */
     uint16_t *d_key, *d_val;
     float *d_cos, *d_sin;
+    unsigned char qkn[MAX_LAYERS]; /* layer has QK-norm */
+    float *d_qn, *d_kn;            /* [n_layers][head_dim] QK-norm weights, or NULL */
     float *d_q, *d_k, *d_v, *d_out; /* staging, sized for stage_tokens rows */
     int stage_tokens;
 } gs;
@@ -58,6 +68,7 @@ int gpu_init(const model_t *m) {
                 c->head_dim);
         return -1;
     }
+    if (c->n_layers < 1 || c->n_layers > MAX_LAYERS) return -1;
     if (plh_init(env_int("PICOLM_HIP_DEVICE", 0)) != 0) {
         fprintf(stderr, "gpu_hip: %s\n", plh_last_error());
         return -1;
@@ -70,6 +81,7 @@ int gpu_init(const model_t *m) {
     gs.max_seq_len = c->max_seq_len;
     gs.rope_type = (int)c->rope_type;
     gs.n_embd = c->n_embd;
+    gs.norm_eps = c->rms_norm_eps;
     gs.gpu_layers = env_int("PICOLM_GPU_LAYERS", c->n_layers);
     return 0;
 }
@@ -99,6 +111,30 @@ static int ensure_stage(int n_tokens) {
     return 0;
 }
 
+/* Per-layer QK-norm weights, as the host dequantized them at load
+ * (model.c:657-670); layers without attn_q_norm keep the plain entry points. */
+static int upload_qk_norm(const model_t *m) {
+    int any = 0;
+    for (int l = 0; l < gs.n_layers; l++) {
+        gs.qkn[l] = m->weights.layers[l].attn_q_norm != NULL;
+        any |= gs.qkn[l];
+    }
+    if (!any) return 0;
+    size_t row = (size_t)gs.head_dim * sizeof(float);
+    gs.d_qn = (float *)plh_malloc((size_t)gs.n_layers * row);
+    gs.d_kn = (float *)plh_malloc((size_t)gs.n_layers * row);
+    if (!gs.d_qn || !gs.d_kn) return -1;
+    for (int l = 0; l < gs.n_layers; l++) {
+        if (!gs.qkn[l]) continue;
+        if (!m->state.attn_q_norm_w[l] || !m->state.attn_k_norm_w[l]) return -1;
+        size_t off = (size_t)l * gs.head_dim;
+        if (plh_memcpy_htod(gs.d_qn + off, m->state.attn_q_norm_w[l], row) != 0 ||
+            plh_memcpy_htod(gs.d_kn + off, m->state.attn_k_norm_w[l], row) != 0)
+            return -1;
+    }
+    return 0;
+}
+
 int gpu_upload_model(const model_t *m) {
     if (!gs.inited) return -1;
     if (gs.uploaded) return 0;
@@ -120,6 +156,10 @@ int gpu_upload_model(const model_t *m) {
         fprintf(stderr, "gpu_hip: upload failed: %s\n", plh_last_error());
         return -1;
     }
+    if (upload_qk_norm(m) != 0) {
+        fprintf(stderr, "gpu_hip: QK-norm weight upload failed: %s\n", plh_last_error());
+        return -1;
+    }
     gs.uploaded = 1;
     return 0;
 }
@@ -138,6 +178,8 @@ void gpu_shutdown(void) {
         plh_free(gs.d_val);
         plh_free(gs.d_cos);
         plh_free(gs.d_sin);
+        plh_free(gs.d_qn);
+        plh_free(gs.d_kn);
         plh_free(gs.d_q);
         plh_free(gs.d_k);
         plh_free(gs.d_v);
@@ -152,7 +194,7 @@ static int same_shape(const model_t *m) {
     return c->n_layers == gs.n_layers && c->n_heads == gs.n_heads &&
            c->n_kv_heads == gs.n_kv_heads && c->head_dim == gs.head_dim &&
            c->max_seq_len == gs.max_seq_len && (int)c->rope_type == gs.rope_type &&
-           c->n_embd == gs.n_embd;
+           c->n_embd == gs.n_embd && c->rms_norm_eps == gs.norm_eps;
 }
 
 /* Copies rows [r0, r0+n) of layer `layer` from the device caches into the
@@ -176,9 +218,19 @@ int gpu_try_attention(model_t *m, int layer, int pos, float *q, float *k, const 
     if (plh_memcpy_htod(gs.d_q, q, q_bytes) != 0 || plh_memcpy_htod(gs.d_k, k, kv_bytes) != 0 ||
         plh_memcpy_htod(gs.d_v, v, kv_bytes) != 0)
         return -1; /* nothing on the device changed yet */
-    if (plh_attn_decode(gs.n_layers, gs.n_heads, gs.n_kv_heads, gs.head_dim, gs.max_seq_len,
-                        gs.rope_type, layer, 1, pos, gs.d_q, gs.d_k, gs.d_v, gs.d_key, gs.d_val,
-                        gs.d_cos, gs.d_sin, gs.d_out) != 0) {
+    int rc;
+    if (gs.qkn[layer]) {
+        size_t off = (size_t)layer * gs.head_dim;
+        rc = plh_attn_decode_qknorm(gs.n_layers, gs.n_heads, gs.n_kv_heads, gs.head_dim,
+                                    gs.max_seq_len, gs.rope_type, layer, 1, pos, gs.d_q, gs.d_k,
+                                    gs.d_v, gs.d_key, gs.d_val, gs.d_cos, gs.d_sin, gs.d_out,
+                                    gs.d_qn + off, gs.d_kn + off, gs.norm_eps);
+    } else {
+        rc = plh_attn_decode(gs.n_layers, gs.n_heads, gs.n_kv_heads, gs.head_dim,
+                             gs.max_seq_len, gs.rope_type, layer, 1, pos, gs.d_q, gs.d_k,
+                             gs.d_v, gs.d_key, gs.d_val, gs.d_cos, gs.d_sin, gs.d_out);
+    }
+    if (rc != 0) {
         backend_lost("plh_attn_decode");
         return -1;
     }
@@ -209,13 +261,24 @@ int gpu_try_attention_prefill(model_t *m, int layer, int start_pos, int n_tokens
         plh_memcpy_htod(gs.d_v, v, (size_t)n_tokens * kv_dim * sizeof(float)) != 0)
         return -1;
     int dev_stride = (int)((q_dim + 3) & ~(size_t)3);
-    if (plh_attn_prefill(gs.n_layers, gs.n_heads, gs.n_kv_heads, gs.head_dim, gs.max_seq_len,
-                         gs.rope_type, layer, 1, start_pos, n_tokens, gs.d_q, gs.d_k, gs.d_v,
-                         gs.d_key, gs.d_val, gs.d_cos, gs.d_sin, gs.d_out, dev_stride) != 0) {
+    int rc;
+    if (gs.qkn[layer]) {
+        size_t off = (size_t)layer * gs.head_dim;
+        rc = plh_attn_prefill_qknorm(gs.n_layers, gs.n_heads, gs.n_kv_heads, gs.head_dim,
+                                     gs.max_seq_len, gs.rope_type, layer, 1, start_pos,
+                                     n_tokens, gs.d_q, gs.d_k, gs.d_v, gs.d_key, gs.d_val,
+                                     gs.d_cos, gs.d_sin, gs.d_out, dev_stride, gs.d_qn + off,
+                                     gs.d_kn + off, gs.norm_eps);
+    } else {
+        rc = plh_attn_prefill(gs.n_layers, gs.n_heads, gs.n_kv_heads, gs.head_dim,
+                              gs.max_seq_len, gs.rope_type, layer, 1, start_pos, n_tokens,
+                              gs.d_q, gs.d_k, gs.d_v, gs.d_key, gs.d_val, gs.d_cos, gs.d_sin,
+                              gs.d_out, dev_stride);
+    }
+    if (rc != 0) {
         backend_lost("plh_attn_prefill");
         return -1;
     }
-    int rc = 0;
     if ((size_t)dev_stride == stride) {
         rc = plh_memcpy_dtoh(out, gs.d_out, (size_t)n_tokens * stride * sizeof(float));
     } else {

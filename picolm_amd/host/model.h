@@ -1,16 +1,19 @@
 /*
  * model.h -- the part of picolm's model_t that the attention backend reads.
  *
- * Field names and meanings follow the reference (model.h:15-36 config,
- * model.h:98-106 run state), so gpu_hip.c compiles unchanged against the
- * reference's own model.h when it is dropped into picolm (only these fields
- * are read).  This cut-down copy of the *names* lets the library and its
- * tests build on their own; its binary layout is not picolm's.
+ * Field names and meanings follow the reference (model.h:9 MAX_LAYERS,
+ * model.h:22-36 config, model.h:40-74 layer weights, model.h:88-129 run
+ * state), so gpu_hip.c compiles unchanged against the reference's own model.h
+ * when it is dropped into picolm (only these fields are read).  This cut-down
+ * copy of the *names* lets the library and its tests build on their own; its
+ * binary layout is not picolm's.
  */
 #ifndef PICOLM_AMD_MODEL_H
 #define PICOLM_AMD_MODEL_H
 
 #include <stdint.h>
+
+#define MAX_LAYERS 64
 
 typedef enum {
     ROPE_TYPE_LLAMA = 0, /* pairs (2i, 2i+1) */
@@ -25,18 +28,33 @@ typedef struct {
     int max_seq_len;
     int head_dim;
     float rope_freq_base;
+    float rms_norm_eps;
     rope_type_t rope_type;
 } model_config_t;
+
+typedef struct {
+    /* Non-null when the layer has Qwen3's QK-norm; the backend only tests it
+     * and reads the dequantized weights from run_state_t. */
+    const void *attn_q_norm;
+    const void *attn_k_norm;
+} layer_weights_t;
+
+typedef struct {
+    layer_weights_t layers[MAX_LAYERS];
+} model_weights_t;
 
 typedef struct {
     uint16_t *key_cache; /* [n_layers][max_seq_len][n_kv_heads*head_dim] fp16 bits */
     uint16_t *val_cache;
     float *rope_cos;     /* [max_seq_len][head_dim/2] */
     float *rope_sin;
+    float *attn_q_norm_w[MAX_LAYERS]; /* [head_dim] each (QK-norm layers) */
+    float *attn_k_norm_w[MAX_LAYERS];
 } run_state_t;
 
 typedef struct {
     model_config_t config;
+    model_weights_t weights;
     run_state_t state;
 } model_t;
 

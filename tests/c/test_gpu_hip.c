@@ -6,9 +6,11 @@
  * work to the caller's CPU block, which this harness records and skips.
  *
  * Usage: test_gpu_hip <input.bin> <output.bin>
- * input : int32 [L, Hq, Hkv, D, S, rope_type, n_prompt, n_decode], float32
- *         theta, then prompt q [L][P][q_dim], k, v [L][P][kv_dim], then
- *         decode q [T][L][q_dim], k, v [T][L][kv_dim]
+ * input : int32 [L, Hq, Hkv, D, S, rope_type, n_prompt, n_decode, qkn_mask],
+ *         float32 theta, rms_norm_eps, then prompt q [L][P][q_dim],
+ *         k, v [L][P][kv_dim], then decode q [T][L][q_dim], k, v [T][L][kv_dim],
+ *         then QK-norm weights q_norm [L][D], k_norm [L][D]; bit l of qkn_mask
+ *         gives layer l a non-null attn_q_norm (Qwen3, model.c:807)
  * output: int32 [rc_init, rc_upload, rc_download_roundtrip, rc_upload_roundtrip],
  *         int32 rc_prefill[L], int32 rc_decode[T][L],
  *         float32 prefill out [L][P][n_embd], decode out [T][L][q_dim],
@@ -35,11 +37,13 @@ int main(int argc, char **argv) {
     if (argc != 3) return 2;
     FILE *fi = fopen(argv[1], "rb");
     if (!fi) return 2;
-    int32_t hdr[8];
-    float theta;
-    if (fread(hdr, 4, 8, fi) != 8 || fread(&theta, 4, 1, fi) != 1) return 2;
+    int32_t hdr[9];
+    float theta, eps;
+    if (fread(hdr, 4, 9, fi) != 9 || fread(&theta, 4, 1, fi) != 1 || fread(&eps, 4, 1, fi) != 1)
+        return 2;
     const int L = hdr[0], Hq = hdr[1], Hkv = hdr[2], D = hdr[3], S = hdr[4], rt = hdr[5];
-    const int P = hdr[6], T = hdr[7];
+    const int P = hdr[6], T = hdr[7], qkn_mask = hdr[8];
+    if (L < 1 || L > 31) return 2;
     const size_t q_dim = (size_t)Hq * D, kv_dim = (size_t)Hkv * D;
     float *pq = xread(fi, (size_t)L * P * q_dim * 4);
     float *pk = xread(fi, (size_t)L * P * kv_dim * 4);
@@ -47,6 +51,8 @@ int main(int argc, char **argv) {
     float *dq = xread(fi, (size_t)T * L * q_dim * 4);
     float *dk = xread(fi, (size_t)T * L * kv_dim * 4);
     float *dv = xread(fi, (size_t)T * L * kv_dim * 4);
+    float *qn = xread(fi, (size_t)L * D * 4);
+    float *kn = xread(fi, (size_t)L * D * 4);
     fclose(fi);
 
     model_t m;
@@ -58,7 +64,15 @@ int main(int argc, char **argv) {
     m.config.max_seq_len = S;
     m.config.head_dim = D;
     m.config.rope_freq_base = theta;
+    m.config.rms_norm_eps = eps;
     m.config.rope_type = (rope_type_t)rt;
+    for (int l = 0; l < L; l++) {
+        /* the backend tests the weight pointer and reads the dequantized rows */
+        m.weights.layers[l].attn_q_norm = ((qkn_mask >> l) & 1) ? (const void *)qn : NULL;
+        m.weights.layers[l].attn_k_norm = m.weights.layers[l].attn_q_norm;
+        m.state.attn_q_norm_w[l] = qn + (size_t)l * D;
+        m.state.attn_k_norm_w[l] = kn + (size_t)l * D;
+    }
     size_t cache_elems = (size_t)L * S * kv_dim;
     m.state.key_cache = calloc(cache_elems, 2); /* zero-filled like model.c:612-619 */
     m.state.val_cache = calloc(cache_elems, 2);

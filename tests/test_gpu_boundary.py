@@ -3,9 +3,11 @@ tests/c/test_gpu_hip the way picolm's forward passes would call it.
 
 Checks: every call handled (0), prefill and decode outputs against the
 oracle, the host KV cache (kept authoritative by the boundary) bit-equal to
-the oracle's, download/upload round trips for kvcache_save/load, and the
-fallback switches: PICOLM_HIP_DISABLE=1 (all -1, nothing touched) and
-PICOLM_GPU_LAYERS=1 (later layers -1, their rows untouched).
+the oracle's, download/upload round trips for kvcache_save/load, Qwen3
+layers (non-null attn_q_norm: QK-norm before RoPE with the layer's weights
+and rms_norm_eps) mixed with plain ones, and the fallback switches:
+PICOLM_HIP_DISABLE=1 (all -1, nothing touched) and PICOLM_GPU_LAYERS=1
+(later layers -1, their rows untouched).
 """
 import os
 import subprocess
@@ -21,7 +23,10 @@ pytestmark = pytest.mark.gpu
 EXE = os.path.join(ROOT, "tests", "c", "test_gpu_hip")
 
 
-def run_case(tmp_path, dims, theta, P, T, seed, env_extra=None):
+EPS = 1e-6  # Qwen3's rms_norm_eps
+
+
+def run_case(tmp_path, dims, theta, P, T, seed, env_extra=None, qkn_mask=0):
     L, Hq, Hkv, D, S, rt = dims
     rng = np.random.default_rng(seed)
     q_dim, kv_dim = Hq * D, Hkv * D
@@ -31,15 +36,17 @@ def run_case(tmp_path, dims, theta, P, T, seed, env_extra=None):
     dq = rng.standard_normal((T, L, q_dim), dtype=np.float32)
     dk = rng.standard_normal((T, L, kv_dim), dtype=np.float32)
     dv = rng.standard_normal((T, L, kv_dim), dtype=np.float32)
+    qn = (1.0 + 0.5 * rng.standard_normal((L, D))).astype(np.float32)
+    kn = (1.0 + 0.5 * rng.standard_normal((L, D))).astype(np.float32)
     fin, fout = tmp_path / "in.bin", tmp_path / "out.bin"
     with open(fin, "wb") as f:
-        np.array([L, Hq, Hkv, D, S, rt, P, T], np.int32).tofile(f)
-        np.array([theta], np.float32).tofile(f)
-        for a in (pq, pk, pv, dq, dk, dv):
+        np.array([L, Hq, Hkv, D, S, rt, P, T, qkn_mask], np.int32).tofile(f)
+        np.array([theta, EPS], np.float32).tofile(f)
+        for a in (pq, pk, pv, dq, dk, dv, qn, kn):
             a.tofile(f)
     env = dict(os.environ)
     env.update(env_extra or {})
-    print(f"[case] dims {dims} P {P} T {T} env {env_extra}", flush=True)
+    print(f"[case] dims {dims} P {P} T {T} qkn {qkn_mask:#x} env {env_extra}", flush=True)
     r = subprocess.run([EXE, str(fin), str(fout)], env=env, capture_output=True, text=True,
                        timeout=240)
     assert r.returncode == 0, r.stderr
@@ -59,14 +66,19 @@ def run_case(tmp_path, dims, theta, P, T, seed, env_extra=None):
     n = L * S * kv_dim
     kc = take(np.uint16, n)
     vc = take(np.uint16, n)
-    return (rc, rc_pre, rc_dec, out_pre, out_dec, kc, vc), (pq, pk, pv, dq, dk, dv)
+    return (rc, rc_pre, rc_dec, out_pre, out_dec, kc, vc), (pq, pk, pv, dq, dk, dv, qn, kn)
 
 
-def oracle_run(O, dims, theta, inputs, layers_gpu):
+def oracle_run(O, dims, theta, inputs, layers_gpu, qkn_mask=0):
     """Reference semantics for the layers that ran on the GPU; layers that fell
     back are left untouched (the harness skips the CPU block)."""
     L, Hq, Hkv, D, S, rt = dims
-    pq, pk, pv, dq, dk, dv = inputs
+    pq, pk, pv, dq, dk, dv, qn, kn = inputs
+
+    def norms(l):
+        if (qkn_mask >> l) & 1:
+            return dict(q_norm=qn[l], k_norm=kn[l], eps=EPS)
+        return {}
     P, T = pq.shape[1], dq.shape[0]
     shp = O.Shape(L, Hq, Hkv, D, S, theta, rt)
     cos_t, sin_t = O.rope_tables(S, D, theta)
@@ -76,11 +88,11 @@ def oracle_run(O, dims, theta, inputs, layers_gpu):
     dec = np.zeros((T, L, Hq * D), np.float32)
     for l in layers_gpu:
         pre[l] = O.attn_prefill(shp, l, 0, P, pq[l].copy(), pk[l].copy(), pv[l], kc, vc,
-                                cos_t, sin_t)
+                                cos_t, sin_t, **norms(l))
     for t in range(T):
         for l in layers_gpu:
             dec[t, l] = O.attn_decode(shp, l, P + t, dq[t, l].copy(), dk[t, l].copy(), dv[t, l],
-                                      kc, vc, cos_t, sin_t)
+                                      kc, vc, cos_t, sin_t, **norms(l))
     return pre, dec, kc, vc
 
 
@@ -100,6 +112,27 @@ def test_boundary_prefill_then_decode(tmp_path, oracle_mod, dims, theta, P, T):
     assert list(rc) == [0, 0, 0, 0], rc
     assert np.all(rc_pre == 0) and np.all(rc_dec == 0)
     pre, dec, okc, ovc = oracle_run(oracle_mod, dims, theta, inputs, range(L))
+    for l in range(L):
+        assert_attn_close(out_pre[l], pre[l], D, 1e-3, f"prefill layer {l}")
+        for t in range(T):
+            assert_attn_close(out_dec[t, l], dec[t, l], D, 1e-3, f"decode t{t} layer {l}")
+    assert np.array_equal(kc, okc) and np.array_equal(vc, ovc)
+
+
+QKN_CASES = [
+    ((3, 16, 8, 128, 400, 1), 1e6, 150, 4, 0b111),  # Qwen3-0.6B head layout, every layer
+    ((3, 32, 4, 64, 300, 1), 1e6, 97, 3, 0b101),    # QK-norm layers mixed with plain ones
+]
+
+
+@pytest.mark.parametrize("dims,theta,P,T,mask", QKN_CASES)
+def test_boundary_qk_norm_layers(tmp_path, oracle_mod, dims, theta, P, T, mask):
+    (rc, rc_pre, rc_dec, out_pre, out_dec, kc, vc), inputs = run_case(
+        tmp_path, dims, theta, P, T, seed=P * T, qkn_mask=mask)
+    L, D = dims[0], dims[3]
+    assert list(rc) == [0, 0, 0, 0], rc
+    assert np.all(rc_pre == 0) and np.all(rc_dec == 0)
+    pre, dec, okc, ovc = oracle_run(oracle_mod, dims, theta, inputs, range(L), qkn_mask=mask)
     for l in range(L):
         assert_attn_close(out_pre[l], pre[l], D, 1e-3, f"prefill layer {l}")
         for t in range(T):
