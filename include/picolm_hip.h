@@ -142,6 +142,26 @@ int plh_attn_prefill_qknorm(int n_layers, int n_heads, int n_kv_heads, int head_
                             int out_stride, const float *q_norm, const float *k_norm,
                             float norm_eps);
 
+/* ---- weight GEMV (gpu_try_matmul's path) --------------------------------- */
+/* Replaces the reference's matmul row loop (tensor.c:200-215) for GGUF types
+ * Q4_K (12), Q6_K (14) and Q8_0 (8) -- the types its Vulkan backend offloads
+ * (gpu.c:595-602): out[i] = vec_dot(row i of W, x), bit-identical to the
+ * reference's fused dequantize + dot products in its x86-64 (AVX2 + FMA)
+ * build (quant.c:390-452, 517-582, 627-659).  W is a d x n matrix, n a
+ * multiple of the block (256, 256, 32).
+ *
+ * plh_gemv_packed_bytes: size of the device copy (0: type or shape has no
+ * kernel).  plh_gemv_upload: packs the reference's row-major blocks (HOST
+ * pointer, d * row_bytes) into that device buffer (synchronous).
+ * plh_gemv_pack_host: the same packing into a HOST buffer (no device use),
+ * for callers that stage uploads themselves.
+ * plh_gemv: x [n] and out [d] fp32 device pointers, W the packed copy;
+ * queued on the library stream. */
+size_t plh_gemv_packed_bytes(int qtype, int n, int d);
+int plh_gemv_upload(int qtype, int n, int d, const void *host_rows, void *dev);
+int plh_gemv_pack_host(int qtype, int n, int d, const void *host_rows, void *host_packed);
+int plh_gemv(int qtype, int n, int d, const void *dev, const float *x, float *out);
+
 /* Tuning knobs (bench sweeps).  key 1: decode target workgroups per launch
  * (0 = default); key 2: decode contexts of at most this many positions are
  * not split (multiple of 128, 0 = default). */

@@ -23,6 +23,12 @@ ROPE_QWEN = 1
 _f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
 _u16p = np.ctypeslib.ndpointer(np.uint16, flags="C_CONTIGUOUS")
 _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
+_u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
+
+# GGUF type ids (quant.h:49-63) of the GEMV path
+TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 8, 12, 14
+BLOCK = {TYPE_F32: (1, 4), TYPE_F16: (1, 2), TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144),
+         TYPE_Q6_K: (256, 210)}   # (weights, bytes) per block
 
 
 def build(ref: bool | None = None) -> None:
@@ -79,6 +85,14 @@ def lib() -> C.CDLL:
         L.orc_attn_prefill_qkn.restype = C.c_int
         L.orc_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_float]
         L.orc_rmsnorm.restype = None
+        for name in ("orc_vec_dot_q4_K", "orc_vec_dot_q6_K", "orc_vec_dot_q8_0",
+                     "orc_vec_dot_f32"):
+            getattr(L, name).argtypes = [_u8p, _f32p, C.c_int]
+            getattr(L, name).restype = C.c_float
+        L.orc_dequantize_row.argtypes = [C.c_int, _u8p, _f32p, C.c_int]
+        L.orc_dequantize_row.restype = None
+        L.orc_matmul.argtypes = [_f32p, _f32p, _u8p, C.c_int, C.c_int, C.c_int]
+        L.orc_matmul.restype = C.c_int
         _lib = L
     return _lib
 
@@ -119,6 +133,14 @@ def ref() -> C.CDLL:
         R.ref_set_qk_norm.restype = None
         R.ref_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_float]
         R.ref_rmsnorm.restype = None
+        for name in ("vec_dot_q4_K_f32", "vec_dot_q6_K_f32", "vec_dot_q8_0_f32",
+                     "vec_dot_f32_f32"):
+            getattr(R, name).argtypes = [_u8p, _f32p, C.c_int]
+            getattr(R, name).restype = C.c_float
+        R.vec_dot.argtypes = [_u8p, _f32p, C.c_int, C.c_int]
+        R.vec_dot.restype = C.c_float
+        R.dequantize_row.argtypes = [_u8p, _f32p, C.c_int, C.c_int]
+        R.dequantize_row.restype = None
         _ref = R
     return _ref
 
@@ -290,3 +312,61 @@ class RefModel:
 
     def __del__(self):
         self.close()
+
+
+# ---------------------------------------------------------------------------
+# weight GEMV (gpu_try_matmul's path)
+# ---------------------------------------------------------------------------
+
+def row_bytes(qtype: int, n: int) -> int:
+    w, b = BLOCK[qtype]
+    return n // w * b
+
+
+def matmul(W: np.ndarray, x: np.ndarray, n: int, d: int, qtype: int) -> np.ndarray:
+    """out[i] = vec_dot(row i of W, x) in the reference's x86-64 (AVX2) order."""
+    out = np.empty(d, np.float32)
+    rc = lib().orc_matmul(out, np.ascontiguousarray(x, np.float32),
+                          np.ascontiguousarray(W, np.uint8).reshape(-1), n, d, qtype)
+    if rc != 0:
+        raise ValueError(f"no fused dot product for type {qtype}")
+    return out
+
+
+def dequantize(W: np.ndarray, n: int, d: int, qtype: int) -> np.ndarray:
+    W = np.ascontiguousarray(W, np.uint8).reshape(d, -1)
+    out = np.empty((d, n), np.float32)
+    for i in range(d):
+        lib().orc_dequantize_row(qtype, np.ascontiguousarray(W[i]), out[i], n)
+    return out
+
+
+def random_weights(rng: np.random.Generator, qtype: int, n: int, d: int,
+                   scale_exp=(-12, -4)) -> np.ndarray:
+    """d rows of random blocks of a GGUF type: every quant byte uniform, the
+    fp16 scales finite with exponents in scale_exp (2^lo .. 2^hi magnitude),
+    Q6_K's int8 scales uniform.  Returns uint8 [d, row_bytes]."""
+    rb = row_bytes(qtype, n)
+    W = rng.integers(0, 256, size=(d, rb), dtype=np.uint8)
+    if qtype == TYPE_F32:
+        W = rng.standard_normal((d, n), dtype=np.float32).view(np.uint8).reshape(d, rb)
+        return np.ascontiguousarray(W)
+    if qtype == TYPE_F16:
+        return np.ascontiguousarray(
+            rng.standard_normal((d, n)).astype(np.float16).view(np.uint8).reshape(d, rb))
+    nb = n // BLOCK[qtype][0]
+    blocks = W.reshape(d, nb, BLOCK[qtype][1])
+
+    def f16_field(shape):
+        mag = np.exp2(rng.uniform(*scale_exp, size=shape)).astype(np.float16)
+        sign = rng.choice(np.array([-1, 1], np.float16), size=shape) if qtype == TYPE_Q8_0 \
+            or qtype == TYPE_Q6_K else np.float16(1)
+        return (mag * sign).astype(np.float16).view(np.uint16)
+    if qtype == TYPE_Q4_K:
+        blocks[:, :, 0:2] = f16_field((d, nb)).view(np.uint8).reshape(d, nb, 2)
+        blocks[:, :, 2:4] = f16_field((d, nb)).view(np.uint8).reshape(d, nb, 2)
+    elif qtype == TYPE_Q6_K:
+        blocks[:, :, 208:210] = f16_field((d, nb)).view(np.uint8).reshape(d, nb, 2)
+    elif qtype == TYPE_Q8_0:
+        blocks[:, :, 0:2] = f16_field((d, nb)).view(np.uint8).reshape(d, nb, 2)
+    return np.ascontiguousarray(W)

@@ -65,6 +65,11 @@ _SIGS = {
     "plh_attn_prefill": (_i, [_i] * 10 + [_vp] * 8 + [_i]),
     "plh_attn_decode_qknorm": (_i, [_i] * 9 + [_vp] * 10 + [C.c_float]),
     "plh_attn_prefill_qknorm": (_i, [_i] * 10 + [_vp] * 8 + [_i, _vp, _vp, C.c_float]),
+    # weight GEMV
+    "plh_gemv_packed_bytes": (_sz, [_i, _i, _i]),
+    "plh_gemv_upload": (_i, [_i, _i, _i, _vp, _vp]),
+    "plh_gemv_pack_host": (_i, [_i, _i, _i, _vp, _vp]),
+    "plh_gemv": (_i, [_i, _i, _i, _vp, _vp, _vp]),
     "plh_set_tuning": (_i, [_i, _i]),
 }
 
