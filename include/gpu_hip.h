@@ -12,6 +12,7 @@
  *   PICOLM_HIP_DISABLE=1  gpu_init fails, everything stays on the CPU
  *   PICOLM_HIP_DEVICE=N   device index (default 0)
  *   PICOLM_GPU_LAYERS=N   only layers < N use the GPU; later layers get -1
+ *   PICOLM_HIP_MATMUL=0   upload no weight matrices (gpu_try_matmul -> -1)
  *
  * Host caches stay authoritative: every successful call copies the rows it
  * appended back into m->state.key_cache / val_cache, so the CPU fallback and
@@ -31,13 +32,19 @@ extern "C" {
 /* gpu.h:12-15 -- select the device, create the stream.  0 or -1. */
 int gpu_init(const model_t *m);
 /* gpu.h:17-20 -- allocate the device FP16 KV cache [L][S][kv_dim] and RoPE
- * tables, upload the host tables and cache.  0 or -1. */
+ * tables, upload the host tables and cache, and (unless PICOLM_HIP_MATMUL=0)
+ * the Q4_K / Q6_K / Q8_0 projection matrices of layers < PICOLM_GPU_LAYERS
+ * and the output matrix (gpu.c:427-464), packed for the GEMV.  0 or -1. */
 int gpu_upload_model(const model_t *m);
 /* gpu.h:22 -- 1 when initialised and uploaded. */
 int gpu_available(void);
-/* gpu.h:24-26 -- weight GEMV offload is not part of this backend: always -1,
- * the caller's CPU matmul runs (tensor.c:202-205). */
-int gpu_try_matmul(float *out, const float *x, const void *W, int n, int d, int qtype);
+/* gpu.h:24-26 -- out[d] = W[d,n] @ x[n] on the device for an uploaded
+ * matrix (found by its host pointer W), bit-identical to the reference's
+ * CPU matmul (x86-64 AVX2 build).  -1 when W was not uploaded, its type has
+ * no kernel, or n / d / qtype differ from the upload: the caller's CPU
+ * matmul runs (tensor.c:202-205). */
+int gpu_try_matmul(float *out, const float *x, const void *W, int n, int d,
+                   gguf_type_t qtype);
 /* gpu.h:28 -- drain and release everything. */
 void gpu_shutdown(void);
 
@@ -63,7 +70,8 @@ int gpu_kv_upload(const model_t *m, int n_pos);
 static inline int gpu_init(const model_t *m) { (void)m; return -1; }
 static inline int gpu_upload_model(const model_t *m) { (void)m; return -1; }
 static inline int gpu_available(void) { return 0; }
-static inline int gpu_try_matmul(float *o, const float *x, const void *W, int n, int d, int qt) {
+static inline int gpu_try_matmul(float *o, const float *x, const void *W, int n, int d,
+                                 gguf_type_t qt) {
     (void)o; (void)x; (void)W; (void)n; (void)d; (void)qt; return -1;
 }
 static inline void gpu_shutdown(void) {}

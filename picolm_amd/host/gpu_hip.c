@@ -12,6 +12,13 @@
  * the device one; a HIP failure after device state may have changed marks the
  * backend unavailable so that every later call falls back to the CPU.
  *
+ * The weight GEMV (gpu_try_matmul, gpu.c:579-702) follows the Vulkan
+ * backend's model too: gpu_upload_model uploads the projection matrices of
+ * layers < PICOLM_GPU_LAYERS and the output matrix once (gpu.c:427-464),
+ * packed for the kernels, and gpu_try_matmul finds a matrix by its host
+ * pointer, copies x in, runs plh_gemv and copies out back.  Q4_K, Q6_K and
+ * Q8_0 (the reference's three pipelines); other types return -1.
+ *
  * Qwen3 layers (a non-null weights.layers[l].attn_q_norm, model.c:807-817
  * and 1029-1037) run on the device too: their dequantized QK-norm weights
  * (state.attn_q_norm_w[l] / attn_k_norm_w[l], model.c:657-670) are uploaded
@@ -19,10 +26,12 @@
  * RoPE, with config.rms_norm_eps.
  *
  * Built with USE_HIP; compiles against either this package's model.h or the
- * reference's (it reads only config.{n_embd, n_heads, n_kv_heads, n_layers,
- * max_seq_len, head_dim, rope_type, rms_norm_eps},
- * weights.layers[].attn_q_norm and state.{key_cache, val_cache, rope_cos,
- * rope_sin, attn_q_norm_w, attn_k_norm_w}).
+ * reference's (it reads only config.{n_embd, n_ffn, n_heads, n_kv_heads,
+ * n_layers, vocab_size, max_seq_len, head_dim, rope_type, rms_norm_eps},
+ * weights.{output, type_output} and weights.layers[].{attn_q, attn_k, attn_v,
+ * attn_output, ffn_gate, ffn_up, ffn_down, their type_* fields, attn_q_norm},
+ * and state.{key_cache, val_cache, rope_cos, rope_sin, attn_q_norm_w,
+ * attn_k_norm_w}).
  */
 #include "gpu_hip.h"
 
@@ -32,6 +41,13 @@
 #include <string.h>
 
 #include "picolm_hip.h"
+
+/* One uploaded weight matrix: found by the caller's host pointer. */
+typedef struct {
+    const void *host;
+    void *dev;
+    int qtype, n, d;
+} gpu_weight_t;
 
 static struct {
     int inited;     /* plh_init succeeded */
@@ -45,6 +61,10 @@ static struct {
     float *d_qn, *d_kn;            /* [n_layers][head_dim] QK-norm weights, or NULL */
     float *d_q, *d_k, *d_v, *d_out; /* staging, sized for stage_tokens rows */
     int stage_tokens;
+    gpu_weight_t *weights;          /* GEMV matrices */
+    int n_weights, cap_weights;
+    float *d_mx, *d_mout;           /* GEMV staging: x [mx_cap], out [mout_cap] */
+    int mx_cap, mout_cap;
 } gs;
 
 static int env_int(const char *name, int dflt) {
@@ -135,6 +155,75 @@ static int upload_qk_norm(const model_t *m) {
     return 0;
 }
 
+/* Uploads one projection matrix (d rows of n) if the GEMV has a kernel for
+ * its type; matrices it cannot run stay on the CPU path. */
+static int upload_weight(const void *host, int qtype, int d, int n) {
+    if (!host) return 0;
+    size_t bytes = plh_gemv_packed_bytes(qtype, n, d);
+    if (bytes == 0) return 0;
+    if (gs.n_weights == gs.cap_weights) {
+        int cap = gs.cap_weights ? 2 * gs.cap_weights : 64;
+        gpu_weight_t *w = (gpu_weight_t *)realloc(gs.weights, (size_t)cap * sizeof *w);
+        if (!w) return -1;
+        gs.weights = w;
+        gs.cap_weights = cap;
+    }
+    void *dev = plh_malloc(bytes);
+    if (!dev) return -1;
+    if (plh_gemv_upload(qtype, n, d, host, dev) != 0) {
+        plh_free(dev);
+        return -1;
+    }
+    gpu_weight_t *w = &gs.weights[gs.n_weights++];
+    w->host = host;
+    w->dev = dev;
+    w->qtype = qtype;
+    w->n = n;
+    w->d = d;
+    if (n > gs.mx_cap) gs.mx_cap = n;
+    if (d > gs.mout_cap) gs.mout_cap = d;
+    return 0;
+}
+
+/* gpu.c:447-458: the seven projections of layers < gpu_layers, then the
+ * output matrix. */
+static int upload_weights(const model_t *m) {
+    const model_config_t *c = &m->config;
+    int kv_dim = c->n_kv_heads * c->head_dim, q_dim = c->n_heads * c->head_dim;
+    for (int l = 0; l < gs.gpu_layers && l < c->n_layers; l++) {
+        const layer_weights_t *lw = &m->weights.layers[l];
+        if (upload_weight(lw->attn_q, (int)lw->type_attn_q, c->n_embd, c->n_embd) ||
+            upload_weight(lw->attn_k, (int)lw->type_attn_k, kv_dim, c->n_embd) ||
+            upload_weight(lw->attn_v, (int)lw->type_attn_v, kv_dim, c->n_embd) ||
+            upload_weight(lw->attn_output, (int)lw->type_attn_output, c->n_embd, q_dim) ||
+            upload_weight(lw->ffn_gate, (int)lw->type_ffn_gate, c->n_ffn, c->n_embd) ||
+            upload_weight(lw->ffn_up, (int)lw->type_ffn_up, c->n_ffn, c->n_embd) ||
+            upload_weight(lw->ffn_down, (int)lw->type_ffn_down, c->n_embd, c->n_ffn))
+            return -1;
+    }
+    if (gs.gpu_layers > 0 &&
+        upload_weight(m->weights.output, (int)m->weights.type_output, c->vocab_size,
+                      c->n_embd))
+        return -1;
+    if (gs.n_weights > 0) {
+        gs.d_mx = (float *)plh_malloc((size_t)gs.mx_cap * sizeof(float));
+        gs.d_mout = (float *)plh_malloc((size_t)gs.mout_cap * sizeof(float));
+        if (!gs.d_mx || !gs.d_mout) return -1;
+    }
+    return 0;
+}
+
+static void free_weights(void) {
+    for (int i = 0; i < gs.n_weights; i++) plh_free(gs.weights[i].dev);
+    free(gs.weights);
+    plh_free(gs.d_mx);
+    plh_free(gs.d_mout);
+    gs.weights = NULL;
+    gs.n_weights = gs.cap_weights = 0;
+    gs.d_mx = gs.d_mout = NULL;
+    gs.mx_cap = gs.mout_cap = 0;
+}
+
 int gpu_upload_model(const model_t *m) {
     if (!gs.inited) return -1;
     if (gs.uploaded) return 0;
@@ -160,15 +249,34 @@ int gpu_upload_model(const model_t *m) {
         fprintf(stderr, "gpu_hip: QK-norm weight upload failed: %s\n", plh_last_error());
         return -1;
     }
+    if (env_int("PICOLM_HIP_MATMUL", 1) && upload_weights(m) != 0) {
+        /* like a failed tensor upload in gpu.c:441-443: the matmuls stay on
+         * the CPU, attention still runs on the device */
+        fprintf(stderr, "gpu_hip: weight upload failed (%s); matmuls stay on the CPU\n",
+                plh_last_error());
+        free_weights();
+    }
     gs.uploaded = 1;
     return 0;
 }
 
 int gpu_available(void) { return gs.inited && gs.uploaded; }
 
-int gpu_try_matmul(float *out, const float *x, const void *W, int n, int d, int qtype) {
-    (void)out; (void)x; (void)W; (void)n; (void)d; (void)qtype;
-    return -1;
+int gpu_try_matmul(float *out, const float *x, const void *W, int n, int d,
+                   gguf_type_t qtype) {
+    if (!gpu_available() || !W || !x || !out) return -1;
+    const gpu_weight_t *w = NULL;
+    for (int i = 0; i < gs.n_weights; i++)   /* gpu.c:583-591: lookup by host pointer */
+        if (gs.weights[i].host == W) {
+            w = &gs.weights[i];
+            break;
+        }
+    if (!w || w->qtype != (int)qtype || w->n != n || w->d != d) return -1;
+    if (plh_memcpy_htod(gs.d_mx, x, (size_t)n * sizeof(float)) != 0) return -1;
+    if (plh_gemv(w->qtype, n, d, w->dev, gs.d_mx, gs.d_mout) != 0) return -1;
+    /* nothing but staging changed: a failure here leaves the CPU path intact */
+    if (plh_memcpy_dtoh(out, gs.d_mout, (size_t)d * sizeof(float)) != 0) return -1;
+    return 0;
 }
 
 void gpu_shutdown(void) {
@@ -184,6 +292,7 @@ void gpu_shutdown(void) {
         plh_free(gs.d_k);
         plh_free(gs.d_v);
         plh_free(gs.d_out);
+        free_weights();
         plh_shutdown();
     }
     memset(&gs, 0, sizeof gs);

@@ -2,8 +2,8 @@
  * model.h -- the part of picolm's model_t that the attention backend reads.
  *
  * Field names and meanings follow the reference (model.h:9 MAX_LAYERS,
- * model.h:22-36 config, model.h:40-74 layer weights, model.h:88-129 run
- * state), so gpu_hip.c compiles unchanged against the reference's own model.h
+ * model.h:22-36 config, model.h:40-84 weights, model.h:88-129 run state;
+ * quant.h:49-63 type ids), so gpu_hip.c compiles unchanged against the reference's own model.h
  * when it is dropped into picolm (only these fields are read).  This cut-down
  * copy of the *names* lets the library and its tests build on their own; its
  * binary layout is not picolm's.
@@ -12,6 +12,8 @@
 #define PICOLM_AMD_MODEL_H
 
 #include <stdint.h>
+
+#include "quant.h"
 
 #define MAX_LAYERS 64
 
@@ -22,9 +24,11 @@ typedef enum {
 
 typedef struct {
     int n_embd;
+    int n_ffn;
     int n_heads;
     int n_kv_heads;
     int n_layers;
+    int vocab_size;
     int max_seq_len;
     int head_dim;
     float rope_freq_base;
@@ -33,13 +37,30 @@ typedef struct {
 } model_config_t;
 
 typedef struct {
+    /* GGUF rows of the projection matrices (host memory, row-major blocks) */
+    const void *attn_q;
+    const void *attn_k;
+    const void *attn_v;
+    const void *attn_output;
     /* Non-null when the layer has Qwen3's QK-norm; the backend only tests it
      * and reads the dequantized weights from run_state_t. */
     const void *attn_q_norm;
     const void *attn_k_norm;
+    const void *ffn_gate;
+    const void *ffn_down;
+    const void *ffn_up;
+    gguf_type_t type_attn_q;
+    gguf_type_t type_attn_k;
+    gguf_type_t type_attn_v;
+    gguf_type_t type_attn_output;
+    gguf_type_t type_ffn_gate;
+    gguf_type_t type_ffn_down;
+    gguf_type_t type_ffn_up;
 } layer_weights_t;
 
 typedef struct {
+    const void *output; /* final projection [vocab_size][n_embd] */
+    gguf_type_t type_output;
     layer_weights_t layers[MAX_LAYERS];
 } model_weights_t;
 
