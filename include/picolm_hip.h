@@ -164,7 +164,8 @@ int plh_gemv(int qtype, int n, int d, const void *dev, const float *x, float *ou
 
 /* Tuning knobs (bench sweeps).  key 1: decode target workgroups per launch
  * (0 = default); key 2: decode contexts of at most this many positions are
- * not split (multiple of 128, 0 = default). */
+ * not split (multiple of 128, 0 = default); key 3: GEMV rows per thread
+ * (1, 2, 4, 8; 0 = default). */
 int plh_set_tuning(int key, int value);
 
 #ifdef __cplusplus

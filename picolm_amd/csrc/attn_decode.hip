@@ -607,6 +607,14 @@ extern "C" int plh_set_tuning(int key, int value) {
     g_min_split = value;
     return 0;
   }
+  if (key == 3) {
+    if (value != 0 && value != 1 && value != 2 && value != 4 && value != 8) {
+      set_error("plh_set_tuning: GEMV rows per thread must be 0, 1, 2, 4 or 8");
+      return -1;
+    }
+    g_gemv_rows_per_thread = value;
+    return 0;
+  }
   set_error("plh_set_tuning: unknown key %d", key);
   return -1;
 }

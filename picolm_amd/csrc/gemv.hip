@@ -7,13 +7,16 @@
 // Those products keep eight running sums (one per 256-bit lane), add them as
 // ((v0+v4)+(v2+v6)) + ((v1+v5)+(v3+v7)) (hsum_avx2, quant.h:33-46) and chain
 // the per-block terms into one sum in block order.  Here every GPU lane owns
-// whole 256-bit-lane chains of one row slice, in the reference's order; the
-// per-term results go to LDS and one lane per row adds them in order.
+// all eight 256-bit-lane chains of one row slice (a Q4_K sub-block, one to
+// four Q6_K groups, a Q8_0 block), in the reference's order; the per-term
+// results go to LDS and one lane per row adds them in order.
 //
-// Weights live on the device in a packed copy made once at upload
-// (plh_gemv_upload): the same bytes, rearranged so that every lane reads its
-// quants with one aligned vector load (the reference's 210- and 34-byte
-// blocks are not 4-byte aligned).  HBM traffic equals the GGUF size.
+// The kernel is VALU-bound near the HBM roof (a weight costs a conversion and
+// a fused multiply-add at least), so the packed device copy made at upload
+// (plh_gemv_upload) is arranged for few instructions: vector loads that are
+// contiguous across adjacent lanes, quant bytes converted straight to float
+// (v_cvt_f32_ubyte0..3), 32-bit plane offsets.  The bytes are the GGUF
+// bytes rearranged: HBM traffic equals the GGUF size.
 #include <stdlib.h>
 #include <string.h>
 
@@ -25,54 +28,69 @@
 
 using namespace plh;
 
+namespace plh {
+int g_gemv_rows_per_thread = 0;
+}
+
 namespace {
 
 constexpr int kThreads = 256;
 constexpr int kTypeQ8_0 = 8, kTypeQ4K = 12, kTypeQ6K = 14;
 constexpr size_t kPlaneAlign = 256;
+constexpr size_t kMaxPacked = (size_t)1 << 31;  // 32-bit plane offsets
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
-// Packed layouts (d rows, nb blocks per row):
-//  Q4_K: the reference's 144-byte blocks, header unchanged; inside each
-//        32-byte sub-block the quant byte of 256-bit lane k = 4h + kk at
-//        step t (original byte 8t + k) moves to byte 16h + 4t + kk, so a
-//        lane owning lanes 4h..4h+3 reads one 16-byte vector.
-//  Q6_K: three planes.  Quants [d][nb][16 groups][12 B]: group j holds
-//        elements 16j..16j+15 of the block as two words of low nibbles
-//        (word w, byte b: element 8w + b low, 8w + b + 4 high) and one word
-//        of high bit pairs (byte b, bits 2s: element b + 4s); then the int8
-//        scales [d][nb][16] and the fp16 scales [d][nb].
-//  Q8_0: the int8 quants [d][nb][32] and the fp16 scales [d][nb].
+// Packed layouts (d rows, nb blocks per row); every plane is row-major over
+// the matrix and starts 256-byte aligned:
+//  Q4_K: headers [d*nb][16 B] (fp16 d, fp16 dmin, 12 scale bytes), then the
+//        quants of each 64-element sub-block in two planes [d*nb*4][16 B]
+//        (bytes 0-15 and 16-31 of the reference's 32-byte sub-block).
+//  Q6_K: per 16-element group g (row-major over the matrix) two words of low
+//        nibbles (L0, L1: word w, byte b holds element 8w + b low, element
+//        8w + b + 4 high) and one word of high bit pairs (H: byte b, bits 2s
+//        hold element b + 4s), each in its own plane [d*n/16] of words; then
+//        the int8 scales [d*n/16] and the fp16 super-block scales [d*nb].
+//  Q8_0: quants 0-15 and 16-31 of every block in two planes [d*nb][16 B],
+//        then the fp16 scales [d*nb].
 struct Layout {
-  int block_w = 0;       // weights per block
-  int nb = 0;            // blocks per row
-  size_t q_bytes = 0;    // quant plane bytes per block
+  int block_w = 0;            // weights per block
+  int nb = 0;                 // blocks per row
+  size_t off[3] = {0, 0, 0};  // plane offsets (Q4_K: header, q0, q1;
+                              // Q6_K: L0, L1, H; Q8_0: lo, hi)
   size_t scales_off = 0, d_off = 0, total = 0;
 };
 
 bool make_layout(int qtype, int n, int d, Layout& L) {
   if (n <= 0 || d <= 0) return false;
   switch (qtype) {
-    case kTypeQ4K: L.block_w = 256; L.q_bytes = 144; break;
-    case kTypeQ6K: L.block_w = 256; L.q_bytes = 192; break;
-    case kTypeQ8_0: L.block_w = 32; L.q_bytes = 32; break;
+    case kTypeQ4K: L.block_w = 256; break;
+    case kTypeQ6K: L.block_w = 256; break;
+    case kTypeQ8_0: L.block_w = 32; break;
     default: return false;
   }
   if (n % L.block_w) return false;
   L.nb = n / L.block_w;
   const size_t blocks = (size_t)d * L.nb;
-  size_t off = align_up(blocks * L.q_bytes, kPlaneAlign);
-  if (qtype == kTypeQ6K) {
-    L.scales_off = off;
-    off = align_up(off + blocks * 16, kPlaneAlign);
+  if (qtype == kTypeQ4K) {
+    L.off[0] = 0;
+    L.off[1] = align_up(blocks * 16, kPlaneAlign);
+    L.off[2] = L.off[1] + align_up(blocks * 64, kPlaneAlign);
+    L.total = L.off[2] + align_up(blocks * 64, kPlaneAlign);
+  } else if (qtype == kTypeQ6K) {
+    const size_t plane = align_up(blocks * 16 * 4, kPlaneAlign);
+    for (int p = 0; p < 3; ++p) L.off[p] = p * plane;
+    L.scales_off = 3 * plane;
+    L.d_off = align_up(L.scales_off + blocks * 16, kPlaneAlign);
+    L.total = align_up(L.d_off + blocks * 2, kPlaneAlign);
+  } else {
+    const size_t plane = align_up(blocks * 16, kPlaneAlign);
+    L.off[0] = 0;
+    L.off[1] = plane;
+    L.d_off = 2 * plane;
+    L.total = align_up(L.d_off + blocks * 2, kPlaneAlign);
   }
-  if (qtype != kTypeQ4K) {
-    L.d_off = off;
-    off = align_up(off + blocks * 2, kPlaneAlign);
-  }
-  L.total = off;
-  return true;
+  return L.total < kMaxPacked;
 }
 
 // The 6-bit value of element e of a reference Q6_K block (quant.c:199-213).
@@ -90,29 +108,27 @@ void pack_rows(int qtype, const Layout& L, int d, const uint8_t* src, uint8_t* d
   if (qtype == kTypeQ4K) {
     for (size_t b = 0; b < blocks; ++b) {
       const uint8_t* s = src + b * 144;
-      uint8_t* o = dst + b * 144;
-      memcpy(o, s, 16);
-      for (int j = 0; j < 4; ++j)
-        for (int h = 0; h < 2; ++h)
-          for (int t = 0; t < 4; ++t)
-            for (int kk = 0; kk < 4; ++kk)
-              o[16 + 32 * j + 16 * h + 4 * t + kk] = s[16 + 32 * j + 8 * t + 4 * h + kk];
+      memcpy(dst + L.off[0] + b * 16, s, 16);
+      for (int j = 0; j < 4; ++j) {
+        memcpy(dst + L.off[1] + (b * 4 + j) * 16, s + 16 + 32 * j, 16);
+        memcpy(dst + L.off[2] + (b * 4 + j) * 16, s + 32 + 32 * j, 16);
+      }
     }
   } else if (qtype == kTypeQ6K) {
     for (size_t b = 0; b < blocks; ++b) {
       const uint8_t* s = src + b * 210;
-      uint8_t* o = dst + b * 192;
       for (int j = 0; j < 16; ++j) {
         int v[16];
         for (int e = 0; e < 16; ++e) v[e] = q6k_value(s, 16 * j + e);
-        uint8_t* g = o + 12 * j;
+        const size_t g = b * 16 + j;  // group index in the matrix
         for (int w = 0; w < 2; ++w)
           for (int bb = 0; bb < 4; ++bb)
-            g[4 * w + bb] = (uint8_t)((v[8 * w + bb] & 15) | ((v[8 * w + bb + 4] & 15) << 4));
+            dst[L.off[w] + 4 * g + bb] =
+                (uint8_t)((v[8 * w + bb] & 15) | ((v[8 * w + bb + 4] & 15) << 4));
         for (int bb = 0; bb < 4; ++bb) {
           int hb = 0;
           for (int sh = 0; sh < 4; ++sh) hb |= ((v[bb + 4 * sh] >> 4) & 3) << (2 * sh);
-          g[8 + bb] = (uint8_t)hb;
+          dst[L.off[2] + 4 * g + bb] = (uint8_t)hb;
         }
       }
       memcpy(dst + L.scales_off + b * 16, s + 192, 16);
@@ -121,7 +137,8 @@ void pack_rows(int qtype, const Layout& L, int d, const uint8_t* src, uint8_t* d
   } else {  // Q8_0
     for (size_t b = 0; b < blocks; ++b) {
       const uint8_t* s = src + b * 34;
-      memcpy(dst + b * 32, s + 2, 32);
+      memcpy(dst + L.off[0] + b * 16, s + 2, 16);
+      memcpy(dst + L.off[1] + b * 16, s + 18, 16);
       memcpy(dst + L.d_off + b * 2, s, 2);
     }
   }
@@ -137,10 +154,10 @@ struct GemvArgs {
   int uspan;            // units covered by one pass of the threads (<= 256)
   int row_par;          // rows worked side by side (kThreads / uspan)
   int unit_iters;       // passes over the units
-  int rows_per_wg;      // rows of one workgroup
+  int rows_per_wg;      // rows of one workgroup (row_par * rows per thread)
   int terms;            // chained terms per row
   int tpitch;           // LDS pitch of a row's terms
-  size_t scales_off, d_off;
+  uint32_t off0, off1, off2, scales_off, d_off;  // plane offsets (bytes)
 };
 
 __device__ __forceinline__ float hsum8(const float (&v)[8]) {
@@ -150,186 +167,239 @@ __device__ __forceinline__ float hsum8(const float (&v)[8]) {
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *(const float4*)p; }
 
-// byte b of a word as a float (exact)
+template <class T>
+__device__ __forceinline__ T ld(const GemvArgs& a, uint32_t off) {
+  return *(const T*)(a.w + off);
+}
+
+// byte B of a word as a float, exact (v_cvt_f32_ubyteB: one instruction)
+template <int B>
+__device__ __forceinline__ float ubyte(uint32_t w) {
+  float r;
+  if constexpr (B == 0) asm("v_cvt_f32_ubyte0 %0, %1" : "=v"(r) : "v"(w));
+  if constexpr (B == 1) asm("v_cvt_f32_ubyte1 %0, %1" : "=v"(r) : "v"(w));
+  if constexpr (B == 2) asm("v_cvt_f32_ubyte2 %0, %1" : "=v"(r) : "v"(w));
+  if constexpr (B == 3) asm("v_cvt_f32_ubyte3 %0, %1" : "=v"(r) : "v"(w));
+  return r;
+}
 __device__ __forceinline__ float ubyte(uint32_t w, int b) {
-  return (float)((w >> (8 * b)) & 0xFFu);
-}
-
-// ---- Q4_K: a unit is half h of 64-element sub-block s (256-bit lanes
-// 4h..4h+3); the pair (s, 0), (s, 1) sits in adjacent lanes -----------------
-struct Q4KUnit {
-  float xl[4][4], xh[4][4];  // x of the unit's lanes, steps t = 0..3
-  float sx1, sx2;            // hsum of the x running sums (row independent)
-};
-
-__device__ __forceinline__ void q4k_load_x(const float* x, int u, Q4KUnit& U) {
-  const int s = u >> 1, h = u & 1;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const float4 a = ld4(x + 64 * s + 8 * t + 4 * h);
-    const float4 b = ld4(x + 64 * s + 32 + 8 * t + 4 * h);
-    U.xl[t][0] = a.x, U.xl[t][1] = a.y, U.xl[t][2] = a.z, U.xl[t][3] = a.w;
-    U.xh[t][0] = b.x, U.xh[t][1] = b.y, U.xh[t][2] = b.z, U.xh[t][3] = b.w;
-  }
-  // sum_x1 / sum_x2 (quant.c:433): lane k adds x[k] + x[8+k], then
-  // x[16+k] + x[24+k], onto zero
-  float s1[4], s2[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    float a = 0.0f + (U.xl[0][kk] + U.xl[1][kk]);
-    s1[kk] = a + (U.xl[2][kk] + U.xl[3][kk]);
-    float b = 0.0f + (U.xh[0][kk] + U.xh[1][kk]);
-    s2[kk] = b + (U.xh[2][kk] + U.xh[3][kk]);
-  }
-  float p1[4], p2[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    p1[kk] = s1[kk] + __shfl_xor(s1[kk], 1, 64);
-    p2[kk] = s2[kk] + __shfl_xor(s2[kk], 1, 64);
-  }
-  U.sx1 = (p1[0] + p1[2]) + (p1[1] + p1[3]);
-  U.sx2 = (p2[0] + p2[2]) + (p2[1] + p2[3]);
-}
-
-// get_scale_min_k4 (quant.c:82-91) on the 12 scale bytes held in three words
-__device__ __forceinline__ void q4k_scale_min(int j, uint32_t s0, uint32_t s1, uint32_t s2,
-                                              int& sc, int& mn) {
-  auto byte = [&](int i) -> int {
-    const uint32_t w = i < 4 ? s0 : (i < 8 ? s1 : s2);
-    return (int)((w >> (8 * (i & 3))) & 0xFFu);
-  };
-  if (j < 4) {
-    sc = byte(j) & 63;
-    mn = byte(j + 4) & 63;
-  } else {
-    sc = (byte(j + 4) & 0x0F) | ((byte(j - 4) >> 6) << 4);
-    mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+  switch (b) {
+    case 0: return ubyte<0>(w);
+    case 1: return ubyte<1>(w);
+    case 2: return ubyte<2>(w);
+    default: return ubyte<3>(w);
   }
 }
-
-// The term of sub-block s for one row: both lanes of the pair return it.
-__device__ __forceinline__ float q4k_term(const uint8_t* row, int u, const Q4KUnit& U) {
-  const int s = u >> 1, h = u & 1;
-  const int blk = s >> 2, j = s & 3;
-  const uint8_t* b = row + (size_t)blk * 144;
-  const uint4 hdr = *(const uint4*)b;
-  const uint4 q = *(const uint4*)(b + 16 + 32 * j + 16 * h);
-  const uint32_t qw[4] = {q.x, q.y, q.z, q.w};
-  float a1[4], a2[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) a1[kk] = a2[kk] = 0.0f;
-#pragma unroll
-  for (int t = 0; t < 4; ++t) {
-    const uint32_t lo = qw[t] & 0x0F0F0F0Fu, hi = (qw[t] >> 4) & 0x0F0F0F0Fu;
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      a1[kk] = __builtin_fmaf(ubyte(lo, kk), U.xl[t][kk], a1[kk]);
-      a2[kk] = __builtin_fmaf(ubyte(hi, kk), U.xh[t][kk], a2[kk]);
-    }
-  }
-  float p1[4], p2[4];
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk) {
-    p1[kk] = a1[kk] + __shfl_xor(a1[kk], 1, 64);
-    p2[kk] = a2[kk] + __shfl_xor(a2[kk], 1, 64);
-  }
-  const float sqx1 = (p1[0] + p1[2]) + (p1[1] + p1[3]);
-  const float sqx2 = (p2[0] + p2[2]) + (p2[1] + p2[3]);
-  const float dd = f16_bits_to_f32((uint16_t)(hdr.x & 0xFFFFu));
-  const float dmin = f16_bits_to_f32((uint16_t)(hdr.x >> 16));
-  int sc, mn;
-  q4k_scale_min(2 * j, hdr.y, hdr.z, hdr.w, sc, mn);
-  const float d1 = dd * (float)sc, m1 = dmin * (float)mn;
-  q4k_scale_min(2 * j + 1, hdr.y, hdr.z, hdr.w, sc, mn);
-  const float d2 = dd * (float)sc, m2 = dmin * (float)mn;
-  const float t0 = d1 * sqx1, t1 = m1 * U.sx1, t2 = d2 * sqx2, t3 = m2 * U.sx2;
-  return ((t0 - t1) + t2) - t3;
-}
-
-// ---- Q6_K: a unit is 16-element group s of a row (block s/16, group s%16)
-struct Q6KUnit {
-  float x[16];
-};
-
-__device__ __forceinline__ void q6k_load_x(const float* x, int u, Q6KUnit& U) {
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float4 a = ld4(x + 16 * u + 4 * i);
-    U.x[4 * i] = a.x, U.x[4 * i + 1] = a.y, U.x[4 * i + 2] = a.z, U.x[4 * i + 3] = a.w;
-  }
-}
-
-__device__ __forceinline__ float q6k_term(const GemvArgs& a, size_t rblk, int u,
-                                          const Q6KUnit& U) {
-  const int blk = u >> 4, j = u & 15;
-  const size_t b = rblk + blk;               // block index in the matrix
-  const uint8_t* g = a.w + b * 192 + 12 * j;
-  const uint32_t L0 = *(const uint32_t*)g, L1 = *(const uint32_t*)(g + 4);
-  const uint32_t H = *(const uint32_t*)(g + 8);
-  const int sc = (int)(int8_t)a.w[a.scales_off + b * 16 + j];
-  const float dd = f16_bits_to_f32(*(const uint16_t*)(a.w + a.d_off + b * 2));
-  // bytes of v for elements 0-3, 4-7, 8-11, 12-15
-  const uint32_t m4 = 0x0F0F0F0Fu, m2 = 0x03030303u;
-  const uint32_t v0 = (L0 & m4) | ((H & m2) << 4);
-  const uint32_t v1 = ((L0 >> 4) & m4) | (((H >> 2) & m2) << 4);
-  const uint32_t v2 = (L1 & m4) | (((H >> 4) & m2) << 4);
-  const uint32_t v3 = ((L1 >> 4) & m4) | (((H >> 6) & m2) << 4);
-  float p[8];
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const float fl0 = ubyte(v0, k) - 32.0f, fl1 = ubyte(v1, k) - 32.0f;
-    const float fh0 = ubyte(v2, k) - 32.0f, fh1 = ubyte(v3, k) - 32.0f;
-    p[k] = __builtin_fmaf(fl0, U.x[k], fh0 * U.x[8 + k]);
-    p[4 + k] = __builtin_fmaf(fl1, U.x[4 + k], fh1 * U.x[12 + k]);
-  }
-  const float ds = dd * (float)sc;
-  return ds * hsum8(p);
-}
-
-// ---- Q8_0: a unit is one 32-element block ---------------------------------
-struct Q80Unit {
-  float x[32];
-};
-
-__device__ __forceinline__ void q80_load_x(const float* x, int u, Q80Unit& U) {
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const float4 a = ld4(x + 32 * u + 4 * i);
-    U.x[4 * i] = a.x, U.x[4 * i + 1] = a.y, U.x[4 * i + 2] = a.z, U.x[4 * i + 3] = a.w;
-  }
-}
-
 __device__ __forceinline__ float sbyte(uint32_t w, int b) {
   return (float)(int)(int8_t)((w >> (8 * b)) & 0xFFu);
 }
 
-__device__ __forceinline__ float q80_term(const GemvArgs& a, size_t rblk, int u,
-                                          const Q80Unit& U) {
-  const size_t b = rblk + u;
-  const uint4 q0 = *(const uint4*)(a.w + b * 32);
-  const uint4 q1 = *(const uint4*)(a.w + b * 32 + 16);
-  const uint32_t qw[8] = {q0.x, q0.y, q0.z, q0.w, q1.x, q1.y, q1.z, q1.w};
-  const float dd = f16_bits_to_f32(*(const uint16_t*)(a.w + a.d_off + b * 2));
-  float acc[8];
-#pragma unroll
-  for (int k = 0; k < 8; ++k) {
-    // element 8t + k sits in word 2t + k/4, byte k%4
-    const float p0 = sbyte(qw[0 + k / 4], k & 3) * U.x[k];
-    const float p1 = sbyte(qw[2 + k / 4], k & 3) * U.x[8 + k];
-    const float p2 = sbyte(qw[4 + k / 4], k & 3) * U.x[16 + k];
-    const float p3 = sbyte(qw[6 + k / 4], k & 3) * U.x[24 + k];
-    acc[k] = (p0 + p1) + (p2 + p3);
+// ---- Q4_K: a unit is 64-element sub-block s = 4 * block + j ---------------
+struct Q4K {
+  static constexpr int kTerms = 1;
+  struct X {
+    float x[64];
+    float sx1, sx2;  // hsum of the x running sums (row independent)
+  };
+  struct Raw {
+    uint4 hdr, q0, q1;
+  };
+  static __device__ __forceinline__ void load_raw(const GemvArgs& a, int row, int u, Raw& r) {
+    const uint32_t s = (uint32_t)row * a.nb * 4 + u;  // sub-block in the matrix
+    r.hdr = ld<uint4>(a, a.off0 + (s >> 2) * 16);
+    r.q0 = ld<uint4>(a, a.off1 + s * 16);
+    r.q1 = ld<uint4>(a, a.off2 + s * 16);
   }
-  return dd * hsum8(acc);
-}
+  static __device__ __forceinline__ void load_x(const float* x, int u, X& U) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const float4 v = ld4(x + 64 * u + 4 * i);
+      U.x[4 * i] = v.x, U.x[4 * i + 1] = v.y, U.x[4 * i + 2] = v.z, U.x[4 * i + 3] = v.w;
+    }
+    // sum_x1 / sum_x2 (quant.c:433): lane k adds x[k] + x[8+k], then
+    // x[16+k] + x[24+k], onto zero
+    float s1[8], s2[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float a1 = 0.0f + (U.x[k] + U.x[8 + k]);
+      s1[k] = a1 + (U.x[16 + k] + U.x[24 + k]);
+      const float a2 = 0.0f + (U.x[32 + k] + U.x[40 + k]);
+      s2[k] = a2 + (U.x[48 + k] + U.x[56 + k]);
+    }
+    U.sx1 = hsum8(s1);
+    U.sx2 = hsum8(s2);
+  }
+  // get_scale_min_k4 (quant.c:82-91) on the 12 scale bytes in hdr.y..w
+  static __device__ __forceinline__ void scale_min(int j, const uint4& hdr, int& sc, int& mn) {
+    auto byte = [&](int i) -> int {
+      const uint32_t w = i < 4 ? hdr.y : (i < 8 ? hdr.z : hdr.w);
+      return (int)((w >> (8 * (i & 3))) & 0xFFu);
+    };
+    if (j < 4) {
+      sc = byte(j) & 63;
+      mn = byte(j + 4) & 63;
+    } else {
+      sc = (byte(j + 4) & 0x0F) | ((byte(j - 4) >> 6) << 4);
+      mn = (byte(j + 4) >> 4) | ((byte(j) >> 6) << 4);
+    }
+  }
+  static __device__ __forceinline__ void terms(int u, const Raw& r, const X& U, float* t) {
+    const int j = u & 3;
+    // byte 8s + k of the sub-block: word 2s + k/4, byte k%4
+    const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    float a1[8], a2[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) a1[k] = a2[k] = 0.0f;
+#pragma unroll
+    for (int st = 0; st < 4; ++st)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const uint32_t word = w[2 * st + h];
+        const uint32_t lo = word & 0x0F0F0F0Fu, hi = (word >> 4) & 0x0F0F0F0Fu;
+        const int k0 = 4 * h;
+        const float* xl = U.x + 8 * st + k0;
+        const float* xh = U.x + 32 + 8 * st + k0;
+        a1[k0 + 0] = __builtin_fmaf(ubyte<0>(lo), xl[0], a1[k0 + 0]);
+        a1[k0 + 1] = __builtin_fmaf(ubyte<1>(lo), xl[1], a1[k0 + 1]);
+        a1[k0 + 2] = __builtin_fmaf(ubyte<2>(lo), xl[2], a1[k0 + 2]);
+        a1[k0 + 3] = __builtin_fmaf(ubyte<3>(lo), xl[3], a1[k0 + 3]);
+        a2[k0 + 0] = __builtin_fmaf(ubyte<0>(hi), xh[0], a2[k0 + 0]);
+        a2[k0 + 1] = __builtin_fmaf(ubyte<1>(hi), xh[1], a2[k0 + 1]);
+        a2[k0 + 2] = __builtin_fmaf(ubyte<2>(hi), xh[2], a2[k0 + 2]);
+        a2[k0 + 3] = __builtin_fmaf(ubyte<3>(hi), xh[3], a2[k0 + 3]);
+      }
+    const float sqx1 = hsum8(a1), sqx2 = hsum8(a2);
+    const float dd = f16_bits_to_f32((uint16_t)(r.hdr.x & 0xFFFFu));
+    const float dmin = f16_bits_to_f32((uint16_t)(r.hdr.x >> 16));
+    int sc, mn;
+    scale_min(2 * j, r.hdr, sc, mn);
+    const float d1 = dd * (float)sc, m1 = dmin * (float)mn;
+    scale_min(2 * j + 1, r.hdr, sc, mn);
+    const float d2 = dd * (float)sc, m2 = dmin * (float)mn;
+    const float t0 = d1 * sqx1, t1 = m1 * U.sx1, t2 = d2 * sqx2, t3 = m2 * U.sx2;
+    t[0] = ((t0 - t1) + t2) - t3;
+  }
+  static __device__ __forceinline__ int term_index(int u) { return u; }
+};
+
+// ---- Q6_K: a unit is G consecutive 16-element groups of one block --------
+template <int G>
+struct Q6K {
+  static constexpr int kTerms = G;
+  struct X {
+    float x[16 * G];
+  };
+  struct Raw {
+    uint32_t q[3][G];  // L0, L1, H words of the G groups
+    uint32_t sc;       // the G int8 scales (low bytes)
+    uint32_t d;        // fp16 super-block scale (low half)
+  };
+  static __device__ __forceinline__ void load_raw(const GemvArgs& a, int row, int u, Raw& r) {
+    const uint32_t g = (uint32_t)row * a.nb * 16 + (uint32_t)u * G;  // first group
+    const uint32_t offs[3] = {a.off0, a.off1, a.off2};
+#pragma unroll
+    for (int p = 0; p < 3; ++p) {
+      if constexpr (G == 4) {
+        const uint4 v = ld<uint4>(a, offs[p] + 4 * g);
+        r.q[p][0] = v.x, r.q[p][1] = v.y, r.q[p][2] = v.z, r.q[p][3] = v.w;
+      } else if constexpr (G == 2) {
+        const uint2 v = ld<uint2>(a, offs[p] + 4 * g);
+        r.q[p][0] = v.x, r.q[p][1] = v.y;
+      } else {
+        r.q[p][0] = ld<uint32_t>(a, offs[p] + 4 * g);
+      }
+    }
+    if constexpr (G == 4)
+      r.sc = ld<uint32_t>(a, a.scales_off + g);
+    else if constexpr (G == 2)
+      r.sc = ld<uint16_t>(a, a.scales_off + g);
+    else
+      r.sc = ld<uint8_t>(a, a.scales_off + g);
+    r.d = ld<uint16_t>(a, a.d_off + (g >> 4) * 2);
+  }
+  static __device__ __forceinline__ void load_x(const float* x, int u, X& U) {
+#pragma unroll
+    for (int i = 0; i < 4 * G; ++i) {
+      const float4 v = ld4(x + 16 * G * u + 4 * i);
+      U.x[4 * i] = v.x, U.x[4 * i + 1] = v.y, U.x[4 * i + 2] = v.z, U.x[4 * i + 3] = v.w;
+    }
+  }
+  // sums[j] of each group (quant.c:559-578), times d * scale (quant.c:581)
+  static __device__ __forceinline__ void terms(int, const Raw& r, const X& U, float* t) {
+    const float dd = f16_bits_to_f32((uint16_t)(r.d & 0xFFFFu));
+    const uint32_t m4 = 0x0F0F0F0Fu, m30 = 0x30303030u;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const uint32_t L0 = r.q[0][g], L1 = r.q[1][g], H = r.q[2][g];
+      // bytes of the 6-bit values of elements 0-3, 4-7, 8-11, 12-15
+      const uint32_t v0 = (L0 & m4) | ((H << 4) & m30);
+      const uint32_t v1 = ((L0 >> 4) & m4) | ((H << 2) & m30);
+      const uint32_t v2 = (L1 & m4) | (H & m30);
+      const uint32_t v3 = ((L1 >> 4) & m4) | ((H >> 2) & m30);
+      const float* xg = U.x + 16 * g;
+      float p[8];
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const float fl0 = ubyte(v0, k) - 32.0f, fl1 = ubyte(v1, k) - 32.0f;
+        const float fh0 = ubyte(v2, k) - 32.0f, fh1 = ubyte(v3, k) - 32.0f;
+        p[k] = __builtin_fmaf(fl0, xg[k], fh0 * xg[8 + k]);
+        p[4 + k] = __builtin_fmaf(fl1, xg[4 + k], fh1 * xg[12 + k]);
+      }
+      const float ds = dd * sbyte(r.sc, g);
+      t[g] = ds * hsum8(p);
+    }
+  }
+  static __device__ __forceinline__ int term_index(int u) { return u * G; }
+};
+
+// ---- Q8_0: a unit is one 32-element block ---------------------------------
+struct Q80 {
+  static constexpr int kTerms = 1;
+  struct X {
+    float x[32];
+  };
+  struct Raw {
+    uint4 q0, q1;
+    uint32_t d;
+  };
+  static __device__ __forceinline__ void load_raw(const GemvArgs& a, int row, int u, Raw& r) {
+    const uint32_t b = (uint32_t)row * a.nb + u;
+    r.q0 = ld<uint4>(a, a.off0 + b * 16);
+    r.q1 = ld<uint4>(a, a.off1 + b * 16);
+    r.d = ld<uint16_t>(a, a.d_off + b * 2);
+  }
+  static __device__ __forceinline__ void load_x(const float* x, int u, X& U) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const float4 v = ld4(x + 32 * u + 4 * i);
+      U.x[4 * i] = v.x, U.x[4 * i + 1] = v.y, U.x[4 * i + 2] = v.z, U.x[4 * i + 3] = v.w;
+    }
+  }
+  static __device__ __forceinline__ void terms(int, const Raw& r, const X& U, float* t) {
+    const uint32_t qw[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    float acc[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      // element 8s + k sits in word 2s + k/4, byte k%4
+      const float p0 = sbyte(qw[0 + k / 4], k & 3) * U.x[k];
+      const float p1 = sbyte(qw[2 + k / 4], k & 3) * U.x[8 + k];
+      const float p2 = sbyte(qw[4 + k / 4], k & 3) * U.x[16 + k];
+      const float p3 = sbyte(qw[6 + k / 4], k & 3) * U.x[24 + k];
+      acc[k] = (p0 + p1) + (p2 + p3);
+    }
+    t[0] = f16_bits_to_f32((uint16_t)(r.d & 0xFFFFu)) * hsum8(acc);
+  }
+  static __device__ __forceinline__ int term_index(int u) { return u; }
+};
 
 // One workgroup: rows [r0, r0 + rows_per_wg).  Phase 1: thread tid owns unit
-// tid % uspan (+ uspan per pass) of rows tid / uspan + row_par * i, keeps the
-// unit's x in registers and writes the unit's term per row to LDS.  Phase 2:
+// tid % uspan (+ uspan per pass) of the RB rows tid / uspan + row_par * k;
+// it issues the loads of all RB rows, then loads the unit's x (kept in
+// registers for the RB rows) and writes the unit's terms to LDS.  Phase 2:
 // one thread per row adds the row's terms in order.
-template <int QT>
+template <class F, int RB>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
-  extern __shared__ float terms[];
+  extern __shared__ __align__(16) float terms[];
   const int tid = threadIdx.x;
   const int r0 = blockIdx.x * a.rows_per_wg;
   const int rows = min(a.rows_per_wg, a.d - r0);
@@ -337,34 +407,64 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   if (rlane < a.row_par) {
     for (int it = 0; it < a.unit_iters; ++it) {
       const int u = tid % a.uspan + it * a.uspan;
-      if (u >= a.units) break;  // pairs of Q4_K units leave together (units even)
-      if (QT == kTypeQ4K) {
-        Q4KUnit U;
-        q4k_load_x(a.x, u, U);
-        const size_t row_bytes = (size_t)a.nb * 144;
-        for (int rr = rlane; rr < rows; rr += a.row_par) {
-          const float t = q4k_term(a.w + (size_t)(r0 + rr) * row_bytes, u, U);
-          if ((u & 1) == 0) terms[rr * a.tpitch + (u >> 1)] = t;
+      if (u >= a.units) break;
+      typename F::Raw raw[RB];
+#pragma unroll
+      for (int k = 0; k < RB; ++k)  // rows past the end re-read the last row
+        F::load_raw(a, r0 + min(rlane + a.row_par * k, rows - 1), u, raw[k]);
+      typename F::X U;
+      F::load_x(a.x, u, U);
+#pragma unroll
+      for (int k = 0; k < RB; ++k) {
+        float t[F::kTerms];
+        F::terms(u, raw[k], U, t);
+        const int rr = rlane + a.row_par * k;
+        if (rr < rows) {
+#pragma unroll
+          for (int g = 0; g < F::kTerms; ++g) terms[rr * a.tpitch + F::term_index(u) + g] = t[g];
         }
-      } else if (QT == kTypeQ6K) {
-        Q6KUnit U;
-        q6k_load_x(a.x, u, U);
-        for (int rr = rlane; rr < rows; rr += a.row_par)
-          terms[rr * a.tpitch + u] = q6k_term(a, (size_t)(r0 + rr) * a.nb, u, U);
-      } else {
-        Q80Unit U;
-        q80_load_x(a.x, u, U);
-        for (int rr = rlane; rr < rows; rr += a.row_par)
-          terms[rr * a.tpitch + u] = q80_term(a, (size_t)(r0 + rr) * a.nb, u, U);
       }
     }
   }
   __syncthreads();
-  if (tid < rows) {
-    const float* t = terms + tid * a.tpitch;
+  // the row's terms in order, 16 per step, the next step's reads in flight
+  for (int rr = tid; rr < rows; rr += kThreads) {
+    const float* t = terms + rr * a.tpitch;  // 16-byte aligned rows
+    const int full = a.terms / 16 * 16;
     float sumf = 0.0f;
-    for (int s = 0; s < a.terms; ++s) sumf = sumf + t[s];
-    a.out[r0 + tid] = sumf;
+    if (full > 0) {
+      float4 nx[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) nx[i] = *(const float4*)(t + 4 * i);
+      for (int s = 0; s < full; s += 16) {
+        float4 cur[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cur[i] = nx[i];
+        if (s + 16 < full) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) nx[i] = *(const float4*)(t + s + 16 + 4 * i);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          sumf = sumf + cur[i].x;
+          sumf = sumf + cur[i].y;
+          sumf = sumf + cur[i].z;
+          sumf = sumf + cur[i].w;
+        }
+      }
+    }
+    for (int s = full; s < a.terms; ++s) sumf = sumf + t[s];
+    a.out[r0 + rr] = sumf;
+  }
+}
+
+template <class F>
+void launch_rb(int rb, int grid, size_t lds, hipStream_t st, const GemvArgs& a) {
+  switch (rb) {
+    case 1: hipLaunchKernelGGL((gemv_kernel<F, 1>), dim3(grid), dim3(kThreads), lds, st, a); break;
+    case 2: hipLaunchKernelGGL((gemv_kernel<F, 2>), dim3(grid), dim3(kThreads), lds, st, a); break;
+    case 4: hipLaunchKernelGGL((gemv_kernel<F, 4>), dim3(grid), dim3(kThreads), lds, st, a); break;
+    default: hipLaunchKernelGGL((gemv_kernel<F, 8>), dim3(grid), dim3(kThreads), lds, st, a); break;
   }
 }
 
@@ -432,41 +532,45 @@ int plh_gemv(int qtype, int n, int d, const void* dev, const float* x, float* ou
   a.out = out;
   a.d = d;
   a.nb = L.nb;
-  a.units = qtype == kTypeQ4K ? n / 32 : (qtype == kTypeQ6K ? n / 16 : n / 32);
-  a.terms = qtype == kTypeQ4K ? n / 64 : a.units;
+  // Q6_K lanes take four groups (64 weights, like a Q4_K sub-block): the
+  // per-row work of a unit (scale, hsum, addressing) is shared by more weights
+  const int q6_groups = 4;
+  a.units = qtype == kTypeQ4K ? n / 64 : (qtype == kTypeQ6K ? n / (16 * q6_groups) : n / 32);
+  a.terms = qtype == kTypeQ4K ? n / 64 : (qtype == kTypeQ6K ? n / 16 : n / 32);
   a.uspan = a.units < kThreads ? a.units : kThreads;
   a.row_par = kThreads / a.uspan;
   a.unit_iters = (a.units + a.uspan - 1) / a.uspan;
-  a.tpitch = a.terms + 1;
-  a.scales_off = L.scales_off;
-  a.d_off = L.d_off;
-  // rows per workgroup: a multiple of row_par, at most 64 (the chain phase
-  // is one wave) and within 64 KiB of terms, aiming at >= 2 workgroups per CU
+  a.tpitch = (a.terms + 3) / 4 * 4 + 4;  // 16-byte rows, staggered banks
+  a.off0 = (uint32_t)L.off[0];
+  a.off1 = (uint32_t)L.off[1];
+  a.off2 = (uint32_t)L.off[2];
+  a.scales_off = (uint32_t)L.scales_off;
+  a.d_off = (uint32_t)L.d_off;
+  // rows per thread: the largest of 4, 2, 1 that still gives at least 0.6
+  // workgroups per CU and keeps the workgroup's terms within 64 KiB of LDS
+  // (measured on the TinyLlama and output-projection shapes: more rows in
+  // flight per thread beat more workgroups until the grid no longer covers
+  // the CUs; 8 rows cost occupancy)
   const int cus = c.num_cus > 0 ? c.num_cus : 256;
-  int per_thread = 1;
-  while (per_thread < 8 && (long)a.row_par * per_thread * 2 * 2 * cus <= d) per_thread *= 2;
-  int rows = a.row_par * per_thread;
   const int lds_rows = (int)((64 * 1024) / (sizeof(float) * (size_t)a.tpitch));
-  if (rows > 64) rows = 64;
-  if (rows > lds_rows) rows = lds_rows;
-  if (rows < 1) {
+  int rb = 4;
+  while (rb > 1 && ((long)(d + a.row_par * rb - 1) / (a.row_par * rb) * 10 < 6L * cus ||
+                    a.row_par * rb > lds_rows))
+    rb /= 2;
+  if (g_gemv_rows_per_thread > 0) rb = g_gemv_rows_per_thread;
+  if (a.row_par * rb > lds_rows) {
     set_error("plh_gemv: row of %d weights too long for the term buffer", n);
     return -1;
   }
-  a.rows_per_wg = rows;
-  const size_t lds = sizeof(float) * (size_t)rows * a.tpitch;
-  const int grid = (d + rows - 1) / rows;
-  switch (qtype) {
-    case kTypeQ4K:
-      hipLaunchKernelGGL(gemv_kernel<kTypeQ4K>, dim3(grid), dim3(kThreads), lds, c.stream, a);
-      break;
-    case kTypeQ6K:
-      hipLaunchKernelGGL(gemv_kernel<kTypeQ6K>, dim3(grid), dim3(kThreads), lds, c.stream, a);
-      break;
-    default:
-      hipLaunchKernelGGL(gemv_kernel<kTypeQ8_0>, dim3(grid), dim3(kThreads), lds, c.stream, a);
-      break;
-  }
+  a.rows_per_wg = a.row_par * rb;
+  const size_t lds = sizeof(float) * (size_t)a.rows_per_wg * a.tpitch;
+  const int grid = (d + a.rows_per_wg - 1) / a.rows_per_wg;
+  if (qtype == kTypeQ4K)
+    launch_rb<Q4K>(rb, grid, lds, c.stream, a);
+  else if (qtype == kTypeQ8_0)
+    launch_rb<Q80>(rb, grid, lds, c.stream, a);
+  else
+    launch_rb<Q6K<4>>(rb, grid, lds, c.stream, a);
   return check_hip(hipGetLastError(), "gemv_kernel launch");
 }
 

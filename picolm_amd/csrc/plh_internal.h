@@ -22,6 +22,10 @@ Context& ctx();
 void set_error(const char* fmt, ...);
 int check_hip(hipError_t e, const char* what);
 
+// GEMV rows per thread forced by plh_set_tuning key 3 (0: the launch's own
+// choice).
+extern int g_gemv_rows_per_thread;
+
 // Makes sure the workspace holds at least `bytes`.  Growing it waits for the
 // queued work (which may still read the old one).  Returns 0 or -1.
 int ensure_workspace(size_t bytes);

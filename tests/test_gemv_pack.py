@@ -14,15 +14,17 @@ ALIGN = 256
 def _planes(qtype, n, d):
     nb = n // G.BLOCK[qtype][0]
     blocks = d * nb
-    q_bytes = {G.TYPE_Q4_K: 144, G.TYPE_Q6_K: 192, G.TYPE_Q8_0: 32}[qtype]
     up = lambda v: (v + ALIGN - 1) // ALIGN * ALIGN  # noqa: E731
-    off = up(blocks * q_bytes)
-    scales_off = d_off = None
+    if qtype == G.TYPE_Q4_K:
+        return nb, None, None, None, up(blocks * 144)
     if qtype == G.TYPE_Q6_K:
-        scales_off, off = off, up(off + blocks * 16)
-    if qtype != G.TYPE_Q4_K:
-        d_off, off = off, up(off + blocks * 2)
-    return nb, scales_off, d_off, off
+        plane = up(blocks * 16 * 4)
+        scales_off = 3 * plane
+        d_off = up(scales_off + blocks * 16)
+        return nb, plane, scales_off, d_off, up(d_off + blocks * 2)
+    plane = up(blocks * 16)
+    d_off = 2 * plane
+    return nb, plane, None, d_off, up(d_off + blocks * 2)
 
 
 def _q6_values(blk):
@@ -44,7 +46,7 @@ def test_pack_roundtrip(oracle_mod, qtype, n, d):
     rng = np.random.default_rng(n + d)
     W = oracle_mod.random_weights(rng, qtype, n, d)
     packed = G.pack_host(qtype, n, d, W)
-    nb, scales_off, d_off, total = _planes(qtype, n, d)
+    nb, plane, scales_off, d_off, total = _planes(qtype, n, d)
     assert packed.size == total == P.lib.plh_gemv_packed_bytes(qtype, n, d)
     rb = G.row_bytes(qtype, n)
     for r in range(d):
@@ -64,9 +66,9 @@ def test_pack_roundtrip(oracle_mod, qtype, n, d):
             elif qtype == G.TYPE_Q6_K:
                 vals = _q6_values(src)
                 for j in range(16):
-                    g = packed[b * 192 + 12 * j:b * 192 + 12 * j + 12]
-                    L0, L1, H = (int.from_bytes(g[4 * w:4 * w + 4].tobytes(), "little")
-                                 for w in range(3))
+                    g = b * 16 + j
+                    L0, L1, H = (int.from_bytes(packed[p * plane + 4 * g:p * plane + 4 * g + 4]
+                                                .tobytes(), "little") for p in range(3))
                     m4, m2 = 0x0F0F0F0F, 0x03030303
                     words = [(L0 & m4) | ((H & m2) << 4),
                              ((L0 >> 4) & m4) | (((H >> 2) & m2) << 4),
@@ -78,7 +80,8 @@ def test_pack_roundtrip(oracle_mod, qtype, n, d):
                                       src[192:208])
                 assert np.array_equal(packed[d_off + 2 * b:d_off + 2 * b + 2], src[208:210])
             else:
-                assert np.array_equal(packed[32 * b:32 * b + 32], src[2:34])
+                assert np.array_equal(packed[16 * b:16 * b + 16], src[2:18])
+                assert np.array_equal(packed[plane + 16 * b:plane + 16 * b + 16], src[18:34])
                 assert np.array_equal(packed[d_off + 2 * b:d_off + 2 * b + 2], src[0:2])
     assert rb * d == W.size
 
