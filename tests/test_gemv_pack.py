@@ -15,8 +15,10 @@ def _planes(qtype, n, d):
     nb = n // G.BLOCK[qtype][0]
     blocks = d * nb
     up = lambda v: (v + ALIGN - 1) // ALIGN * ALIGN  # noqa: E731
-    if qtype == G.TYPE_Q4_K:
-        return nb, None, None, None, up(blocks * 144)
+    if qtype == G.TYPE_Q4_K:   # header plane, then two 16-byte quant planes
+        q0 = up(blocks * 16)
+        q1 = q0 + up(blocks * 64)
+        return nb, (q0, q1), None, None, q1 + up(blocks * 64)
     if qtype == G.TYPE_Q6_K:
         plane = up(blocks * 16 * 4)
         scales_off = 3 * plane
@@ -54,15 +56,14 @@ def test_pack_roundtrip(oracle_mod, qtype, n, d):
             b = r * nb + i
             src = W[r, i * G.BLOCK[qtype][1]:(i + 1) * G.BLOCK[qtype][1]]
             if qtype == G.TYPE_Q4_K:
-                blk = packed[b * 144:(b + 1) * 144]
-                assert np.array_equal(blk[:16], src[:16])
+                q0, q1 = plane
+                assert np.array_equal(packed[16 * b:16 * b + 16], src[:16])
                 for j in range(4):
-                    for h in range(2):
-                        for t in range(4):
-                            for kk in range(4):
-                                pb = blk[16 + 32 * j + 16 * h + 4 * t + kk]
-                                ob = src[16 + 32 * j + 8 * t + 4 * h + kk]
-                                assert pb == ob
+                    s = 4 * b + j      # sub-block in the matrix
+                    assert np.array_equal(packed[q0 + 16 * s:q0 + 16 * s + 16],
+                                          src[16 + 32 * j:32 + 32 * j])
+                    assert np.array_equal(packed[q1 + 16 * s:q1 + 16 * s + 16],
+                                          src[32 + 32 * j:48 + 32 * j])
             elif qtype == G.TYPE_Q6_K:
                 vals = _q6_values(src)
                 for j in range(16):
