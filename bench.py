@@ -31,7 +31,13 @@ Method:
     reference runs its attention on one thread whatever its -j;
     cpu_baseline_head_parallel: the same arithmetic with the q heads split
     over up to 16 host threads, an upper bound only; "host" records nproc,
-    the CPU model and the C library.
+    the CPU model and the C library;
+  * gemv: every weight GEMV of one TinyLlama Q4_K_M-style token (the
+    gpu_try_matmul path: 22 x (q, k, v, o, gate, up, down) + output, 670 MB
+    of GGUF weights), graph-replayed, against the HBM roof; its CPU baseline
+    is the oracle matmul with rows split over the host threads like the
+    reference's matmul pool, and the sampled GPU outputs are checked bit for
+    bit against it.
 Prints one JSON line.
 """
 from __future__ import annotations
@@ -69,6 +75,111 @@ WORKLOADS = {
     "qwen3_prefill_512": dict(L=28, Hq=16, Hkv=8, D=128, S=2048, theta=1e6, start=0, n=512,
                               rt=1, qkn=1e-6),
 }
+
+
+# The weight GEMVs of one token of a TinyLlama-1.1B Q4_K_M-style model (the
+# matmuls picolm hands to gpu_try_matmul): per layer q, k, v, o, gate, up,
+# down (v and down Q6_K, the rest Q4_K), then the Q6_K output projection.
+GEMV_TOKEN = dict(L=22, n_embd=2048, n_ffn=5632, kv_dim=256, vocab=32000)
+GEMV_WORKLOAD = "tinyllama_q4km_gemv_token"
+Q4K, Q6K = 12, 14
+
+
+def gemv_matrices(g=GEMV_TOKEN):
+    """(qtype, n, d) of every GEMV of one token, in forward-pass order."""
+    e, f, kv = g["n_embd"], g["n_ffn"], g["kv_dim"]
+    layer = [(Q4K, e, e), (Q4K, e, kv), (Q6K, e, kv), (Q4K, e, e), (Q4K, e, f), (Q4K, e, f),
+             (Q6K, f, e)]
+    return layer * g["L"] + [(Q6K, e, g["vocab"])]
+
+
+def gemv_bytes(mats) -> int:
+    """GGUF weight bytes + fp32 x in + fp32 out, per token."""
+    total = 0
+    for qt, n, d in mats:
+        rb = n // 256 * (144 if qt == Q4K else 210)
+        total += d * rb + n * 4 + d * 4
+    return total
+
+
+def run_gemv(P, steps, warmup):
+    """One step = every weight GEMV of one token (155 launches, device
+    pointers, graph-replayed); the 670 MB of weights exceed the Infinity
+    Cache, so each step streams them from HBM."""
+    from oracle import oracle as O
+    from picolm_amd import gemv as G
+    mats = gemv_matrices()
+    rng = np.random.default_rng(155)
+    host = {}
+    for key in sorted(set(mats)):   # one random matrix per shape, one device copy per use
+        host[key] = O.random_weights(rng, *(key[0], key[1], key[2]))
+    dev, xs, outs = [], [], []
+    for qt, n, d in mats:
+        dev.append(G.QMatrix(qt, n, d, host[(qt, n, d)]))
+        xs.append(P.DeviceBuffer.from_numpy(rng.standard_normal(n).astype(np.float32)))
+        outs.append(P.DeviceBuffer(d * 4))
+    P.synchronize()
+
+    def launch():
+        for W, x, o in zip(dev, xs, outs):
+            G.matmul(o.ptr, x.ptr, W)
+
+    for _ in range(max(1, warmup)):
+        launch()
+    P.synchronize()
+    with P.Graph() as g:
+        for _ in range(steps):
+            launch()
+    g.launch()
+    P.synchronize()
+    e0, e1 = P.Event(), P.Event()
+    t0 = time.perf_counter()
+    e0.record()
+    g.launch()
+    e1.record()
+    P.synchronize()
+    wall = time.perf_counter() - t0
+    ms = e0.elapsed_ms(e1) / steps
+    algo = gemv_bytes(mats)
+    achieved = algo / (ms * 1e-3) / 1e9
+    return {
+        "us_per_token": wall * 1e6 / steps,
+        "gbs": algo / (wall / steps) / 1e9,
+        "launches_per_token": len(mats),
+        "algorithmic_bytes_per_step": algo,
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+        "_inputs": (mats, host, xs, outs),
+    }
+
+
+def cpu_baseline_gemv(res, budget_s=8.0):
+    """The oracle's matmul (bit-identical to the reference's x86-64 AVX2
+    vec_dot) on the host's cores, rows split over threads like the
+    reference's matmul pool, over a bounded sample of the token's GEMVs;
+    with a bit-exact check of the GPU outputs of the sampled GEMVs."""
+    from oracle import oracle as O
+    mats, host, xs, outs = res.pop("_inputs")
+    n_thr = min(os.cpu_count() or 1, HOST_THREADS_MAX)
+    t_total, done_bytes, checked, exact = 0.0, 0, 0, True
+    for i, (qt, n, d) in enumerate(mats):
+        if t_total >= budget_s:
+            break
+        x = xs[i].download(np.float32, (n,))
+        W = host[(qt, n, d)]
+        t0 = time.perf_counter()
+        ref = O.matmul_mt(W, x, n, d, qt, n_thr)
+        t_total += time.perf_counter() - t0
+        done_bytes += d * (n // 256) * (144 if qt == Q4K else 210) + n * 4 + d * 4
+        got = outs[i].download(np.float32, (d,))
+        exact = exact and bool(np.array_equal(got.view(np.uint32), ref.view(np.uint32)))
+        checked += 1
+    return {"cpu_baseline": {"value": done_bytes / t_total / 1e9, "unit": "GB/s",
+                             "cores": n_thr, "kind": "port",
+                             "us_per_token": t_total / done_bytes * gemv_bytes(mats) * 1e6,
+                             "sample": f"the first {checked} of {len(mats)} GEMVs of the token, "
+                                       f"oracle rows split over {n_thr} threads"},
+            "parity_bit_exact_sampled": exact, "parity_gemvs_checked": checked}
 
 
 def qkn_bytes(w) -> int:
@@ -439,10 +550,13 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="tinyllama_decode_pos2047", choices=sorted(WORKLOADS))
+    ap.add_argument("--workload", default="tinyllama_decode_pos2047",
+                    choices=sorted(WORKLOADS) + [GEMV_WORKLOAD])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the secondary prefill measurement")
+    ap.add_argument("--no-gemv", action="store_true",
+                    help="skip the weight-GEMV measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; the attention block needs no "
@@ -451,6 +565,21 @@ def main():
         sys.exit(2)
     import picolm_amd as P
     P.init(0)
+    if args.workload == GEMV_WORKLOAD:   # the weight GEMVs of one token as the headline
+        steps = max(1, args.steps // 50)
+        gres = run_gemv(P, steps, min(args.warmup, 3))
+        gextra = {} if args.no_cpu else cpu_baseline_gemv(gres)
+        gres.pop("_inputs", None)
+        line = {"metric": METRIC, "value": gres.pop("gbs"), "unit": "GB/s", "n_gpus": 1,
+                "steps": steps, "warmup": min(args.warmup, 3),
+                "ms_per_step": gres["us_per_token"] / 1e3, "higher_is_better": True,
+                "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+                "config": {"workload": GEMV_WORKLOAD, "matrices": len(gemv_matrices()),
+                           **GEMV_TOKEN, "types": "Q4_K (q,k,o,gate,up), Q6_K (v,down,output)"}}
+        line.update(gres)
+        line.update(gextra)
+        print(json.dumps(line), flush=True)
+        return
     w = WORKLOADS[args.workload]
     if "n" in w:   # a prefill workload as the headline
         res = run_prefill(P, w, max(1, args.steps // 10), args.warmup)
@@ -507,6 +636,14 @@ def main():
         pres["workload"] = "tinyllama_prefill_512"
         pres.update(pextra)
         line["prefill"] = pres
+    if not args.no_gemv:
+        # the gpu_try_matmul path: every weight GEMV of one TinyLlama token
+        gres = run_gemv(P, 10, 2)
+        gextra = {} if args.no_cpu else cpu_baseline_gemv(gres)
+        gres.pop("_inputs", None)
+        gres["workload"] = GEMV_WORKLOAD
+        gres.update(gextra)
+        line["gemv"] = gres
     print(json.dumps(line), flush=True)
 
 

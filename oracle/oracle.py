@@ -93,6 +93,8 @@ def lib() -> C.CDLL:
         L.orc_dequantize_row.restype = None
         L.orc_matmul.argtypes = [_f32p, _f32p, _u8p, C.c_int, C.c_int, C.c_int]
         L.orc_matmul.restype = C.c_int
+        L.orc_matmul_mt.argtypes = [_f32p, _f32p, _u8p, C.c_int, C.c_int, C.c_int, C.c_int]
+        L.orc_matmul_mt.restype = C.c_int
         _lib = L
     return _lib
 
@@ -328,6 +330,18 @@ def matmul(W: np.ndarray, x: np.ndarray, n: int, d: int, qtype: int) -> np.ndarr
     out = np.empty(d, np.float32)
     rc = lib().orc_matmul(out, np.ascontiguousarray(x, np.float32),
                           np.ascontiguousarray(W, np.uint8).reshape(-1), n, d, qtype)
+    if rc != 0:
+        raise ValueError(f"no fused dot product for type {qtype}")
+    return out
+
+
+def matmul_mt(W: np.ndarray, x: np.ndarray, n: int, d: int, qtype: int,
+              n_threads: int) -> np.ndarray:
+    """matmul with rows split over n_threads host threads (bit-identical)."""
+    out = np.empty(d, np.float32)
+    rc = lib().orc_matmul_mt(out, np.ascontiguousarray(x, np.float32),
+                             np.ascontiguousarray(W, np.uint8).reshape(-1), n, d, qtype,
+                             n_threads)
     if rc != 0:
         raise ValueError(f"no fused dot product for type {qtype}")
     return out

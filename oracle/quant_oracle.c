@@ -10,6 +10,7 @@
 #include "quant_oracle.h"
 
 #include <math.h>
+#include <pthread.h>
 #include <string.h>
 
 #include "attn_oracle.h"
@@ -227,5 +228,49 @@ int orc_matmul(float *out, const float *x, const void *W, int n, int d, int qtyp
     }
     const size_t rb = orc_row_bytes(qtype, n);
     for (int i = 0; i < d; i++) out[i] = dot((const uint8_t *)W + (size_t)i * rb, x, n);
+    return 0;
+}
+
+/* matmul with the rows split over n_threads pthreads, the way the reference's
+ * thread pool splits them (tensor.c:217-236); every row's dot product is the
+ * same function, so the output is bit-identical to orc_matmul. */
+typedef struct {
+    float *out;
+    const float *x;
+    const uint8_t *W;
+    int n, qtype, r0, r1;
+    size_t rb;
+} mm_task_t;
+
+static void *mm_worker(void *p) {
+    mm_task_t *t = (mm_task_t *)p;
+    orc_matmul(t->out + t->r0, t->x, t->W + (size_t)t->r0 * t->rb, t->n, t->r1 - t->r0, t->qtype);
+    return NULL;
+}
+
+int orc_matmul_mt(float *out, const float *x, const void *W, int n, int d, int qtype,
+                  int n_threads) {
+    if (orc_row_bytes(qtype, n) == 0 && qtype != ORC_TYPE_F32) return -1;
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads > 64) n_threads = 64;
+    if (n_threads > d) n_threads = d > 0 ? d : 1;
+    pthread_t th[64];
+    mm_task_t task[64];
+    const int per = d / n_threads, extra = d % n_threads;
+    int row = 0;
+    for (int t = 0; t < n_threads; t++) {
+        task[t].out = out;
+        task[t].x = x;
+        task[t].W = (const uint8_t *)W;
+        task[t].n = n;
+        task[t].qtype = qtype;
+        task[t].rb = orc_row_bytes(qtype, n);
+        task[t].r0 = row;
+        row += per + (t < extra ? 1 : 0);
+        task[t].r1 = row;
+    }
+    for (int t = 1; t < n_threads; t++) pthread_create(&th[t], NULL, mm_worker, &task[t]);
+    mm_worker(&task[0]);
+    for (int t = 1; t < n_threads; t++) pthread_join(th[t], NULL);
     return 0;
 }

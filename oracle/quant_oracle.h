@@ -56,6 +56,11 @@ void orc_dequantize_row(int qtype, const void *row, float *dst, int n);
  * for i < d.  Returns -1 for a type without a fused dot product. */
 int orc_matmul(float *out, const float *x, const void *W, int n, int d, int qtype);
 
+/* orc_matmul with the rows split over n_threads threads like the reference's
+ * matmul thread pool (tensor.c:217-236); bit-identical output. */
+int orc_matmul_mt(float *out, const float *x, const void *W, int n, int d, int qtype,
+                  int n_threads);
+
 #ifdef __cplusplus
 }
 #endif
