@@ -172,3 +172,18 @@ def test_known_answers(oracle_mod):
 def test_unsupported_type_rejected(oracle_mod):
     with pytest.raises(ValueError):
         oracle_mod.matmul(np.zeros(18, np.uint8), np.zeros(32, np.float32), 32, 1, 2)
+
+
+def test_threaded_matmul_is_bit_identical(oracle_mod):
+    """The CPU baseline's row-split matmul (the reference's pool split) gives
+    exactly the single-thread oracle's outputs."""
+    O = oracle_mod
+    rng = np.random.default_rng(21)
+    for name in ("q4_K", "q6_K", "q8_0"):
+        n, d = 512, 37
+        W = _rows(O, rng, name, n, d)
+        x = rng.standard_normal(n).astype(np.float32)
+        a = O.matmul(W, x, n, d, TYPES[name])
+        for thr in (1, 3, 8):
+            b = O.matmul_mt(W, x, n, d, TYPES[name], thr)
+            assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), (name, thr)
