@@ -547,7 +547,10 @@ __global__ __launch_bounds__(kCombineThreads) void attn_decode_combine_kernel(De
   const int nh = min(16, G - h0);
   float* out_base = a.out + (size_t)li * a.n_heads * D + (size_t)(kvh * G + h0) * D;
   const int u0 = group * a.n_split;
-  for (int idx = threadIdx.x; idx < nh * D; idx += kCombineThreads) {
+  // blockIdx.y slices the group's (head, d) elements: one element per thread,
+  // so each thread's loads make a single memory round trip
+  for (int idx = blockIdx.y * kCombineThreads + threadIdx.x; idx < nh * D;
+       idx += kCombineThreads * gridDim.y) {
     const int h = idx / D, d = idx - (idx / D) * D;
     // the loads of a chunk of splits are issued together, then merged
     float M = kNegBig, L = 0.f, O = 0.f;
@@ -729,10 +732,14 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
   if (check_hip(hipGetLastError(), "attn_decode_kernel")) return -1;
   if (n_split == 1) return 0;
   if (head_dim == 64)
-    hipLaunchKernelGGL(attn_decode_combine_kernel<64>, dim3((unsigned)n_groups), cblock, 0,
+    hipLaunchKernelGGL(attn_decode_combine_kernel<64>,
+                       dim3((unsigned)n_groups, (16 * 64 + kCombineThreads - 1) / kCombineThreads),
+                       cblock, 0,
                        c.stream, a);
   else
-    hipLaunchKernelGGL(attn_decode_combine_kernel<128>, dim3((unsigned)n_groups), cblock, 0,
+    hipLaunchKernelGGL(attn_decode_combine_kernel<128>,
+                       dim3((unsigned)n_groups, (16 * 128 + kCombineThreads - 1) / kCombineThreads),
+                       cblock, 0,
                        c.stream, a);
   return check_hip(hipGetLastError(), "attn_decode_combine_kernel");
 }
