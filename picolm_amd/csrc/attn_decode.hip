@@ -538,7 +538,12 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
 // sum_s l_s 2^(m_s-M) with M the largest m_s.
 template <int D>
 __global__ __launch_bounds__(kCombineThreads) void attn_decode_combine_kernel(DecodeArgs a) {
-  const int group = blockIdx.x;
+  // group g runs on the XCD whose L2 holds its partials: the main kernel put
+  // group g's splits on XCD g / (per_xcd / n_split), and consecutive
+  // workgroup ids go to consecutive XCDs
+  const int gpx = a.per_xcd / a.n_split;
+  const int group = (int)(blockIdx.x & 7) * gpx + (int)(blockIdx.x >> 3);
+  if (group >= a.n_units / a.n_split) return;
   const int hblk = group % a.n_hblk;
   const int kvh = (group / a.n_hblk) % a.n_kv_heads;
   const int li = group / (a.n_hblk * a.n_kv_heads);
@@ -733,12 +738,14 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
   if (n_split == 1) return 0;
   if (head_dim == 64)
     hipLaunchKernelGGL(attn_decode_combine_kernel<64>,
-                       dim3((unsigned)n_groups, (16 * 64 + kCombineThreads - 1) / kCombineThreads),
+                       dim3((unsigned)(8 * groups_per_xcd),
+                            (16 * 64 + kCombineThreads - 1) / kCombineThreads),
                        cblock, 0,
                        c.stream, a);
   else
     hipLaunchKernelGGL(attn_decode_combine_kernel<128>,
-                       dim3((unsigned)n_groups, (16 * 128 + kCombineThreads - 1) / kCombineThreads),
+                       dim3((unsigned)(8 * groups_per_xcd),
+                            (16 * 128 + kCombineThreads - 1) / kCombineThreads),
                        cblock, 0,
                        c.stream, a);
   return check_hip(hipGetLastError(), "attn_decode_combine_kernel");
