@@ -106,13 +106,13 @@ def run_gemv(P, steps, warmup):
     """One step = every weight GEMV of one token (155 launches, device
     pointers, graph-replayed); the 670 MB of weights exceed the Infinity
     Cache, so each step streams them from HBM."""
-    from oracle import oracle as O
     from picolm_amd import gemv as G
+    from picolm_amd import synth as S
     mats = gemv_matrices()
     rng = np.random.default_rng(155)
     host = {}
     for key in sorted(set(mats)):   # one random matrix per shape, one device copy per use
-        host[key] = O.random_weights(rng, *(key[0], key[1], key[2]))
+        host[key] = S.random_weights(rng, *(key[0], key[1], key[2]))
     dev, xs, outs = [], [], []
     for qt, n, d in mats:
         dev.append(G.QMatrix(qt, n, d, host[(qt, n, d)]))

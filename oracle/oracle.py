@@ -26,9 +26,9 @@ _i32p = np.ctypeslib.ndpointer(np.int32, flags="C_CONTIGUOUS")
 _u8p = np.ctypeslib.ndpointer(np.uint8, flags="C_CONTIGUOUS")
 
 # GGUF type ids (quant.h:49-63) of the GEMV path
-TYPE_F32, TYPE_F16, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 8, 12, 14
-BLOCK = {TYPE_F32: (1, 4), TYPE_F16: (1, 2), TYPE_Q8_0: (32, 34), TYPE_Q4_K: (256, 144),
-         TYPE_Q6_K: (256, 210)}   # (weights, bytes) per block
+TYPE_F32, TYPE_F16, TYPE_Q4_0, TYPE_Q8_0, TYPE_Q4_K, TYPE_Q6_K = 0, 1, 2, 8, 12, 14
+BLOCK = {TYPE_F32: (1, 4), TYPE_F16: (1, 2), TYPE_Q4_0: (32, 18), TYPE_Q8_0: (32, 34),
+         TYPE_Q4_K: (256, 144), TYPE_Q6_K: (256, 210)}   # (weights, bytes) per block
 
 
 def build(ref: bool | None = None) -> None:
@@ -40,6 +40,29 @@ def build(ref: bool | None = None) -> None:
         subprocess.run(["make", "-s", "-C", HERE, "ref"], check=True)
 
 
+class OrcMatrix(C.Structure):
+    _fields_ = [("qtype", C.c_int), ("rows", C.c_void_p)]
+
+
+class OrcLayer(C.Structure):
+    _fields_ = [("attn_norm", C.c_void_p), ("ffn_norm", C.c_void_p),
+                ("q", OrcMatrix), ("k", OrcMatrix), ("v", OrcMatrix), ("o", OrcMatrix),
+                ("gate", OrcMatrix), ("up", OrcMatrix), ("down", OrcMatrix),
+                ("q_bias", C.c_void_p), ("k_bias", C.c_void_p), ("v_bias", C.c_void_p),
+                ("o_bias", C.c_void_p), ("q_norm", C.c_void_p), ("k_norm", C.c_void_p)]
+
+
+class OrcModel(C.Structure):
+    _fields_ = [("n_layers", C.c_int), ("n_embd", C.c_int), ("n_ffn", C.c_int),
+                ("n_heads", C.c_int), ("n_kv_heads", C.c_int), ("head_dim", C.c_int),
+                ("vocab_size", C.c_int), ("max_seq_len", C.c_int), ("rope_type", C.c_int),
+                ("rms_norm_eps", C.c_float), ("token_embd", OrcMatrix),
+                ("output_norm", C.c_void_p), ("output", OrcMatrix), ("key_cache", C.c_void_p),
+                ("val_cache", C.c_void_p), ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p),
+                ("layers", C.POINTER(OrcLayer))]
+
+
+_nf = C.POINTER(C.c_float)   # nullable float*
 _lib = None
 _ref = None
 
@@ -75,7 +98,6 @@ def lib() -> C.CDLL:
         L.orc_attn_prefill.restype = C.c_int
         L.orc_attn_core.argtypes = [C.c_int] * 6 + [_f32p, _u16p, _u16p, _f32p]
         L.orc_attn_core.restype = C.c_int
-        _nf = C.POINTER(C.c_float)   # nullable
         L.orc_attn_decode_qkn.argtypes = dims + [_f32p, _f32p, _f32p, _u16p, _u16p, _f32p, _f32p,
                                                  _f32p, _nf, _nf, C.c_float]
         L.orc_attn_decode_qkn.restype = C.c_int
@@ -95,6 +117,13 @@ def lib() -> C.CDLL:
         L.orc_matmul.restype = C.c_int
         L.orc_matmul_mt.argtypes = [_f32p, _f32p, _u8p, C.c_int, C.c_int, C.c_int, C.c_int]
         L.orc_matmul_mt.restype = C.c_int
+        L.orc_silu.argtypes = [C.c_float]
+        L.orc_silu.restype = C.c_float
+        L.orc_forward.argtypes = [C.POINTER(OrcModel), C.c_int, C.c_int, _f32p, _nf, C.c_int]
+        L.orc_forward.restype = C.c_int
+        L.orc_forward_prefill.argtypes = [C.POINTER(OrcModel), _i32p, C.c_int, C.c_int, _f32p,
+                                          _nf, C.c_int]
+        L.orc_forward_prefill.restype = C.c_int
         _lib = L
     return _lib
 
@@ -143,6 +172,15 @@ def ref() -> C.CDLL:
         R.vec_dot.restype = C.c_float
         R.dequantize_row.argtypes = [_u8p, _f32p, C.c_int, C.c_int]
         R.dequantize_row.restype = None
+        R.ref_model_new_full.argtypes = [_i32p, C.c_float, C.c_float, C.POINTER(C.c_void_p),
+                                         _i32p]
+        R.ref_model_new_full.restype = C.c_void_p
+        R.ref_forward.argtypes = [C.c_void_p, C.c_int, C.c_int, _f32p, _f32p]
+        R.ref_forward.restype = None
+        R.ref_forward_prefill.argtypes = [C.c_void_p, _i32p, C.c_int, C.c_int, _f32p, _f32p]
+        R.ref_forward_prefill.restype = None
+        R.ref_silu.argtypes = [_f32p, C.c_int]
+        R.ref_silu.restype = None
         _ref = R
     return _ref
 
@@ -355,32 +393,110 @@ def dequantize(W: np.ndarray, n: int, d: int, qtype: int) -> np.ndarray:
     return out
 
 
-def random_weights(rng: np.random.Generator, qtype: int, n: int, d: int,
-                   scale_exp=(-12, -4)) -> np.ndarray:
-    """d rows of random blocks of a GGUF type: every quant byte uniform, the
-    fp16 scales finite with exponents in scale_exp (2^lo .. 2^hi magnitude),
-    Q6_K's int8 scales uniform.  Returns uint8 [d, row_bytes]."""
-    rb = row_bytes(qtype, n)
-    W = rng.integers(0, 256, size=(d, rb), dtype=np.uint8)
-    if qtype == TYPE_F32:
-        W = rng.standard_normal((d, n), dtype=np.float32).view(np.uint8).reshape(d, rb)
-        return np.ascontiguousarray(W)
-    if qtype == TYPE_F16:
-        return np.ascontiguousarray(
-            rng.standard_normal((d, n)).astype(np.float16).view(np.uint8).reshape(d, rb))
-    nb = n // BLOCK[qtype][0]
-    blocks = W.reshape(d, nb, BLOCK[qtype][1])
+# ---------------------------------------------------------------------------
+# whole forward pass (model_forward / model_forward_prefill)
+# ---------------------------------------------------------------------------
 
-    def f16_field(shape):
-        mag = np.exp2(rng.uniform(*scale_exp, size=shape)).astype(np.float16)
-        sign = rng.choice(np.array([-1, 1], np.float16), size=shape) if qtype == TYPE_Q8_0 \
-            or qtype == TYPE_Q6_K else np.float16(1)
-        return (mag * sign).astype(np.float16).view(np.uint16)
-    if qtype == TYPE_Q4_K:
-        blocks[:, :, 0:2] = f16_field((d, nb)).view(np.uint8).reshape(d, nb, 2)
-        blocks[:, :, 2:4] = f16_field((d, nb)).view(np.uint8).reshape(d, nb, 2)
-    elif qtype == TYPE_Q6_K:
-        blocks[:, :, 208:210] = f16_field((d, nb)).view(np.uint8).reshape(d, nb, 2)
-    elif qtype == TYPE_Q8_0:
-        blocks[:, :, 0:2] = f16_field((d, nb)).view(np.uint8).reshape(d, nb, 2)
-    return np.ascontiguousarray(W)
+LAYER_MATRICES = ("q", "k", "v", "o", "gate", "up", "down")
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data
+
+
+class OracleForward:
+    """The oracle's forward pass over a host model (attributes as in the
+    product's synth.SynthModel: config ints, rope_base, eps, embd_type,
+    token_embd, output_norm, output_type, output, layers), with its own
+    zero-filled host KV caches and RoPE tables."""
+
+    def __init__(self, h):
+        self.h = h
+        self.kc = np.zeros(h.cache_elems(), np.uint16)
+        self.vc = np.zeros(h.cache_elems(), np.uint16)
+        self.cos, self.sin = rope_tables(h.max_seq_len, h.head_dim, h.rope_base)
+        self.layers = (OrcLayer * h.n_layers)()
+        for li, L in enumerate(h.layers):
+            ol = self.layers[li]
+            ol.attn_norm, ol.ffn_norm = _ptr(L["attn_norm"]), _ptr(L["ffn_norm"])
+            for name in LAYER_MATRICES:
+                qt, rows = L[name]
+                setattr(ol, name, OrcMatrix(qt, rows.ctypes.data))
+            for name in ("q_bias", "k_bias", "v_bias", "o_bias", "q_norm", "k_norm"):
+                setattr(ol, name, _ptr(L[name]))
+        self.m = OrcModel(h.n_layers, h.n_embd, h.n_ffn, h.n_heads, h.n_kv_heads, h.head_dim,
+                          h.vocab_size, h.max_seq_len, h.rope_type, h.eps,
+                          OrcMatrix(h.embd_type, h.token_embd.ctypes.data),
+                          h.output_norm.ctypes.data, OrcMatrix(h.output_type, h.output.ctypes.data),
+                          self.kc.ctypes.data, self.vc.ctypes.data, self.cos.ctypes.data,
+                          self.sin.ctypes.data, C.cast(self.layers, C.POINTER(OrcLayer)))
+
+    def forward(self, token: int, pos: int, n_threads: int = 1):
+        logits = np.empty(self.h.vocab_size, np.float32)
+        x = np.empty(self.h.n_embd, np.float32)
+        rc = lib().orc_forward(C.byref(self.m), token, pos, logits,
+                               x.ctypes.data_as(_nf), n_threads)
+        if rc != 0:
+            raise ValueError("orc_forward rejected its arguments")
+        return logits, x
+
+    def prefill(self, tokens, start_pos: int, n_threads: int = 1):
+        t = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(self.h.vocab_size, np.float32)
+        x = np.empty(self.h.n_embd, np.float32)
+        rc = lib().orc_forward_prefill(C.byref(self.m), t, len(t), start_pos, logits,
+                                       x.ctypes.data_as(_nf), n_threads)
+        if rc != 0:
+            raise ValueError("orc_forward_prefill rejected its arguments")
+        return logits, x
+
+
+class RefForward:
+    """The reference's own model_forward / model_forward_prefill on the same
+    host buffers (oracle/_ref, ref_harness.c ref_model_new_full)."""
+
+    def __init__(self, h):
+        R = ref()
+        self.h = h
+        cfg = np.array([h.n_layers, h.n_embd, h.n_ffn, h.n_heads, h.n_kv_heads, h.head_dim,
+                        h.vocab_size, h.max_seq_len, h.rope_type], np.int32)
+        ptrs = [h.token_embd, h.output_norm, h.output]
+        types = [h.embd_type, TYPE_F32, h.output_type]
+        for L in h.layers:
+            ptrs += [L["attn_norm"], L["q"][1], L["k"][1], L["v"][1], L["o"][1], L["q_norm"],
+                     L["k_norm"], L["ffn_norm"], L["gate"][1], L["down"][1], L["up"][1],
+                     L["q_bias"], L["k_bias"], L["v_bias"], L["o_bias"]]
+            types += [TYPE_F32, L["q"][0], L["k"][0], L["v"][0], L["o"][0], TYPE_F32, TYPE_F32,
+                      TYPE_F32, L["gate"][0], L["down"][0], L["up"][0], TYPE_F32, TYPE_F32,
+                      TYPE_F32, TYPE_F32]
+        self._ptrs = (C.c_void_p * len(ptrs))(*[_ptr(a) for a in ptrs])
+        self.handle = R.ref_model_new_full(cfg, h.rope_base, h.eps, self._ptrs,
+                                           np.array(types, np.int32))
+        if not self.handle:
+            raise MemoryError("ref_model_new_full failed")
+        p = [C.c_void_p() for _ in range(4)]
+        R.ref_cache_ptrs(self.handle, *[C.byref(x) for x in p])
+        n = h.cache_elems()
+        self.kc = np.ctypeslib.as_array(C.cast(p[0], C.POINTER(C.c_uint16)), (n,))
+        self.vc = np.ctypeslib.as_array(C.cast(p[1], C.POINTER(C.c_uint16)), (n,))
+
+    def forward(self, token: int, pos: int):
+        logits = np.empty(self.h.vocab_size, np.float32)
+        x = np.empty(self.h.n_embd, np.float32)
+        ref().ref_forward(self.handle, token, pos, logits, x)
+        return logits, x
+
+    def prefill(self, tokens, start_pos: int):
+        t = np.ascontiguousarray(tokens, np.int32)
+        logits = np.empty(self.h.vocab_size, np.float32)
+        x = np.empty(self.h.n_embd, np.float32)
+        ref().ref_forward_prefill(self.handle, t, len(t), start_pos, logits, x)
+        return logits, x
+
+    def close(self):
+        if self.handle:
+            ref().ref_model_free(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        self.close()

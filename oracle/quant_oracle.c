@@ -29,6 +29,7 @@ size_t orc_row_bytes(int qtype, int n) {
     switch (qtype) {
         case ORC_TYPE_F32: return (size_t)n * 4;
         case ORC_TYPE_F16: return (size_t)n * 2;
+        case ORC_TYPE_Q4_0: return (size_t)(n / 32) * 18;
         case ORC_TYPE_Q8_0: return (size_t)(n / 32) * 34;
         case ORC_TYPE_Q4_K: return (size_t)(n / 256) * 144;
         case ORC_TYPE_Q6_K: return (size_t)(n / 256) * 210;
@@ -174,6 +175,15 @@ void orc_dequantize_row(int qtype, const void *row, float *dst, int n) {
         case ORC_TYPE_F16:
             for (int i = 0; i < n; i++) dst[i] = orc_f16_to_f32(rd16(blk + 2 * i));
             break;
+        case ORC_TYPE_Q4_0: /* quant.c:236-252: {fp16 d, qs[16]}, low nibbles first */
+            for (int i = 0; i < n / 32; i++, blk += 18) {
+                const float d = orc_f16_to_f32(rd16(blk));
+                for (int j = 0; j < 32; j++) {
+                    const int nib = j < 16 ? (blk[2 + j] & 0x0F) : (blk[2 + j - 16] >> 4);
+                    dst[32 * i + j] = d * ((float)nib - 8.0f);
+                }
+            }
+            break;
         case ORC_TYPE_Q8_0:
             for (int i = 0; i < n / 32; i++, blk += 34) {
                 const float d = orc_f16_to_f32(rd16(blk));
@@ -250,7 +260,9 @@ static void *mm_worker(void *p) {
 
 int orc_matmul_mt(float *out, const float *x, const void *W, int n, int d, int qtype,
                   int n_threads) {
-    if (orc_row_bytes(qtype, n) == 0 && qtype != ORC_TYPE_F32) return -1;
+    if (qtype != ORC_TYPE_Q4_K && qtype != ORC_TYPE_Q6_K && qtype != ORC_TYPE_Q8_0 &&
+        qtype != ORC_TYPE_F32)
+        return -1; /* the types orc_matmul has a fused dot for */
     if (n_threads < 1) n_threads = 1;
     if (n_threads > 64) n_threads = 64;
     if (n_threads > d) n_threads = d > 0 ? d : 1;

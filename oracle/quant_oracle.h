@@ -33,6 +33,7 @@ extern "C" {
 /* GGUF type ids, quant.h:49-63 */
 #define ORC_TYPE_F32 0
 #define ORC_TYPE_F16 1
+#define ORC_TYPE_Q4_0 2
 #define ORC_TYPE_Q8_0 8
 #define ORC_TYPE_Q4_K 12
 #define ORC_TYPE_Q6_K 14
@@ -49,7 +50,7 @@ float orc_vec_dot_q8_0(const void *row, const float *x, int n);
 /* quant.c:340-352 (AVX2 path) */
 float orc_vec_dot_f32(const void *row, const float *x, int n);
 
-/* quant.c:96-128, 193-222, 224-234 */
+/* quant.c:96-128, 193-262 (Q4_K, Q6_K, Q8_0, Q4_0, F16, F32) */
 void orc_dequantize_row(int qtype, const void *row, float *dst, int n);
 
 /* tensor.c:200-215 with quant.c:713-730's dispatch: out[i] = dot(row i, x)

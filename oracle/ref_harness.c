@@ -302,3 +302,86 @@ void ref_set_qk_norm(void *hv, int layer, const float *q_w, const float *k_w, fl
 void ref_rmsnorm(float *out, const float *x, const float *w, int size, float eps) {
     rmsnorm(out, x, w, size, eps);
 }
+
+/* A model assembled from caller-owned buffers, for pinning the oracle's
+ * whole forward pass against model_forward / model_forward_prefill.
+ * cfg = {n_layers, n_embd, n_ffn, n_heads, n_kv_heads, head_dim, vocab_size,
+ * max_seq_len, rope_type}.  ptrs/types hold, in this order, token_embd,
+ * output_norm, output, then per layer attn_norm, attn_q, attn_k, attn_v,
+ * attn_output, attn_q_norm, attn_k_norm, ffn_norm, ffn_gate, ffn_down,
+ * ffn_up, attn_q_b, attn_k_b, attn_v_b, attn_output_b (NULL = absent).
+ * allocate_run_state then dequantizes norms and biases and builds the RoPE
+ * tables exactly as model_load does (model.c:721-730). */
+#define REF_LAYER_SLOTS 15
+void *ref_model_new_full(const int *cfg, float rope_base, float eps, const void *const *ptrs,
+                         const int *types) {
+    if (cfg[0] < 1 || cfg[0] > MAX_LAYERS) return NULL;
+    ref_handle *h = (ref_handle *)calloc(1, sizeof(ref_handle));
+    if (!h) return NULL;
+    model_t *m = &h->m;
+    model_config_t *c = &m->config;
+    c->n_layers = cfg[0];
+    c->n_embd = cfg[1];
+    c->n_ffn = cfg[2];
+    c->n_heads = cfg[3];
+    c->n_kv_heads = cfg[4];
+    c->head_dim = cfg[5];
+    c->vocab_size = cfg[6];
+    c->max_seq_len = cfg[7];
+    c->rope_type = (rope_type_t)cfg[8];
+    c->rope_freq_base = rope_base;
+    c->rms_norm_eps = eps;
+    c->weight_type = GGUF_TYPE_F32;
+    model_weights_t *w = &m->weights;
+    w->token_embd = ptrs[0];
+    w->type_token_embd = (gguf_type_t)types[0];
+    w->output_norm = ptrs[1];
+    w->type_output_norm = (gguf_type_t)types[1];
+    w->output = ptrs[2];
+    w->type_output = (gguf_type_t)types[2];
+    for (int l = 0; l < c->n_layers; l++) {
+        const void *const *p = ptrs + 3 + (size_t)l * REF_LAYER_SLOTS;
+        const int *t = types + 3 + (size_t)l * REF_LAYER_SLOTS;
+        layer_weights_t *lw = &w->layers[l];
+        lw->attn_norm = p[0];     lw->type_attn_norm = (gguf_type_t)t[0];
+        lw->attn_q = p[1];        lw->type_attn_q = (gguf_type_t)t[1];
+        lw->attn_k = p[2];        lw->type_attn_k = (gguf_type_t)t[2];
+        lw->attn_v = p[3];        lw->type_attn_v = (gguf_type_t)t[3];
+        lw->attn_output = p[4];   lw->type_attn_output = (gguf_type_t)t[4];
+        lw->attn_q_norm = p[5];   lw->type_attn_q_norm = (gguf_type_t)t[5];
+        lw->attn_k_norm = p[6];   lw->type_attn_k_norm = (gguf_type_t)t[6];
+        lw->ffn_norm = p[7];      lw->type_ffn_norm = (gguf_type_t)t[7];
+        lw->ffn_gate = p[8];      lw->type_ffn_gate = (gguf_type_t)t[8];
+        lw->ffn_down = p[9];      lw->type_ffn_down = (gguf_type_t)t[9];
+        lw->ffn_up = p[10];       lw->type_ffn_up = (gguf_type_t)t[10];
+        lw->attn_q_b = p[11];     lw->type_attn_q_b = (gguf_type_t)t[11];
+        lw->attn_k_b = p[12];     lw->type_attn_k_b = (gguf_type_t)t[12];
+        lw->attn_v_b = p[13];     lw->type_attn_v_b = (gguf_type_t)t[13];
+        lw->attn_output_b = p[14]; lw->type_attn_output_b = (gguf_type_t)t[14];
+    }
+    if (allocate_run_state(m) != 0) {
+        free(h);
+        return NULL;
+    }
+    return h;
+}
+
+/* model_forward (model.c:742-744): logits and the final normalised residual. */
+void ref_forward(void *hv, int token, int pos, float *logits, float *x_out) {
+    ref_handle *h = (ref_handle *)hv;
+    float *lg = model_forward(&h->m, token, pos);
+    memcpy(logits, lg, (size_t)h->m.config.vocab_size * sizeof(float));
+    memcpy(x_out, h->m.state.x, (size_t)h->m.config.n_embd * sizeof(float));
+}
+
+/* model_forward_prefill (model.c:939-1144). */
+void ref_forward_prefill(void *hv, const int *tokens, int n_tokens, int start_pos,
+                         float *logits, float *x_out) {
+    ref_handle *h = (ref_handle *)hv;
+    model_forward_prefill(&h->m, tokens, n_tokens, start_pos);
+    memcpy(logits, h->m.state.logits, (size_t)h->m.config.vocab_size * sizeof(float));
+    memcpy(x_out, h->m.state.x, (size_t)h->m.config.n_embd * sizeof(float));
+}
+
+/* tensor.c:605-609 over an array (silu in place). */
+void ref_silu(float *x, int n) { silu(x, n); }

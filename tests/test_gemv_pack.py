@@ -7,6 +7,7 @@ import pytest
 
 import picolm_amd as P
 from picolm_amd import gemv as G
+from picolm_amd import synth as S
 
 ALIGN = 256
 
@@ -46,7 +47,7 @@ def _q6_values(blk):
                                        (G.TYPE_Q8_0, 96, 9), (G.TYPE_Q8_0, 2048, 2)])
 def test_pack_roundtrip(oracle_mod, qtype, n, d):
     rng = np.random.default_rng(n + d)
-    W = oracle_mod.random_weights(rng, qtype, n, d)
+    W = S.random_weights(rng, qtype, n, d)
     packed = G.pack_host(qtype, n, d, W)
     nb, plane, scales_off, d_off, total = _planes(qtype, n, d)
     assert packed.size == total == P.lib.plh_gemv_packed_bytes(qtype, n, d)

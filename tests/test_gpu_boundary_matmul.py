@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 
 from conftest import ROOT
+from picolm_amd import synth as S
 
 pytestmark = pytest.mark.gpu
 
@@ -39,7 +40,7 @@ def run(tmp_path, O, dims, types, type_out, seed, env_extra=None):
         np.array(dims, np.int32).tofile(f)
         np.array([t for row in types for t in row] + [type_out], np.int32).tofile(f)
         for qt, n, d in mats:
-            W = O.random_weights(rng, qt, n, d)
+            W = S.random_weights(rng, qt, n, d)
             x = rng.standard_normal(n).astype(np.float32)
             W.tofile(f)
             x.tofile(f)

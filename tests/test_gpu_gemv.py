@@ -12,6 +12,7 @@ import pytest
 
 import picolm_amd as P
 from picolm_amd import gemv as G
+from picolm_amd import synth as S
 
 pytestmark = pytest.mark.gpu
 
@@ -30,7 +31,7 @@ def test_gemv_bit_exact(gpu, oracle_mod, qtype, n, d):
     O = oracle_mod
     rng = np.random.default_rng(n * 7 + d + qtype)
     print(f"[case] gemv type {qtype} n {n} d {d}", flush=True)
-    W = O.random_weights(rng, qtype, n, d)
+    W = S.random_weights(rng, qtype, n, d)
     Wd = G.QMatrix(qtype, n, d, W)
     for trial, xs in enumerate((1.0, 1e-3, 40.0)):
         x = (rng.standard_normal(n) * xs).astype(np.float32)
@@ -52,7 +53,7 @@ def test_gemv_repeat_and_special_blocks(gpu, oracle_mod):
     rng = np.random.default_rng(5)
     n, d = 512, 64
     for qtype in (G.TYPE_Q4_K, G.TYPE_Q6_K, G.TYPE_Q8_0):
-        W = O.random_weights(rng, qtype, n, d)
+        W = S.random_weights(rng, qtype, n, d)
         rb = G.row_bytes(qtype, n)
         blocks = W.reshape(d, -1, G.BLOCK[qtype][1])
         if qtype == G.TYPE_Q4_K:

@@ -15,6 +15,7 @@ import numpy as np
 import pytest
 
 from conftest import needs_ref
+from picolm_amd import synth as S
 
 TYPES = {"q4_K": 12, "q6_K": 14, "q8_0": 8, "f32": 0}
 ROW_LENS = {"q4_K": [256, 512, 2048, 5632], "q6_K": [256, 2048, 5632],
@@ -22,7 +23,7 @@ ROW_LENS = {"q4_K": [256, 512, 2048, 5632], "q6_K": [256, 2048, 5632],
 
 
 def _rows(O, rng, name, n, d, scale_exp=(-12, -4)):
-    return O.random_weights(rng, TYPES[name], n, d, scale_exp)
+    return S.random_weights(rng, TYPES[name], n, d, scale_exp)
 
 
 @needs_ref
