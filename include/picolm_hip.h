@@ -41,6 +41,10 @@ int plh_free(void *dptr);
 int plh_memcpy_htod(void *dst, const void *src, size_t bytes);
 int plh_memcpy_dtoh(void *dst, const void *src, size_t bytes);
 int plh_memcpy_dtod(void *dst, const void *src, size_t bytes);
+/* height rows of width bytes, row i from src + i*spitch to dst + i*dpitch
+ * (blocking): the per-layer rows of one position in one call. */
+int plh_memcpy2d_dtoh(void *dst, size_t dpitch, const void *src, size_t spitch,
+                      size_t width, size_t height);
 int plh_memset(void *dst, int value, size_t bytes);
 int plh_synchronize(void);
 
@@ -161,6 +165,80 @@ size_t plh_gemv_packed_bytes(int qtype, int n, int d);
 int plh_gemv_upload(int qtype, int n, int d, const void *host_rows, void *dev);
 int plh_gemv_pack_host(int qtype, int n, int d, const void *host_rows, void *host_packed);
 int plh_gemv(int qtype, int n, int d, const void *dev, const float *x, float *out);
+/* plh_gemv with the forward pass's epilogues, in the reference's order
+ * (matmul_bias tensor.c:256-264, silu + elemwise_mul tensor.c:605-633,
+ * vec_add tensor.c:635-657):
+ *     v = vec_dot(row i, x)
+ *     v = v + bias[i]        if bias            (matmul_bias)
+ *     v = v + 0.0f           if bias_zero       (matmul_bias with a zeroed bias)
+ *     v = silu(gate[i]) * v  if gate            (hb = silu(hb) * hb2)
+ *     out[i] = resid[i] + v  if resid, else v   (x += ...)
+ * gate and resid may alias out (read before the row is written).  All but
+ * silu's expf are bit-identical to the reference. */
+int plh_gemv_ex(int qtype, int n, int d, const void *dev, const float *x, float *out,
+                const float *bias, int bias_zero, const float *gate, const float *resid);
+
+/* ---- forward pass (model_forward_ex, model.c:746-925) --------------------- */
+/* tensor.c:425-492 rmsnorm, bit-identical to the reference's x86-64 AVX2
+ * build: out[i] = (x[i] * (1/sqrtf(sum(x^2)/n + eps))) * w[i], the sum in the
+ * reference's eight-lane order.  Device pointers; out may alias x;
+ * n <= 12288. */
+int plh_rmsnorm(const float *x, const float *w, float *out, int n, float eps);
+/* quant.c:265-276 dequantize_row on the device for F32, F16, Q4_0, Q8_0,
+ * Q4_K and Q6_K rows (row: device pointer to the GGUF bytes), bit-identical. */
+int plh_dequantize_row(int qtype, const void *row, float *out, int n);
+
+/* One weight matrix of the forward pass: GGUF type id (Q4_K, Q6_K, Q8_0) and
+ * its packed device copy (plh_gemv_upload). */
+typedef struct {
+    int qtype;
+    const void *w;
+} plh_matrix;
+
+/* One layer (model.h:40-74 and the run state's dequantized copies,
+ * model.c:644-707); fp32 device arrays. */
+typedef struct {
+    const float *attn_norm; /* [n_embd] */
+    const float *ffn_norm;  /* [n_embd] */
+    plh_matrix q, k, v, o, gate, up, down;
+    const float *q_bias;    /* [n_heads*head_dim]; NULL adds zeros (model.c:781-782) */
+    const float *k_bias;    /* [kv_dim] or NULL (model.c:792-795) */
+    const float *v_bias;    /* [kv_dim] or NULL (model.c:797-800) */
+    const float *o_bias;    /* [n_embd]; NULL adds zeros (model.c:895-896) */
+    const float *q_norm;    /* [head_dim] Qwen3 QK-norm weights, or NULL */
+    const float *k_norm;    /* [head_dim]; NULL exactly when q_norm is */
+} plh_layer;
+
+/* The model as plh_forward reads it (model.h:22-120 and model.c:545-556);
+ * all pointers but `layers` are device memory. */
+typedef struct {
+    int n_layers, n_embd, n_ffn, n_heads, n_kv_heads, head_dim, vocab_size,
+        max_seq_len, rope_type;
+    float rms_norm_eps;
+    int embd_type;            /* GGUF type of token_embd */
+    const void *token_embd;   /* [vocab_size] GGUF rows of n_embd, as in the file */
+    const float *output_norm; /* [n_embd] */
+    plh_matrix output;        /* [vocab_size] x n_embd */
+    uint16_t *key_cache;      /* the KV-cache layout above */
+    uint16_t *val_cache;
+    const float *rope_cos;    /* [max_seq_len][head_dim/2] */
+    const float *rope_sin;
+    const plh_layer *layers;  /* HOST array [n_layers] */
+} plh_model;
+
+/* Bytes of the activation workspace plh_forward needs for this model. */
+size_t plh_forward_workspace_bytes(const plh_model *m);
+/* Replaces model_forward_ex(m, token, pos, n_layers) (model.c:746-925): the
+ * embedding row of `token`, every layer (rmsnorm, q/k/v projections and
+ * biases, QK-norm if present, RoPE, FP16 append of row pos, attention over
+ * rows 0..pos, output projection + bias + residual, rmsnorm, gate/up, silu,
+ * down + residual), the final rmsnorm and the output projection into
+ * logits [vocab_size] (device).  x_out (device, may be NULL) receives the
+ * final normalised residual (the reference's s->x).  workspace: device,
+ * plh_forward_workspace_bytes(m).  Head dims 64 / 128; matrices Q4_K, Q6_K
+ * or Q8_0.  Queued on the library stream. */
+int plh_forward(const plh_model *m, int token, int pos, void *workspace, float *logits,
+                float *x_out);
 
 /* Tuning knobs (bench sweeps).  key 1: decode target workgroups per launch
  * (0 = default); key 2: decode contexts of at most this many positions are

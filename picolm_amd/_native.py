@@ -31,6 +31,30 @@ _vp = C.c_void_p
 _i = C.c_int
 _sz = C.c_size_t
 
+
+# plh_model and its parts (include/picolm_hip.h)
+class PlhMatrix(C.Structure):
+    _fields_ = [("qtype", C.c_int), ("w", _vp)]
+
+
+class PlhLayer(C.Structure):
+    _fields_ = [("attn_norm", _vp), ("ffn_norm", _vp),
+                ("q", PlhMatrix), ("k", PlhMatrix), ("v", PlhMatrix), ("o", PlhMatrix),
+                ("gate", PlhMatrix), ("up", PlhMatrix), ("down", PlhMatrix),
+                ("q_bias", _vp), ("k_bias", _vp), ("v_bias", _vp), ("o_bias", _vp),
+                ("q_norm", _vp), ("k_norm", _vp)]
+
+
+class PlhModel(C.Structure):
+    _fields_ = [("n_layers", C.c_int), ("n_embd", C.c_int), ("n_ffn", C.c_int),
+                ("n_heads", C.c_int), ("n_kv_heads", C.c_int), ("head_dim", C.c_int),
+                ("vocab_size", C.c_int), ("max_seq_len", C.c_int), ("rope_type", C.c_int),
+                ("rms_norm_eps", C.c_float), ("embd_type", C.c_int), ("token_embd", _vp),
+                ("output_norm", _vp), ("output", PlhMatrix), ("key_cache", _vp),
+                ("val_cache", _vp), ("rope_cos", _vp), ("rope_sin", _vp),
+                ("layers", C.POINTER(PlhLayer))]
+
+
 _SIGS = {
     # lifecycle
     "plh_init": (_i, [_i]),
@@ -44,6 +68,7 @@ _SIGS = {
     "plh_memcpy_htod": (_i, [_vp, _vp, _sz]),
     "plh_memcpy_dtoh": (_i, [_vp, _vp, _sz]),
     "plh_memcpy_dtod": (_i, [_vp, _vp, _sz]),
+    "plh_memcpy2d_dtoh": (_i, [_vp, _sz, _vp, _sz, _sz, _sz]),
     "plh_memset": (_i, [_vp, _i, _sz]),
     "plh_synchronize": (_i, []),
     # events
@@ -70,6 +95,12 @@ _SIGS = {
     "plh_gemv_upload": (_i, [_i, _i, _i, _vp, _vp]),
     "plh_gemv_pack_host": (_i, [_i, _i, _i, _vp, _vp]),
     "plh_gemv": (_i, [_i, _i, _i, _vp, _vp, _vp]),
+    "plh_gemv_ex": (_i, [_i, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _vp]),
+    # forward pass
+    "plh_rmsnorm": (_i, [_vp, _vp, _vp, _i, C.c_float]),
+    "plh_dequantize_row": (_i, [_i, _vp, _vp, _i]),
+    "plh_forward_workspace_bytes": (_sz, [C.POINTER(PlhModel)]),
+    "plh_forward": (_i, [C.POINTER(PlhModel), _i, _i, _vp, _vp, _vp]),
     "plh_set_tuning": (_i, [_i, _i]),
 }
 

@@ -158,7 +158,19 @@ struct GemvArgs {
   int terms;            // chained terms per row
   int tpitch;           // LDS pitch of a row's terms
   uint32_t off0, off1, off2, scales_off, d_off;  // plane offsets (bytes)
+  // Epilogue, in the reference's order (tensor.c:256-264, 605-657):
+  // v = dot; v = v + bias[i] (bias_mode 1) or v + 0.0f (bias_mode 2, a
+  // zero-filled bias); v = silu(gate[i]) * v; v = resid[i] + v.
+  const float* bias;
+  const float* gate;
+  const float* resid;
+  int bias_mode;
 };
+
+// tensor.c:605-609: x / (1 + expf(-x)).  expf is the device library's, not
+// glibc's (which is not correctly rounded), so results can differ from the
+// host's in the last place.
+__device__ __forceinline__ float silu(float x) { return x / (1.0f + expf(-x)); }
 
 __device__ __forceinline__ float hsum8(const float (&v)[8]) {
   const float a0 = v[0] + v[4], a1 = v[1] + v[5], a2 = v[2] + v[6], a3 = v[3] + v[7];
@@ -454,7 +466,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
       }
     }
     for (int s = full; s < a.terms; ++s) sumf = sumf + t[s];
-    a.out[r0 + rr] = sumf;
+    const int r = r0 + rr;
+    if (a.bias_mode == 1) sumf = sumf + a.bias[r];
+    if (a.bias_mode == 2) sumf = sumf + 0.0f;
+    if (a.gate) sumf = silu(a.gate[r]) * sumf;
+    if (a.resid) sumf = a.resid[r] + sumf;
+    a.out[r] = sumf;
   }
 }
 
@@ -512,6 +529,11 @@ int plh_gemv_upload(int qtype, int n, int d, const void* host_rows, void* dev) {
 }
 
 int plh_gemv(int qtype, int n, int d, const void* dev, const float* x, float* out) {
+  return plh_gemv_ex(qtype, n, d, dev, x, out, nullptr, 0, nullptr, nullptr);
+}
+
+int plh_gemv_ex(int qtype, int n, int d, const void* dev, const float* x, float* out,
+                const float* bias, int bias_zero, const float* gate, const float* resid) {
   Layout L;
   if (!make_layout(qtype, n, d, L)) {
     set_error("plh_gemv: no GEMV for type %d with n=%d d=%d", qtype, n, d);
@@ -519,6 +541,10 @@ int plh_gemv(int qtype, int n, int d, const void* dev, const float* x, float* ou
   }
   if (!dev || !x || !out) {
     set_error("plh_gemv: null pointer");
+    return -1;
+  }
+  if (bias && bias_zero) {
+    set_error("plh_gemv_ex: a bias and bias_zero together");
     return -1;
   }
   Context& c = ctx();
@@ -546,6 +572,10 @@ int plh_gemv(int qtype, int n, int d, const void* dev, const float* x, float* ou
   a.off2 = (uint32_t)L.off[2];
   a.scales_off = (uint32_t)L.scales_off;
   a.d_off = (uint32_t)L.d_off;
+  a.bias = bias;
+  a.gate = gate;
+  a.resid = resid;
+  a.bias_mode = bias ? 1 : (bias_zero ? 2 : 0);
   // rows per thread: the largest of 4, 2, 1 that still gives at least 0.6
   // workgroups per CU and keeps the workgroup's terms within 64 KiB of LDS
   // (measured on the TinyLlama and output-projection shapes: more rows in

@@ -129,6 +129,16 @@ int plh_memcpy_dtoh(void* dst, const void* src, size_t bytes) {
   return check_hip(hipStreamSynchronize(g_ctx.stream), "dtoh sync");
 }
 
+int plh_memcpy2d_dtoh(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width,
+                      size_t height) {
+  if (height == 0 || width == 0) return 0;
+  if (check_hip(hipMemcpy2DAsync(dst, dpitch, src, spitch, width, height, hipMemcpyDeviceToHost,
+                                 g_ctx.stream),
+                "dtoh 2d"))
+    return -1;
+  return check_hip(hipStreamSynchronize(g_ctx.stream), "dtoh 2d sync");
+}
+
 int plh_memcpy_dtod(void* dst, const void* src, size_t bytes) {
   return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_ctx.stream), "dtod");
 }

@@ -1,0 +1,201 @@
+"""The device forward pass (plh_forward, picolm's model_forward) and its new
+pieces against the oracle, on the GPU.
+
+Bit-exact: rmsnorm (every size class: vector part, tail, odd lengths,
+in-place), embedding dequantisation of every supported type, the GEMV
+epilogues (bias, zero bias, residual), and the layer-0 KV rows of every
+forward step (embedding -> rmsnorm -> GEMV -> RoPE -> fp16 involve no
+transcendental).  Within tolerance (the device's expf in silu and the
+split-K exp2 softmax differ from glibc's expf in the last bits): silu * up
+per element, and the logits / final residual / later-layer KV rows of whole
+forward passes over LLaMA- and Qwen-shaped models, with the greedy token
+checked where the oracle's top two logits are apart.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from picolm_amd import synth as S
+
+pytestmark = pytest.mark.gpu
+
+Q4K, Q6K, Q8, Q40, F32, F16 = (S.TYPE_Q4_K, S.TYPE_Q6_K, S.TYPE_Q8_0, S.TYPE_Q4_0,
+                               S.TYPE_F32, S.TYPE_F16)
+
+
+def bits(a):
+    return np.ascontiguousarray(a, np.float32).view(np.uint32)
+
+
+@pytest.mark.parametrize("n", [1, 7, 8, 64, 100, 2048, 2051, 5632, 12288])
+def test_rmsnorm_bit_exact(gpu, oracle_mod, n):
+    P, O = gpu, oracle_mod
+    rng = np.random.default_rng(n)
+    for scale, eps in ((1.0, 1e-5), (1e-3, 1e-6), (300.0, 1e-5)):
+        x = (rng.standard_normal(n) * scale).astype(np.float32)
+        w = rng.uniform(0.5, 1.5, n).astype(np.float32)
+        dx, dw, do = P.DeviceBuffer.from_numpy(x), P.DeviceBuffer.from_numpy(w), P.DeviceBuffer(4 * n)
+        P.check(P.lib.plh_rmsnorm(dx.ptr, dw.ptr, do.ptr, n, C.c_float(eps)), "plh_rmsnorm")
+        want = O.rmsnorm(x, w, eps)
+        assert np.array_equal(bits(do.download(np.float32, (n,))), bits(want)), (n, scale)
+        # in place
+        P.check(P.lib.plh_rmsnorm(dx.ptr, dw.ptr, dx.ptr, n, C.c_float(eps)), "plh_rmsnorm")
+        assert np.array_equal(bits(dx.download(np.float32, (n,))), bits(want))
+
+
+def test_rmsnorm_rejects_oversize(gpu):
+    P = gpu
+    b = P.DeviceBuffer(4 * 16)
+    assert P.lib.plh_rmsnorm(b.ptr, b.ptr, b.ptr, 12289, C.c_float(1e-5)) == -1
+    assert P.lib.plh_rmsnorm(b.ptr, b.ptr, b.ptr, 0, C.c_float(1e-5)) == -1
+
+
+@pytest.mark.parametrize("qtype", [F32, F16, Q40, Q8, Q4K, Q6K])
+def test_dequantize_row_bit_exact(gpu, oracle_mod, qtype):
+    P, O = gpu, oracle_mod
+    rng = np.random.default_rng(qtype)
+    for n in (256, 2048, 5632):
+        for scale_exp in ((-14, -6), (2, 10)):
+            rows = S.random_weights(rng, qtype, n, 3, scale_exp)
+            dr = P.DeviceBuffer.from_numpy(rows)
+            out = P.DeviceBuffer(4 * n)
+            for r in range(3):
+                rb = rows.shape[1]
+                P.check(P.lib.plh_dequantize_row(qtype, dr.ptr + r * rb, out.ptr, n),
+                        "plh_dequantize_row")
+                want = O.dequantize(rows[r], n, 1, qtype)[0]
+                got = out.download(np.float32, (n,))
+                assert np.array_equal(bits(got), bits(want)), (qtype, n, r)
+
+
+def test_dequantize_row_rejects(gpu):
+    P = gpu
+    b = P.DeviceBuffer(4096)
+    assert P.lib.plh_dequantize_row(Q4K, b.ptr, b.ptr, 100) == -1      # not whole blocks
+    assert P.lib.plh_dequantize_row(11, b.ptr, b.ptr, 256) == -1       # Q3_K: no kernel
+
+
+@pytest.mark.parametrize("qtype,n,d", [(Q4K, 2048, 2048), (Q6K, 5632, 2048), (Q8, 2048, 256)])
+def test_gemv_epilogues(gpu, oracle_mod, qtype, n, d):
+    P, O = gpu, oracle_mod
+    rng = np.random.default_rng(n + d)
+    W = S.random_weights(rng, qtype, n, d, S.unit_scale_exp(qtype, n))
+    x = rng.standard_normal(n).astype(np.float32)
+    bias = rng.standard_normal(d).astype(np.float32)
+    resid = rng.standard_normal(d).astype(np.float32)
+    gate = (rng.standard_normal(d) * 4).astype(np.float32)
+    dot = O.matmul(W, x, n, d, qtype)
+    G = P.QMatrix(qtype, n, d, W)
+    dx = P.DeviceBuffer.from_numpy(x)
+    db, dr = P.DeviceBuffer.from_numpy(bias), P.DeviceBuffer.from_numpy(resid)
+    out = P.DeviceBuffer(4 * d)
+    vp = C.c_void_p
+
+    def run(b, bz, r, o):
+        """plh_gemv_ex into buffer o; returns o's contents."""
+        P.check(P.lib.plh_gemv_ex(qtype, n, d, vp(G.ptr), vp(dx.ptr), vp(o.ptr),
+                                  b and vp(b.ptr), bz, None, r and vp(r.ptr)), "plh_gemv_ex")
+        return o.download(np.float32, (d,))
+
+    assert np.array_equal(bits(run(None, 0, None, out)), bits(dot))
+    assert np.array_equal(bits(run(db, 0, None, out)), bits(dot + bias))
+    assert np.array_equal(bits(run(None, 1, None, out)), bits(dot + np.float32(0.0)))
+    # x = x + (dot + bias), in place on the residual
+    assert np.array_equal(bits(run(db, 0, dr, dr)), bits(resid + (dot + bias)))
+    # hb = silu(hb) * dot, in place on the gate: within the expf difference
+    dg2 = P.DeviceBuffer.from_numpy(gate)
+    P.check(P.lib.plh_gemv_ex(qtype, n, d, vp(G.ptr), vp(dx.ptr), vp(dg2.ptr), None, 0,
+                              vp(dg2.ptr), None), "plh_gemv_ex")
+    got = dg2.download(np.float32, (d,))
+    silu = np.array([O.lib().orc_silu(float(v)) for v in gate], np.float32)
+    want = silu * dot
+    tol = 4 * np.spacing(np.abs(want)) + 1e-37
+    assert np.all(np.abs(got - want) <= tol), np.max(np.abs(got - want) / tol)
+    with pytest.raises(P.PicolmHipError):
+        P.check(P.lib.plh_gemv_ex(qtype, n, d, vp(G.ptr), vp(dx.ptr), vp(out.ptr), vp(db.ptr),
+                                  1, None, None), "plh_gemv_ex")
+
+
+LLAMA = dict(n_layers=3, n_embd=512, n_ffn=1024, n_heads=8, n_kv_heads=2, head_dim=64,
+             vocab_size=1000, max_seq_len=256, rope_type=0, rope_base=1e4, eps=1e-5,
+             types=dict(embd=Q4K, output=Q6K, q=Q4K, k=Q8, v=Q6K, o=Q4K, gate=Q4K, up=Q8,
+                        down=Q6K))
+QWEN = dict(n_layers=2, n_embd=512, n_ffn=768, n_heads=4, n_kv_heads=2, head_dim=128,
+            vocab_size=700, max_seq_len=128, rope_type=1, rope_base=1e6, eps=1e-6,
+            types=dict(embd=Q8, output=Q8, q=Q8, k=Q4K, v=Q6K, o=Q8, gate=Q6K, up=Q4K,
+                       down=Q4K), biases=True, qk_norm=True)
+# normwise tolerance of logits and residual (relative to the vector's max);
+# measured differences are ~1e-6
+FWD_TOL = 2e-4
+KV_TOL = 2e-5   # normwise part of the later-layer KV bound
+
+
+def normwise(a, b):
+    return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
+
+
+@pytest.mark.parametrize("cfg", [LLAMA, QWEN], ids=["llama", "qwen"])
+def test_forward_matches_oracle(gpu, oracle_mod, cfg):
+    P, O = gpu, oracle_mod
+    h = S.SynthModel(**cfg, seed=11)
+    dm = P.DeviceModel(h)
+    orc = O.OracleForward(h)
+    rng = np.random.default_rng(12)
+    kv_layer = h.max_seq_len * h.kv_dim
+    worst = 0.0
+    try:
+        for pos in list(range(6)) + [40, 41]:
+            tok = int(rng.integers(0, h.vocab_size))
+            print(f"[case] forward {h.n_layers}x{h.n_embd} hd {h.head_dim} pos {pos} tok {tok}",
+                  flush=True)
+            dm.forward(tok, pos)
+            P.synchronize()
+            lg, x = dm.fetch_logits(), dm.fetch_x()
+            lo, xo = orc.forward(tok, pos, n_threads=8)
+            e = max(normwise(lg, lo), normwise(x, xo))
+            worst = max(worst, e)
+            assert e <= FWD_TOL, (pos, e)
+            top = np.argsort(lo)[-2:]
+            if lo[top[1]] - lo[top[0]] > 4 * FWD_TOL * np.max(np.abs(lo)):
+                assert int(np.argmax(lg)) == int(top[1]), pos
+            kc, vc = dm.fetch_cache()
+            # layer 0's rows involve no transcendental: bit-exact
+            assert np.array_equal(kc[:kv_layer], orc.kc[:kv_layer]), pos
+            assert np.array_equal(vc[:kv_layer], orc.vc[:kv_layer]), pos
+            # later layers: inputs equal up to a normwise ~1e-6, so a value
+            # may round to the neighbouring fp16 step, plus that input error
+            for dev_bits, orc_bits in ((kc, orc.kc), (vc, orc.vc)):
+                a = O.f16_to_f32(dev_bits[kv_layer:])
+                b = O.f16_to_f32(orc_bits[kv_layer:])
+                step = np.spacing(np.maximum(np.abs(a), np.abs(b)).astype(np.float16))
+                bound = step.astype(np.float32) + KV_TOL * np.max(np.abs(b))
+                assert np.all(np.abs(a - b) <= bound), (pos, np.max(np.abs(a - b) / bound))
+            # positions 6..39 are skipped: copy the oracle's rows over so both
+            # caches agree (the reference's kvcache_load does the same)
+            if pos == 5:
+                dm.load_cache(orc.kc, orc.vc)
+        print(f"forward {cfg['n_layers']} layers: worst normwise error {worst:.2e}")
+    finally:
+        dm.free()
+
+
+def test_forward_rejects_bad_calls(gpu):
+    P = gpu
+    h = S.SynthModel(**dict(LLAMA, n_layers=1), seed=13)
+    dm = P.DeviceModel(h)
+    try:
+        for tok, pos in ((-1, 0), (h.vocab_size, 0), (0, -1), (0, h.max_seq_len)):
+            with pytest.raises(P.PicolmHipError):
+                dm.forward(tok, pos)
+        # a matrix type the GEMV has no kernel for: nothing is queued
+        saved = dm.layers[0].up.qtype
+        dm.layers[0].up.qtype = F32
+        with pytest.raises(P.PicolmHipError, match="GEMV-capable"):
+            dm.forward(0, 0)
+        dm.layers[0].up.qtype = saved
+        dm.layers[0].k_norm = dm.layers[0].attn_norm   # only one of the QK-norm pair
+        with pytest.raises(P.PicolmHipError, match="q_norm"):
+            dm.forward(0, 0)
+    finally:
+        dm.free()
