@@ -165,10 +165,11 @@ size_t plh_gemv_packed_bytes(int qtype, int n, int d);
 int plh_gemv_upload(int qtype, int n, int d, const void *host_rows, void *dev);
 int plh_gemv_pack_host(int qtype, int n, int d, const void *host_rows, void *host_packed);
 int plh_gemv(int qtype, int n, int d, const void *dev, const float *x, float *out);
-/* plh_gemv with the forward pass's epilogues, in the reference's order
- * (matmul_bias tensor.c:256-264, silu + elemwise_mul tensor.c:605-633,
- * vec_add tensor.c:635-657):
- *     v = vec_dot(row i, x)
+/* plh_gemv with the forward pass's prologue and epilogues, in the
+ * reference's order (rmsnorm tensor.c:425-492, matmul_bias tensor.c:256-264,
+ * silu + elemwise_mul tensor.c:605-633, vec_add tensor.c:635-657):
+ *     xn = rmsnorm(x, norm_w, norm_eps)  if norm_w (n <= 12288), else x
+ *     v = vec_dot(row i, xn)
  *     v = v + bias[i]        if bias            (matmul_bias)
  *     v = v + 0.0f           if bias_zero       (matmul_bias with a zeroed bias)
  *     v = silu(gate[i]) * v  if gate            (hb = silu(hb) * hb2)
@@ -176,7 +177,8 @@ int plh_gemv(int qtype, int n, int d, const void *dev, const float *x, float *ou
  * gate and resid may alias out (read before the row is written).  All but
  * silu's expf are bit-identical to the reference. */
 int plh_gemv_ex(int qtype, int n, int d, const void *dev, const float *x, float *out,
-                const float *bias, int bias_zero, const float *gate, const float *resid);
+                const float *norm_w, float norm_eps, const float *bias, int bias_zero,
+                const float *gate, const float *resid);
 
 /* ---- forward pass (model_forward_ex, model.c:746-925) --------------------- */
 /* tensor.c:425-492 rmsnorm, bit-identical to the reference's x86-64 AVX2

@@ -217,3 +217,56 @@ __device__ __forceinline__ float shfl_xor_f(float v, int mask) {
 }
 
 }  // namespace plh
+
+namespace plh {
+
+// ---- rmsnorm scale of a whole vector by one workgroup -----------------------
+// tensor.c:425-492 in the reference's x86-64 AVX2 order: eight lane sums
+// acc[j] += x[8i+j]^2 (product rounded, then sum) over i in increasing order,
+// folded as ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)), the tail x[i]^2 for
+// i >= 8*(n/8) added one by one, then 1/sqrtf(ss/n + eps).  The workgroup
+// writes the squares to LDS transposed (chain j's squares contiguous, pitch
+// rms_sq_pitch(n)), eight lanes run the chains with batched LDS reads, and
+// every thread folds the eight sums itself, so all return the same scale.
+// sq: 8 * rms_sq_pitch(n) floats of LDS (free again once this returns);
+// red: 8 floats of LDS.  Every thread of the workgroup must call it.
+__host__ __device__ inline int rms_sq_pitch(int n) { return (n / 8 + 3) / 4 * 4 + 4; }
+
+template <int NT>
+__device__ __forceinline__ float rms_scale_block(const float* x, int n, float eps, float* sq,
+                                                 float* red) {
+  const int tid = threadIdx.x;
+  const int n8 = n / 8, pitch = rms_sq_pitch(n);
+  for (int idx = tid; idx < 8 * n8; idx += NT) {
+    const float v = x[idx];
+    sq[(idx & 7) * pitch + (idx >> 3)] = v * v;
+  }
+  __syncthreads();
+  if (tid < 8) {
+    const float* s = sq + tid * pitch;
+    float acc = 0.0f;
+    int i = 0;
+    for (; i + 32 <= n8; i += 32) {
+      float4 v[8];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) v[k] = *(const float4*)(s + i + 4 * k);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        acc = acc + v[k].x;
+        acc = acc + v[k].y;
+        acc = acc + v[k].z;
+        acc = acc + v[k].w;
+      }
+    }
+    for (; i < n8; ++i) acc = acc + s[i];
+    red[tid] = acc;
+  }
+  __syncthreads();
+  const float l0 = red[0] + red[4], l1 = red[1] + red[5];
+  const float l2 = red[2] + red[6], l3 = red[3] + red[7];
+  float ss = (l0 + l2) + (l1 + l3);
+  for (int i = 8 * n8; i < n; ++i) ss = ss + x[i] * x[i];
+  return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+}  // namespace plh

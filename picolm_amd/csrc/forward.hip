@@ -25,52 +25,15 @@ constexpr int kNormThreads = 256;
 constexpr int kMaxNormSize = 12288;  // the squares of a row must fit 48 KiB of LDS
 
 // ---- rmsnorm (tensor.c:425-492, x86-64 AVX2 path) --------------------------
-// The reference keeps eight lane sums acc[j] += x[8i+j]^2 (product, then
-// sum) over i in order, folds them as ((a0+a4)+(a2+a6)) + ((a1+a5)+(a3+a7)),
-// adds the tail x[i]^2 for i >= 8*(n/8) one by one, takes
-// 1/sqrtf(ss/n + eps) and writes (x*scale)*w.  Here the workgroup squares x
-// into LDS transposed (chain j's squares contiguous), eight lanes run the
-// eight chains, lane 0 folds, and every thread writes its outputs.  Device
-// division and square root are correctly rounded, so the scale is the
-// reference's bit for bit.
+// One workgroup: the reference's scale (rms_scale_block), then
+// out[i] = (x[i] * scale) * w[i].  Device division and square root are
+// correctly rounded, so the output is the reference's bit for bit.
 __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, const float* w,
                                                                float* out, int n, float eps) {
   extern __shared__ __align__(16) float sq[];
-  __shared__ float chain[8];
-  __shared__ float scale_s;
-  const int tid = threadIdx.x;
-  const int n8 = n / 8;
-  const int pitch = (n8 + 3) / 4 * 4 + 4;
-  for (int idx = tid; idx < 8 * n8; idx += kNormThreads) {
-    const float v = x[idx];
-    sq[(idx & 7) * pitch + (idx >> 3)] = v * v;
-  }
-  __syncthreads();
-  if (tid < 8) {
-    const float* s = sq + tid * pitch;
-    float acc = 0.0f;
-    int i = 0;
-    for (; i + 4 <= n8; i += 4) {
-      const float4 v = *(const float4*)(s + i);
-      acc = acc + v.x;
-      acc = acc + v.y;
-      acc = acc + v.z;
-      acc = acc + v.w;
-    }
-    for (; i < n8; ++i) acc = acc + s[i];
-    chain[tid] = acc;
-  }
-  __syncthreads();
-  if (tid == 0) {
-    const float l0 = chain[0] + chain[4], l1 = chain[1] + chain[5];
-    const float l2 = chain[2] + chain[6], l3 = chain[3] + chain[7];
-    float ss = (l0 + l2) + (l1 + l3);
-    for (int i = 8 * n8; i < n; ++i) ss = ss + x[i] * x[i];
-    scale_s = 1.0f / sqrtf(ss / (float)n + eps);
-  }
-  __syncthreads();
-  const float scale = scale_s;
-  for (int i = tid; i < n; i += kNormThreads) {
+  __shared__ float red[8];
+  const float scale = rms_scale_block<kNormThreads>(x, n, eps, sq, red);
+  for (int i = threadIdx.x; i < n; i += kNormThreads) {
     const float t = x[i] * scale;
     out[i] = t * w[i];
   }
@@ -93,10 +56,8 @@ __device__ __forceinline__ void q4k_scale_min(int j, const uint8_t* q, int& sc, 
   }
 }
 
-__global__ __launch_bounds__(256) void dequant_row_kernel(int qtype, const uint8_t* row,
-                                                          float* out, int n) {
-  const int e = blockIdx.x * 256 + threadIdx.x;
-  if (e >= n) return;
+// Element e of a GGUF row.
+__device__ __forceinline__ float dequant_elem(int qtype, const uint8_t* row, int e) {
   float y = 0.0f;
   switch (qtype) {
     case kTypeF32: {
@@ -144,7 +105,13 @@ __global__ __launch_bounds__(256) void dequant_row_kernel(int qtype, const uint8
     default:
       break;
   }
-  out[e] = y;
+  return y;
+}
+
+__global__ __launch_bounds__(256) void dequant_row_kernel(int qtype, const uint8_t* row,
+                                                          float* out, int n) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e < n) out[e] = dequant_elem(qtype, row, e);
 }
 
 size_t embd_row_bytes(int qtype, int n) {
@@ -159,7 +126,7 @@ size_t embd_row_bytes(int qtype, int n) {
   }
 }
 
-size_t norm_lds_bytes(int n) { return sizeof(float) * 8 * (size_t)((n / 8 + 3) / 4 * 4 + 4); }
+size_t norm_lds_bytes(int n) { return sizeof(float) * 8 * (size_t)rms_sq_pitch(n); }
 
 int launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps) {
   hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(kNormThreads), norm_lds_bytes(n), ctx().stream,
@@ -169,7 +136,7 @@ int launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps)
 
 // Workspace carve-up of plh_forward, 256-byte aligned pieces.
 struct Acts {
-  float *x, *xb, *q, *k, *v, *att, *hb;
+  float *x, *q, *k, *v, *att, *hb;
   size_t bytes;
 };
 
@@ -178,14 +145,11 @@ size_t piece(size_t floats) { return (floats * sizeof(float) + 255) / 256 * 256;
 Acts carve(const plh_model* m, void* base) {
   const size_t q_dim = (size_t)m->n_heads * m->head_dim;
   const size_t kv_dim = (size_t)m->n_kv_heads * m->head_dim;
-  const size_t wide = q_dim > (size_t)m->n_embd ? q_dim : (size_t)m->n_embd;
-  const size_t sizes[7] = {(size_t)m->n_embd, wide, q_dim, kv_dim, kv_dim, q_dim, (size_t)m->n_ffn};
-  float** dst[7];
+  const size_t sizes[6] = {(size_t)m->n_embd, q_dim, kv_dim, kv_dim, q_dim, (size_t)m->n_ffn};
   Acts a{};
-  dst[0] = &a.x, dst[1] = &a.xb, dst[2] = &a.q, dst[3] = &a.k, dst[4] = &a.v, dst[5] = &a.att,
-  dst[6] = &a.hb;
+  float** dst[6] = {&a.x, &a.q, &a.k, &a.v, &a.att, &a.hb};
   size_t off = 0;
-  for (int i = 0; i < 7; ++i) {
+  for (int i = 0; i < 6; ++i) {
     *dst[i] = base ? (float*)((char*)base + off) : nullptr;
     off += piece(sizes[i]);
   }
@@ -301,14 +265,22 @@ int plh_forward(const plh_model* m, int token, int pos, void* workspace, float* 
   if (plh_dequantize_row(m->embd_type, (const uint8_t*)m->token_embd + (size_t)token * rb, a.x,
                          E))
     return -1;
+  // every GEMV that reads rmsnorm(x) forms it itself (tensor.c:425-492)
+  auto gemv = [&](const plh_matrix& w, int n, int d, const float* x, float* out,
+                  const float* norm_w, const float* bias, int bias_zero, const float* gate,
+                  const float* resid) {
+    GemvCall g{};
+    g.qtype = w.qtype, g.n = n, g.d = d, g.w = w.w, g.x = x, g.out = out;
+    g.norm_w = norm_w, g.norm_eps = eps;
+    g.bias = bias, g.bias_zero = bias_zero, g.gate = gate, g.resid = resid;
+    return gemv_launch(g);
+  };
   for (int l = 0; l < m->n_layers; ++l) {
     const plh_layer& L = m->layers[l];
     // attention block (model.c:777-897)
-    if (launch_rmsnorm(a.x, L.attn_norm, a.xb, E, eps)) return -1;
-    if (plh_gemv_ex(L.q.qtype, E, Q, L.q.w, a.xb, a.q, L.q_bias, L.q_bias == nullptr, nullptr,
-                    nullptr) ||
-        plh_gemv_ex(L.k.qtype, E, KV, L.k.w, a.xb, a.k, L.k_bias, 0, nullptr, nullptr) ||
-        plh_gemv_ex(L.v.qtype, E, KV, L.v.w, a.xb, a.v, L.v_bias, 0, nullptr, nullptr))
+    if (gemv(L.q, E, Q, a.x, a.q, L.attn_norm, L.q_bias, L.q_bias == nullptr, nullptr, nullptr) ||
+        gemv(L.k, E, KV, a.x, a.k, L.attn_norm, L.k_bias, 0, nullptr, nullptr) ||
+        gemv(L.v, E, KV, a.x, a.v, L.attn_norm, L.v_bias, 0, nullptr, nullptr))
       return -1;
     const int rc = L.q_norm ? plh_attn_decode_qknorm(m->n_layers, m->n_heads, m->n_kv_heads,
                                                      m->head_dim, m->max_seq_len, m->rope_type, l,
@@ -321,22 +293,20 @@ int plh_forward(const plh_model* m, int token, int pos, void* workspace, float* 
                                               m->rope_cos, m->rope_sin, a.att);
     if (rc) return -1;
     // x = x + (Wo att + o_bias)
-    if (plh_gemv_ex(L.o.qtype, Q, E, L.o.w, a.att, a.x, L.o_bias, L.o_bias == nullptr, nullptr,
-                    a.x))
+    if (gemv(L.o, Q, E, a.att, a.x, nullptr, L.o_bias, L.o_bias == nullptr, nullptr, a.x))
       return -1;
-    // SwiGLU block (model.c:899-922)
-    if (launch_rmsnorm(a.x, L.ffn_norm, a.xb, E, eps)) return -1;
-    if (plh_gemv_ex(L.gate.qtype, E, F, L.gate.w, a.xb, a.hb, nullptr, 0, nullptr, nullptr) ||
-        plh_gemv_ex(L.up.qtype, E, F, L.up.w, a.xb, a.hb, nullptr, 0, a.hb, nullptr) ||
-        plh_gemv_ex(L.down.qtype, F, E, L.down.w, a.hb, a.x, nullptr, 0, nullptr, a.x))
+    // SwiGLU block (model.c:899-922): hb = silu(gate xn) * (up xn), xn = rmsnorm(x);
+    // then x = x + Wdown hb
+    if (gemv(L.gate, E, F, a.x, a.hb, L.ffn_norm, nullptr, 0, nullptr, nullptr) ||
+        gemv(L.up, E, F, a.x, a.hb, L.ffn_norm, nullptr, 0, a.hb, nullptr) ||
+        gemv(L.down, F, E, a.hb, a.x, nullptr, nullptr, 0, nullptr, a.x))
       return -1;
   }
   // final norm and logits (model.c:918-922)
-  if (launch_rmsnorm(a.x, m->output_norm, a.xb, E, eps)) return -1;
-  if (plh_gemv_ex(m->output.qtype, E, m->vocab_size, m->output.w, a.xb, logits, nullptr, 0,
-                  nullptr, nullptr))
+  if (gemv(m->output, E, m->vocab_size, a.x, logits, m->output_norm, nullptr, 0, nullptr,
+           nullptr))
     return -1;
-  if (x_out && plh_memcpy_dtod(x_out, a.xb, (size_t)E * sizeof(float))) return -1;
+  if (x_out && launch_rmsnorm(a.x, m->output_norm, x_out, E, eps)) return -1;
   return 0;
 }
 

@@ -38,6 +38,7 @@ constexpr int kThreads = 256;
 constexpr int kTypeQ8_0 = 8, kTypeQ4K = 12, kTypeQ6K = 14;
 constexpr size_t kPlaneAlign = 256;
 constexpr size_t kMaxPacked = (size_t)1 << 31;  // 32-bit plane offsets
+constexpr int kMaxNormN = 12288;                 // rmsnorm squares within 48 KiB of LDS
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -165,6 +166,11 @@ struct GemvArgs {
   const float* gate;
   const float* resid;
   int bias_mode;
+  // Prologue (gemv_kernel<..., true>): x is rmsnorm(x, norm_w) of length n
+  // (tensor.c:425-492), formed by every workgroup itself.
+  const float* norm_w;
+  float norm_eps;
+  int n;
 };
 
 // tensor.c:605-609: x / (1 + expf(-x)).  expf is the device library's, not
@@ -178,6 +184,28 @@ __device__ __forceinline__ float hsum8(const float (&v)[8]) {
 }
 
 __device__ __forceinline__ float4 ld4(const float* p) { return *(const float4*)p; }
+
+// The x operand as the formats read it, four elements at a time: the vector
+// itself, or its rmsnorm (x * scale) * w formed on the fly, rounded as the
+// reference's rmsnorm rounds it.
+struct PlainX {
+  const float* x;
+  __device__ __forceinline__ float4 operator()(int i) const { return ld4(x + i); }
+};
+struct NormX {
+  const float* x;
+  const float* w;
+  float scale;
+  __device__ __forceinline__ float4 operator()(int i) const {
+    const float4 v = ld4(x + i), g = ld4(w + i);
+    float4 r;
+    r.x = (v.x * scale) * g.x;
+    r.y = (v.y * scale) * g.y;
+    r.z = (v.z * scale) * g.z;
+    r.w = (v.w * scale) * g.w;
+    return r;
+  }
+};
 
 template <class T>
 __device__ __forceinline__ T ld(const GemvArgs& a, uint32_t off) {
@@ -222,10 +250,11 @@ struct Q4K {
     r.q0 = ld<uint4>(a, a.off1 + s * 16);
     r.q1 = ld<uint4>(a, a.off2 + s * 16);
   }
-  static __device__ __forceinline__ void load_x(const float* x, int u, X& U) {
+  template <class XS>
+  static __device__ __forceinline__ void load_x(const XS& x, int u, X& U) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      const float4 v = ld4(x + 64 * u + 4 * i);
+      const float4 v = x(64 * u + 4 * i);
       U.x[4 * i] = v.x, U.x[4 * i + 1] = v.y, U.x[4 * i + 2] = v.z, U.x[4 * i + 3] = v.w;
     }
     // sum_x1 / sum_x2 (quant.c:433): lane k adds x[k] + x[8+k], then
@@ -329,10 +358,11 @@ struct Q6K {
       r.sc = ld<uint8_t>(a, a.scales_off + g);
     r.d = ld<uint16_t>(a, a.d_off + (g >> 4) * 2);
   }
-  static __device__ __forceinline__ void load_x(const float* x, int u, X& U) {
+  template <class XS>
+  static __device__ __forceinline__ void load_x(const XS& x, int u, X& U) {
 #pragma unroll
     for (int i = 0; i < 4 * G; ++i) {
-      const float4 v = ld4(x + 16 * G * u + 4 * i);
+      const float4 v = x(16 * G * u + 4 * i);
       U.x[4 * i] = v.x, U.x[4 * i + 1] = v.y, U.x[4 * i + 2] = v.z, U.x[4 * i + 3] = v.w;
     }
   }
@@ -380,10 +410,11 @@ struct Q80 {
     r.q1 = ld<uint4>(a, a.off1 + b * 16);
     r.d = ld<uint16_t>(a, a.d_off + b * 2);
   }
-  static __device__ __forceinline__ void load_x(const float* x, int u, X& U) {
+  template <class XS>
+  static __device__ __forceinline__ void load_x(const XS& x, int u, X& U) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
-      const float4 v = ld4(x + 32 * u + 4 * i);
+      const float4 v = x(32 * u + 4 * i);
       U.x[4 * i] = v.x, U.x[4 * i + 1] = v.y, U.x[4 * i + 2] = v.z, U.x[4 * i + 3] = v.w;
     }
   }
@@ -404,39 +435,76 @@ struct Q80 {
   static __device__ __forceinline__ int term_index(int u) { return u; }
 };
 
+// The terms of unit u of the RB rows whose weights are in raw, into LDS.
+template <class F, int RB, class XS>
+__device__ __forceinline__ void unit_terms(const GemvArgs& a, const XS& xs, float* terms,
+                                           int rows, int rlane, int u,
+                                           const typename F::Raw (&raw)[RB]) {
+  typename F::X U;
+  F::load_x(xs, u, U);
+#pragma unroll
+  for (int k = 0; k < RB; ++k) {
+    float t[F::kTerms];
+    F::terms(u, raw[k], U, t);
+    const int rr = rlane + a.row_par * k;
+    if (rr < rows) {
+#pragma unroll
+      for (int g = 0; g < F::kTerms; ++g) terms[rr * a.tpitch + F::term_index(u) + g] = t[g];
+    }
+  }
+}
+
+// Units it0, it0 + 1, ... of this thread (loads of each pass, then terms).
+template <class F, int RB, class XS>
+__device__ __forceinline__ void unit_passes(const GemvArgs& a, const XS& xs, float* terms,
+                                            int r0, int rows, int rlane, int it0) {
+  for (int it = it0; it < a.unit_iters; ++it) {
+    const int u = threadIdx.x % a.uspan + it * a.uspan;
+    if (u >= a.units) break;
+    typename F::Raw raw[RB];
+#pragma unroll
+    for (int k = 0; k < RB; ++k)  // rows past the end re-read the last row
+      F::load_raw(a, r0 + min(rlane + a.row_par * k, rows - 1), u, raw[k]);
+    unit_terms<F, RB>(a, xs, terms, rows, rlane, u, raw);
+  }
+}
+
 // One workgroup: rows [r0, r0 + rows_per_wg).  Phase 1: thread tid owns unit
 // tid % uspan (+ uspan per pass) of the RB rows tid / uspan + row_par * k;
 // it issues the loads of all RB rows, then loads the unit's x (kept in
 // registers for the RB rows) and writes the unit's terms to LDS.  Phase 2:
-// one thread per row adds the row's terms in order.
-template <class F, int RB>
+// one thread per row adds the row's terms in order.  NORM: x is first
+// rmsnorm-ed by the workgroup (rms_scale_block, its squares in the LDS that
+// the terms take afterwards); the first pass's weight loads are issued
+// before, so their latency covers the sum of squares.
+template <class F, int RB, bool NORM>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) float terms[];
   const int tid = threadIdx.x;
   const int r0 = blockIdx.x * a.rows_per_wg;
   const int rows = min(a.rows_per_wg, a.d - r0);
   const int rlane = tid / a.uspan;
-  if (rlane < a.row_par) {
-    for (int it = 0; it < a.unit_iters; ++it) {
-      const int u = tid % a.uspan + it * a.uspan;
-      if (u >= a.units) break;
-      typename F::Raw raw[RB];
+  const bool active = rlane < a.row_par;
+  if constexpr (NORM) {
+    __shared__ float red[8];
+    const int u = tid % a.uspan;
+    const bool first = active && u < a.units;
+    typename F::Raw raw[RB];
+    if (first) {
 #pragma unroll
-      for (int k = 0; k < RB; ++k)  // rows past the end re-read the last row
+      for (int k = 0; k < RB; ++k)
         F::load_raw(a, r0 + min(rlane + a.row_par * k, rows - 1), u, raw[k]);
-      typename F::X U;
-      F::load_x(a.x, u, U);
-#pragma unroll
-      for (int k = 0; k < RB; ++k) {
-        float t[F::kTerms];
-        F::terms(u, raw[k], U, t);
-        const int rr = rlane + a.row_par * k;
-        if (rr < rows) {
-#pragma unroll
-          for (int g = 0; g < F::kTerms; ++g) terms[rr * a.tpitch + F::term_index(u) + g] = t[g];
-        }
-      }
     }
+    // lanes 0..7 finish reading the squares before the helper's second
+    // barrier, so the terms may overwrite them once it returns
+    const float scale = rms_scale_block<kThreads>(a.x, a.n, a.norm_eps, terms, red);
+    const NormX xs{a.x, a.norm_w, scale};
+    if (first) {
+      unit_terms<F, RB>(a, xs, terms, rows, rlane, u, raw);
+      unit_passes<F, RB>(a, xs, terms, r0, rows, rlane, 1);
+    }
+  } else {
+    if (active) unit_passes<F, RB>(a, PlainX{a.x}, terms, r0, rows, rlane, 0);
   }
   __syncthreads();
   // the row's terms in order, 16 per step, the next step's reads in flight
@@ -475,14 +543,30 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   }
 }
 
-template <class F>
+template <class F, bool NORM>
 void launch_rb(int rb, int grid, size_t lds, hipStream_t st, const GemvArgs& a) {
   switch (rb) {
-    case 1: hipLaunchKernelGGL((gemv_kernel<F, 1>), dim3(grid), dim3(kThreads), lds, st, a); break;
-    case 2: hipLaunchKernelGGL((gemv_kernel<F, 2>), dim3(grid), dim3(kThreads), lds, st, a); break;
-    case 4: hipLaunchKernelGGL((gemv_kernel<F, 4>), dim3(grid), dim3(kThreads), lds, st, a); break;
-    default: hipLaunchKernelGGL((gemv_kernel<F, 8>), dim3(grid), dim3(kThreads), lds, st, a); break;
+    case 1:
+      hipLaunchKernelGGL((gemv_kernel<F, 1, NORM>), dim3(grid), dim3(kThreads), lds, st, a);
+      break;
+    case 2:
+      hipLaunchKernelGGL((gemv_kernel<F, 2, NORM>), dim3(grid), dim3(kThreads), lds, st, a);
+      break;
+    case 4:
+      hipLaunchKernelGGL((gemv_kernel<F, 4, NORM>), dim3(grid), dim3(kThreads), lds, st, a);
+      break;
+    default:
+      hipLaunchKernelGGL((gemv_kernel<F, 8, NORM>), dim3(grid), dim3(kThreads), lds, st, a);
+      break;
   }
+}
+
+template <class F>
+void launch_fmt(bool norm, int rb, int grid, size_t lds, hipStream_t st, const GemvArgs& a) {
+  if (norm)
+    launch_rb<F, true>(rb, grid, lds, st, a);
+  else
+    launch_rb<F, false>(rb, grid, lds, st, a);
 }
 
 }  // namespace
@@ -529,11 +613,30 @@ int plh_gemv_upload(int qtype, int n, int d, const void* host_rows, void* dev) {
 }
 
 int plh_gemv(int qtype, int n, int d, const void* dev, const float* x, float* out) {
-  return plh_gemv_ex(qtype, n, d, dev, x, out, nullptr, 0, nullptr, nullptr);
+  return plh_gemv_ex(qtype, n, d, dev, x, out, nullptr, 0.0f, nullptr, 0, nullptr, nullptr);
 }
 
 int plh_gemv_ex(int qtype, int n, int d, const void* dev, const float* x, float* out,
-                const float* bias, int bias_zero, const float* gate, const float* resid) {
+                const float* norm_w, float norm_eps, const float* bias, int bias_zero,
+                const float* gate, const float* resid) {
+  GemvCall g{};
+  g.qtype = qtype, g.n = n, g.d = d, g.w = dev, g.x = x, g.out = out;
+  g.norm_w = norm_w, g.norm_eps = norm_eps, g.bias = bias, g.bias_zero = bias_zero;
+  g.gate = gate, g.resid = resid;
+  return gemv_launch(g);
+}
+
+}  // extern "C"
+
+namespace plh {
+
+int gemv_launch(const GemvCall& g) {
+  const int qtype = g.qtype, n = g.n, d = g.d;
+  const void* dev = g.w;
+  const float *x = g.x, *norm_w = g.norm_w, *bias = g.bias, *gate = g.gate, *resid = g.resid;
+  float* out = g.out;
+  const int bias_zero = g.bias_zero;
+  const float norm_eps = g.norm_eps;
   Layout L;
   if (!make_layout(qtype, n, d, L)) {
     set_error("plh_gemv: no GEMV for type %d with n=%d d=%d", qtype, n, d);
@@ -547,6 +650,11 @@ int plh_gemv_ex(int qtype, int n, int d, const void* dev, const float* x, float*
     set_error("plh_gemv_ex: a bias and bias_zero together");
     return -1;
   }
+  if (norm_w && n > kMaxNormN) {
+    set_error("plh_gemv_ex: rmsnorm of %d elements exceeds %d", n, kMaxNormN);
+    return -1;
+  }
+
   Context& c = ctx();
   if (!c.stream) {
     set_error("plh_gemv: plh_init has not been called");
@@ -576,6 +684,10 @@ int plh_gemv_ex(int qtype, int n, int d, const void* dev, const float* x, float*
   a.gate = gate;
   a.resid = resid;
   a.bias_mode = bias ? 1 : (bias_zero ? 2 : 0);
+  a.norm_w = norm_w;
+  a.norm_eps = norm_eps;
+  a.n = n;
+
   // rows per thread: the largest of 4, 2, 1 that still gives at least 0.6
   // workgroups per CU and keeps the workgroup's terms within 64 KiB of LDS
   // (measured on the TinyLlama and output-projection shapes: more rows in
@@ -593,15 +705,20 @@ int plh_gemv_ex(int qtype, int n, int d, const void* dev, const float* x, float*
     return -1;
   }
   a.rows_per_wg = a.row_par * rb;
-  const size_t lds = sizeof(float) * (size_t)a.rows_per_wg * a.tpitch;
+  size_t lds = sizeof(float) * (size_t)a.rows_per_wg * a.tpitch;
+  if (norm_w) {  // the squares of the rmsnorm share the terms' LDS
+    const size_t sq = sizeof(float) * 8 * (size_t)rms_sq_pitch(n);
+    if (sq > lds) lds = sq;
+  }
   const int grid = (d + a.rows_per_wg - 1) / a.rows_per_wg;
+  const bool norm = norm_w != nullptr;
   if (qtype == kTypeQ4K)
-    launch_rb<Q4K>(rb, grid, lds, c.stream, a);
+    launch_fmt<Q4K>(norm, rb, grid, lds, c.stream, a);
   else if (qtype == kTypeQ8_0)
-    launch_rb<Q80>(rb, grid, lds, c.stream, a);
+    launch_fmt<Q80>(norm, rb, grid, lds, c.stream, a);
   else
-    launch_rb<Q6K<4>>(rb, grid, lds, c.stream, a);
+    launch_fmt<Q6K<4>>(norm, rb, grid, lds, c.stream, a);
   return check_hip(hipGetLastError(), "gemv_kernel launch");
 }
 
-}  // extern "C"
+}  // namespace plh

@@ -26,6 +26,22 @@ int check_hip(hipError_t e, const char* what);
 // choice).
 extern int g_gemv_rows_per_thread;
 
+// One weight GEMV with the forward pass's prologue and epilogues (the
+// arguments of plh_gemv_ex).
+struct GemvCall {
+  int qtype, n, d;
+  const void* w;
+  const float* x;
+  float* out;
+  const float* norm_w;
+  float norm_eps;
+  const float* bias;
+  int bias_zero;
+  const float* gate;
+  const float* resid;
+};
+int gemv_launch(const GemvCall& g);
+
 // Makes sure the workspace holds at least `bytes`.  Growing it waits for the
 // queued work (which may still read the old one).  Returns 0 or -1.
 int ensure_workspace(size_t bytes);

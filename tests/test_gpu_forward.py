@@ -92,10 +92,11 @@ def test_gemv_epilogues(gpu, oracle_mod, qtype, n, d):
     out = P.DeviceBuffer(4 * d)
     vp = C.c_void_p
 
-    def run(b, bz, r, o):
+    def run(b, bz, r, o, nw=None, eps=0.0):
         """plh_gemv_ex into buffer o; returns o's contents."""
         P.check(P.lib.plh_gemv_ex(qtype, n, d, vp(G.ptr), vp(dx.ptr), vp(o.ptr),
-                                  b and vp(b.ptr), bz, None, r and vp(r.ptr)), "plh_gemv_ex")
+                                  nw and vp(nw.ptr), C.c_float(eps), b and vp(b.ptr), bz, None,
+                                  r and vp(r.ptr)), "plh_gemv_ex")
         return o.download(np.float32, (d,))
 
     assert np.array_equal(bits(run(None, 0, None, out)), bits(dot))
@@ -103,18 +104,25 @@ def test_gemv_epilogues(gpu, oracle_mod, qtype, n, d):
     assert np.array_equal(bits(run(None, 1, None, out)), bits(dot + np.float32(0.0)))
     # x = x + (dot + bias), in place on the residual
     assert np.array_equal(bits(run(db, 0, dr, dr)), bits(resid + (dot + bias)))
+    # the rmsnorm prologue: W @ rmsnorm(x, w), bit-exact, with a bias
+    nw = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    dnw = P.DeviceBuffer.from_numpy(nw)
+    for eps in (1e-5, 1e-6):
+        xn = O.rmsnorm(x, nw, eps)
+        want = O.matmul(W, xn, n, d, qtype) + bias
+        assert np.array_equal(bits(run(db, 0, None, out, dnw, eps)), bits(want)), eps
     # hb = silu(hb) * dot, in place on the gate: within the expf difference
     dg2 = P.DeviceBuffer.from_numpy(gate)
-    P.check(P.lib.plh_gemv_ex(qtype, n, d, vp(G.ptr), vp(dx.ptr), vp(dg2.ptr), None, 0,
-                              vp(dg2.ptr), None), "plh_gemv_ex")
+    P.check(P.lib.plh_gemv_ex(qtype, n, d, vp(G.ptr), vp(dx.ptr), vp(dg2.ptr), None,
+                              C.c_float(0.0), None, 0, vp(dg2.ptr), None), "plh_gemv_ex")
     got = dg2.download(np.float32, (d,))
     silu = np.array([O.lib().orc_silu(float(v)) for v in gate], np.float32)
     want = silu * dot
     tol = 4 * np.spacing(np.abs(want)) + 1e-37
     assert np.all(np.abs(got - want) <= tol), np.max(np.abs(got - want) / tol)
     with pytest.raises(P.PicolmHipError):
-        P.check(P.lib.plh_gemv_ex(qtype, n, d, vp(G.ptr), vp(dx.ptr), vp(out.ptr), vp(db.ptr),
-                                  1, None, None), "plh_gemv_ex")
+        P.check(P.lib.plh_gemv_ex(qtype, n, d, vp(G.ptr), vp(dx.ptr), vp(out.ptr), None,
+                                  C.c_float(0.0), vp(db.ptr), 1, None, None), "plh_gemv_ex")
 
 
 LLAMA = dict(n_layers=3, n_embd=512, n_ffn=1024, n_heads=8, n_kv_heads=2, head_dim=64,
