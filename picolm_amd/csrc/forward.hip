@@ -266,22 +266,23 @@ int plh_forward(const plh_model* m, int token, int pos, void* workspace, float* 
                          E))
     return -1;
   // every GEMV that reads rmsnorm(x) forms it itself (tensor.c:425-492)
-  auto gemv = [&](const plh_matrix& w, int n, int d, const float* x, float* out,
+  auto call = [&](const plh_matrix& w, int n, int d, const float* x, float* out,
                   const float* norm_w, const float* bias, int bias_zero, const float* gate,
                   const float* resid) {
     GemvCall g{};
     g.qtype = w.qtype, g.n = n, g.d = d, g.w = w.w, g.x = x, g.out = out;
     g.norm_w = norm_w, g.norm_eps = eps;
     g.bias = bias, g.bias_zero = bias_zero, g.gate = gate, g.resid = resid;
-    return gemv_launch(g);
+    return g;
   };
   for (int l = 0; l < m->n_layers; ++l) {
     const plh_layer& L = m->layers[l];
-    // attention block (model.c:777-897)
-    if (gemv(L.q, E, Q, a.x, a.q, L.attn_norm, L.q_bias, L.q_bias == nullptr, nullptr, nullptr) ||
-        gemv(L.k, E, KV, a.x, a.k, L.attn_norm, L.k_bias, 0, nullptr, nullptr) ||
-        gemv(L.v, E, KV, a.x, a.v, L.attn_norm, L.v_bias, 0, nullptr, nullptr))
-      return -1;
+    // attention block (model.c:777-897): q, k, v in one launch
+    const GemvCall qkv[3] = {
+        call(L.q, E, Q, a.x, a.q, L.attn_norm, L.q_bias, L.q_bias == nullptr, nullptr, nullptr),
+        call(L.k, E, KV, a.x, a.k, L.attn_norm, L.k_bias, 0, nullptr, nullptr),
+        call(L.v, E, KV, a.x, a.v, L.attn_norm, L.v_bias, 0, nullptr, nullptr)};
+    if (gemv_multi_launch(qkv, 3)) return -1;
     const int rc = L.q_norm ? plh_attn_decode_qknorm(m->n_layers, m->n_heads, m->n_kv_heads,
                                                      m->head_dim, m->max_seq_len, m->rope_type, l,
                                                      1, pos, a.q, a.k, a.v, m->key_cache,
@@ -293,18 +294,25 @@ int plh_forward(const plh_model* m, int token, int pos, void* workspace, float* 
                                               m->rope_cos, m->rope_sin, a.att);
     if (rc) return -1;
     // x = x + (Wo att + o_bias)
-    if (gemv(L.o, Q, E, a.att, a.x, nullptr, L.o_bias, L.o_bias == nullptr, nullptr, a.x))
+    if (gemv_launch(call(L.o, Q, E, a.att, a.x, nullptr, L.o_bias, L.o_bias == nullptr, nullptr,
+                         a.x)))
       return -1;
-    // SwiGLU block (model.c:899-922): hb = silu(gate xn) * (up xn), xn = rmsnorm(x);
-    // then x = x + Wdown hb
-    if (gemv(L.gate, E, F, a.x, a.hb, L.ffn_norm, nullptr, 0, nullptr, nullptr) ||
-        gemv(L.up, E, F, a.x, a.hb, L.ffn_norm, nullptr, 0, a.hb, nullptr) ||
-        gemv(L.down, F, E, a.hb, a.x, nullptr, nullptr, 0, nullptr, a.x))
-      return -1;
+    // SwiGLU block (model.c:899-922): hb = silu(gate xn) * (up xn), xn = rmsnorm(x),
+    // in one launch when gate and up share a type; then x = x + Wdown hb
+    const GemvCall gate = call(L.gate, E, F, a.x, a.hb, L.ffn_norm, nullptr, 0, nullptr, nullptr);
+    const GemvCall up = call(L.up, E, F, a.x, a.hb, L.ffn_norm, nullptr, 0, nullptr, nullptr);
+    if (L.gate.qtype == L.up.qtype) {
+      if (gemv_pair_launch(gate, up)) return -1;
+    } else {
+      GemvCall up_g = up;
+      up_g.gate = a.hb;
+      if (gemv_launch(gate) || gemv_launch(up_g)) return -1;
+    }
+    if (gemv_launch(call(L.down, F, E, a.hb, a.x, nullptr, nullptr, 0, nullptr, a.x))) return -1;
   }
   // final norm and logits (model.c:918-922)
-  if (gemv(m->output, E, m->vocab_size, a.x, logits, m->output_norm, nullptr, 0, nullptr,
-           nullptr))
+  if (gemv_launch(call(m->output, E, m->vocab_size, a.x, logits, m->output_norm, nullptr, 0,
+                       nullptr, nullptr)))
     return -1;
   if (x_out && launch_rmsnorm(a.x, m->output_norm, x_out, E, eps)) return -1;
   return 0;

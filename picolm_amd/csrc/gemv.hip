@@ -171,6 +171,9 @@ struct GemvArgs {
   const float* norm_w;
   float norm_eps;
   int n;
+  // Gate/up pair (gemv_body<..., true>): virtual row 2r is row r of w (gate),
+  // 2r + 1 row r of w2 (up, same type and shape); out[r] = silu(gate) * up.
+  const uint8_t* w2;
 };
 
 // tensor.c:605-609: x / (1 + expf(-x)).  expf is the device library's, not
@@ -208,8 +211,8 @@ struct NormX {
 };
 
 template <class T>
-__device__ __forceinline__ T ld(const GemvArgs& a, uint32_t off) {
-  return *(const T*)(a.w + off);
+__device__ __forceinline__ T ld(const uint8_t* w, uint32_t off) {
+  return *(const T*)(w + off);
 }
 
 // byte B of a word as a float, exact (v_cvt_f32_ubyteB: one instruction)
@@ -244,11 +247,12 @@ struct Q4K {
   struct Raw {
     uint4 hdr, q0, q1;
   };
-  static __device__ __forceinline__ void load_raw(const GemvArgs& a, int row, int u, Raw& r) {
+  static __device__ __forceinline__ void load_raw(const GemvArgs& a, const uint8_t* w, int row,
+                                                  int u, Raw& r) {
     const uint32_t s = (uint32_t)row * a.nb * 4 + u;  // sub-block in the matrix
-    r.hdr = ld<uint4>(a, a.off0 + (s >> 2) * 16);
-    r.q0 = ld<uint4>(a, a.off1 + s * 16);
-    r.q1 = ld<uint4>(a, a.off2 + s * 16);
+    r.hdr = ld<uint4>(w, a.off0 + (s >> 2) * 16);
+    r.q0 = ld<uint4>(w, a.off1 + s * 16);
+    r.q1 = ld<uint4>(w, a.off2 + s * 16);
   }
   template <class XS>
   static __device__ __forceinline__ void load_x(const XS& x, int u, X& U) {
@@ -335,28 +339,29 @@ struct Q6K {
     uint32_t sc;       // the G int8 scales (low bytes)
     uint32_t d;        // fp16 super-block scale (low half)
   };
-  static __device__ __forceinline__ void load_raw(const GemvArgs& a, int row, int u, Raw& r) {
+  static __device__ __forceinline__ void load_raw(const GemvArgs& a, const uint8_t* w, int row,
+                                                  int u, Raw& r) {
     const uint32_t g = (uint32_t)row * a.nb * 16 + (uint32_t)u * G;  // first group
     const uint32_t offs[3] = {a.off0, a.off1, a.off2};
 #pragma unroll
     for (int p = 0; p < 3; ++p) {
       if constexpr (G == 4) {
-        const uint4 v = ld<uint4>(a, offs[p] + 4 * g);
+        const uint4 v = ld<uint4>(w, offs[p] + 4 * g);
         r.q[p][0] = v.x, r.q[p][1] = v.y, r.q[p][2] = v.z, r.q[p][3] = v.w;
       } else if constexpr (G == 2) {
-        const uint2 v = ld<uint2>(a, offs[p] + 4 * g);
+        const uint2 v = ld<uint2>(w, offs[p] + 4 * g);
         r.q[p][0] = v.x, r.q[p][1] = v.y;
       } else {
-        r.q[p][0] = ld<uint32_t>(a, offs[p] + 4 * g);
+        r.q[p][0] = ld<uint32_t>(w, offs[p] + 4 * g);
       }
     }
     if constexpr (G == 4)
-      r.sc = ld<uint32_t>(a, a.scales_off + g);
+      r.sc = ld<uint32_t>(w, a.scales_off + g);
     else if constexpr (G == 2)
-      r.sc = ld<uint16_t>(a, a.scales_off + g);
+      r.sc = ld<uint16_t>(w, a.scales_off + g);
     else
-      r.sc = ld<uint8_t>(a, a.scales_off + g);
-    r.d = ld<uint16_t>(a, a.d_off + (g >> 4) * 2);
+      r.sc = ld<uint8_t>(w, a.scales_off + g);
+    r.d = ld<uint16_t>(w, a.d_off + (g >> 4) * 2);
   }
   template <class XS>
   static __device__ __forceinline__ void load_x(const XS& x, int u, X& U) {
@@ -404,11 +409,12 @@ struct Q80 {
     uint4 q0, q1;
     uint32_t d;
   };
-  static __device__ __forceinline__ void load_raw(const GemvArgs& a, int row, int u, Raw& r) {
+  static __device__ __forceinline__ void load_raw(const GemvArgs& a, const uint8_t* w, int row,
+                                                  int u, Raw& r) {
     const uint32_t b = (uint32_t)row * a.nb + u;
-    r.q0 = ld<uint4>(a, a.off0 + b * 16);
-    r.q1 = ld<uint4>(a, a.off1 + b * 16);
-    r.d = ld<uint16_t>(a, a.d_off + b * 2);
+    r.q0 = ld<uint4>(w, a.off0 + b * 16);
+    r.q1 = ld<uint4>(w, a.off1 + b * 16);
+    r.d = ld<uint16_t>(w, a.d_off + b * 2);
   }
   template <class XS>
   static __device__ __forceinline__ void load_x(const XS& x, int u, X& U) {
@@ -454,17 +460,30 @@ __device__ __forceinline__ void unit_terms(const GemvArgs& a, const XS& xs, floa
   }
 }
 
+// The raw unit u of the RB rows of this thread (rows past the end re-read
+// the last row).  PAIR: virtual row v is row v/2 of w (v even) or w2 (odd).
+template <class F, int RB, bool PAIR>
+__device__ __forceinline__ void load_rows(const GemvArgs& a, int r0, int rows, int rlane, int u,
+                                          typename F::Raw (&raw)[RB]) {
+#pragma unroll
+  for (int k = 0; k < RB; ++k) {
+    const int v = r0 + min(rlane + a.row_par * k, rows - 1);
+    if constexpr (PAIR)
+      F::load_raw(a, (v & 1) ? a.w2 : a.w, v >> 1, u, raw[k]);
+    else
+      F::load_raw(a, a.w, v, u, raw[k]);
+  }
+}
+
 // Units it0, it0 + 1, ... of this thread (loads of each pass, then terms).
-template <class F, int RB, class XS>
+template <class F, int RB, bool PAIR, class XS>
 __device__ __forceinline__ void unit_passes(const GemvArgs& a, const XS& xs, float* terms,
                                             int r0, int rows, int rlane, int it0) {
   for (int it = it0; it < a.unit_iters; ++it) {
     const int u = threadIdx.x % a.uspan + it * a.uspan;
     if (u >= a.units) break;
     typename F::Raw raw[RB];
-#pragma unroll
-    for (int k = 0; k < RB; ++k)  // rows past the end re-read the last row
-      F::load_raw(a, r0 + min(rlane + a.row_par * k, rows - 1), u, raw[k]);
+    load_rows<F, RB, PAIR>(a, r0, rows, rlane, u, raw);
     unit_terms<F, RB>(a, xs, terms, rows, rlane, u, raw);
   }
 }
@@ -477,12 +496,11 @@ __device__ __forceinline__ void unit_passes(const GemvArgs& a, const XS& xs, flo
 // rmsnorm-ed by the workgroup (rms_scale_block, its squares in the LDS that
 // the terms take afterwards); the first pass's weight loads are issued
 // before, so their latency covers the sum of squares.
-template <class F, int RB, bool NORM>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
-  extern __shared__ __align__(16) float terms[];
+template <class F, int RB, bool NORM, bool PAIR>
+__device__ __forceinline__ void gemv_body(const GemvArgs& a, int wg, float* terms) {
   const int tid = threadIdx.x;
-  const int r0 = blockIdx.x * a.rows_per_wg;
-  const int rows = min(a.rows_per_wg, a.d - r0);
+  const int r0 = wg * a.rows_per_wg;
+  const int rows = min(a.rows_per_wg, (PAIR ? 2 * a.d : a.d) - r0);
   const int rlane = tid / a.uspan;
   const bool active = rlane < a.row_par;
   if constexpr (NORM) {
@@ -490,21 +508,17 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     const int u = tid % a.uspan;
     const bool first = active && u < a.units;
     typename F::Raw raw[RB];
-    if (first) {
-#pragma unroll
-      for (int k = 0; k < RB; ++k)
-        F::load_raw(a, r0 + min(rlane + a.row_par * k, rows - 1), u, raw[k]);
-    }
+    if (first) load_rows<F, RB, PAIR>(a, r0, rows, rlane, u, raw);
     // lanes 0..7 finish reading the squares before the helper's second
     // barrier, so the terms may overwrite them once it returns
     const float scale = rms_scale_block<kThreads>(a.x, a.n, a.norm_eps, terms, red);
     const NormX xs{a.x, a.norm_w, scale};
     if (first) {
       unit_terms<F, RB>(a, xs, terms, rows, rlane, u, raw);
-      unit_passes<F, RB>(a, xs, terms, r0, rows, rlane, 1);
+      unit_passes<F, RB, PAIR>(a, xs, terms, r0, rows, rlane, 1);
     }
   } else {
-    if (active) unit_passes<F, RB>(a, PlainX{a.x}, terms, r0, rows, rlane, 0);
+    if (active) unit_passes<F, RB, PAIR>(a, PlainX{a.x}, terms, r0, rows, rlane, 0);
   }
   __syncthreads();
   // the row's terms in order, 16 per step, the next step's reads in flight
@@ -535,38 +549,206 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
     }
     for (int s = full; s < a.terms; ++s) sumf = sumf + t[s];
     const int r = r0 + rr;
-    if (a.bias_mode == 1) sumf = sumf + a.bias[r];
-    if (a.bias_mode == 2) sumf = sumf + 0.0f;
-    if (a.gate) sumf = silu(a.gate[r]) * sumf;
-    if (a.resid) sumf = a.resid[r] + sumf;
-    a.out[r] = sumf;
+    if constexpr (PAIR) {
+      // rows come in (gate, up) pairs on adjacent lanes (r0 and rows even)
+      const float g = __shfl_xor(sumf, 1);
+      if (r & 1) a.out[r >> 1] = silu(g) * sumf;
+    } else {
+      if (a.bias_mode == 1) sumf = sumf + a.bias[r];
+      if (a.bias_mode == 2) sumf = sumf + 0.0f;
+      if (a.gate) sumf = silu(a.gate[r]) * sumf;
+      if (a.resid) sumf = a.resid[r] + sumf;
+      a.out[r] = sumf;
+    }
   }
 }
 
-template <class F, bool NORM>
+template <class F, int RB, bool NORM, bool PAIR>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
+  extern __shared__ __align__(16) float terms[];
+  gemv_body<F, RB, NORM, PAIR>(a, blockIdx.x, terms);
+}
+
+// Several GEMVs over the same x in one launch (the q, k and v projections),
+// each a segment of the grid with its own type, or one gate/up pair.
+constexpr int kMaxSeg = 3;
+struct MultiArgs {
+  GemvArgs seg[kMaxSeg];
+  int qtype[kMaxSeg];
+  int wg0[kMaxSeg + 1];  // first workgroup of each segment, then the grid size
+  int nseg;
+};
+
+template <int RB, bool NORM, bool PAIR>
+__global__ __launch_bounds__(kThreads) void gemv_multi_kernel(MultiArgs m) {
+  extern __shared__ __align__(16) float terms[];
+  int s = 0;
+  while (s + 1 < m.nseg && (int)blockIdx.x >= m.wg0[s + 1]) ++s;
+  const int wg = blockIdx.x - m.wg0[s];
+  switch (m.qtype[s]) {
+    case kTypeQ4K: gemv_body<Q4K, RB, NORM, PAIR>(m.seg[s], wg, terms); break;
+    case kTypeQ8_0: gemv_body<Q80, RB, NORM, PAIR>(m.seg[s], wg, terms); break;
+    default: gemv_body<Q6K<4>, RB, NORM, PAIR>(m.seg[s], wg, terms); break;
+  }
+}
+
+template <class F, bool NORM, bool PAIR>
 void launch_rb(int rb, int grid, size_t lds, hipStream_t st, const GemvArgs& a) {
   switch (rb) {
     case 1:
-      hipLaunchKernelGGL((gemv_kernel<F, 1, NORM>), dim3(grid), dim3(kThreads), lds, st, a);
+      hipLaunchKernelGGL((gemv_kernel<F, 1, NORM, PAIR>), dim3(grid), dim3(kThreads), lds, st, a);
       break;
     case 2:
-      hipLaunchKernelGGL((gemv_kernel<F, 2, NORM>), dim3(grid), dim3(kThreads), lds, st, a);
+      hipLaunchKernelGGL((gemv_kernel<F, 2, NORM, PAIR>), dim3(grid), dim3(kThreads), lds, st, a);
       break;
     case 4:
-      hipLaunchKernelGGL((gemv_kernel<F, 4, NORM>), dim3(grid), dim3(kThreads), lds, st, a);
+      hipLaunchKernelGGL((gemv_kernel<F, 4, NORM, PAIR>), dim3(grid), dim3(kThreads), lds, st, a);
       break;
     default:
-      hipLaunchKernelGGL((gemv_kernel<F, 8, NORM>), dim3(grid), dim3(kThreads), lds, st, a);
+      hipLaunchKernelGGL((gemv_kernel<F, 8, NORM, PAIR>), dim3(grid), dim3(kThreads), lds, st, a);
       break;
   }
 }
 
+// A gate/up pair always reads rmsnorm(x) (the FFN input), so only that
+// combination is instantiated.
 template <class F>
-void launch_fmt(bool norm, int rb, int grid, size_t lds, hipStream_t st, const GemvArgs& a) {
-  if (norm)
-    launch_rb<F, true>(rb, grid, lds, st, a);
+void launch_fmt(bool norm, bool pair, int rb, int grid, size_t lds, hipStream_t st,
+                const GemvArgs& a) {
+  if (pair)
+    launch_rb<F, true, true>(rb, grid, lds, st, a);
+  else if (norm)
+    launch_rb<F, true, false>(rb, grid, lds, st, a);
   else
-    launch_rb<F, false>(rb, grid, lds, st, a);
+    launch_rb<F, false, false>(rb, grid, lds, st, a);
+}
+
+template <bool NORM>
+void launch_multi(int rb, int grid, size_t lds, hipStream_t st, const MultiArgs& m) {
+  switch (rb) {
+    case 1:
+      hipLaunchKernelGGL((gemv_multi_kernel<1, NORM, false>), dim3(grid), dim3(kThreads), lds, st,
+                         m);
+      break;
+    case 2:
+      hipLaunchKernelGGL((gemv_multi_kernel<2, NORM, false>), dim3(grid), dim3(kThreads), lds, st,
+                         m);
+      break;
+    default:
+      hipLaunchKernelGGL((gemv_multi_kernel<4, NORM, false>), dim3(grid), dim3(kThreads), lds, st,
+                         m);
+      break;
+  }
+}
+
+// Fills everything of a but rows_per_wg from one call.  0 or -1 (error set).
+int prepare(const GemvCall& g, GemvArgs& a) {
+  Layout L;
+  if (!make_layout(g.qtype, g.n, g.d, L)) {
+    set_error("plh_gemv: no GEMV for type %d with n=%d d=%d", g.qtype, g.n, g.d);
+    return -1;
+  }
+  if (!g.w || !g.x || !g.out) {
+    set_error("plh_gemv: null pointer");
+    return -1;
+  }
+  if (g.bias && g.bias_zero) {
+    set_error("plh_gemv_ex: a bias and bias_zero together");
+    return -1;
+  }
+  if (g.norm_w && g.n > kMaxNormN) {
+    set_error("plh_gemv_ex: rmsnorm of %d elements exceeds %d", g.n, kMaxNormN);
+    return -1;
+  }
+  const int n = g.n, qtype = g.qtype;
+  a = GemvArgs{};
+  a.w = (const uint8_t*)g.w;
+  a.x = g.x;
+  a.out = g.out;
+  a.d = g.d;
+  a.nb = L.nb;
+  // Q6_K lanes take four groups (64 weights, like a Q4_K sub-block): the
+  // per-row work of a unit (scale, hsum, addressing) is shared by more weights
+  const int q6_groups = 4;
+  a.units = qtype == kTypeQ4K ? n / 64 : (qtype == kTypeQ6K ? n / (16 * q6_groups) : n / 32);
+  a.terms = qtype == kTypeQ4K ? n / 64 : (qtype == kTypeQ6K ? n / 16 : n / 32);
+  a.uspan = a.units < kThreads ? a.units : kThreads;
+  a.row_par = kThreads / a.uspan;
+  a.unit_iters = (a.units + a.uspan - 1) / a.uspan;
+  a.tpitch = (a.terms + 3) / 4 * 4 + 4;  // 16-byte rows, staggered banks
+  a.off0 = (uint32_t)L.off[0];
+  a.off1 = (uint32_t)L.off[1];
+  a.off2 = (uint32_t)L.off[2];
+  a.scales_off = (uint32_t)L.scales_off;
+  a.d_off = (uint32_t)L.d_off;
+  a.bias = g.bias;
+  a.gate = g.gate;
+  a.resid = g.resid;
+  a.bias_mode = g.bias ? 1 : (g.bias_zero ? 2 : 0);
+  a.norm_w = g.norm_w;
+  a.norm_eps = g.norm_eps;
+  a.n = n;
+  return 0;
+}
+
+int lds_rows(const GemvArgs& a) { return (int)((64 * 1024) / (sizeof(float) * (size_t)a.tpitch)); }
+
+// Rows per thread for a launch over these segments (rows[s]: the segment's
+// rows, 2d for a gate/up pair): the largest of 4, 2, 1 that still gives at
+// least 0.6 workgroups per CU and keeps every workgroup's terms within 64 KiB
+// of LDS (measured on the TinyLlama and output-projection shapes: more rows
+// in flight per thread beat more workgroups until the grid no longer covers
+// the CUs; 8 rows cost occupancy).  A pair needs an even row count per
+// workgroup.  -1 when a row is too long for the term buffer.
+int pick_rb(const GemvArgs* seg, const int* rows, int nseg, bool pair, int max_rb) {
+  const int cus = ctx().num_cus > 0 ? ctx().num_cus : 256;
+  auto grid_of = [&](int rb) {
+    long g = 0;
+    for (int s = 0; s < nseg; ++s) g += (rows[s] + seg[s].row_par * rb - 1) / (seg[s].row_par * rb);
+    return g;
+  };
+  auto lds_ok = [&](int rb) {
+    for (int s = 0; s < nseg; ++s)
+      if (seg[s].row_par * rb > lds_rows(seg[s])) return false;
+    return true;
+  };
+  int rb = 4;
+  while (rb > 1 && (grid_of(rb) * 10 < 6L * cus || !lds_ok(rb))) rb /= 2;
+  if (g_gemv_rows_per_thread > 0) rb = g_gemv_rows_per_thread;
+  if (rb > max_rb) rb = max_rb;
+  if (pair && (seg[0].row_par * rb) % 2) rb *= 2;
+  if (!lds_ok(rb)) {
+    set_error("plh_gemv: row of %d weights too long for the term buffer", seg[0].n);
+    return -1;
+  }
+  return rb;
+}
+
+size_t lds_bytes(const GemvArgs& a) {
+  size_t lds = sizeof(float) * (size_t)a.rows_per_wg * a.tpitch;
+  if (a.norm_w) {  // the squares of the rmsnorm share the terms' LDS
+    const size_t sq = sizeof(float) * 8 * (size_t)rms_sq_pitch(a.n);
+    if (sq > lds) lds = sq;
+  }
+  return lds;
+}
+
+int launch_single(int qtype, bool pair, const GemvArgs& a0, int rows) {
+  GemvArgs a = a0;
+  const int rb = pick_rb(&a, &rows, 1, pair, 8);
+  if (rb < 0) return -1;
+  a.rows_per_wg = a.row_par * rb;
+  const int grid = (rows + a.rows_per_wg - 1) / a.rows_per_wg;
+  const size_t lds = lds_bytes(a);
+  hipStream_t st = ctx().stream;
+  const bool norm = a.norm_w != nullptr;
+  if (qtype == kTypeQ4K)
+    launch_fmt<Q4K>(norm, pair, rb, grid, lds, st, a);
+  else if (qtype == kTypeQ8_0)
+    launch_fmt<Q80>(norm, pair, rb, grid, lds, st, a);
+  else
+    launch_fmt<Q6K<4>>(norm, pair, rb, grid, lds, st, a);
+  return check_hip(hipGetLastError(), "gemv_kernel launch");
 }
 
 }  // namespace
@@ -631,94 +813,75 @@ int plh_gemv_ex(int qtype, int n, int d, const void* dev, const float* x, float*
 namespace plh {
 
 int gemv_launch(const GemvCall& g) {
-  const int qtype = g.qtype, n = g.n, d = g.d;
-  const void* dev = g.w;
-  const float *x = g.x, *norm_w = g.norm_w, *bias = g.bias, *gate = g.gate, *resid = g.resid;
-  float* out = g.out;
-  const int bias_zero = g.bias_zero;
-  const float norm_eps = g.norm_eps;
-  Layout L;
-  if (!make_layout(qtype, n, d, L)) {
-    set_error("plh_gemv: no GEMV for type %d with n=%d d=%d", qtype, n, d);
-    return -1;
-  }
-  if (!dev || !x || !out) {
-    set_error("plh_gemv: null pointer");
-    return -1;
-  }
-  if (bias && bias_zero) {
-    set_error("plh_gemv_ex: a bias and bias_zero together");
-    return -1;
-  }
-  if (norm_w && n > kMaxNormN) {
-    set_error("plh_gemv_ex: rmsnorm of %d elements exceeds %d", n, kMaxNormN);
-    return -1;
-  }
-
-  Context& c = ctx();
-  if (!c.stream) {
+  if (!ctx().stream) {
     set_error("plh_gemv: plh_init has not been called");
     return -1;
   }
-  GemvArgs a{};
-  a.w = (const uint8_t*)dev;
-  a.x = x;
-  a.out = out;
-  a.d = d;
-  a.nb = L.nb;
-  // Q6_K lanes take four groups (64 weights, like a Q4_K sub-block): the
-  // per-row work of a unit (scale, hsum, addressing) is shared by more weights
-  const int q6_groups = 4;
-  a.units = qtype == kTypeQ4K ? n / 64 : (qtype == kTypeQ6K ? n / (16 * q6_groups) : n / 32);
-  a.terms = qtype == kTypeQ4K ? n / 64 : (qtype == kTypeQ6K ? n / 16 : n / 32);
-  a.uspan = a.units < kThreads ? a.units : kThreads;
-  a.row_par = kThreads / a.uspan;
-  a.unit_iters = (a.units + a.uspan - 1) / a.uspan;
-  a.tpitch = (a.terms + 3) / 4 * 4 + 4;  // 16-byte rows, staggered banks
-  a.off0 = (uint32_t)L.off[0];
-  a.off1 = (uint32_t)L.off[1];
-  a.off2 = (uint32_t)L.off[2];
-  a.scales_off = (uint32_t)L.scales_off;
-  a.d_off = (uint32_t)L.d_off;
-  a.bias = bias;
-  a.gate = gate;
-  a.resid = resid;
-  a.bias_mode = bias ? 1 : (bias_zero ? 2 : 0);
-  a.norm_w = norm_w;
-  a.norm_eps = norm_eps;
-  a.n = n;
+  GemvArgs a;
+  if (prepare(g, a)) return -1;
+  return launch_single(g.qtype, false, a, g.d);
+}
 
-  // rows per thread: the largest of 4, 2, 1 that still gives at least 0.6
-  // workgroups per CU and keeps the workgroup's terms within 64 KiB of LDS
-  // (measured on the TinyLlama and output-projection shapes: more rows in
-  // flight per thread beat more workgroups until the grid no longer covers
-  // the CUs; 8 rows cost occupancy)
-  const int cus = c.num_cus > 0 ? c.num_cus : 256;
-  const int lds_rows = (int)((64 * 1024) / (sizeof(float) * (size_t)a.tpitch));
-  int rb = 4;
-  while (rb > 1 && ((long)(d + a.row_par * rb - 1) / (a.row_par * rb) * 10 < 6L * cus ||
-                    a.row_par * rb > lds_rows))
-    rb /= 2;
-  if (g_gemv_rows_per_thread > 0) rb = g_gemv_rows_per_thread;
-  if (a.row_par * rb > lds_rows) {
-    set_error("plh_gemv: row of %d weights too long for the term buffer", n);
+int gemv_multi_launch(const GemvCall* g, int n) {
+  if (!ctx().stream) {
+    set_error("plh_gemv: plh_init has not been called");
     return -1;
   }
-  a.rows_per_wg = a.row_par * rb;
-  size_t lds = sizeof(float) * (size_t)a.rows_per_wg * a.tpitch;
-  if (norm_w) {  // the squares of the rmsnorm share the terms' LDS
-    const size_t sq = sizeof(float) * 8 * (size_t)rms_sq_pitch(n);
-    if (sq > lds) lds = sq;
+  if (n < 1 || n > kMaxSeg) {
+    set_error("gemv_multi_launch: %d segments (1..%d)", n, kMaxSeg);
+    return -1;
   }
-  const int grid = (d + a.rows_per_wg - 1) / a.rows_per_wg;
-  const bool norm = norm_w != nullptr;
-  if (qtype == kTypeQ4K)
-    launch_fmt<Q4K>(norm, rb, grid, lds, c.stream, a);
-  else if (qtype == kTypeQ8_0)
-    launch_fmt<Q80>(norm, rb, grid, lds, c.stream, a);
+  MultiArgs m{};
+  int rows[kMaxSeg];
+  for (int s = 0; s < n; ++s) {
+    if (g[s].x != g[0].x || (g[s].norm_w == nullptr) != (g[0].norm_w == nullptr)) {
+      set_error("gemv_multi_launch: segments must share x and the rmsnorm prologue");
+      return -1;
+    }
+    if (prepare(g[s], m.seg[s])) return -1;
+    m.qtype[s] = g[s].qtype;
+    rows[s] = g[s].d;
+  }
+  const int rb = pick_rb(m.seg, rows, n, false, 4);
+  if (rb < 0) return -1;
+  size_t lds = 0;
+  m.nseg = n;
+  m.wg0[0] = 0;
+  for (int s = 0; s < n; ++s) {
+    m.seg[s].rows_per_wg = m.seg[s].row_par * rb;
+    m.wg0[s + 1] = m.wg0[s] + (rows[s] + m.seg[s].rows_per_wg - 1) / m.seg[s].rows_per_wg;
+    const size_t b = lds_bytes(m.seg[s]);
+    if (b > lds) lds = b;
+  }
+  if (g[0].norm_w)
+    launch_multi<true>(rb, m.wg0[n], lds, ctx().stream, m);
   else
-    launch_fmt<Q6K<4>>(norm, rb, grid, lds, c.stream, a);
-  return check_hip(hipGetLastError(), "gemv_kernel launch");
+    launch_multi<false>(rb, m.wg0[n], lds, ctx().stream, m);
+  return check_hip(hipGetLastError(), "gemv_multi_kernel launch");
+}
+
+int gemv_pair_launch(const GemvCall& gate, const GemvCall& up) {
+  if (!ctx().stream) {
+    set_error("plh_gemv: plh_init has not been called");
+    return -1;
+  }
+  if (gate.qtype != up.qtype || gate.n != up.n || gate.d != up.d || gate.x != up.x ||
+      !gate.norm_w || gate.norm_w != up.norm_w || gate.norm_eps != up.norm_eps || gate.bias ||
+      up.bias || gate.bias_zero || up.bias_zero || gate.gate || up.gate || gate.resid ||
+      up.resid) {
+    set_error("gemv_pair_launch: gate and up must match in type, shape, x and rmsnorm, "
+              "without other epilogues");
+    return -1;
+  }
+  GemvArgs a;
+  if (prepare(up, a)) return -1;
+  a.w = (const uint8_t*)gate.w;
+  a.w2 = (const uint8_t*)up.w;
+  if (!a.w) {
+    set_error("plh_gemv: null pointer");
+    return -1;
+  }
+  return launch_single(up.qtype, true, a, 2 * up.d);
 }
 
 }  // namespace plh

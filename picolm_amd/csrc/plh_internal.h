@@ -41,6 +41,12 @@ struct GemvCall {
   const float* resid;
 };
 int gemv_launch(const GemvCall& g);
+// Up to three GEMVs over the same x (and the same rmsnorm prologue, if any)
+// in one launch: the q, k and v projections.
+int gemv_multi_launch(const GemvCall* g, int n);
+// hb = silu(gate(xn)) * up(xn) in one launch (model.c:906-916), gate and up
+// of the same type and shape, both with the rmsnorm prologue; out = up.out.
+int gemv_pair_launch(const GemvCall& gate, const GemvCall& up);
 
 // Makes sure the workspace holds at least `bytes`.  Growing it waits for the
 // queued work (which may still read the old one).  Returns 0 or -1.
