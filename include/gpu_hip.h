@@ -13,6 +13,7 @@
  *   PICOLM_HIP_DEVICE=N   device index (default 0)
  *   PICOLM_GPU_LAYERS=N   only layers < N use the GPU; later layers get -1
  *   PICOLM_HIP_MATMUL=0   upload no weight matrices (gpu_try_matmul -> -1)
+ *   PICOLM_HIP_FORWARD=0  no whole-forward offload (gpu_try_forward* -> -1)
  *
  * Host caches stay authoritative: every successful call copies the rows it
  * appended back into m->state.key_cache / val_cache, so the CPU fallback and
@@ -59,6 +60,20 @@ int gpu_try_attention(model_t *m, int layer, int pos, float *q, float *k,
  * out + bi*n_embd (model.c:1057). */
 int gpu_try_attention_prefill(model_t *m, int layer, int start_pos, int n_tokens,
                               float *q, float *k, const float *v, float *out);
+/* Replaces model_forward_ex(m, token, pos, n_layers) (model.c:746-925) with
+ * the whole forward pass on the device: fills m->state.logits and m->state.x
+ * (the final normalised residual) and appends row pos of every layer's
+ * caches (device and host).  Available when gpu_upload_model put every
+ * layer's seven projections and the output matrix on the device (GEMV
+ * types), the embedding type is F32/F16/Q4_0/Q8_0/Q4_K/Q6_K and the q /
+ * output biases are F32 in the file; -1 otherwise (nothing changed).  The
+ * logits match the reference's to the attention/silu exp tolerance; the
+ * first layer's KV rows bit for bit. */
+int gpu_try_forward(model_t *m, int token, int pos);
+/* Replaces model_forward_prefill(m, tokens, n_tokens, start_pos)
+ * (model.c:939-1144): logits / x of the last token, rows start_pos.. of
+ * every layer appended. */
+int gpu_try_forward_prefill(model_t *m, const int *tokens, int n_tokens, int start_pos);
 /* KV coherence for kvcache_save / kvcache_load (model.c:1146-1259): copy rows
  * 0..n_pos-1 of every layer device -> host (download) or host -> device
  * (upload). 0 or -1. */
@@ -82,6 +97,12 @@ static inline int gpu_try_attention(model_t *m, int l, int p, float *q, float *k
 static inline int gpu_try_attention_prefill(model_t *m, int l, int s, int n, float *q,
                                             float *k, const float *v, float *o) {
     (void)m; (void)l; (void)s; (void)n; (void)q; (void)k; (void)v; (void)o; return -1;
+}
+static inline int gpu_try_forward(model_t *m, int t, int p) {
+    (void)m; (void)t; (void)p; return -1;
+}
+static inline int gpu_try_forward_prefill(model_t *m, const int *t, int n, int s) {
+    (void)m; (void)t; (void)n; (void)s; return -1;
 }
 static inline int gpu_kv_download(const model_t *m, int n) { (void)m; (void)n; return -1; }
 static inline int gpu_kv_upload(const model_t *m, int n) { (void)m; (void)n; return -1; }

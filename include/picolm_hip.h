@@ -241,6 +241,15 @@ size_t plh_forward_workspace_bytes(const plh_model *m);
  * or Q8_0.  Queued on the library stream. */
 int plh_forward(const plh_model *m, int token, int pos, void *workspace, float *logits,
                 float *x_out);
+/* Replaces model_forward_prefill(m, tokens, n_tokens, start_pos)
+ * (model.c:939-1144): the prompt tokens (HOST array) at positions
+ * start_pos.., rows start_pos..start_pos+n_tokens-1 of every layer's caches
+ * appended, logits and x_out of the last token only.  Bit-for-bit the
+ * reference's per-token arithmetic (q and output biases only when present,
+ * model.c:1002-1017, 1095-1099); tokens run one after another through the
+ * decode path. */
+int plh_forward_prefill(const plh_model *m, const int *tokens, int n_tokens, int start_pos,
+                        void *workspace, float *logits, float *x_out);
 
 /* Tuning knobs (bench sweeps).  key 1: decode target workgroups per launch
  * (0 = default); key 2: decode contexts of at most this many positions are

@@ -101,6 +101,7 @@ _SIGS = {
     "plh_dequantize_row": (_i, [_i, _vp, _vp, _i]),
     "plh_forward_workspace_bytes": (_sz, [C.POINTER(PlhModel)]),
     "plh_forward": (_i, [C.POINTER(PlhModel), _i, _i, _vp, _vp, _vp]),
+    "plh_forward_prefill": (_i, [C.POINTER(PlhModel), _vp, _i, _i, _vp, _vp, _vp]),
     "plh_set_tuning": (_i, [_i, _i]),
 }
 

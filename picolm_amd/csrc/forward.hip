@@ -244,19 +244,18 @@ size_t plh_forward_workspace_bytes(const plh_model* m) {
   return carve(m, nullptr).bytes;
 }
 
-int plh_forward(const plh_model* m, int token, int pos, void* workspace, float* logits,
-                float* x_out) {
-  Context& c = ctx();
-  if (!c.stream) {
-    set_error("plh_forward: plh_init has not been called");
-    return -1;
-  }
-  if (!model_ok(m)) return -1;
-  if (token < 0 || token >= m->vocab_size || pos < 0 || pos >= m->max_seq_len || !workspace ||
-      !logits) {
-    set_error("plh_forward: token %d / pos %d out of range or null buffer", token, pos);
-    return -1;
-  }
+}  // extern "C"
+
+namespace {
+
+// One token through every layer (arguments checked by the caller).
+// bias_always: model_forward_ex's handling of the q and output biases (added
+// always, zeros when absent, model.c:781-782 / 895-896) rather than
+// model_forward_prefill's (added only when present, model.c:1002-1006 /
+// 1095-1099).  logits == NULL stops after the last layer (a prompt token
+// whose logits nobody reads).
+int forward_token(const plh_model* m, int token, int pos, void* workspace, bool bias_always,
+                  float* logits, float* x_out) {
   const int E = m->n_embd, F = m->n_ffn;
   const int Q = m->n_heads * m->head_dim, KV = m->n_kv_heads * m->head_dim;
   const float eps = m->rms_norm_eps;
@@ -279,7 +278,8 @@ int plh_forward(const plh_model* m, int token, int pos, void* workspace, float* 
     const plh_layer& L = m->layers[l];
     // attention block (model.c:777-897): q, k, v in one launch
     const GemvCall qkv[3] = {
-        call(L.q, E, Q, a.x, a.q, L.attn_norm, L.q_bias, L.q_bias == nullptr, nullptr, nullptr),
+        call(L.q, E, Q, a.x, a.q, L.attn_norm, L.q_bias, bias_always && !L.q_bias, nullptr,
+             nullptr),
         call(L.k, E, KV, a.x, a.k, L.attn_norm, L.k_bias, 0, nullptr, nullptr),
         call(L.v, E, KV, a.x, a.v, L.attn_norm, L.v_bias, 0, nullptr, nullptr)};
     if (gemv_multi_launch(qkv, 3)) return -1;
@@ -294,8 +294,8 @@ int plh_forward(const plh_model* m, int token, int pos, void* workspace, float* 
                                               m->rope_cos, m->rope_sin, a.att);
     if (rc) return -1;
     // x = x + (Wo att + o_bias)
-    if (gemv_launch(call(L.o, Q, E, a.att, a.x, nullptr, L.o_bias, L.o_bias == nullptr, nullptr,
-                         a.x)))
+    if (gemv_launch(call(L.o, Q, E, a.att, a.x, nullptr, L.o_bias, bias_always && !L.o_bias,
+                         nullptr, a.x)))
       return -1;
     // SwiGLU block (model.c:899-922): hb = silu(gate xn) * (up xn), xn = rmsnorm(x),
     // in one launch when gate and up share a type; then x = x + Wdown hb
@@ -310,11 +310,58 @@ int plh_forward(const plh_model* m, int token, int pos, void* workspace, float* 
     }
     if (gemv_launch(call(L.down, F, E, a.hb, a.x, nullptr, nullptr, 0, nullptr, a.x))) return -1;
   }
+  if (!logits) return 0;
   // final norm and logits (model.c:918-922)
   if (gemv_launch(call(m->output, E, m->vocab_size, a.x, logits, m->output_norm, nullptr, 0,
                        nullptr, nullptr)))
     return -1;
   if (x_out && launch_rmsnorm(a.x, m->output_norm, x_out, E, eps)) return -1;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int plh_forward(const plh_model* m, int token, int pos, void* workspace, float* logits,
+                float* x_out) {
+  if (!ctx().stream) {
+    set_error("plh_forward: plh_init has not been called");
+    return -1;
+  }
+  if (!model_ok(m)) return -1;
+  if (token < 0 || token >= m->vocab_size || pos < 0 || pos >= m->max_seq_len || !workspace ||
+      !logits) {
+    set_error("plh_forward: token %d / pos %d out of range or null buffer", token, pos);
+    return -1;
+  }
+  return forward_token(m, token, pos, workspace, true, logits, x_out);
+}
+
+int plh_forward_prefill(const plh_model* m, const int* tokens, int n_tokens, int start_pos,
+                        void* workspace, float* logits, float* x_out) {
+  if (!ctx().stream) {
+    set_error("plh_forward_prefill: plh_init has not been called");
+    return -1;
+  }
+  if (!model_ok(m)) return -1;
+  if (!tokens || n_tokens < 1 || start_pos < 0 ||
+      (long)start_pos + n_tokens > (long)m->max_seq_len || !workspace || !logits) {
+    set_error("plh_forward_prefill: %d tokens at %d do not fit %d positions (or null buffer)",
+              n_tokens, start_pos, m->max_seq_len);
+    return -1;
+  }
+  for (int bi = 0; bi < n_tokens; ++bi)
+    if (tokens[bi] < 0 || tokens[bi] >= m->vocab_size) {
+      set_error("plh_forward_prefill: token %d out of range", tokens[bi]);
+      return -1;
+    }
+  for (int bi = 0; bi < n_tokens; ++bi) {
+    const bool last = bi == n_tokens - 1;
+    if (forward_token(m, tokens[bi], start_pos + bi, workspace, false, last ? logits : nullptr,
+                      last ? x_out : nullptr))
+      return -1;
+  }
   return 0;
 }
 

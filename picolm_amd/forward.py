@@ -82,6 +82,17 @@ class DeviceModel:
                               self.logits.ptr if logits is None else logits,
                               self.x_out.ptr if x_out is None else x_out), "plh_forward")
 
+    def prefill(self, tokens, start_pos: int, logits: int | None = None,
+                x_out: int | None = None) -> None:
+        """Queues model_forward_prefill(tokens, start_pos): logits of the
+        last token."""
+        t = np.ascontiguousarray(tokens, np.int32)
+        check(lib.plh_forward_prefill(C.byref(self.desc), t.ctypes.data, len(t), int(start_pos),
+                                      self.workspace.ptr,
+                                      self.logits.ptr if logits is None else logits,
+                                      self.x_out.ptr if x_out is None else x_out),
+              "plh_forward_prefill")
+
     def fetch_logits(self) -> np.ndarray:
         return self.logits.download(np.float32, (self.host.vocab_size,))
 

@@ -25,13 +25,22 @@
  * with the tables and the *_qknorm entry points normalise q and k before
  * RoPE, with config.rms_norm_eps.
  *
+ * When every matrix of the model is on the device, gpu_try_forward and
+ * gpu_try_forward_prefill run the whole forward pass there (plh_forward):
+ * the run state's dequantized norms and biases (model.c:644-707) and the raw
+ * embedding rows are uploaded too; a call copies back the logits, the final
+ * normalised residual (state.x) and the KV rows it appended.
+ *
  * Built with USE_HIP; compiles against either this package's model.h or the
  * reference's (it reads only config.{n_embd, n_ffn, n_heads, n_kv_heads,
  * n_layers, vocab_size, max_seq_len, head_dim, rope_type, rms_norm_eps},
- * weights.{output, type_output} and weights.layers[].{attn_q, attn_k, attn_v,
- * attn_output, ffn_gate, ffn_up, ffn_down, their type_* fields, attn_q_norm},
- * and state.{key_cache, val_cache, rope_cos, rope_sin, attn_q_norm_w,
- * attn_k_norm_w}).
+ * weights.{token_embd, type_token_embd, output, type_output} and
+ * weights.layers[].{attn_q, attn_k, attn_v, attn_output, ffn_gate, ffn_up,
+ * ffn_down, their type_* fields, attn_q_norm, attn_q_b, attn_k_b, attn_v_b,
+ * attn_output_b, type_attn_q_b, type_attn_output_b}, and state.{x, logits,
+ * key_cache, val_cache, rope_cos, rope_sin, attn_norm_w, ffn_norm_w,
+ * attn_q_norm_w, attn_k_norm_w, output_norm_w, attn_q_bias, attn_k_bias,
+ * attn_v_bias, attn_output_bias}).
  */
 #include "gpu_hip.h"
 
@@ -65,6 +74,14 @@ static struct {
     int n_weights, cap_weights;
     float *d_mx, *d_mout;           /* GEMV staging: x [mx_cap], out [mout_cap] */
     int mx_cap, mout_cap;
+    /* whole forward pass (gpu_try_forward): NULL model when unavailable */
+    plh_model fwd;
+    plh_layer fwd_layers[MAX_LAYERS];
+    float *d_fwd_vecs;              /* norms and biases, one block */
+    void *d_embd;                   /* raw token_embd rows */
+    void *d_fwd_ws;                 /* plh_forward workspace */
+    float *d_logits, *d_x;
+    int fwd_ready;
 } gs;
 
 static int env_int(const char *name, int dflt) {
@@ -224,6 +241,147 @@ static void free_weights(void) {
     gs.mx_cap = gs.mout_cap = 0;
 }
 
+static const gpu_weight_t *find_weight(const void *host) {
+    for (int i = 0; i < gs.n_weights; i++)
+        if (gs.weights[i].host == host) return &gs.weights[i];
+    return NULL;
+}
+
+static int fwd_matrix(plh_matrix *pm, const void *host, gguf_type_t qtype, int n, int d) {
+    const gpu_weight_t *w = find_weight(host);
+    if (!w || w->qtype != (int)qtype || w->n != n || w->d != d) return -1;
+    pm->qtype = w->qtype;
+    pm->w = w->dev;
+    return 0;
+}
+
+/* Bytes of one embedding row for the types plh_forward dequantises on the
+ * device (quant.c:283-325). */
+static size_t embd_row_bytes(gguf_type_t t, int n) {
+    switch ((int)t) {
+        case GGUF_TYPE_F32: return (size_t)n * 4;
+        case GGUF_TYPE_F16: return (size_t)n * 2;
+        case GGUF_TYPE_Q4_0: return n % 32 ? 0 : (size_t)(n / 32) * 18;
+        case GGUF_TYPE_Q8_0: return n % 32 ? 0 : (size_t)(n / 32) * 34;
+        case GGUF_TYPE_Q4_K: return n % 256 ? 0 : (size_t)(n / 256) * 144;
+        case GGUF_TYPE_Q6_K: return n % 256 ? 0 : (size_t)(n / 256) * 210;
+        default: return 0;
+    }
+}
+
+static void free_forward(void) {
+    plh_free(gs.d_fwd_vecs);
+    plh_free(gs.d_embd);
+    plh_free(gs.d_fwd_ws);
+    plh_free(gs.d_logits);
+    plh_free(gs.d_x);
+    gs.d_fwd_vecs = NULL;
+    gs.d_embd = gs.d_fwd_ws = NULL;
+    gs.d_logits = gs.d_x = NULL;
+    gs.fwd_ready = 0;
+}
+
+/* The device model of gpu_try_forward: every layer's seven projections and
+ * the output matrix must already be uploaded (GEMV types), the embedding of
+ * a type the device dequantises, the biases fp32 (the reference adds the
+ * pre-dequantized q and output biases through dequantize_row of their file
+ * type, model.c:781-782, which only an F32 file type leaves intact).  Returns
+ * 0 with gs.fwd_ready set, 1 when the model does not qualify (the per-op
+ * hooks still run), -1 on a device failure. */
+static int upload_forward(const model_t *m) {
+    const model_config_t *c = &m->config;
+    const model_weights_t *w = &m->weights;
+    const run_state_t *st = &m->state;
+    const int E = c->n_embd, F = c->n_ffn, Q = c->n_heads * c->head_dim;
+    const int KV = c->n_kv_heads * c->head_dim;
+    if (gs.gpu_layers < c->n_layers || E > 12288 || !w->token_embd || !st->logits || !st->x)
+        return 1;
+    const size_t rb = embd_row_bytes(w->type_token_embd, E);
+    if (rb == 0) return 1;
+    plh_model *pm = &gs.fwd;
+    memset(pm, 0, sizeof *pm);
+    if (fwd_matrix(&pm->output, w->output, w->type_output, E, c->vocab_size)) return 1;
+    /* fp32 vectors: per layer attn_norm, ffn_norm [E], q_bias [Q], k_bias,
+     * v_bias [KV], o_bias [E]; then output_norm [E] */
+    const size_t per_layer = (size_t)3 * E + Q + 2 * (size_t)KV;
+    for (int l = 0; l < c->n_layers; l++) {
+        const layer_weights_t *lw = &w->layers[l];
+        plh_layer *pl = &gs.fwd_layers[l];
+        memset(pl, 0, sizeof *pl);
+        if (fwd_matrix(&pl->q, lw->attn_q, lw->type_attn_q, E, Q) ||
+            fwd_matrix(&pl->k, lw->attn_k, lw->type_attn_k, E, KV) ||
+            fwd_matrix(&pl->v, lw->attn_v, lw->type_attn_v, E, KV) ||
+            fwd_matrix(&pl->o, lw->attn_output, lw->type_attn_output, Q, E) ||
+            fwd_matrix(&pl->gate, lw->ffn_gate, lw->type_ffn_gate, E, F) ||
+            fwd_matrix(&pl->up, lw->ffn_up, lw->type_ffn_up, E, F) ||
+            fwd_matrix(&pl->down, lw->ffn_down, lw->type_ffn_down, F, E))
+            return 1;
+        if ((lw->attn_q_b && lw->type_attn_q_b != GGUF_TYPE_F32) ||
+            (lw->attn_output_b && lw->type_attn_output_b != GGUF_TYPE_F32))
+            return 1;
+        if (!st->attn_norm_w[l] || !st->ffn_norm_w[l] || !st->attn_q_bias[l] ||
+            !st->attn_output_bias[l] || (lw->attn_k_b && !st->attn_k_bias[l]) ||
+            (lw->attn_v_b && !st->attn_v_bias[l]))
+            return 1;
+    }
+    if (!st->output_norm_w) return 1;
+    size_t nvec = per_layer * (size_t)c->n_layers + (size_t)E;
+    gs.d_fwd_vecs = (float *)plh_malloc(nvec * sizeof(float));
+    gs.d_embd = plh_malloc(rb * (size_t)c->vocab_size);
+    gs.d_logits = (float *)plh_malloc((size_t)c->vocab_size * sizeof(float));
+    gs.d_x = (float *)plh_malloc((size_t)E * sizeof(float));
+    if (!gs.d_fwd_vecs || !gs.d_embd || !gs.d_logits || !gs.d_x) return -1;
+    if (plh_memcpy_htod(gs.d_embd, w->token_embd, rb * (size_t)c->vocab_size)) return -1;
+    float *dv = gs.d_fwd_vecs;
+#define PUT(dst, src, count)                                                   \
+    do {                                                                       \
+        if (plh_memcpy_htod(dv, (src), (size_t)(count) * sizeof(float))) return -1; \
+        (dst) = dv;                                                            \
+        dv += (count);                                                         \
+    } while (0)
+    for (int l = 0; l < c->n_layers; l++) {
+        const layer_weights_t *lw = &w->layers[l];
+        plh_layer *pl = &gs.fwd_layers[l];
+        PUT(pl->attn_norm, st->attn_norm_w[l], E);
+        PUT(pl->ffn_norm, st->ffn_norm_w[l], E);
+        /* q and output biases: the run state's buffers, zeros when the
+         * layer has none -- added either way, as model_forward_ex does */
+        PUT(pl->q_bias, st->attn_q_bias[l], Q);
+        PUT(pl->o_bias, st->attn_output_bias[l], E);
+        if (lw->attn_k_b) PUT(pl->k_bias, st->attn_k_bias[l], KV);
+        else dv += KV;
+        if (lw->attn_v_b) PUT(pl->v_bias, st->attn_v_bias[l], KV);
+        else dv += KV;
+        if (gs.qkn[l]) {
+            pl->q_norm = gs.d_qn + (size_t)l * c->head_dim;
+            pl->k_norm = gs.d_kn + (size_t)l * c->head_dim;
+        }
+    }
+    PUT(pm->output_norm, st->output_norm_w, E);
+#undef PUT
+    pm->n_layers = c->n_layers;
+    pm->n_embd = E;
+    pm->n_ffn = F;
+    pm->n_heads = c->n_heads;
+    pm->n_kv_heads = c->n_kv_heads;
+    pm->head_dim = c->head_dim;
+    pm->vocab_size = c->vocab_size;
+    pm->max_seq_len = c->max_seq_len;
+    pm->rope_type = (int)c->rope_type;
+    pm->rms_norm_eps = c->rms_norm_eps;
+    pm->embd_type = (int)w->type_token_embd;
+    pm->token_embd = gs.d_embd;
+    pm->key_cache = gs.d_key;
+    pm->val_cache = gs.d_val;
+    pm->rope_cos = gs.d_cos;
+    pm->rope_sin = gs.d_sin;
+    pm->layers = gs.fwd_layers;
+    gs.d_fwd_ws = plh_malloc(plh_forward_workspace_bytes(pm));
+    if (!gs.d_fwd_ws) return -1;
+    gs.fwd_ready = 1;
+    return 0;
+}
+
 int gpu_upload_model(const model_t *m) {
     if (!gs.inited) return -1;
     if (gs.uploaded) return 0;
@@ -255,6 +413,13 @@ int gpu_upload_model(const model_t *m) {
         fprintf(stderr, "gpu_hip: weight upload failed (%s); matmuls stay on the CPU\n",
                 plh_last_error());
         free_weights();
+    }
+    if (gs.n_weights > 0 && env_int("PICOLM_HIP_FORWARD", 1)) {
+        const int rc = upload_forward(m);
+        if (rc != 0) free_forward();
+        if (rc < 0)
+            fprintf(stderr, "gpu_hip: forward-pass upload failed (%s); per-op offload only\n",
+                    plh_last_error());
     }
     gs.uploaded = 1;
     return 0;
@@ -292,6 +457,7 @@ void gpu_shutdown(void) {
         plh_free(gs.d_k);
         plh_free(gs.d_v);
         plh_free(gs.d_out);
+        free_forward();
         free_weights();
         plh_shutdown();
     }
@@ -427,3 +593,52 @@ static int kv_copy(const model_t *m, int n_pos, int to_host) {
 int gpu_kv_download(const model_t *m, int n_pos) { return kv_copy(m, n_pos, 1); }
 
 int gpu_kv_upload(const model_t *m, int n_pos) { return kv_copy(m, n_pos, 0); }
+
+/* The rows of position pos0..pos0+n-1 of every layer, device -> host caches,
+ * in one strided copy per cache. */
+static int pos_rows_to_host(const model_t *m, int pos0, int n) {
+    const size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
+    const size_t off = (size_t)pos0 * kv_dim;
+    const size_t pitch = (size_t)gs.max_seq_len * kv_dim * sizeof(uint16_t);
+    const size_t width = (size_t)n * kv_dim * sizeof(uint16_t);
+    if (plh_memcpy2d_dtoh(m->state.key_cache + off, pitch, gs.d_key + off, pitch, width,
+                          (size_t)gs.n_layers) != 0)
+        return -1;
+    return plh_memcpy2d_dtoh(m->state.val_cache + off, pitch, gs.d_val + off, pitch, width,
+                             (size_t)gs.n_layers);
+}
+
+static int forward_done(model_t *m, int pos0, int n) {
+    const model_config_t *c = &m->config;
+    if (plh_memcpy_dtoh(m->state.logits, gs.d_logits, (size_t)c->vocab_size * sizeof(float)) ||
+        plh_memcpy_dtoh(m->state.x, gs.d_x, (size_t)c->n_embd * sizeof(float)) ||
+        pos_rows_to_host(m, pos0, n)) {
+        backend_lost("copy back");
+        return -1;
+    }
+    return 0;
+}
+
+int gpu_try_forward(model_t *m, int token, int pos) {
+    if (!gpu_available() || !gs.fwd_ready || !same_shape(m)) return -1;
+    if (token < 0 || token >= m->config.vocab_size || pos < 0 || pos >= gs.max_seq_len) return -1;
+    if (plh_forward(&gs.fwd, token, pos, gs.d_fwd_ws, gs.d_logits, gs.d_x) != 0) {
+        backend_lost("plh_forward");
+        return -1;
+    }
+    return forward_done(m, pos, 1);
+}
+
+int gpu_try_forward_prefill(model_t *m, const int *tokens, int n_tokens, int start_pos) {
+    if (!gpu_available() || !gs.fwd_ready || !same_shape(m) || !tokens) return -1;
+    if (n_tokens < 1 || start_pos < 0 || (long)start_pos + n_tokens > (long)gs.max_seq_len)
+        return -1;
+    for (int i = 0; i < n_tokens; i++)
+        if (tokens[i] < 0 || tokens[i] >= m->config.vocab_size) return -1;
+    if (plh_forward_prefill(&gs.fwd, tokens, n_tokens, start_pos, gs.d_fwd_ws, gs.d_logits,
+                            gs.d_x) != 0) {
+        backend_lost("plh_forward_prefill");
+        return -1;
+    }
+    return forward_done(m, start_pos, n_tokens);
+}

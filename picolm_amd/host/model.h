@@ -38,6 +38,7 @@ typedef struct {
 
 typedef struct {
     /* GGUF rows of the projection matrices (host memory, row-major blocks) */
+    const void *attn_norm;
     const void *attn_q;
     const void *attn_k;
     const void *attn_v;
@@ -46,9 +47,15 @@ typedef struct {
      * and reads the dequantized weights from run_state_t. */
     const void *attn_q_norm;
     const void *attn_k_norm;
+    const void *ffn_norm;
     const void *ffn_gate;
     const void *ffn_down;
     const void *ffn_up;
+    /* biases (Qwen2); NULL when absent */
+    const void *attn_q_b;
+    const void *attn_k_b;
+    const void *attn_v_b;
+    const void *attn_output_b;
     gguf_type_t type_attn_q;
     gguf_type_t type_attn_k;
     gguf_type_t type_attn_v;
@@ -56,21 +63,37 @@ typedef struct {
     gguf_type_t type_ffn_gate;
     gguf_type_t type_ffn_down;
     gguf_type_t type_ffn_up;
+    gguf_type_t type_attn_q_b;
+    gguf_type_t type_attn_k_b;
+    gguf_type_t type_attn_v_b;
+    gguf_type_t type_attn_output_b;
 } layer_weights_t;
 
 typedef struct {
+    const void *token_embd; /* [vocab_size] GGUF rows of n_embd */
+    gguf_type_t type_token_embd;
     const void *output; /* final projection [vocab_size][n_embd] */
     gguf_type_t type_output;
     layer_weights_t layers[MAX_LAYERS];
 } model_weights_t;
 
 typedef struct {
+    float *x;            /* residual stream [n_embd] */
+    float *logits;       /* [vocab_size] */
     uint16_t *key_cache; /* [n_layers][max_seq_len][n_kv_heads*head_dim] fp16 bits */
     uint16_t *val_cache;
     float *rope_cos;     /* [max_seq_len][head_dim/2] */
     float *rope_sin;
+    /* dequantized norm weights and biases (model.c:644-707) */
+    float *attn_norm_w[MAX_LAYERS];   /* [n_embd] */
+    float *ffn_norm_w[MAX_LAYERS];    /* [n_embd] */
     float *attn_q_norm_w[MAX_LAYERS]; /* [head_dim] each (QK-norm layers) */
     float *attn_k_norm_w[MAX_LAYERS];
+    float *output_norm_w;             /* [n_embd] */
+    float *attn_q_bias[MAX_LAYERS];   /* [n_heads*head_dim], zeros when absent */
+    float *attn_k_bias[MAX_LAYERS];   /* [kv_dim] */
+    float *attn_v_bias[MAX_LAYERS];   /* [kv_dim] */
+    float *attn_output_bias[MAX_LAYERS]; /* [n_embd], zeros when absent */
 } run_state_t;
 
 typedef struct {

@@ -188,6 +188,41 @@ def test_forward_matches_oracle(gpu, oracle_mod, cfg):
         dm.free()
 
 
+@pytest.mark.parametrize("cfg", [LLAMA, QWEN], ids=["llama", "qwen"])
+def test_prefill_matches_oracle(gpu, oracle_mod, cfg):
+    """model_forward_prefill: chunks of a prompt over a cached prefix, then a
+    decode step; logits of each chunk's last token, layer-0 KV rows exact."""
+    P, O = gpu, oracle_mod
+    h = S.SynthModel(**cfg, seed=21)
+    dm = P.DeviceModel(h)
+    orc = O.OracleForward(h)
+    rng = np.random.default_rng(22)
+    kv_layer = h.max_seq_len * h.kv_dim
+    try:
+        start = 0
+        for n in (7, 1, 12):
+            toks = rng.integers(0, h.vocab_size, n).astype(np.int32)
+            print(f"[case] prefill {h.n_layers}x{h.n_embd} start {start} n {n}", flush=True)
+            dm.prefill(toks, start)
+            P.synchronize()
+            lo, xo = orc.prefill(toks, start, n_threads=8)
+            assert max(normwise(dm.fetch_logits(), lo), normwise(dm.fetch_x(), xo)) <= FWD_TOL
+            kc, vc = dm.fetch_cache()
+            assert np.array_equal(kc[:kv_layer], orc.kc[:kv_layer]), start
+            assert np.array_equal(vc[:kv_layer], orc.vc[:kv_layer]), start
+            start += n
+        dm.forward(5, start)
+        P.synchronize()
+        lo, xo = orc.forward(5, start, n_threads=8)
+        assert normwise(dm.fetch_logits(), lo) <= FWD_TOL
+        with pytest.raises(P.PicolmHipError):
+            dm.prefill([1, 2], h.max_seq_len - 1)
+        with pytest.raises(P.PicolmHipError):
+            dm.prefill([h.vocab_size], 0)
+    finally:
+        dm.free()
+
+
 def test_forward_rejects_bad_calls(gpu):
     P = gpu
     h = S.SynthModel(**dict(LLAMA, n_layers=1), seed=13)
