@@ -37,7 +37,14 @@ Method:
     of GGUF weights), graph-replayed, against the HBM roof; its CPU baseline
     is the oracle matmul with rows split over the host threads like the
     reference's matmul pool, and the sampled GPU outputs are checked bit for
-    bit against it.
+    bit against it;
+  * forward: the whole forward pass on the device (plh_forward) for a
+    TinyLlama-shaped Q4_K_M-style synthetic model: prefill of a 128-token
+    prompt, decode tok/s (tokens queued back to back) and greedy-generation
+    tok/s (logits to the host and argmax every token); its CPU baseline is
+    the oracle forward pass (bit-identical to the reference's model_forward)
+    on the host threads, and the GPU logits of the sampled tokens are
+    checked against it.
 Prints one JSON line.
 """
 from __future__ import annotations
@@ -180,6 +187,113 @@ def cpu_baseline_gemv(res, budget_s=8.0):
                              "sample": f"the first {checked} of {len(mats)} GEMVs of the token, "
                                        f"oracle rows split over {n_thr} threads"},
             "parity_bit_exact_sampled": exact, "parity_gemvs_checked": checked}
+
+
+# The whole forward pass (model_forward on the device, plh_forward): a
+# TinyLlama-1.1B-shaped Q4_K_M-style synthetic model (Q4_K embedding, q, k,
+# o, gate, up; Q6_K v, down, output).
+FWD_MODEL = dict(n_layers=22, n_embd=2048, n_ffn=5632, n_heads=32, n_kv_heads=4, head_dim=64,
+                 vocab_size=32000, max_seq_len=2048)
+FWD_WORKLOAD = "tinyllama_q4km_forward"
+
+
+def run_forward(P, n_prompt=128, n_decode=64, n_check=8):
+    """Prefill of an n_prompt-token prompt (plh_forward_prefill), then two
+    decode loops from position n_prompt: `decode` queues n_decode tokens
+    back to back (token ids fixed in advance, device time per token), and
+    `generate` is greedy generation as picolm's loop runs it: every token's
+    logits copied to the host, argmax, the next call (host round trip
+    included).  The first n_check tokens of the prompt are also run as
+    decode steps from position 0 and kept for the CPU leg's parity check."""
+    from picolm_amd import synth as S
+    t0 = time.perf_counter()
+    h = S.SynthModel(**FWD_MODEL, seed=7, share_layers=True)
+    dm = P.DeviceModel(h)
+    P.synchronize()
+    setup_s = time.perf_counter() - t0
+    rng = np.random.default_rng(8)
+    prompt = rng.integers(0, h.vocab_size, n_prompt).astype(np.int32)
+    check = []
+    for i in range(n_check):
+        dm.forward(int(prompt[i]), i)
+        P.synchronize()
+        check.append(dm.fetch_logits())
+    # prefill over the whole prompt (rows 0..n_check-1 are rewritten)
+    dm.prefill(prompt, 0)
+    P.synchronize()
+    t0 = time.perf_counter()
+    dm.prefill(prompt, 0)
+    P.synchronize()
+    prefill_s = time.perf_counter() - t0
+    toks = rng.integers(0, h.vocab_size, n_decode + 4)
+    for i in range(4):
+        dm.forward(int(toks[i]), n_prompt + i)
+    P.synchronize()
+    e0, e1 = P.Event(), P.Event()
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(n_decode):
+        dm.forward(int(toks[4 + i]), n_prompt + 4 + i)
+    e1.record()
+    P.synchronize()
+    wall = (time.perf_counter() - t0) / n_decode
+    dev_ms = e0.elapsed_ms(e1) / n_decode
+    pos = n_prompt + 4 + n_decode
+    tok = int(toks[-1])
+    t0 = time.perf_counter()
+    for i in range(n_decode):
+        dm.forward(tok, pos + i)
+        tok = int(np.argmax(dm.fetch_logits()))
+    gen = (time.perf_counter() - t0) / n_decode
+    wb = h.weight_bytes_per_token()
+    gbs = wb / (dev_ms * 1e-3) / 1e9
+    res = {
+        "workload": FWD_WORKLOAD,
+        "config": dict(FWD_MODEL, types="Q4_K embd/q/k/o/gate/up, Q6_K v/down/output",
+                       prompt=n_prompt),
+        "decode_tok_s": 1.0 / wall,
+        "decode_us_per_token": wall * 1e6,
+        "decode_device_us_per_token": dev_ms * 1e3,
+        "generate_tok_s": 1.0 / gen,
+        "generate_us_per_token": gen * 1e6,
+        "prefill_tok_s": n_prompt / prefill_s,
+        "prefill_ms": prefill_s * 1e3,
+        "weight_bytes_per_token": wb,
+        "roofline": {"bound": "hbm", "achieved": gbs, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": gbs / HBM_PEAK_GBS, "traffic": None,
+                     "note": "GGUF weight bytes per token / device time per decode token"},
+        "setup_s": setup_s,
+        "_check": (h, prompt[:n_check], check),
+    }
+    dm.free()
+    return res
+
+
+def cpu_baseline_forward(res):
+    """The oracle's forward pass (bit-identical to the reference's
+    model_forward, pinned against it) on the host's cores, matmul rows split
+    over threads like the reference's pool, for the first tokens of the
+    prompt from position 0; the GPU logits of the same steps are checked
+    against it (normwise, the attention/silu exp tolerance) with the greedy
+    token."""
+    from oracle import oracle as O
+    h, toks, gpu_logits = res.pop("_check")
+    n_thr = min(os.cpu_count() or 1, HOST_THREADS_MAX)
+    orc = O.OracleForward(h)
+    worst, same_argmax, t_total = 0.0, True, 0.0
+    for i, t in enumerate(toks):
+        t0 = time.perf_counter()
+        lo, _ = orc.forward(int(t), i, n_threads=n_thr)
+        t_total += time.perf_counter() - t0
+        g = gpu_logits[i]
+        worst = max(worst, float(np.max(np.abs(g - lo)) / np.max(np.abs(lo))))
+        same_argmax = same_argmax and int(np.argmax(g)) == int(np.argmax(lo))
+    return {"cpu_baseline": {"value": len(toks) / t_total, "unit": "tok/s", "cores": n_thr,
+                             "kind": "port",
+                             "sample": f"oracle model_forward of the first {len(toks)} prompt "
+                                       f"tokens (positions 0..{len(toks) - 1}), matmul rows "
+                                       f"over {n_thr} threads"},
+            "parity_logits_normwise_max": worst, "parity_greedy_token_same": same_argmax}
 
 
 def qkn_bytes(w) -> int:
@@ -551,12 +665,14 @@ def main():
     ap.add_argument("--steps", type=int, default=500)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="tinyllama_decode_pos2047",
-                    choices=sorted(WORKLOADS) + [GEMV_WORKLOAD])
+                    choices=sorted(WORKLOADS) + [GEMV_WORKLOAD, FWD_WORKLOAD])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
     ap.add_argument("--no-prefill", action="store_true",
                     help="skip the secondary prefill measurement")
     ap.add_argument("--no-gemv", action="store_true",
                     help="skip the weight-GEMV measurement")
+    ap.add_argument("--no-forward", action="store_true",
+                    help="skip the whole-forward-pass measurement")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; the attention block needs no "
@@ -578,6 +694,20 @@ def main():
                            **GEMV_TOKEN, "types": "Q4_K (q,k,o,gate,up), Q6_K (v,down,output)"}}
         line.update(gres)
         line.update(gextra)
+        print(json.dumps(line), flush=True)
+        return
+    if args.workload == FWD_WORKLOAD:   # the whole forward pass as the headline
+        n_decode = max(8, min(args.steps, 256))
+        fres = run_forward(P, n_decode=n_decode)
+        fextra = {} if args.no_cpu else cpu_baseline_forward(fres)
+        fres.pop("_check", None)
+        line = {"metric": METRIC, "value": fres.pop("decode_tok_s"), "unit": "tok/s",
+                "n_gpus": 1, "steps": n_decode, "warmup": 4,
+                "ms_per_step": fres["decode_us_per_token"] / 1e3, "higher_is_better": True,
+                "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+                "config": {"workload": FWD_WORKLOAD, **fres.pop("config")}}
+        line.update(fres)
+        line.update(fextra)
         print(json.dumps(line), flush=True)
         return
     w = WORKLOADS[args.workload]
@@ -644,6 +774,13 @@ def main():
         gres["workload"] = GEMV_WORKLOAD
         gres.update(gextra)
         line["gemv"] = gres
+    if not args.no_forward:
+        # the whole forward pass on the device (gpu_try_forward's path)
+        fres = run_forward(P)
+        fextra = {} if args.no_cpu else cpu_baseline_forward(fres)
+        fres.pop("_check", None)
+        fres.update(fextra)
+        line["forward"] = fres
     print(json.dumps(line), flush=True)
 
 
