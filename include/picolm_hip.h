@@ -168,7 +168,7 @@ int plh_gemv(int qtype, int n, int d, const void *dev, const float *x, float *ou
 /* plh_gemv with the forward pass's prologue and epilogues, in the
  * reference's order (rmsnorm tensor.c:425-492, matmul_bias tensor.c:256-264,
  * silu + elemwise_mul tensor.c:605-633, vec_add tensor.c:635-657):
- *     xn = rmsnorm(x, norm_w, norm_eps)  if norm_w (n <= 12288), else x
+ *     xn = rmsnorm(x, norm_w, norm_eps)  if norm_w (n <= 7680), else x
  *     v = vec_dot(row i, xn)
  *     v = v + bias[i]        if bias            (matmul_bias)
  *     v = v + 0.0f           if bias_zero       (matmul_bias with a zeroed bias)
@@ -179,6 +179,15 @@ int plh_gemv(int qtype, int n, int d, const void *dev, const float *x, float *ou
 int plh_gemv_ex(int qtype, int n, int d, const void *dev, const float *x, float *out,
                 const float *norm_w, float norm_eps, const float *bias, int bias_zero,
                 const float *gate, const float *resid);
+
+/* The SwiGLU input of the FFN in one launch (model.c:906-916 -- gate and up
+ * projections, silu, elemwise_mul): out[i] = silu(vec_dot(gate row i, xn)) *
+ * vec_dot(up row i, xn), xn = rmsnorm(x, norm_w, norm_eps) when norm_w is
+ * set (else x).  gate_dev / up_dev: packed copies of two d x n matrices of
+ * the same type.  The dot products and the norm are bit-identical to the
+ * reference; silu uses the device expf. */
+int plh_gemv_swiglu(int qtype, int n, int d, const void *gate_dev, const void *up_dev,
+                    const float *x, float *out, const float *norm_w, float norm_eps);
 
 /* ---- forward pass (model_forward_ex, model.c:746-925) --------------------- */
 /* tensor.c:425-492 rmsnorm, bit-identical to the reference's x86-64 AVX2
@@ -254,7 +263,9 @@ int plh_forward_prefill(const plh_model *m, const int *tokens, int n_tokens, int
 /* Tuning knobs (bench sweeps).  key 1: decode target workgroups per launch
  * (0 = default); key 2: decode contexts of at most this many positions are
  * not split (multiple of 128, 0 = default); key 3: GEMV rows per thread
- * (1, 2, 4, 8; 0 = default). */
+ * (1, 2, 4, 8; 0 = default); key 4: plh_forward forms each rmsnorm in a
+ * launch of its own (1) instead of inside the GEMVs that read it (0,
+ * default). */
 int plh_set_tuning(int key, int value);
 
 #ifdef __cplusplus

@@ -232,15 +232,13 @@ namespace plh {
 // red: 8 floats of LDS.  Every thread of the workgroup must call it.
 __host__ __device__ inline int rms_sq_pitch(int n) { return (n / 8 + 3) / 4 * 4 + 4; }
 
+// The eight chains and the fold, once every square x[8i+j]^2 of the vector
+// sits at sq[j * pitch + i] (see rms_scale_block).
 template <int NT>
-__device__ __forceinline__ float rms_scale_block(const float* x, int n, float eps, float* sq,
-                                                 float* red) {
+__device__ __forceinline__ float rms_chain_fold(const float* x, int n, float eps, const float* sq,
+                                                float* red) {
   const int tid = threadIdx.x;
   const int n8 = n / 8, pitch = rms_sq_pitch(n);
-  for (int idx = tid; idx < 8 * n8; idx += NT) {
-    const float v = x[idx];
-    sq[(idx & 7) * pitch + (idx >> 3)] = v * v;
-  }
   __syncthreads();
   if (tid < 8) {
     const float* s = sq + tid * pitch;
@@ -267,6 +265,45 @@ __device__ __forceinline__ float rms_scale_block(const float* x, int n, float ep
   float ss = (l0 + l2) + (l1 + l3);
   for (int i = 8 * n8; i < n; ++i) ss = ss + x[i] * x[i];
   return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+template <int NT>
+__device__ __forceinline__ float rms_scale_block(const float* x, int n, float eps, float* sq,
+                                                 float* red) {
+  const int tid = threadIdx.x;
+  const int n8 = n / 8, pitch = rms_sq_pitch(n);
+  for (int idx = tid; idx < 8 * n8; idx += NT) {
+    const float v = x[idx];
+    sq[(idx & 7) * pitch + (idx >> 3)] = v * v;
+  }
+  return rms_chain_fold<NT>(x, n, eps, sq, red);
+}
+
+// rms_scale_block split in two for callers that have other loads to issue:
+// rms_prefetch loads this thread's elements x[tid + NT*k] (k < K, vectors of
+// at most NT*K elements) into registers; rms_scale_prefetched squares them
+// into LDS and finishes.  Loads issued between the two calls do not delay
+// the squares (the x loads were issued first and complete first).
+template <int NT, int K>
+__device__ __forceinline__ void rms_prefetch(const float* x, int n, float (&xv)[K]) {
+  const int lim = 8 * (n / 8);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int idx = threadIdx.x + NT * k;
+    xv[k] = idx < lim ? x[idx] : 0.0f;
+  }
+}
+template <int NT, int K>
+__device__ __forceinline__ float rms_scale_prefetched(const float* x, int n, float eps,
+                                                      const float (&xv)[K], float* sq,
+                                                      float* red) {
+  const int lim = 8 * (n / 8), pitch = rms_sq_pitch(n);
+#pragma unroll
+  for (int k = 0; k < K; ++k) {
+    const int idx = threadIdx.x + NT * k;
+    if (idx < lim) sq[(idx & 7) * pitch + (idx >> 3)] = xv[k] * xv[k];
+  }
+  return rms_chain_fold<NT>(x, n, eps, sq, red);
 }
 
 }  // namespace plh

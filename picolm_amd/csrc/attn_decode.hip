@@ -623,6 +623,14 @@ extern "C" int plh_set_tuning(int key, int value) {
     g_gemv_rows_per_thread = value;
     return 0;
   }
+  if (key == 4) {
+    if (value != 0 && value != 1) {
+      set_error("plh_set_tuning: forward rmsnorm placement must be 0 or 1");
+      return -1;
+    }
+    g_fwd_norm_separate = value;
+    return 0;
+  }
   set_error("plh_set_tuning: unknown key %d", key);
   return -1;
 }

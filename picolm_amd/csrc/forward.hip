@@ -17,6 +17,10 @@
 
 using namespace plh;
 
+namespace plh {
+int g_fwd_norm_separate = 0;
+}
+
 namespace {
 
 constexpr int kTypeF32 = 0, kTypeF16 = 1, kTypeQ4_0 = 2, kTypeQ8_0 = 8, kTypeQ4K = 12,
@@ -136,7 +140,7 @@ int launch_rmsnorm(const float* x, const float* w, float* out, int n, float eps)
 
 // Workspace carve-up of plh_forward, 256-byte aligned pieces.
 struct Acts {
-  float *x, *q, *k, *v, *att, *hb;
+  float *x, *xb, *q, *k, *v, *att, *hb;
   size_t bytes;
 };
 
@@ -145,11 +149,12 @@ size_t piece(size_t floats) { return (floats * sizeof(float) + 255) / 256 * 256;
 Acts carve(const plh_model* m, void* base) {
   const size_t q_dim = (size_t)m->n_heads * m->head_dim;
   const size_t kv_dim = (size_t)m->n_kv_heads * m->head_dim;
-  const size_t sizes[6] = {(size_t)m->n_embd, q_dim, kv_dim, kv_dim, q_dim, (size_t)m->n_ffn};
+  const size_t sizes[7] = {(size_t)m->n_embd, (size_t)m->n_embd, q_dim, kv_dim, kv_dim, q_dim,
+                           (size_t)m->n_ffn};
   Acts a{};
-  float** dst[6] = {&a.x, &a.q, &a.k, &a.v, &a.att, &a.hb};
+  float** dst[7] = {&a.x, &a.xb, &a.q, &a.k, &a.v, &a.att, &a.hb};
   size_t off = 0;
-  for (int i = 0; i < 6; ++i) {
+  for (int i = 0; i < 7; ++i) {
     *dst[i] = base ? (float*)((char*)base + off) : nullptr;
     off += piece(sizes[i]);
   }
@@ -274,14 +279,23 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, bool 
     g.bias = bias, g.bias_zero = bias_zero, g.gate = gate, g.resid = resid;
     return g;
   };
+  // rmsnorm(x, w): inside the GEMVs that read it, or (tuning key 4) one
+  // launch of its own into xb; returns the GEMV operand and its prologue
+  const bool separate = g_fwd_norm_separate != 0 || E > kGemvNormMax;
+  auto normed = [&](const float* w, const float** xin, const float** nw) {
+    *xin = separate ? a.xb : a.x;
+    *nw = separate ? nullptr : w;
+    return separate ? launch_rmsnorm(a.x, w, a.xb, E, eps) : 0;
+  };
+  const float *xin, *nw;
   for (int l = 0; l < m->n_layers; ++l) {
     const plh_layer& L = m->layers[l];
     // attention block (model.c:777-897): q, k, v in one launch
+    if (normed(L.attn_norm, &xin, &nw)) return -1;
     const GemvCall qkv[3] = {
-        call(L.q, E, Q, a.x, a.q, L.attn_norm, L.q_bias, bias_always && !L.q_bias, nullptr,
-             nullptr),
-        call(L.k, E, KV, a.x, a.k, L.attn_norm, L.k_bias, 0, nullptr, nullptr),
-        call(L.v, E, KV, a.x, a.v, L.attn_norm, L.v_bias, 0, nullptr, nullptr)};
+        call(L.q, E, Q, xin, a.q, nw, L.q_bias, bias_always && !L.q_bias, nullptr, nullptr),
+        call(L.k, E, KV, xin, a.k, nw, L.k_bias, 0, nullptr, nullptr),
+        call(L.v, E, KV, xin, a.v, nw, L.v_bias, 0, nullptr, nullptr)};
     if (gemv_multi_launch(qkv, 3)) return -1;
     const int rc = L.q_norm ? plh_attn_decode_qknorm(m->n_layers, m->n_heads, m->n_kv_heads,
                                                      m->head_dim, m->max_seq_len, m->rope_type, l,
@@ -299,8 +313,9 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, bool 
       return -1;
     // SwiGLU block (model.c:899-922): hb = silu(gate xn) * (up xn), xn = rmsnorm(x),
     // in one launch when gate and up share a type; then x = x + Wdown hb
-    const GemvCall gate = call(L.gate, E, F, a.x, a.hb, L.ffn_norm, nullptr, 0, nullptr, nullptr);
-    const GemvCall up = call(L.up, E, F, a.x, a.hb, L.ffn_norm, nullptr, 0, nullptr, nullptr);
+    if (normed(L.ffn_norm, &xin, &nw)) return -1;
+    const GemvCall gate = call(L.gate, E, F, xin, a.hb, nw, nullptr, 0, nullptr, nullptr);
+    const GemvCall up = call(L.up, E, F, xin, a.hb, nw, nullptr, 0, nullptr, nullptr);
     if (L.gate.qtype == L.up.qtype) {
       if (gemv_pair_launch(gate, up)) return -1;
     } else {
@@ -312,8 +327,9 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, bool 
   }
   if (!logits) return 0;
   // final norm and logits (model.c:918-922)
-  if (gemv_launch(call(m->output, E, m->vocab_size, a.x, logits, m->output_norm, nullptr, 0,
-                       nullptr, nullptr)))
+  if (normed(m->output_norm, &xin, &nw) ||
+      gemv_launch(call(m->output, E, m->vocab_size, xin, logits, nw, nullptr, 0, nullptr,
+                       nullptr)))
     return -1;
   if (x_out && launch_rmsnorm(a.x, m->output_norm, x_out, E, eps)) return -1;
   return 0;

@@ -38,7 +38,8 @@ constexpr int kThreads = 256;
 constexpr int kTypeQ8_0 = 8, kTypeQ4K = 12, kTypeQ6K = 14;
 constexpr size_t kPlaneAlign = 256;
 constexpr size_t kMaxPacked = (size_t)1 << 31;  // 32-bit plane offsets
-constexpr int kMaxNormN = 12288;                 // rmsnorm squares within 48 KiB of LDS
+constexpr int kMaxNormN = kGemvNormMax;          // squares + staged x within 64 KiB of LDS
+constexpr int kNormPrefetch = 16;                // x elements per thread loaded up front
 
 size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
@@ -171,6 +172,7 @@ struct GemvArgs {
   const float* norm_w;
   float norm_eps;
   int n;
+  int xs_off;  // floats from the LDS base to the staged rmsnorm(x)
   // Gate/up pair (gemv_body<..., true>): virtual row 2r is row r of w (gate),
   // 2r + 1 row r of w2 (up, same type and shape); out[r] = silu(gate) * up.
   const uint8_t* w2;
@@ -195,18 +197,15 @@ struct PlainX {
   const float* x;
   __device__ __forceinline__ float4 operator()(int i) const { return ld4(x + i); }
 };
-struct NormX {
-  const float* x;
-  const float* w;
-  float scale;
+// rmsnorm(x) staged in LDS by the workgroup, element i at xs_index(i): four
+// padding floats after every 64 elements, so that lanes reading the units
+// of one row side by side (64 or 32 elements apart) hit different banks.
+__host__ __device__ inline int xs_index(int i) { return i + (i >> 6) * 4; }
+__host__ __device__ inline int xs_floats(int n) { return xs_index(n) + 4; }
+struct LdsX {
+  const float* xs;
   __device__ __forceinline__ float4 operator()(int i) const {
-    const float4 v = ld4(x + i), g = ld4(w + i);
-    float4 r;
-    r.x = (v.x * scale) * g.x;
-    r.y = (v.y * scale) * g.y;
-    r.z = (v.z * scale) * g.z;
-    r.w = (v.w * scale) * g.w;
-    return r;
+    return *(const float4*)(xs + xs_index(i));
   }
 };
 
@@ -507,15 +506,52 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int wg, float* term
     __shared__ float red[8];
     const int u = tid % a.uspan;
     const bool first = active && u < a.units;
+    // x's and the norm weights' loads go first, so that the squares need not
+    // wait for the weight loads issued next (loads complete in order);
+    // vectors longer than kThreads * kNormPrefetch elements load them after
+    float xv[kNormPrefetch], wv[kNormPrefetch];
+    const bool pre = a.n <= kThreads * kNormPrefetch;
+    if (pre) {
+#pragma unroll
+      for (int k = 0; k < kNormPrefetch; ++k) {
+        const int idx = tid + kThreads * k;
+        xv[k] = idx < a.n ? a.x[idx] : 0.0f;
+        wv[k] = idx < a.n ? a.norm_w[idx] : 0.0f;
+      }
+    }
     typename F::Raw raw[RB];
     if (first) load_rows<F, RB, PAIR>(a, r0, rows, rlane, u, raw);
     // lanes 0..7 finish reading the squares before the helper's second
     // barrier, so the terms may overwrite them once it returns
-    const float scale = rms_scale_block<kThreads>(a.x, a.n, a.norm_eps, terms, red);
-    const NormX xs{a.x, a.norm_w, scale};
+    float scale;
+    if (pre) {
+      const int lim = 8 * (a.n / 8), pitch = rms_sq_pitch(a.n);
+#pragma unroll
+      for (int k = 0; k < kNormPrefetch; ++k) {
+        const int idx = tid + kThreads * k;
+        if (idx < lim) terms[(idx & 7) * pitch + (idx >> 3)] = xv[k] * xv[k];
+      }
+      scale = rms_chain_fold<kThreads>(a.x, a.n, a.norm_eps, terms, red);
+    } else {
+      scale = rms_scale_block<kThreads>(a.x, a.n, a.norm_eps, terms, red);
+    }
+    // xn = (x * scale) * w, as the reference's rmsnorm rounds it, into LDS
+    float* xs = terms + a.xs_off;
+    if (pre) {
+#pragma unroll
+      for (int k = 0; k < kNormPrefetch; ++k) {
+        const int idx = tid + kThreads * k;
+        if (idx < a.n) xs[xs_index(idx)] = (xv[k] * scale) * wv[k];
+      }
+    } else {
+      for (int idx = tid; idx < a.n; idx += kThreads)
+        xs[xs_index(idx)] = (a.x[idx] * scale) * a.norm_w[idx];
+    }
+    __syncthreads();
+    const LdsX xsrc{xs};
     if (first) {
-      unit_terms<F, RB>(a, xs, terms, rows, rlane, u, raw);
-      unit_passes<F, RB, PAIR>(a, xs, terms, r0, rows, rlane, 1);
+      unit_terms<F, RB>(a, xsrc, terms, rows, rlane, u, raw);
+      unit_passes<F, RB, PAIR>(a, xsrc, terms, r0, rows, rlane, 1);
     }
   } else {
     if (active) unit_passes<F, RB, PAIR>(a, PlainX{a.x}, terms, r0, rows, rlane, 0);
@@ -610,13 +646,13 @@ void launch_rb(int rb, int grid, size_t lds, hipStream_t st, const GemvArgs& a) 
   }
 }
 
-// A gate/up pair always reads rmsnorm(x) (the FFN input), so only that
-// combination is instantiated.
 template <class F>
 void launch_fmt(bool norm, bool pair, int rb, int grid, size_t lds, hipStream_t st,
                 const GemvArgs& a) {
-  if (pair)
+  if (pair && norm)
     launch_rb<F, true, true>(rb, grid, lds, st, a);
+  else if (pair)
+    launch_rb<F, false, true>(rb, grid, lds, st, a);
   else if (norm)
     launch_rb<F, true, false>(rb, grid, lds, st, a);
   else
@@ -714,6 +750,10 @@ int pick_rb(const GemvArgs* seg, const int* rows, int nseg, bool pair, int max_r
   };
   int rb = 4;
   while (rb > 1 && (grid_of(rb) * 10 < 6L * cus || !lds_ok(rb))) rb /= 2;
+  // with the rmsnorm prologue every workgroup pays the norm's latency, and
+  // workgroups sharing a CU measured to pay it one after the other: 8 rows
+  // per thread when 4 would need more than one workgroup per CU
+  if (seg[0].norm_w && rb == 4 && max_rb >= 8 && grid_of(4) > cus && lds_ok(8)) rb = 8;
   if (g_gemv_rows_per_thread > 0) rb = g_gemv_rows_per_thread;
   if (rb > max_rb) rb = max_rb;
   if (pair && (seg[0].row_par * rb) % 2) rb *= 2;
@@ -724,11 +764,17 @@ int pick_rb(const GemvArgs* seg, const int* rows, int nseg, bool pair, int max_r
   return rb;
 }
 
-size_t lds_bytes(const GemvArgs& a) {
+// LDS of a launch, and the staged x's offset: the terms, which reuse the
+// rmsnorm squares' space, then rmsnorm(x).
+size_t lds_bytes(GemvArgs& a) {
   size_t lds = sizeof(float) * (size_t)a.rows_per_wg * a.tpitch;
-  if (a.norm_w) {  // the squares of the rmsnorm share the terms' LDS
+  a.xs_off = 0;
+  if (a.norm_w) {
     const size_t sq = sizeof(float) * 8 * (size_t)rms_sq_pitch(a.n);
     if (sq > lds) lds = sq;
+    lds = (lds + 15) / 16 * 16;
+    a.xs_off = (int)(lds / sizeof(float));
+    lds += sizeof(float) * (size_t)xs_floats(a.n);
   }
   return lds;
 }
@@ -796,6 +842,20 @@ int plh_gemv_upload(int qtype, int n, int d, const void* host_rows, void* dev) {
 
 int plh_gemv(int qtype, int n, int d, const void* dev, const float* x, float* out) {
   return plh_gemv_ex(qtype, n, d, dev, x, out, nullptr, 0.0f, nullptr, 0, nullptr, nullptr);
+}
+
+int plh_gemv_swiglu(int qtype, int n, int d, const void* gate_dev, const void* up_dev,
+                    const float* x, float* out, const float* norm_w, float norm_eps) {
+  GemvCall g{}, u{};
+  g.qtype = qtype, g.n = n, g.d = d, g.w = gate_dev, g.x = x, g.out = out;
+  g.norm_w = norm_w, g.norm_eps = norm_eps;
+  u = g;
+  u.w = up_dev;
+  if (!up_dev) {
+    set_error("plh_gemv: null pointer");
+    return -1;
+  }
+  return gemv_pair_launch(g, u);
 }
 
 int plh_gemv_ex(int qtype, int n, int d, const void* dev, const float* x, float* out,
@@ -866,7 +926,7 @@ int gemv_pair_launch(const GemvCall& gate, const GemvCall& up) {
     return -1;
   }
   if (gate.qtype != up.qtype || gate.n != up.n || gate.d != up.d || gate.x != up.x ||
-      !gate.norm_w || gate.norm_w != up.norm_w || gate.norm_eps != up.norm_eps || gate.bias ||
+      gate.norm_w != up.norm_w || gate.norm_eps != up.norm_eps || gate.bias ||
       up.bias || gate.bias_zero || up.bias_zero || gate.gate || up.gate || gate.resid ||
       up.resid) {
     set_error("gemv_pair_launch: gate and up must match in type, shape, x and rmsnorm, "

@@ -25,6 +25,13 @@ int check_hip(hipError_t e, const char* what);
 // GEMV rows per thread forced by plh_set_tuning key 3 (0: the launch's own
 // choice).
 extern int g_gemv_rows_per_thread;
+// plh_set_tuning key 4: 1 = the forward pass forms rmsnorm(x) in a launch of
+// its own instead of inside the GEMVs that read it.
+extern int g_fwd_norm_separate;
+
+// Longest x the GEMV's rmsnorm prologue takes (its squares and the staged
+// normalised x share 64 KiB of LDS).
+constexpr int kGemvNormMax = 7680;
 
 // One weight GEMV with the forward pass's prologue and epilogues (the
 // arguments of plh_gemv_ex).
@@ -44,8 +51,9 @@ int gemv_launch(const GemvCall& g);
 // Up to three GEMVs over the same x (and the same rmsnorm prologue, if any)
 // in one launch: the q, k and v projections.
 int gemv_multi_launch(const GemvCall* g, int n);
-// hb = silu(gate(xn)) * up(xn) in one launch (model.c:906-916), gate and up
-// of the same type and shape, both with the rmsnorm prologue; out = up.out.
+// hb = silu(gate(x)) * up(x) in one launch (model.c:906-916), gate and up of
+// the same type and shape and the same rmsnorm prologue (or none); out =
+// up.out.
 int gemv_pair_launch(const GemvCall& gate, const GemvCall& up);
 
 // Makes sure the workspace holds at least `bytes`.  Growing it waits for the
