@@ -42,9 +42,10 @@ Method:
     TinyLlama-shaped Q4_K_M-style synthetic model: prefill of a 128-token
     prompt, decode tok/s (tokens queued back to back) and greedy-generation
     tok/s (logits to the host and argmax every token); its CPU baseline is
-    the oracle forward pass (bit-identical to the reference's model_forward)
-    on the host threads, and the GPU logits of the sampled tokens are
-    checked against it.
+    the reference's own model_forward compiled from its sources
+    (oracle/_ref, the oracle forward pass where that library is absent) on
+    the host threads, and the GPU logits of the sampled tokens are checked
+    against it.
 Prints one JSON line.
 """
 from __future__ import annotations
@@ -270,29 +271,38 @@ def run_forward(P, n_prompt=128, n_decode=64, n_check=8):
 
 
 def cpu_baseline_forward(res):
-    """The oracle's forward pass (bit-identical to the reference's
-    model_forward, pinned against it) on the host's cores, matmul rows split
-    over threads like the reference's pool, for the first tokens of the
-    prompt from position 0; the GPU logits of the same steps are checked
-    against it (normwise, the attention/silu exp tolerance) with the greedy
-    token."""
+    """picolm's own model_forward (the reference's model.c / tensor.c /
+    quant.c compiled from its sources into oracle/_ref, AVX2 build, its
+    matmul thread pool at the host's threads) on the first tokens of the
+    prompt from position 0; without that library the oracle's forward pass
+    (bit-identical to it) stands in.  The GPU logits of the same steps are
+    checked against the CPU's (normwise, the attention/silu exp tolerance)
+    with the greedy token."""
     from oracle import oracle as O
     h, toks, gpu_logits = res.pop("_check")
     n_thr = min(os.cpu_count() or 1, HOST_THREADS_MAX)
-    orc = O.OracleForward(h)
+    if O.ref_available():
+        O.ref().ref_set_threads(n_thr)
+        cpu, kind, what = O.RefForward(h), "reference", "picolm model_forward (oracle/_ref)"
+        step = cpu.forward
+    else:
+        cpu, kind, what = O.OracleForward(h), "port", "oracle model_forward"
+        step = lambda t, p: cpu.forward(t, p, n_threads=n_thr)   # noqa: E731
     worst, same_argmax, t_total = 0.0, True, 0.0
     for i, t in enumerate(toks):
         t0 = time.perf_counter()
-        lo, _ = orc.forward(int(t), i, n_threads=n_thr)
+        lo, _ = step(int(t), i)
         t_total += time.perf_counter() - t0
         g = gpu_logits[i]
         worst = max(worst, float(np.max(np.abs(g - lo)) / np.max(np.abs(lo))))
         same_argmax = same_argmax and int(np.argmax(g)) == int(np.argmax(lo))
+    if kind == "reference":
+        O.ref().ref_set_threads(1)
+        cpu.close()
     return {"cpu_baseline": {"value": len(toks) / t_total, "unit": "tok/s", "cores": n_thr,
-                             "kind": "port",
-                             "sample": f"oracle model_forward of the first {len(toks)} prompt "
-                                       f"tokens (positions 0..{len(toks) - 1}), matmul rows "
-                                       f"over {n_thr} threads"},
+                             "kind": kind,
+                             "sample": f"{what} of the first {len(toks)} prompt tokens "
+                                       f"(positions 0..{len(toks) - 1}), {n_thr} matmul threads"},
             "parity_logits_normwise_max": worst, "parity_greedy_token_same": same_argmax}
 
 
@@ -673,6 +683,8 @@ def main():
                     help="skip the weight-GEMV measurement")
     ap.add_argument("--no-forward", action="store_true",
                     help="skip the whole-forward-pass measurement")
+    ap.add_argument("--prompt", type=int, default=128,
+                    help="prompt tokens of the forward-pass workload")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU; the attention block needs no "
@@ -698,7 +710,7 @@ def main():
         return
     if args.workload == FWD_WORKLOAD:   # the whole forward pass as the headline
         n_decode = max(8, min(args.steps, 256))
-        fres = run_forward(P, n_decode=n_decode)
+        fres = run_forward(P, n_prompt=max(8, args.prompt), n_decode=n_decode)
         fextra = {} if args.no_cpu else cpu_baseline_forward(fres)
         fres.pop("_check", None)
         line = {"metric": METRIC, "value": fres.pop("decode_tok_s"), "unit": "tok/s",

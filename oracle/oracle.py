@@ -181,6 +181,8 @@ def ref() -> C.CDLL:
         R.ref_forward_prefill.restype = None
         R.ref_silu.argtypes = [_f32p, C.c_int]
         R.ref_silu.restype = None
+        R.ref_set_threads.argtypes = [C.c_int]
+        R.ref_set_threads.restype = None
         _ref = R
     return _ref
 

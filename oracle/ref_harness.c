@@ -385,3 +385,6 @@ void ref_forward_prefill(void *hv, const int *tokens, int n_tokens, int start_po
 
 /* tensor.c:605-609 over an array (silu in place). */
 void ref_silu(float *x, int n) { silu(x, n); }
+
+/* tensor.c:190-195: the matmul thread-pool size of every later call. */
+void ref_set_threads(int n) { tensor_set_threads(n); }

@@ -147,3 +147,20 @@ def test_bad_arguments_rejected(oracle_mod):
             orc.forward(tok, pos)
     with pytest.raises(ValueError):
         orc.prefill([1, 2, 3], h.max_seq_len - 2)
+
+
+@needs_ref
+def test_tinyllama_shape_matches_reference_bits(oracle_mod):
+    """The full TinyLlama-1.1B Q4_K_M shape (22 layers, n_embd 2048, n_ffn
+    5632, GQA 32/4, vocab 32000; layer bytes shared): two decode steps."""
+    O = oracle_mod
+    h = S.SynthModel(22, 2048, 5632, 32, 4, 64, 32000, 2048, seed=7, share_layers=True)
+    orc, ref = O.OracleForward(h), O.RefForward(h)
+    O.ref().ref_set_threads(4)
+    try:
+        for pos, tok in enumerate((1, 31999)):
+            assert_same(orc.forward(tok, pos, n_threads=8), ref.forward(tok, pos), f"pos {pos}")
+        assert np.array_equal(orc.kc, ref.kc) and np.array_equal(orc.vc, ref.vc)
+    finally:
+        O.ref().ref_set_threads(1)
+        ref.close()
