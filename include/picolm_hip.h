@@ -180,6 +180,11 @@ int plh_gemv_ex(int qtype, int n, int d, const void *dev, const float *x, float 
                 const float *norm_w, float norm_eps, const float *bias, int bias_zero,
                 const float *gate, const float *resid);
 
+/* tensor.c:322-366 matmul_batch on the device: out[b*d + i] = vec_dot(row i
+ * of W, x + b*n) for b < n_batch, each bit-identical to plh_gemv's. */
+int plh_matmul_batch(int qtype, int n, int d, const void *dev, const float *x, int n_batch,
+                     float *out);
+
 /* The SwiGLU input of the FFN in one launch (model.c:906-916 -- gate and up
  * projections, silu, elemwise_mul): out[i] = silu(vec_dot(gate row i, xn)) *
  * vec_dot(up row i, xn), xn = rmsnorm(x, norm_w, norm_eps) when norm_w is
@@ -253,10 +258,12 @@ int plh_forward(const plh_model *m, int token, int pos, void *workspace, float *
 /* Replaces model_forward_prefill(m, tokens, n_tokens, start_pos)
  * (model.c:939-1144): the prompt tokens (HOST array) at positions
  * start_pos.., rows start_pos..start_pos+n_tokens-1 of every layer's caches
- * appended, logits and x_out of the last token only.  Bit-for-bit the
- * reference's per-token arithmetic (q and output biases only when present,
- * model.c:1002-1017, 1095-1099); tokens run one after another through the
- * decode path. */
+ * appended, logits and x_out of the last token only.  Chunks of up to 128
+ * tokens go through each layer together (batched GEMVs reading each weight
+ * about once per chunk, the prefill attention kernel); every (row, token)
+ * product keeps the reference's arithmetic, q and output biases only when
+ * present (model.c:1002-1017, 1095-1099).  Its activations live in a
+ * library-owned buffer (grown on first use); `workspace` is not used. */
 int plh_forward_prefill(const plh_model *m, const int *tokens, int n_tokens, int start_pos,
                         void *workspace, float *logits, float *x_out);
 

@@ -97,6 +97,7 @@ _SIGS = {
     "plh_gemv": (_i, [_i, _i, _i, _vp, _vp, _vp]),
     "plh_gemv_ex": (_i, [_i, _i, _i, _vp, _vp, _vp, _vp, C.c_float, _vp, _i, _vp, _vp]),
     "plh_gemv_swiglu": (_i, [_i, _i, _i, _vp, _vp, _vp, _vp, _vp, C.c_float]),
+    "plh_matmul_batch": (_i, [_i, _i, _i, _vp, _vp, _i, _vp]),
     # forward pass
     "plh_rmsnorm": (_i, [_vp, _vp, _vp, _i, C.c_float]),
     "plh_dequantize_row": (_i, [_i, _vp, _vp, _i]),

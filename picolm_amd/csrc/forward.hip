@@ -43,6 +43,21 @@ __global__ __launch_bounds__(kNormThreads) void rmsnorm_kernel(const float* x, c
   }
 }
 
+// rmsnorm of n_rows rows (one workgroup each), rows `stride` floats apart.
+__global__ __launch_bounds__(kNormThreads) void rmsnorm_rows_kernel(const float* x,
+                                                                    const float* w, float* out,
+                                                                    int n, int stride, float eps) {
+  extern __shared__ __align__(16) float sq[];
+  __shared__ float red[8];
+  const float* xr = x + (size_t)blockIdx.x * stride;
+  float* orow = out + (size_t)blockIdx.x * stride;
+  const float scale = rms_scale_block<kNormThreads>(xr, n, eps, sq, red);
+  for (int i = threadIdx.x; i < n; i += kNormThreads) {
+    const float t = xr[i] * scale;
+    orow[i] = t * w[i];
+  }
+}
+
 // ---- one GGUF row to fp32 (quant.c:96-128, 193-262) ------------------------
 __device__ __forceinline__ uint32_t rd8(const uint8_t* p) { return p[0]; }
 __device__ __forceinline__ uint16_t rd16(const uint8_t* p) {
@@ -116,6 +131,24 @@ __global__ __launch_bounds__(256) void dequant_row_kernel(int qtype, const uint8
                                                           float* out, int n) {
   const int e = blockIdx.x * 256 + threadIdx.x;
   if (e < n) out[e] = dequant_elem(qtype, row, e);
+}
+
+// The embedding rows of up to kEmbedTokens tokens (model.c:976-982), one
+// workgroup row per token, rows `stride` floats apart.
+constexpr int kEmbedTokens = 64;
+struct EmbedArgs {
+  int tokens[kEmbedTokens];
+  int n_tok, qtype, n, stride;
+  size_t row_bytes;
+  const uint8_t* table;
+  float* x;
+};
+__global__ __launch_bounds__(256) void embed_rows_kernel(EmbedArgs a) {
+  const int t = blockIdx.y;
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (t >= a.n_tok || e >= a.n) return;
+  a.x[(size_t)t * a.stride + e] =
+      dequant_elem(a.qtype, a.table + (size_t)a.tokens[t] * a.row_bytes, e);
 }
 
 size_t embd_row_bytes(int qtype, int n) {
@@ -335,6 +368,120 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, bool 
   return 0;
 }
 
+
+// ---- prompt chunks (model_forward_prefill, model.c:939-1144) ---------------
+// A chunk of up to kPrefillChunk prompt tokens goes through each layer
+// together: the batched GEMVs (matmul_batch) read every weight about once per
+// chunk, the prefill attention kernel appends and attends the chunk's rows.
+constexpr int kPrefillChunk = 128;
+
+struct ChunkActs {
+  float *x, *xn, *q, *k, *v, *att, *hb;
+  size_t bytes;
+};
+
+ChunkActs carve_chunk(const plh_model* m, int T, void* base) {
+  const size_t q_dim = (size_t)m->n_heads * m->head_dim;
+  const size_t kv_dim = (size_t)m->n_kv_heads * m->head_dim;
+  const size_t E = (size_t)m->n_embd, F = (size_t)m->n_ffn;
+  const size_t sizes[7] = {T * E, T * E, T * q_dim, T * kv_dim, T * kv_dim, T * q_dim, T * F};
+  ChunkActs a{};
+  float** dst[7] = {&a.x, &a.xn, &a.q, &a.k, &a.v, &a.att, &a.hb};
+  size_t off = 0;
+  for (int i = 0; i < 7; ++i) {
+    *dst[i] = base ? (float*)((char*)base + off) : nullptr;
+    off += piece(sizes[i]);
+  }
+  a.bytes = off;
+  return a;
+}
+
+int ensure_prefill_ws(size_t bytes) {
+  Context& c = ctx();
+  if (c.pf_ws && c.pf_ws_bytes >= bytes) return 0;
+  if (c.pf_ws) {
+    if (check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize")) return -1;
+    if (check_hip(hipFree(c.pf_ws), "hipFree(prefill workspace)")) return -1;
+    c.pf_ws = nullptr;
+    c.pf_ws_bytes = 0;
+  }
+  if (check_hip(hipMalloc(&c.pf_ws, bytes), "hipMalloc(prefill workspace)")) {
+    c.pf_ws = nullptr;
+    return -1;
+  }
+  c.pf_ws_bytes = bytes;
+  return 0;
+}
+
+int launch_rmsnorm_rows(const float* x, const float* w, float* out, int n, int rows, float eps) {
+  hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(rows), dim3(kNormThreads), norm_lds_bytes(n),
+                     ctx().stream, x, w, out, n, n, eps);
+  return check_hip(hipGetLastError(), "rmsnorm_rows_kernel launch");
+}
+
+// Tokens [0, T) of the chunk at positions pos0.. through every layer; on
+// return a.x holds their residual streams.
+int prefill_chunk(const plh_model* m, const int* tokens, int T, int pos0, const ChunkActs& a) {
+  const int E = m->n_embd, F = m->n_ffn;
+  const int Q = m->n_heads * m->head_dim, KV = m->n_kv_heads * m->head_dim;
+  const float eps = m->rms_norm_eps;
+  const size_t rb = embd_row_bytes(m->embd_type, E);
+  for (int t0 = 0; t0 < T; t0 += kEmbedTokens) {
+    EmbedArgs ea{};
+    ea.n_tok = min(kEmbedTokens, T - t0);
+    for (int i = 0; i < ea.n_tok; ++i) ea.tokens[i] = tokens[t0 + i];
+    ea.qtype = m->embd_type, ea.n = E, ea.stride = E, ea.row_bytes = rb;
+    ea.table = (const uint8_t*)m->token_embd;
+    ea.x = a.x + (size_t)t0 * E;
+    hipLaunchKernelGGL(embed_rows_kernel, dim3((E + 255) / 256, ea.n_tok), dim3(256), 0,
+                       ctx().stream, ea);
+    if (check_hip(hipGetLastError(), "embed_rows_kernel launch")) return -1;
+  }
+  auto call = [&](const plh_matrix& w, int n, int d, const float* x, int x_stride, float* out,
+                  int out_stride, const float* bias, const float* gate, const float* resid) {
+    GemvCall g{};
+    g.qtype = w.qtype, g.n = n, g.d = d, g.w = w.w, g.x = x, g.out = out;
+    g.bias = bias, g.gate = gate, g.resid = resid;
+    g.n_tok = T, g.x_stride = x_stride, g.out_stride = out_stride;
+    return g;
+  };
+  for (int l = 0; l < m->n_layers; ++l) {
+    const plh_layer& L = m->layers[l];
+    // model.c:988-1017: rmsnorm, q / k / v projections, biases where present
+    if (launch_rmsnorm_rows(a.x, L.attn_norm, a.xn, E, T, eps) ||
+        gemv_launch(call(L.q, E, Q, a.xn, E, a.q, Q, L.q_bias, nullptr, nullptr)) ||
+        gemv_launch(call(L.k, E, KV, a.xn, E, a.k, KV, L.k_bias, nullptr, nullptr)) ||
+        gemv_launch(call(L.v, E, KV, a.xn, E, a.v, KV, L.v_bias, nullptr, nullptr)))
+      return -1;
+    // model.c:1019-1090: QK-norm, RoPE, fp16 append and attention per token
+    const int rc =
+        L.q_norm ? plh_attn_prefill_qknorm(m->n_layers, m->n_heads, m->n_kv_heads, m->head_dim,
+                                           m->max_seq_len, m->rope_type, l, 1, pos0, T, a.q, a.k,
+                                           a.v, m->key_cache, m->val_cache, m->rope_cos,
+                                           m->rope_sin, a.att, Q, L.q_norm, L.k_norm, eps)
+                 : plh_attn_prefill(m->n_layers, m->n_heads, m->n_kv_heads, m->head_dim,
+                                    m->max_seq_len, m->rope_type, l, 1, pos0, T, a.q, a.k, a.v,
+                                    m->key_cache, m->val_cache, m->rope_cos, m->rope_sin, a.att,
+                                    Q);
+    if (rc) return -1;
+    // model.c:1092-1107: output projection, its bias where present, residual
+    if (gemv_launch(call(L.o, Q, E, a.att, Q, a.x, E, L.o_bias, nullptr, a.x))) return -1;
+    // model.c:1109-1139: rmsnorm, gate / up, silu * up, down, residual
+    if (launch_rmsnorm_rows(a.x, L.ffn_norm, a.xn, E, T, eps)) return -1;
+    const GemvCall gate = call(L.gate, E, F, a.xn, E, a.hb, F, nullptr, nullptr, nullptr);
+    const GemvCall up = call(L.up, E, F, a.xn, E, a.hb, F, nullptr, nullptr, nullptr);
+    if (L.gate.qtype == L.up.qtype) {
+      if (gemv_pair_launch(gate, up)) return -1;
+    } else {
+      GemvCall up_g = up;
+      up_g.gate = a.hb;
+      if (gemv_launch(gate) || gemv_launch(up_g)) return -1;
+    }
+    if (gemv_launch(call(L.down, F, E, a.hb, F, a.x, E, nullptr, nullptr, a.x))) return -1;
+  }
+  return 0;
+}
+
 }  // namespace
 
 extern "C" {
@@ -372,12 +519,28 @@ int plh_forward_prefill(const plh_model* m, const int* tokens, int n_tokens, int
       set_error("plh_forward_prefill: token %d out of range", tokens[bi]);
       return -1;
     }
-  for (int bi = 0; bi < n_tokens; ++bi) {
-    const bool last = bi == n_tokens - 1;
-    if (forward_token(m, tokens[bi], start_pos + bi, workspace, false, last ? logits : nullptr,
-                      last ? x_out : nullptr))
-      return -1;
+  const int chunk = min(n_tokens, kPrefillChunk);
+  const ChunkActs sized = carve_chunk(m, chunk, nullptr);
+  if (ensure_prefill_ws(sized.bytes)) return -1;
+  const ChunkActs a = carve_chunk(m, chunk, ctx().pf_ws);
+  int T = 0;
+  for (int t0 = 0; t0 < n_tokens; t0 += chunk) {
+    T = min(chunk, n_tokens - t0);
+    if (prefill_chunk(m, tokens + t0, T, start_pos + t0, a)) return -1;
   }
+  // model.c:1138-1143: final rmsnorm and logits of the last token
+  const int E = m->n_embd;
+  const float* xl = a.x + (size_t)(T - 1) * E;
+  GemvCall g{};
+  g.qtype = m->output.qtype, g.n = E, g.d = m->vocab_size, g.w = m->output.w, g.x = xl;
+  g.out = logits, g.norm_w = m->output_norm, g.norm_eps = m->rms_norm_eps;
+  if (E > kGemvNormMax) {  // too long for the prologue: normalise first
+    if (launch_rmsnorm(xl, m->output_norm, a.xn, E, m->rms_norm_eps)) return -1;
+    g.x = a.xn, g.norm_w = nullptr;
+  }
+  if (gemv_launch(g)) return -1;
+  if (x_out && launch_rmsnorm(xl, m->output_norm, x_out, E, m->rms_norm_eps)) return -1;
+  (void)workspace;
   return 0;
 }
 

@@ -599,6 +599,86 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int wg, float* term
   }
 }
 
+// ---- batched GEMV: matmul_batch (tensor.c:322-366) ------------------------
+// out[t][i] = vec_dot(row i, x[t]) for the tokens of a prompt chunk, each
+// (row, token) with exactly the single-vector kernel's arithmetic.  A
+// workgroup holds its rows' weights in registers and runs up to kTokTile
+// tokens over them; the token tiles of one row tile share an XCD (and its
+// L2), so the weights come from HBM about once per chunk.
+constexpr int kTokTile = 8;
+
+struct BatchArgs {
+  GemvArgs a;
+  int n_tok, x_stride, out_stride;  // tokens, floats between x rows / out rows
+  int row_tiles, tok_tiles;
+};
+
+template <class F, int RB, bool PAIR>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(BatchArgs b) {
+  extern __shared__ __align__(16) float terms[];  // [row][token][tpitch]
+  const GemvArgs& a = b.a;
+  const int xcd = blockIdx.x & 7, k = blockIdx.x >> 3;
+  const int r_tile = (k / b.tok_tiles) * 8 + xcd;
+  const int t_tile = k % b.tok_tiles;
+  if (r_tile >= b.row_tiles) return;
+  const int tid = threadIdx.x;
+  const int r0 = r_tile * a.rows_per_wg;
+  const int rows = min(a.rows_per_wg, (PAIR ? 2 * a.d : a.d) - r0);
+  const int tk0 = t_tile * kTokTile;
+  const int toks = min(kTokTile, b.n_tok - tk0);
+  const int rlane = tid / a.uspan;
+  if (rlane < a.row_par) {
+    for (int it = 0; it < a.unit_iters; ++it) {
+      const int u = tid % a.uspan + it * a.uspan;
+      if (u >= a.units) break;
+      typename F::Raw raw[RB];
+      load_rows<F, RB, PAIR>(a, r0, rows, rlane, u, raw);
+      for (int t = 0; t < toks; ++t) {
+        typename F::X U;
+        F::load_x(PlainX{a.x + (size_t)(tk0 + t) * b.x_stride}, u, U);
+#pragma unroll
+        for (int kk = 0; kk < RB; ++kk) {
+          float tt[F::kTerms];
+          F::terms(u, raw[kk], U, tt);
+          const int rr = rlane + a.row_par * kk;
+          if (rr < rows) {
+#pragma unroll
+            for (int g = 0; g < F::kTerms; ++g)
+              terms[(rr * kTokTile + t) * a.tpitch + F::term_index(u) + g] = tt[g];
+          }
+        }
+      }
+    }
+  }
+  __syncthreads();
+  // one thread per (row, token): idx = t * rows + rr keeps a gate/up pair on
+  // adjacent lanes (rows even)
+  for (int idx = tid; idx < rows * toks; idx += kThreads) {
+    const int t = idx / rows, rr = idx - t * rows;
+    const float* tp = terms + (rr * kTokTile + t) * a.tpitch;
+    float sumf = 0.0f;
+    for (int s = 0; s < a.terms; s += 4) {
+      const float4 v = *(const float4*)(tp + s);
+      sumf = sumf + v.x;
+      if (s + 1 < a.terms) sumf = sumf + v.y;
+      if (s + 2 < a.terms) sumf = sumf + v.z;
+      if (s + 3 < a.terms) sumf = sumf + v.w;
+    }
+    const int r = r0 + rr;
+    const size_t o = (size_t)(tk0 + t) * b.out_stride;
+    if constexpr (PAIR) {
+      const float g = __shfl_xor(sumf, 1);
+      if (r & 1) a.out[o + (r >> 1)] = silu(g) * sumf;
+    } else {
+      if (a.bias_mode == 1) sumf = sumf + a.bias[r];
+      if (a.bias_mode == 2) sumf = sumf + 0.0f;
+      if (a.gate) sumf = silu(a.gate[o + r]) * sumf;
+      if (a.resid) sumf = a.resid[o + r] + sumf;
+      a.out[o + r] = sumf;
+    }
+  }
+}
+
 template <class F, int RB, bool NORM, bool PAIR>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(GemvArgs a) {
   extern __shared__ __align__(16) float terms[];
@@ -797,6 +877,61 @@ int launch_single(int qtype, bool pair, const GemvArgs& a0, int rows) {
   return check_hip(hipGetLastError(), "gemv_kernel launch");
 }
 
+template <class F, bool PAIR>
+void launch_batch(int rb, int grid, size_t lds, hipStream_t st, const BatchArgs& b) {
+  switch (rb) {
+    case 1:
+      hipLaunchKernelGGL((gemm_kernel<F, 1, PAIR>), dim3(grid), dim3(kThreads), lds, st, b);
+      break;
+    case 2:
+      hipLaunchKernelGGL((gemm_kernel<F, 2, PAIR>), dim3(grid), dim3(kThreads), lds, st, b);
+      break;
+    default:
+      hipLaunchKernelGGL((gemm_kernel<F, 4, PAIR>), dim3(grid), dim3(kThreads), lds, st, b);
+      break;
+  }
+}
+
+// Batched launch over n_tok tokens (x rows x_stride apart, out rows
+// out_stride apart; gate and resid indexed like out).  No rmsnorm prologue.
+int launch_batched(int qtype, bool pair, const GemvArgs& a0, int rows, int n_tok, int x_stride,
+                   int out_stride) {
+  if (a0.norm_w) {
+    set_error("batched GEMV: no rmsnorm prologue (normalise the rows first)");
+    return -1;
+  }
+  BatchArgs b{};
+  b.a = a0;
+  // rows per thread: the most (4, 2, 1) whose term buffer for kTokTile tokens
+  // fits 64 KiB of LDS
+  int rb = 4;
+  while (rb > 1 &&
+         (size_t)b.a.row_par * rb * kTokTile * b.a.tpitch * sizeof(float) > 64 * 1024)
+    rb /= 2;
+  if (pair && (b.a.row_par * rb) % 2) rb *= 2;
+  const size_t lds = (size_t)b.a.row_par * rb * kTokTile * b.a.tpitch * sizeof(float);
+  if (lds > 64 * 1024) {
+    set_error("batched GEMV: row of %d weights too long for the term buffer", b.a.n);
+    return -1;
+  }
+  b.a.rows_per_wg = b.a.row_par * rb;
+  b.n_tok = n_tok;
+  b.x_stride = x_stride;
+  b.out_stride = out_stride;
+  b.row_tiles = (rows + b.a.rows_per_wg - 1) / b.a.rows_per_wg;
+  b.tok_tiles = (n_tok + kTokTile - 1) / kTokTile;
+  const int grid = 8 * ((b.row_tiles + 7) / 8) * b.tok_tiles;
+  hipStream_t st = ctx().stream;
+  if (qtype == kTypeQ4K)
+    pair ? launch_batch<Q4K, true>(rb, grid, lds, st, b) : launch_batch<Q4K, false>(rb, grid, lds, st, b);
+  else if (qtype == kTypeQ8_0)
+    pair ? launch_batch<Q80, true>(rb, grid, lds, st, b) : launch_batch<Q80, false>(rb, grid, lds, st, b);
+  else
+    pair ? launch_batch<Q6K<4>, true>(rb, grid, lds, st, b)
+         : launch_batch<Q6K<4>, false>(rb, grid, lds, st, b);
+  return check_hip(hipGetLastError(), "gemm_kernel launch");
+}
+
 }  // namespace
 
 extern "C" {
@@ -840,6 +975,19 @@ int plh_gemv_upload(int qtype, int n, int d, const void* host_rows, void* dev) {
   return check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize");
 }
 
+int plh_matmul_batch(int qtype, int n, int d, const void* dev, const float* x, int n_batch,
+                     float* out) {
+  if (n_batch < 1) {
+    set_error("plh_matmul_batch: n_batch %d", n_batch);
+    return -1;
+  }
+  GemvCall g{};
+  g.qtype = qtype, g.n = n, g.d = d, g.w = dev, g.x = x, g.out = out;
+  g.n_tok = n_batch, g.x_stride = n, g.out_stride = d;
+  if (n_batch == 1) g.n_tok = 0;
+  return gemv_launch(g);
+}
+
 int plh_gemv(int qtype, int n, int d, const void* dev, const float* x, float* out) {
   return plh_gemv_ex(qtype, n, d, dev, x, out, nullptr, 0.0f, nullptr, 0, nullptr, nullptr);
 }
@@ -879,6 +1027,8 @@ int gemv_launch(const GemvCall& g) {
   }
   GemvArgs a;
   if (prepare(g, a)) return -1;
+  if (g.n_tok > 1)
+    return launch_batched(g.qtype, false, a, g.d, g.n_tok, g.x_stride, g.out_stride);
   return launch_single(g.qtype, false, a, g.d);
 }
 
@@ -941,6 +1091,8 @@ int gemv_pair_launch(const GemvCall& gate, const GemvCall& up) {
     set_error("plh_gemv: null pointer");
     return -1;
   }
+  if (up.n_tok > 1)
+    return launch_batched(up.qtype, true, a, 2 * up.d, up.n_tok, up.x_stride, up.out_stride);
   return launch_single(up.qtype, true, a, 2 * up.d);
 }
 

@@ -15,6 +15,8 @@ struct Context {
   hipStream_t stream = nullptr;
   void* ws = nullptr;          // split-K partials
   size_t ws_bytes = 0;
+  void* pf_ws = nullptr;       // prompt-chunk activations of plh_forward_prefill
+  size_t pf_ws_bytes = 0;
   int num_cus = 0;
 };
 
@@ -46,6 +48,9 @@ struct GemvCall {
   int bias_zero;
   const float* gate;
   const float* resid;
+  // n_tok > 1: a batch of tokens (matmul_batch), x rows x_stride floats
+  // apart and out / gate / resid rows out_stride apart; no rmsnorm prologue
+  int n_tok, x_stride, out_stride;
 };
 int gemv_launch(const GemvCall& g);
 // Up to three GEMVs over the same x (and the same rmsnorm prologue, if any)

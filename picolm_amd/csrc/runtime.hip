@@ -92,6 +92,7 @@ void plh_shutdown(void) {
   if (c.stream) {
     (void)hipStreamSynchronize(c.stream);
     if (c.ws) (void)hipFree(c.ws);
+    if (c.pf_ws) (void)hipFree(c.pf_ws);
     (void)hipStreamDestroy(c.stream);
   }
   c = Context();

@@ -84,3 +84,26 @@ def test_gemv_rejects_bad_calls(gpu):
     assert P.lib.plh_gemv(G.TYPE_Q4_K, 100, 4, buf.ptr, buf.ptr, buf.ptr) != 0
     assert P.lib.plh_gemv(G.TYPE_Q8_0, 32, 1, None, buf.ptr, buf.ptr) != 0
     buf.free()
+
+
+@pytest.mark.parametrize("qtype,n,d,nb", [
+    (G.TYPE_Q4_K, 2048, 2048, 13), (G.TYPE_Q6_K, 5632, 2048, 9),
+    (G.TYPE_Q8_0, 2048, 256, 17), (G.TYPE_Q6_K, 2048, 256, 8),
+    (G.TYPE_Q4_K, 2048, 5632, 3)])
+def test_matmul_batch_bit_exact(gpu, oracle_mod, qtype, n, d, nb):
+    """tensor.c:322-366 matmul_batch: every (row, token) equals the oracle's
+    single-vector matmul bit for bit, for token counts around the tile."""
+    import ctypes as C
+    P, O = gpu, oracle_mod
+    rng = np.random.default_rng(qtype * 7 + nb)
+    W = S.random_weights(rng, qtype, n, d, S.unit_scale_exp(qtype, n))
+    X = rng.standard_normal((nb, n)).astype(np.float32)
+    M = G.QMatrix(qtype, n, d, W)
+    dx = P.DeviceBuffer.from_numpy(X)
+    out = P.DeviceBuffer(4 * nb * d)
+    P.check(P.lib.plh_matmul_batch(qtype, n, d, C.c_void_p(M.ptr), C.c_void_p(dx.ptr), nb,
+                                   C.c_void_p(out.ptr)), "plh_matmul_batch")
+    got = out.download(np.float32, (nb, d))
+    for b in range(nb):
+        want = O.matmul(W, X[b], n, d, qtype)
+        assert np.array_equal(got[b].view(np.uint32), want.view(np.uint32)), b
