@@ -360,11 +360,11 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, bool 
   }
   if (!logits) return 0;
   // final norm and logits (model.c:918-922)
-  if (normed(m->output_norm, &xin, &nw) ||
-      gemv_launch(call(m->output, E, m->vocab_size, xin, logits, nw, nullptr, 0, nullptr,
-                       nullptr)))
-    return -1;
-  if (x_out && launch_rmsnorm(a.x, m->output_norm, x_out, E, eps)) return -1;
+  if (normed(m->output_norm, &xin, &nw)) return -1;
+  GemvCall out = call(m->output, E, m->vocab_size, xin, logits, nw, nullptr, 0, nullptr, nullptr);
+  out.xn_out = nw ? x_out : nullptr;  // the prologue's rmsnorm(x) is state.x
+  if (gemv_launch(out)) return -1;
+  if (x_out && !nw && plh_memcpy_dtod(x_out, xin, (size_t)E * sizeof(float))) return -1;
   return 0;
 }
 
@@ -538,8 +538,9 @@ int plh_forward_prefill(const plh_model* m, const int* tokens, int n_tokens, int
     if (launch_rmsnorm(xl, m->output_norm, a.xn, E, m->rms_norm_eps)) return -1;
     g.x = a.xn, g.norm_w = nullptr;
   }
+  g.xn_out = g.norm_w ? x_out : nullptr;
   if (gemv_launch(g)) return -1;
-  if (x_out && launch_rmsnorm(xl, m->output_norm, x_out, E, m->rms_norm_eps)) return -1;
+  if (x_out && !g.norm_w && plh_memcpy_dtod(x_out, a.xn, (size_t)E * sizeof(float))) return -1;
   (void)workspace;
   return 0;
 }

@@ -173,6 +173,7 @@ struct GemvArgs {
   float norm_eps;
   int n;
   int xs_off;  // floats from the LDS base to the staged rmsnorm(x)
+  float* xn_out;  // workgroup 0 also stores rmsnorm(x) here (or null)
   // Gate/up pair (gemv_body<..., true>): virtual row 2r is row r of w (gate),
   // 2r + 1 row r of w2 (up, same type and shape); out[r] = silu(gate) * up.
   const uint8_t* w2;
@@ -548,6 +549,8 @@ __device__ __forceinline__ void gemv_body(const GemvArgs& a, int wg, float* term
         xs[xs_index(idx)] = (a.x[idx] * scale) * a.norm_w[idx];
     }
     __syncthreads();
+    if (a.xn_out && wg == 0)
+      for (int idx = tid; idx < a.n; idx += kThreads) a.xn_out[idx] = xs[xs_index(idx)];
     const LdsX xsrc{xs};
     if (first) {
       unit_terms<F, RB>(a, xsrc, terms, rows, rlane, u, raw);
@@ -804,6 +807,7 @@ int prepare(const GemvCall& g, GemvArgs& a) {
   a.norm_w = g.norm_w;
   a.norm_eps = g.norm_eps;
   a.n = n;
+  a.xn_out = g.norm_w ? g.xn_out : nullptr;
   return 0;
 }
 

@@ -51,6 +51,8 @@ struct GemvCall {
   // n_tok > 1: a batch of tokens (matmul_batch), x rows x_stride floats
   // apart and out / gate / resid rows out_stride apart; no rmsnorm prologue
   int n_tok, x_stride, out_stride;
+  // with the rmsnorm prologue: also store rmsnorm(x) [n] here (or null)
+  float* xn_out;
 };
 int gemv_launch(const GemvCall& g);
 // Up to three GEMVs over the same x (and the same rmsnorm prologue, if any)

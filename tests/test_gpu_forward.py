@@ -223,6 +223,28 @@ def test_prefill_matches_oracle(gpu, oracle_mod, cfg):
         dm.free()
 
 
+def test_forward_separate_norm_launches(gpu, oracle_mod):
+    """Tuning key 4 forms each rmsnorm in a launch of its own (the path of
+    n_embd > 7680): same logits and state.x as the fused prologue."""
+    P, O = gpu, oracle_mod
+    h = S.SynthModel(**dict(LLAMA, n_layers=2), seed=41)
+    dm = P.DeviceModel(h)
+    try:
+        got = {}
+        for mode in (0, 1):
+            P.check(P.lib.plh_set_tuning(4, mode), "plh_set_tuning")
+            dm.load_cache(np.zeros(h.cache_elems(), np.uint16), np.zeros(h.cache_elems(), np.uint16))
+            for pos, tok in enumerate((5, 6, 7)):
+                dm.forward(tok, pos)
+            P.synchronize()
+            got[mode] = (dm.fetch_logits(), dm.fetch_x())
+        assert np.array_equal(got[0][0].view(np.uint32), got[1][0].view(np.uint32))
+        assert np.array_equal(got[0][1].view(np.uint32), got[1][1].view(np.uint32))
+    finally:
+        P.check(P.lib.plh_set_tuning(4, 0), "plh_set_tuning")
+        dm.free()
+
+
 def test_forward_rejects_bad_calls(gpu):
     P = gpu
     h = S.SynthModel(**dict(LLAMA, n_layers=1), seed=13)
