@@ -286,14 +286,13 @@ size_t plh_forward_workspace_bytes(const plh_model* m) {
 
 namespace {
 
-// One token through every layer (arguments checked by the caller).
-// bias_always: model_forward_ex's handling of the q and output biases (added
-// always, zeros when absent, model.c:781-782 / 895-896) rather than
-// model_forward_prefill's (added only when present, model.c:1002-1006 /
-// 1095-1099).  logits == NULL stops after the last layer (a prompt token
-// whose logits nobody reads).
-int forward_token(const plh_model* m, int token, int pos, void* workspace, bool bias_always,
-                  float* logits, float* x_out) {
+// One token through every layer, the final norm and the logits (arguments
+// checked by the caller).  The q and output biases follow model_forward_ex:
+// added always, zeros when absent (model.c:781-782 / 895-896), which turns a
+// -0 sum into +0 where model_forward_prefill, adding only present biases,
+// would not.
+int forward_token(const plh_model* m, int token, int pos, void* workspace, float* logits,
+                  float* x_out) {
   const int E = m->n_embd, F = m->n_ffn;
   const int Q = m->n_heads * m->head_dim, KV = m->n_kv_heads * m->head_dim;
   const float eps = m->rms_norm_eps;
@@ -326,7 +325,7 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, bool 
     // attention block (model.c:777-897): q, k, v in one launch
     if (normed(L.attn_norm, &xin, &nw)) return -1;
     const GemvCall qkv[3] = {
-        call(L.q, E, Q, xin, a.q, nw, L.q_bias, bias_always && !L.q_bias, nullptr, nullptr),
+        call(L.q, E, Q, xin, a.q, nw, L.q_bias, !L.q_bias, nullptr, nullptr),
         call(L.k, E, KV, xin, a.k, nw, L.k_bias, 0, nullptr, nullptr),
         call(L.v, E, KV, xin, a.v, nw, L.v_bias, 0, nullptr, nullptr)};
     if (gemv_multi_launch(qkv, 3)) return -1;
@@ -341,8 +340,7 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, bool 
                                               m->rope_cos, m->rope_sin, a.att);
     if (rc) return -1;
     // x = x + (Wo att + o_bias)
-    if (gemv_launch(call(L.o, Q, E, a.att, a.x, nullptr, L.o_bias, bias_always && !L.o_bias,
-                         nullptr, a.x)))
+    if (gemv_launch(call(L.o, Q, E, a.att, a.x, nullptr, L.o_bias, !L.o_bias, nullptr, a.x)))
       return -1;
     // SwiGLU block (model.c:899-922): hb = silu(gate xn) * (up xn), xn = rmsnorm(x),
     // in one launch when gate and up share a type; then x = x + Wdown hb
@@ -358,7 +356,6 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, bool 
     }
     if (gemv_launch(call(L.down, F, E, a.hb, a.x, nullptr, nullptr, 0, nullptr, a.x))) return -1;
   }
-  if (!logits) return 0;
   // final norm and logits (model.c:918-922)
   if (normed(m->output_norm, &xin, &nw)) return -1;
   GemvCall out = call(m->output, E, m->vocab_size, xin, logits, nw, nullptr, 0, nullptr, nullptr);
@@ -498,7 +495,7 @@ int plh_forward(const plh_model* m, int token, int pos, void* workspace, float* 
     set_error("plh_forward: token %d / pos %d out of range or null buffer", token, pos);
     return -1;
   }
-  return forward_token(m, token, pos, workspace, true, logits, x_out);
+  return forward_token(m, token, pos, workspace, logits, x_out);
 }
 
 int plh_forward_prefill(const plh_model* m, const int* tokens, int n_tokens, int start_pos,
