@@ -223,6 +223,36 @@ def test_prefill_matches_oracle(gpu, oracle_mod, cfg):
         dm.free()
 
 
+def test_prefill_long_prompt_chunks(gpu, oracle_mod):
+    """A 200-token prompt after a 5-token prefix: two 128-token chunks (the
+    second ragged), embedding launches of 64 tokens, then a decode step."""
+    P, O = gpu, oracle_mod
+    h = S.SynthModel(**dict(LLAMA, n_layers=2, max_seq_len=256), seed=43)
+    dm = P.DeviceModel(h)
+    orc = O.OracleForward(h)
+    rng = np.random.default_rng(44)
+    kv_layer = h.max_seq_len * h.kv_dim
+    try:
+        start = 0
+        for n in (5, 200):
+            toks = rng.integers(0, h.vocab_size, n).astype(np.int32)
+            print(f"[case] long prefill start {start} n {n}", flush=True)
+            dm.prefill(toks, start)
+            P.synchronize()
+            lo, xo = orc.prefill(toks, start, n_threads=8)
+            assert max(normwise(dm.fetch_logits(), lo), normwise(dm.fetch_x(), xo)) <= FWD_TOL
+            start += n
+        kc, vc = dm.fetch_cache()
+        assert np.array_equal(kc[:kv_layer], orc.kc[:kv_layer])
+        assert np.array_equal(vc[:kv_layer], orc.vc[:kv_layer])
+        dm.forward(9, start)
+        P.synchronize()
+        lo, _ = orc.forward(9, start, n_threads=8)
+        assert normwise(dm.fetch_logits(), lo) <= FWD_TOL
+    finally:
+        dm.free()
+
+
 def test_forward_separate_norm_launches(gpu, oracle_mod):
     """Tuning key 4 forms each rmsnorm in a launch of its own (the path of
     n_embd > 7680): same logits and state.x as the fused prologue."""
