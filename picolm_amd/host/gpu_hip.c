@@ -203,13 +203,17 @@ static int upload_weight(const void *host, int qtype, int d, int n) {
 }
 
 /* gpu.c:447-458: the seven projections of layers < gpu_layers, then the
- * output matrix. */
+ * output matrix.  attn_q is uploaded with the q_dim = n_heads*head_dim rows
+ * that model.c:779-781 multiplies with; gpu.c:451 passes n_embd, the same
+ * number for every model the reference loads (head_dim = n_embd / n_heads,
+ * model.c:408), but for a hand-built layout it would read past the host
+ * tensor when q_dim < n_embd. */
 static int upload_weights(const model_t *m) {
     const model_config_t *c = &m->config;
     int kv_dim = c->n_kv_heads * c->head_dim, q_dim = c->n_heads * c->head_dim;
     for (int l = 0; l < gs.gpu_layers && l < c->n_layers; l++) {
         const layer_weights_t *lw = &m->weights.layers[l];
-        if (upload_weight(lw->attn_q, (int)lw->type_attn_q, c->n_embd, c->n_embd) ||
+        if (upload_weight(lw->attn_q, (int)lw->type_attn_q, q_dim, c->n_embd) ||
             upload_weight(lw->attn_k, (int)lw->type_attn_k, kv_dim, c->n_embd) ||
             upload_weight(lw->attn_v, (int)lw->type_attn_v, kv_dim, c->n_embd) ||
             upload_weight(lw->attn_output, (int)lw->type_attn_output, c->n_embd, q_dim) ||
@@ -296,6 +300,10 @@ static int upload_forward(const model_t *m) {
     const int KV = c->n_kv_heads * c->head_dim;
     if (gs.gpu_layers < c->n_layers || E > 12288 || !w->token_embd || !st->logits || !st->x)
         return 1;
+    /* The reference's loader sets head_dim = n_embd / n_heads (model.c:408),
+     * so its forward pass only ever runs q_dim == n_embd (its q and xb buffers
+     * hold n_embd floats, model.c:568-571); other layouts keep the CPU path. */
+    if (Q != E) return 1;
     const size_t rb = embd_row_bytes(w->type_token_embd, E);
     if (rb == 0) return 1;
     plh_model *pm = &gs.fwd;

@@ -87,7 +87,7 @@ int main(int argc, char **argv) {
         gguf_type_t *tys[7] = {&lw->type_attn_q, &lw->type_attn_k, &lw->type_attn_v,
                                &lw->type_attn_output, &lw->type_ffn_gate, &lw->type_ffn_up,
                                &lw->type_ffn_down};
-        const int dims[7][2] = {{c->n_embd, c->n_embd}, {kv_dim, c->n_embd},
+        const int dims[7][2] = {{q_dim, c->n_embd},     {kv_dim, c->n_embd},
                                 {kv_dim, c->n_embd},    {c->n_embd, q_dim},
                                 {c->n_ffn, c->n_embd},  {c->n_ffn, c->n_embd},
                                 {c->n_embd, c->n_ffn}};

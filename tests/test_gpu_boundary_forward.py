@@ -5,8 +5,9 @@ model_forward_prefill would call them, against the oracle's forward pass.
 Checks: a prompt in two prefill chunks then decode steps returns 0 each
 time; logits and state.x match the oracle's within the forward tolerance;
 the host caches hold the appended rows (layer 0 bit-exact, later layers to
-one fp16 step); PICOLM_HIP_FORWARD=0, a model with an F32 projection and
-PICOLM_GPU_LAYERS below the layer count fall back (-1, nothing written)."""
+one fp16 step); PICOLM_HIP_FORWARD=0, a model with an F32 projection, models
+whose q_dim is not n_embd and PICOLM_GPU_LAYERS below the layer count fall
+back (-1, nothing written)."""
 import os
 import subprocess
 
@@ -131,3 +132,12 @@ def test_forward_fallbacks(tmp_path):
     rcs, res, kc, vc = run(tmp_path, h32, steps)
     assert rcs == (0, 0)
     assert all(rc == -1 for rc, _, _ in res)
+    # q_dim = n_heads * head_dim other than n_embd: the reference's loader
+    # never builds one (head_dim = n_embd / n_heads, model.c:408), so the
+    # whole-forward hooks decline and the CPU path runs
+    for heads, seed in ((16, 35), (4, 36)):
+        hq = S.SynthModel(**dict(CFG, n_heads=heads, n_kv_heads=2,
+                                 types=dict(CFG["types"], o=Q8)), seed=seed)
+        rcs, res, kc, vc = run(tmp_path, hq, steps)
+        assert rcs == (0, 0)
+        assert all(rc == -1 and not lg.any() for rc, lg, _ in res)

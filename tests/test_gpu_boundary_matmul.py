@@ -7,7 +7,8 @@ oracle's matmul (the reference's x86-64 AVX2 vec_dot); F32 / F16 matrices
 fall back (-1, nothing written); an unknown pointer, a wrong d or a wrong
 type fall back; PICOLM_GPU_LAYERS=1 leaves later layers' matrices on the CPU
 (the output matrix stays on the GPU, gpu.c:457-458); PICOLM_HIP_MATMUL=0
-uploads nothing."""
+uploads nothing.  Head layouts with q_dim = n_heads * head_dim equal to,
+twice and half of n_embd (the q projection has q_dim rows)."""
 import os
 import subprocess
 
@@ -27,7 +28,7 @@ def run(tmp_path, O, dims, types, type_out, seed, env_extra=None):
     L, n_embd, n_ffn, n_heads, n_kv, hd, vocab = dims
     rng = np.random.default_rng(seed)
     kv_dim, q_dim = n_kv * hd, n_heads * hd
-    shapes = [(n_embd, n_embd), (kv_dim, n_embd), (kv_dim, n_embd), (n_embd, q_dim),
+    shapes = [(q_dim, n_embd), (kv_dim, n_embd), (kv_dim, n_embd), (n_embd, q_dim),
               (n_ffn, n_embd), (n_ffn, n_embd), (n_embd, n_ffn)]
     mats = []
     for l in range(L):
@@ -73,9 +74,15 @@ TYPES = [[Q4K, Q6K, Q8, Q4K, Q4K, Q8, Q6K],
          [Q6K, Q4K, F32, Q8, F16, Q4K, Q4K]]
 
 
-def test_matmul_offload_bit_exact(tmp_path, oracle_mod):
+# q_dim = n_heads * head_dim differs from n_embd: Qwen3-style (q_dim 2 n_embd)
+# and the other way round; the q and o projections are d x n and n x d
+QDIMS = [DIMS, (2, 256, 512, 4, 2, 128, 700), (2, 512, 512, 2, 1, 128, 300)]
+
+
+@pytest.mark.parametrize("dims", QDIMS, ids=["q=e", "q=2e", "q=e/2"])
+def test_matmul_offload_bit_exact(tmp_path, oracle_mod, dims):
     O = oracle_mod
-    rcs, mats, data, res, neg = run(tmp_path, O, DIMS, TYPES, Q6K, seed=1)
+    rcs, mats, data, res, neg = run(tmp_path, O, dims, TYPES, Q6K, seed=1)
     assert rcs == (0, 0)
     for (qt, n, d), (W, x), (rc, out) in zip(mats, data, res):
         if qt in (F32, F16):
