@@ -499,8 +499,12 @@ int gpu_try_attention(model_t *m, int layer, int pos, float *q, float *k, const 
     size_t q_bytes = (size_t)gs.n_heads * gs.head_dim * sizeof(float);
     size_t kv_bytes = (size_t)gs.n_kv_heads * gs.head_dim * sizeof(float);
     if (plh_memcpy_htod(gs.d_q, q, q_bytes) != 0 || plh_memcpy_htod(gs.d_k, k, kv_bytes) != 0 ||
-        plh_memcpy_htod(gs.d_v, v, kv_bytes) != 0)
-        return -1; /* nothing on the device changed yet */
+        plh_memcpy_htod(gs.d_v, v, kv_bytes) != 0) {
+        /* nothing on the device changed, but the CPU path now appends a row the
+         * device cache will not hold: later calls must not use the device */
+        backend_lost("staging copy");
+        return -1;
+    }
     int rc;
     if (gs.qkn[layer]) {
         size_t off = (size_t)layer * gs.head_dim;
@@ -541,8 +545,10 @@ int gpu_try_attention_prefill(model_t *m, int layer, int start_pos, int n_tokens
     if (stride < q_dim) return -1;
     if (plh_memcpy_htod(gs.d_q, q, (size_t)n_tokens * q_dim * sizeof(float)) != 0 ||
         plh_memcpy_htod(gs.d_k, k, (size_t)n_tokens * kv_dim * sizeof(float)) != 0 ||
-        plh_memcpy_htod(gs.d_v, v, (size_t)n_tokens * kv_dim * sizeof(float)) != 0)
+        plh_memcpy_htod(gs.d_v, v, (size_t)n_tokens * kv_dim * sizeof(float)) != 0) {
+        backend_lost("staging copy"); /* as in gpu_try_attention */
         return -1;
+    }
     int dev_stride = (int)((q_dim + 3) & ~(size_t)3);
     int rc;
     if (gs.qkn[layer]) {
