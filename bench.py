@@ -687,8 +687,9 @@ def main():
                     help="prompt tokens of the forward-pass workload")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU; the attention block needs no "
-                                   "collectives (see DESIGN.md for how it would shard)",
+        print(json.dumps({"error": "one GPU only: the attention block would shard by kv head "
+                                   "(no exchange) or by sequence (one merge of the split "
+                                   "partials per layer); neither is built",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     import picolm_amd as P
