@@ -68,7 +68,7 @@ MALL_DEFEAT_BYTES = 512 << 20
 
 MFMA_F16_PEAK_TFS = 2516.6
 
-HOST_THREADS_MAX = 16   # the GPU box's host CPU share for one GPU
+HOST_THREADS_MAX = 16   # host CPU threads available per GPU
 
 WORKLOADS = {
     "tinyllama_decode_pos2047": dict(L=22, Hq=32, Hkv=4, D=64, S=2048, theta=1e4, pos=2047),

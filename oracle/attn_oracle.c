@@ -2,7 +2,8 @@
  * attn_oracle.c -- CPU restatement of picolm's attention block (test oracle).
  *
  * TEST INFRASTRUCTURE ONLY: loaded by tests/, the smoke entry and the bench's
- * CPU-baseline leg as the checker.  Never linked into the product library.
+ * CPU-baseline leg to check results against.  Never linked into the product
+ * library.
  *
  * Build: gcc -O2 -std=c11 -ffp-contract=off (oracle/Makefile).  The reference
  * builds with -O2 -std=c11 (picolm/Makefile:2), whose ISO mode disables FMA

@@ -1,7 +1,7 @@
 /*
  * attn_oracle.h -- CPU restatement of picolm's attention block.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the checker: tests/, the smoke
+ * TEST INFRASTRUCTURE ONLY.  Results are checked against it: tests/, the smoke
  * entry and the bench's CPU-baseline leg load it; the product (libpicolm_hip)
  * never links, calls or falls back to it.
  *

@@ -5,7 +5,7 @@
  * GEMV restatements of attn_oracle.h and quant_oracle.h.
  *
  * TEST INFRASTRUCTURE ONLY: tests/, the smoke entry and the bench's CPU leg
- * load it as the checker; the product never links or calls it.
+ * load it to check results against; the product never links or calls it.
  *
  * Pinning (tests/test_oracle_forward.py): logits, final residual and every
  * appended KV row bit-exact against the reference's own model_forward and

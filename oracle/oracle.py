@@ -2,7 +2,8 @@
 reference harness (oracle/_ref/libpicolm_ref.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, the smoke entry and the bench's
-CPU-baseline leg, as the checker.  The product package never imports it.
+CPU-baseline leg, to check results against.  The product package never
+imports it.
 """
 from __future__ import annotations
 

@@ -6,7 +6,7 @@
  * and matmul's row loop (tensor.c:200-215).
  *
  * TEST INFRASTRUCTURE ONLY: tests/, the smoke entry and the bench's CPU leg
- * load it as the checker; the product never links or calls it.
+ * load it to check results against; the product never links or calls it.
  *
  * The AVX2 paths keep eight running sums (one per 256-bit lane) and reduce
  * them with hsum_avx2 (quant.h:33-46), which adds as

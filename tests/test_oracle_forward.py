@@ -1,5 +1,5 @@
-"""Pins the oracle's whole forward pass (forward_oracle.c) -- the checker of
-the device forward -- against the reference's own model_forward and
+"""Pins the oracle's whole forward pass (forward_oracle.c) -- what the device
+forward is checked against -- against the reference's own model_forward and
 model_forward_prefill (model.c:742-925, 939-1144, compiled into oracle/_ref
 and driven by ref_harness.c on the same host buffers).
 
