@@ -448,6 +448,22 @@ def run_decode(P, w, steps, warmup, name):
     P.synchronize()
     pl_ms = e0.elapsed_ms(e1) / pl_steps
 
+    # warm: every step reuses copy 0, so a cache that fits the 256 MiB
+    # Infinity Cache is served from it (reported apart, never the headline)
+    def launch_warm(i):
+        q, k, v, o = qkv[0]
+        call(0, L, q.ptr, k.ptr, v.ptr, 0, o.ptr)
+    with P.Graph() as g3:
+        for i in range(steps):
+            launch_warm(i)
+    g3.launch()
+    P.synchronize()
+    e0.record()
+    g3.launch()
+    e1.record()
+    P.synchronize()
+    warm_ms = e0.elapsed_ms(e1) / steps
+
     algo = decode_bytes(w)
     ms_step = wall * 1e3 / steps
     achieved = algo / (k_mean * 1e-3) / 1e9
@@ -465,6 +481,10 @@ def run_decode(P, w, steps, warmup, name):
         "per_layer_launches": {"us_per_token": pl_ms * 1e3,
                                "gbs": algo / (pl_ms * 1e-3) / 1e9,
                                "launches_per_token": L},
+        "warm": {"us_per_token": warm_ms * 1e3,
+                 "gbs": algo / (warm_ms * 1e-3) / 1e9,
+                 "note": "one cache copy reused every step: Infinity-Cache resident when "
+                         "it fits in 256 MiB; not the headline"},
     }
     # keep what the CPU baseline needs (copy 0 before further appends)
     result["_cpu_inputs"] = (cfg, keys[0], vals[0], qkv[0], cos_t, sin_t, d_qn, d_kn)
