@@ -73,7 +73,7 @@ template <>
 struct DecodeShape<128> {
   static constexpr int W = 4, PF = 1;
 };
-constexpr int kCombineChunk = 16;  // split partials loaded together by the combine
+constexpr int kCombineChunk = 16;  // most split partials loaded together by the combine
 
 template <int D>
 struct Tile {
@@ -535,8 +535,9 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
 }
 
 // Merges the n_split partials of one group: out = sum_s O_s 2^(m_s-M) /
-// sum_s l_s 2^(m_s-M) with M the largest m_s.
-template <int D>
+// sum_s l_s 2^(m_s-M) with M the largest m_s.  CH partials are loaded
+// together (8 when there are at most 8 splits, else kCombineChunk).
+template <int D, int CH>
 __global__ __launch_bounds__(kCombineThreads) void attn_decode_combine_kernel(DecodeArgs a) {
   // group g runs on the XCD whose L2 holds its partials: the main kernel put
   // group g's splits on XCD g / (per_xcd / n_split), and consecutive
@@ -559,10 +560,10 @@ __global__ __launch_bounds__(kCombineThreads) void attn_decode_combine_kernel(De
     const int h = idx / D, d = idx - (idx / D) * D;
     // the loads of a chunk of splits are issued together, then merged
     float M = kNegBig, L = 0.f, O = 0.f;
-    for (int s0 = 0; s0 < a.n_split; s0 += kCombineChunk) {
-      float mi[kCombineChunk], li[kCombineChunk], oi[kCombineChunk];
+    for (int s0 = 0; s0 < a.n_split; s0 += CH) {
+      float mi[CH], li[CH], oi[CH];
 #pragma unroll
-      for (int j = 0; j < kCombineChunk; ++j) {
+      for (int j = 0; j < CH; ++j) {
         const size_t u = (size_t)(u0 + min(s0 + j, a.n_split - 1)) * 16 + h;
         mi[j] = a.part_m[u];
         li[j] = a.part_l[u];
@@ -570,13 +571,13 @@ __global__ __launch_bounds__(kCombineThreads) void attn_decode_combine_kernel(De
       }
       float Mc = M;
 #pragma unroll
-      for (int j = 0; j < kCombineChunk; ++j)
+      for (int j = 0; j < CH; ++j)
         if (s0 + j < a.n_split) Mc = fmaxf(Mc, mi[j]);
       const float r = fast_exp2(M - Mc);
       L *= r;
       O *= r;
 #pragma unroll
-      for (int j = 0; j < kCombineChunk; ++j) {
+      for (int j = 0; j < CH; ++j) {
         if (s0 + j < a.n_split) {
           const float w = fast_exp2(mi[j] - Mc);
           L = __builtin_fmaf(li[j], w, L);
@@ -744,17 +745,20 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
     hipLaunchKernelGGL((attn_decode_kernel<128, true>), grid, b128, 0, c.stream, a);
   if (check_hip(hipGetLastError(), "attn_decode_kernel")) return -1;
   if (n_split == 1) return 0;
-  if (head_dim == 64)
-    hipLaunchKernelGGL(attn_decode_combine_kernel<64>,
-                       dim3((unsigned)(8 * groups_per_xcd),
-                            (16 * 64 + kCombineThreads - 1) / kCombineThreads),
-                       cblock, 0,
+  const dim3 cgrid64((unsigned)(8 * groups_per_xcd),
+                     (16 * 64 + kCombineThreads - 1) / kCombineThreads);
+  const dim3 cgrid128((unsigned)(8 * groups_per_xcd),
+                      (16 * 128 + kCombineThreads - 1) / kCombineThreads);
+  const bool few = n_split <= 8;
+  if (head_dim == 64 && few)
+    hipLaunchKernelGGL((attn_decode_combine_kernel<64, 8>), cgrid64, cblock, 0, c.stream, a);
+  else if (head_dim == 64)
+    hipLaunchKernelGGL((attn_decode_combine_kernel<64, kCombineChunk>), cgrid64, cblock, 0,
                        c.stream, a);
+  else if (few)
+    hipLaunchKernelGGL((attn_decode_combine_kernel<128, 8>), cgrid128, cblock, 0, c.stream, a);
   else
-    hipLaunchKernelGGL(attn_decode_combine_kernel<128>,
-                       dim3((unsigned)(8 * groups_per_xcd),
-                            (16 * 128 + kCombineThreads - 1) / kCombineThreads),
-                       cblock, 0,
+    hipLaunchKernelGGL((attn_decode_combine_kernel<128, kCombineChunk>), cgrid128, cblock, 0,
                        c.stream, a);
   return check_hip(hipGetLastError(), "attn_decode_combine_kernel");
 }
