@@ -25,10 +25,14 @@ Method:
             + Hq*D*4 (out) ]
   * per_layer_launches: the same token as L sequential one-layer calls (how
     a per-layer forward pass uses the block), also graph-replayed;
-  * cpu_baseline: the oracle (the reference's attention restated in C, same
-    op order, out-of-line fp16 widening as in the reference build) timed on
-    one host thread over a bounded sample of the same workload -- the
-    reference runs its attention on one thread whatever its -j;
+  * cpu_baseline: the reference's own decode attention where oracle/_ref (its
+    sources compiled) exists: its model_forward at position pos minus the same
+    token at position 0, on the forward workload's model (same attention
+    shape), matmuls on the host threads -- the reference runs its attention
+    loop on one thread whatever its -j; cpu_baseline_port (or cpu_baseline
+    without oracle/_ref or with --no-forward): the oracle (the attention
+    restated in C, same op order, out-of-line fp16 widening as in the
+    reference build) on one host thread over a bounded sample;
     cpu_baseline_head_parallel: the same arithmetic with the q heads split
     over up to 16 host threads, an upper bound only; "host" records nproc,
     the CPU model and the C library;
@@ -304,6 +308,52 @@ def cpu_baseline_forward(res):
                              "sample": f"{what} of the first {len(toks)} prompt tokens "
                                        f"(positions 0..{len(toks) - 1}), {n_thr} matmul threads"},
             "parity_logits_normwise_max": worst, "parity_greedy_token_same": same_argmax}
+
+
+def cpu_reference_attention(h, w, reps=3):
+    """The reference's own decode attention (model.c:828-892) timed inside its
+    model_forward (oracle/_ref): the same TinyLlama-shaped model run at
+    position pos over rows 0..pos-1 of N(0,1) fp16 cache rows, minus the same
+    token at position 0 (everything but the attention loop costs the same at
+    both positions).  The matmuls use the host threads; the attention loop
+    runs on one thread whatever -j is (model.c:848-892).  None without
+    oracle/_ref or when the model's attention shape is not the workload's."""
+    from oracle import oracle as O
+    if not O.ref_available():
+        return None
+    if (h.n_layers, h.n_heads, h.n_kv_heads, h.head_dim, h.max_seq_len) != (
+            w["L"], w["Hq"], w["Hkv"], w["D"], w["S"]) or h.rope_type != w.get("rt", 0):
+        return None
+    pos = w["pos"]
+    n_thr = min(os.cpu_count() or 1, HOST_THREADS_MAX)
+    O.ref().ref_set_threads(n_thr)
+    ref = O.RefForward(h)
+    try:
+        rng = np.random.default_rng(2047)
+        kv = h.n_kv_heads * h.head_dim
+        for cache in (ref.kc, ref.vc):
+            view = cache.reshape(h.n_layers, h.max_seq_len, kv)
+            for layer in range(h.n_layers):
+                view[layer, :pos] = O.f32_to_f16(
+                    rng.standard_normal((pos, kv), dtype=np.float32)).reshape(pos, kv)
+        ref.forward(1, pos)                       # warm-up (writes row pos only)
+        t_long, t_short = [], []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            ref.forward(1, pos)
+            t_long.append(time.perf_counter() - t0)
+            t0 = time.perf_counter()
+            ref.forward(1, 0)
+            t_short.append(time.perf_counter() - t0)
+    finally:
+        O.ref().ref_set_threads(1)
+        ref.close()
+    attn_s = float(np.median(t_long) - np.median(t_short))
+    return {"value": decode_bytes(w) / attn_s / 1e9, "unit": "GB/s", "cores": 1,
+            "kind": "reference", "us_per_token": attn_s * 1e6,
+            "sample": f"picolm model_forward (oracle/_ref) at pos {pos} minus pos 0, {reps} "
+                      f"runs each, on the forward workload's model (same attention shape); "
+                      f"matmuls on {n_thr} threads, the attention loop on one"}
 
 
 def qkn_bytes(w) -> int:
@@ -810,7 +860,14 @@ def main():
     if not args.no_forward:
         # the whole forward pass on the device (gpu_try_forward's path)
         fres = run_forward(P)
+        h_fwd = fres["_check"][0]
         fextra = {} if args.no_cpu else cpu_baseline_forward(fres)
+        if not args.no_cpu and "cpu_baseline" in line:
+            # the headline's baseline from the reference itself where it runs
+            refb = cpu_reference_attention(h_fwd, w)
+            if refb is not None:
+                line["cpu_baseline_port"] = line["cpu_baseline"]
+                line["cpu_baseline"] = refb
         fres.pop("_check", None)
         fres.update(fextra)
         line["forward"] = fres
