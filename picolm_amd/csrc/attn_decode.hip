@@ -745,10 +745,12 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
     hipLaunchKernelGGL((attn_decode_kernel<128, true>), grid, b128, 0, c.stream, a);
   if (check_hip(hipGetLastError(), "attn_decode_kernel")) return -1;
   if (n_split == 1) return 0;
+  // one thread per (q head of the block, d): no workgroup without work
+  const int nh_max = G < 16 ? G : 16;
   const dim3 cgrid64((unsigned)(8 * groups_per_xcd),
-                     (16 * 64 + kCombineThreads - 1) / kCombineThreads);
+                     (nh_max * 64 + kCombineThreads - 1) / kCombineThreads);
   const dim3 cgrid128((unsigned)(8 * groups_per_xcd),
-                      (16 * 128 + kCombineThreads - 1) / kCombineThreads);
+                      (nh_max * 128 + kCombineThreads - 1) / kCombineThreads);
   const bool few = n_split <= 8;
   if (head_dim == 64 && few)
     hipLaunchKernelGGL((attn_decode_combine_kernel<64, 8>), cgrid64, cblock, 0, c.stream, a);
