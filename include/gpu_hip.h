@@ -75,8 +75,9 @@ int gpu_try_forward(model_t *m, int token, int pos);
  * every layer appended. */
 int gpu_try_forward_prefill(model_t *m, const int *tokens, int n_tokens, int start_pos);
 /* KV coherence for kvcache_save / kvcache_load (model.c:1146-1259): copy rows
- * 0..n_pos-1 of every layer device -> host (download) or host -> device
- * (upload). 0 or -1. */
+ * 0..n_pos-1 of every layer the device handles (layers < PICOLM_GPU_LAYERS)
+ * device -> host (download) or host -> device (upload); the other layers'
+ * rows live in the host cache only and are left alone.  0 or -1. */
 int gpu_kv_download(const model_t *m, int n_pos);
 int gpu_kv_upload(const model_t *m, int n_pos);
 

@@ -58,7 +58,9 @@ void plh_event_destroy(void *ev);
 /* Everything queued between begin and end (decode launches, event records) is
  * captured instead of run; plh_graph_launch replays it.  Decode launches need
  * no memset and allocate nothing once the workspace has been sized by one
- * eager call of the same shape, so they can be captured. */
+ * eager call of the same shape, so they can be captured.  A later, larger
+ * call moves to a bigger workspace; the old one stays allocated until
+ * plh_shutdown, so graphs captured earlier keep replaying correctly. */
 int plh_capture_begin(void);
 void *plh_capture_end(void); /* instantiated graph, or NULL */
 int plh_graph_launch(void *graph);
@@ -90,8 +92,10 @@ int plh_f16_checksum(uint64_t first, uint64_t count, uint64_t *checksum);
  *   out + li*n_heads*head_dim     fp32 attention output
  * The kernel rotates q and k with table row `pos`, writes f16(k_rot), f16(v)
  * into row `pos` of layer layer0+li of the caches, and attends over rows
- * 0..pos.  Supported: head_dim 64 or 128, n_heads % n_kv_heads == 0,
- * |q| < 65504. */
+ * 0..pos.  Supported: head_dim 64 or 128, n_heads % n_kv_heads == 0.  Any
+ * finite q is handled: a q head with some |element| >= 2^15 is scaled by a
+ * power of two before its fp16 split and the factor moves into its score
+ * scale (exact). */
 int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int head_dim,
                     int max_seq_len, int rope_type, int layer0,
                     int n_launch_layers, int pos, const float *q,

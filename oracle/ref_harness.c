@@ -136,6 +136,10 @@ void *ref_model_new(int n_layers, int n_heads, int n_kv_heads, int head_dim,
     return h;
 }
 
+/* The reference's own model_t of a handle (run state from allocate_run_state),
+ * for harnesses built against picolm's model.h. */
+model_t *ref_model(void *hv) { return &((ref_handle *)hv)->m; }
+
 void ref_model_free(void *hv) {
     ref_handle *h = (ref_handle *)hv;
     if (!h) return;

@@ -73,10 +73,27 @@ __device__ __forceinline__ void rope_rotate_fused(float& a, float& b, float c, f
 
 // Splits an fp32 value into fp16 hi + lo so that an fp16 MFMA over both parts
 // reproduces the fp32 operand to ~2^-22 relative (hi keeps 11 bits, lo the
-// next 11).  Values must be below 65504 in magnitude.
+// next 11).  Values must be below 65504 in magnitude (q columns are brought
+// there by q_range_scale).
 __device__ __forceinline__ void split_hi_lo(float x, _Float16& hi, _Float16& lo) {
   hi = (_Float16)x;
   lo = (_Float16)(x - (float)hi);
+}
+
+// Range of a q column for the fp16 split.  amax is the largest |element| of
+// the column (NaN-propagating maximum).  Columns with amax >= 2^15 are
+// multiplied by 2^-e, with e chosen so that the largest element lands in
+// [2^14, 2^15): a change of exponent, exact for every element that stays a
+// normal number, and elements it pushes below fp16's range are below 2^-38
+// of the largest one.  The column's score is then (K . q 2^-e) 2^e, so 2^e
+// goes into its score scale.  Returns 2^-e (1 for ordinary columns, so their
+// arithmetic is unchanged); *up gets 2^e.  inf / NaN columns get a finite
+// scale and stay inf / NaN, as in the reference's fp32 arithmetic.
+__device__ __forceinline__ float q_range_scale(float amax, float* up) {
+  const int ex = (int)((__float_as_uint(amax) >> 23) & 0xFFu) - 127;  // floor(log2 amax)
+  const int e = ex >= 15 ? ex - 14 : 0;                                // 0 .. 114
+  *up = __uint_as_float((uint32_t)(127 + e) << 23);
+  return __uint_as_float((uint32_t)(127 - e) << 23);
 }
 
 // Same split for a pair of values (|x| below 65504; used for q and for

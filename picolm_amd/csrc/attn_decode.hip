@@ -410,12 +410,22 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
   // keep the scheduler from hoisting q's uses (and their waits) above the tiles
   __builtin_amdgcn_sched_barrier(0);
   rope_q<D, QKN>(a.rope_type, col < nh, grp, a.norm_eps, qr);
+  // the column's range for the fp16 split (a power-of-two scale, folded into
+  // its score scale; 1 unless some |q| >= 2^15)
+  float amax = 0.f;
+#pragma unroll
+  for (int db = 0; db < ND; ++db)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = vmax(amax, fabsf(qr.q[db][j]));
+  amax = max_xor32(max_xor16(amax));
+  float qup;
+  const float qdown = q_range_scale(amax, &qup);
 #pragma unroll
   for (int db = 0; db < ND; ++db)
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       _Float16 hi, lo;
-      split_hi_lo(qr.q[db][j], hi, lo);
+      split_hi_lo(qr.q[db][j] * qdown, hi, lo);
       qhi[db][j] = hi;
       qlo[db][j] = lo;
     }
@@ -462,7 +472,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
 
   // ---- stream the split's cached rows, one tile ahead ----------------------
   _Float16* vt = reinterpret_cast<_Float16*>(smem) + wave * (kTile * VP);
-  const float sscale = a.score_scale;
+  const float sscale = a.score_scale * qup;       // this lane's column
   float m = kNegBig;                              // running max (scaled, log2 units)
   float4_t lsum = float4_t{0.f, 0.f, 0.f, 0.f};  // running sum (all entries equal)
   half8_t ones;

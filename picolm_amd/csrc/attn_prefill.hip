@@ -239,6 +239,7 @@ void prefill_attn_kernel(PrefillArgs a) {
   // Columns past the prompt (cvalid false) read the last token's row and are
   // never stored; each column's softmax is independent, so they need no mask.
   half8_t qhi[ND], qlo[ND];
+  float qup;  // 2^e of the column's range scale
   {
     const float* qrow = a.q + ((size_t)li * a.n_tokens + tok_c) * q_dim +
                         (size_t)(kvh * G + (cvalid ? hh : 0)) * D;
@@ -291,12 +292,21 @@ void prefill_attn_kernel(PrefillArgs a) {
         rope_rotate_fused(qf[db][6], qf[db][7], c4.w, s4.w);
       }
     }
+    // the column's range for the fp16 split (a power-of-two scale, folded
+    // into its score scale; 1 unless some |q| >= 2^15)
+    float amax = 0.f;
+#pragma unroll
+    for (int db = 0; db < ND; ++db)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) amax = vmax(amax, fabsf(qf[db][j]));
+    amax = max_xor32(max_xor16(amax));
+    const float qdown = q_range_scale(amax, &qup);
 #pragma unroll
     for (int db = 0; db < ND; ++db)
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
         half2_t hi, lo;
-        split_pair_rtz(qf[db][j], qf[db][j + 1], hi, lo);
+        split_pair_rtz(qf[db][j] * qdown, qf[db][j + 1] * qdown, hi, lo);
         qhi[db][j] = hi[0], qhi[db][j + 1] = hi[1];
         qlo[db][j] = lo[0], qlo[db][j + 1] = lo[1];
       }
@@ -305,7 +315,7 @@ void prefill_attn_kernel(PrefillArgs a) {
   store_lds(0);
   __syncthreads();
 
-  const float sscale = a.score_scale;
+  const float sscale = a.score_scale * qup;  // this lane's column
   float ms = kNegBig;            // running max (scaled, log2 units)
   float4_t lsum = float4_t{0.f, 0.f, 0.f, 0.f};  // running sum (all 4 entries equal)
   half8_t ones;

@@ -396,18 +396,7 @@ ChunkActs carve_chunk(const plh_model* m, int T, void* base) {
 int ensure_prefill_ws(size_t bytes) {
   Context& c = ctx();
   if (c.pf_ws && c.pf_ws_bytes >= bytes) return 0;
-  if (c.pf_ws) {
-    if (check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize")) return -1;
-    if (check_hip(hipFree(c.pf_ws), "hipFree(prefill workspace)")) return -1;
-    c.pf_ws = nullptr;
-    c.pf_ws_bytes = 0;
-  }
-  if (check_hip(hipMalloc(&c.pf_ws, bytes), "hipMalloc(prefill workspace)")) {
-    c.pf_ws = nullptr;
-    return -1;
-  }
-  c.pf_ws_bytes = bytes;
-  return 0;
+  return grow_buffer(&c.pf_ws, &c.pf_ws_bytes, bytes, "hipMalloc(prefill workspace)");
 }
 
 int launch_rmsnorm_rows(const float* x, const float* w, float* out, int n, int rows, float eps) {

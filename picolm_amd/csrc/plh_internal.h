@@ -18,7 +18,17 @@ struct Context {
   void* pf_ws = nullptr;       // prompt-chunk activations of plh_forward_prefill
   size_t pf_ws_bytes = 0;
   int num_cus = 0;
+  // Workspaces outgrown by a larger call.  A graph captured before the growth
+  // still holds their addresses in its kernel nodes, so they stay allocated
+  // until plh_shutdown.
+  static constexpr int kMaxRetired = 32;
+  void* retired[kMaxRetired] = {};
+  int n_retired = 0;
 };
+
+// Replaces the buffer *p of *bytes bytes by a new one of `want` bytes (the
+// old one is retired, not freed).  0 or -1.
+int grow_buffer(void** p, size_t* bytes, size_t want, const char* what);
 
 Context& ctx();
 void set_error(const char* fmt, ...);
@@ -63,8 +73,8 @@ int gemv_multi_launch(const GemvCall* g, int n);
 // up.out.
 int gemv_pair_launch(const GemvCall& gate, const GemvCall& up);
 
-// Makes sure the workspace holds at least `bytes`.  Growing it waits for the
-// queued work (which may still read the old one).  Returns 0 or -1.
+// Makes sure the workspace holds at least `bytes` (the outgrown one is
+// retired until plh_shutdown).  Returns 0 or -1.
 int ensure_workspace(size_t bytes);
 
 // Decode kernel arguments (all device pointers).

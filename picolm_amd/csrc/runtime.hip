@@ -28,23 +28,32 @@ int check_hip(hipError_t e, const char* what) {
   return -1;
 }
 
+int grow_buffer(void** p, size_t* bytes, size_t want, const char* what) {
+  Context& c = g_ctx;
+  if (*p) {
+    if (c.n_retired == Context::kMaxRetired) {
+      // out of slots: wait for queued work and free the oldest for real
+      if (check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize")) return -1;
+      (void)hipFree(c.retired[0]);
+      memmove(c.retired, c.retired + 1, sizeof(void*) * (Context::kMaxRetired - 1));
+      --c.n_retired;
+    }
+    c.retired[c.n_retired++] = *p;
+    *p = nullptr;
+    *bytes = 0;
+  }
+  if (check_hip(hipMalloc(p, want), what)) {
+    *p = nullptr;
+    return -1;
+  }
+  *bytes = want;
+  return 0;
+}
+
 int ensure_workspace(size_t bytes) {
   Context& c = g_ctx;
   if (c.ws && c.ws_bytes >= bytes) return 0;
-  if (c.ws) {
-    // the old workspace may still be read by queued work
-    if (check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize")) return -1;
-    if (check_hip(hipFree(c.ws), "hipFree(workspace)")) return -1;
-    c.ws = nullptr;
-    c.ws_bytes = 0;
-  }
-  size_t grow = bytes + bytes / 2;
-  if (check_hip(hipMalloc(&c.ws, grow), "hipMalloc(workspace)")) {
-    c.ws = nullptr;
-    return -1;
-  }
-  c.ws_bytes = grow;
-  return 0;
+  return grow_buffer(&c.ws, &c.ws_bytes, bytes + bytes / 2, "hipMalloc(workspace)");
 }
 
 }  // namespace plh
@@ -93,6 +102,7 @@ void plh_shutdown(void) {
     (void)hipStreamSynchronize(c.stream);
     if (c.ws) (void)hipFree(c.ws);
     if (c.pf_ws) (void)hipFree(c.pf_ws);
+    for (int i = 0; i < c.n_retired; ++i) (void)hipFree(c.retired[i]);
     (void)hipStreamDestroy(c.stream);
   }
   c = Context();

@@ -582,11 +582,15 @@ int gpu_try_attention_prefill(model_t *m, int layer, int start_pos, int n_tokens
     return 0;
 }
 
+/* Rows 0..n_pos-1 of the layers the device handles (l < gpu_layers).  The
+ * other layers' rows exist only in the host cache (their CPU block appends
+ * them there), so they are neither overwritten by a download nor needed on
+ * the device. */
 static int kv_copy(const model_t *m, int n_pos, int to_host) {
     if (!gpu_available() || !same_shape(m) || n_pos < 0 || n_pos > gs.max_seq_len) return -1;
     size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
     size_t bytes = (size_t)n_pos * kv_dim * sizeof(uint16_t);
-    for (int l = 0; l < gs.n_layers; l++) {
+    for (int l = 0; l < gs.n_layers && l < gs.gpu_layers; l++) {
         size_t off = (size_t)l * gs.max_seq_len * kv_dim;
         int rc;
         if (to_host) {

@@ -14,7 +14,10 @@
  * output: int32 [rc_init, rc_upload, rc_download_roundtrip, rc_upload_roundtrip],
  *         int32 rc_prefill[L], int32 rc_decode[T][L],
  *         float32 prefill out [L][P][n_embd], decode out [T][L][q_dim],
- *         uint16 host key cache, val cache.
+ *         uint16 host key cache, val cache.  Layers whose calls returned -1
+ *         hold a stand-in for the CPU block's rows in rows 0..P+T-1:
+ *         key 0x3C00 | ((l + 3r + i) & 0xFF), val 0x4000 | ((l + 5r + i) & 0xFF)
+ *         for element i of row r of layer l.
  */
 #include <stdint.h>
 #include <stdio.h>
@@ -104,23 +107,48 @@ int main(int argc, char **argv) {
                                           dv + i * kv_dim, out_dec + i * q_dim);
         }
 
-    /* kvcache_save / kvcache_load coherence: download into a cleared host
-     * cache must give back the same bytes; upload then download too */
+    /* Layers whose calls fell back: the caller's CPU block appends their
+     * rows to the host cache only.  Stand-in rows (a fixed pattern) take
+     * that place here; the device never sees them, and downloads must
+     * leave them as they are. */
     int n_pos = P + T;
+    unsigned char *dev_layer = calloc((size_t)L, 1);
+    for (int l = 0; l < L; l++) {
+        int ok = P == 0 || rc_pre[l] == 0;
+        for (int t = 0; t < T; t++) ok = ok && rc_dec[(size_t)t * L + l] == 0;
+        dev_layer[l] = (unsigned char)ok;
+        if (ok || !gpu_available()) continue;
+        for (int r = 0; r < n_pos; r++)
+            for (size_t i = 0; i < kv_dim; i++) {
+                size_t at = ((size_t)l * S + r) * kv_dim + i;
+                m.state.key_cache[at] = (uint16_t)(0x3C00u | ((l + 3u * r + i) & 0xFFu));
+                m.state.val_cache[at] = (uint16_t)(0x4000u | ((l + 5u * r + i) & 0xFFu));
+            }
+    }
+    /* kvcache_save / kvcache_load coherence: download into cleared host rows
+     * of the device's layers must give back the same bytes and leave the
+     * CPU layers' rows alone; upload then download too */
+    const size_t layer_elems = (size_t)S * kv_dim;
     uint16_t *kcopy = malloc(cache_elems * 2), *vcopy = malloc(cache_elems * 2);
     memcpy(kcopy, m.state.key_cache, cache_elems * 2);
     memcpy(vcopy, m.state.val_cache, cache_elems * 2);
     if (gpu_available()) {
-        memset(m.state.key_cache, 0, cache_elems * 2);
-        memset(m.state.val_cache, 0, cache_elems * 2);
+        for (int l = 0; l < L; l++)
+            if (dev_layer[l]) {
+                memset(m.state.key_cache + (size_t)l * layer_elems, 0, layer_elems * 2);
+                memset(m.state.val_cache + (size_t)l * layer_elems, 0, layer_elems * 2);
+            }
         rc[2] = gpu_kv_download(&m, n_pos);
         if (rc[2] == 0 && (memcmp(kcopy, m.state.key_cache, cache_elems * 2) ||
                            memcmp(vcopy, m.state.val_cache, cache_elems * 2)))
             rc[2] = 1;
         rc[3] = gpu_kv_upload(&m, n_pos);
         if (rc[3] == 0) {
-            memset(m.state.key_cache, 0, cache_elems * 2);
-            memset(m.state.val_cache, 0, cache_elems * 2);
+            for (int l = 0; l < L; l++)
+                if (dev_layer[l]) {
+                    memset(m.state.key_cache + (size_t)l * layer_elems, 0, layer_elems * 2);
+                    memset(m.state.val_cache + (size_t)l * layer_elems, 0, layer_elems * 2);
+                }
             rc[3] = gpu_kv_download(&m, n_pos);
             if (rc[3] == 0 && (memcmp(kcopy, m.state.key_cache, cache_elems * 2) ||
                                memcmp(vcopy, m.state.val_cache, cache_elems * 2)))

@@ -15,10 +15,10 @@ LIB = os.path.join(ROOT, "picolm_amd", "lib", "libpicolm_hip.so")
 REF_PICOLM = "/root/reference/picolm"
 
 
-def declared_functions():
+def declared_functions(header=None):
     names = set()
     for h in sorted(os.listdir(INCLUDE)):
-        if not h.endswith(".h"):
+        if not h.endswith(".h") or (header and h != header):
             continue
         text = open(os.path.join(INCLUDE, h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
@@ -32,12 +32,41 @@ def declared_functions():
     return names
 
 
-def test_library_exports_every_declared_function():
+def exported(path):
+    r = subprocess.run(["nm", "-D", "--defined-only", path], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
+    return {line.split()[-1] for line in r.stdout.splitlines() if " T " in line}
+
+
+def test_library_exports_every_device_function():
     lib = C.CDLL(LIB)
-    names = declared_functions()
+    names = declared_functions("picolm_hip.h")
     assert len(names) >= 30
     missing = [n for n in sorted(names) if not hasattr(lib, n)]
     assert not missing, missing
+
+
+def test_library_exports_plh_only():
+    """The kernel library carries no gpu_* symbol: gpu_hip.c reads the host
+    program's model_t and is compiled inside that program against its own
+    model.h, so no copy built against another layout can be linked by
+    mistake."""
+    syms = exported(LIB)
+    assert not [s for s in syms if s.startswith("gpu_")]
+    assert declared_functions("picolm_hip.h") <= syms
+
+
+def test_boundary_source_defines_every_gpu_function(tmp_path):
+    """Every gpu_* declared by include/gpu_hip.h is defined by gpu_hip.c."""
+    obj = tmp_path / "gpu_hip.o"
+    r = _gcc(["-c", "-fPIC", "-DUSE_HIP", "-I" + INCLUDE,
+              "-I" + os.path.join(ROOT, "picolm_amd", "host"),
+              os.path.join(ROOT, "picolm_amd", "host", "gpu_hip.c"), "-o", str(obj)])
+    assert r.returncode == 0, r.stderr
+    r = subprocess.run(["nm", "--defined-only", str(obj)], capture_output=True, text=True)
+    defined = {line.split()[-1] for line in r.stdout.splitlines() if " T " in line}
+    want = declared_functions("gpu_hip.h")
+    assert len(want) >= 10 and want <= defined, sorted(want - defined)
 
 
 def test_python_binding_covers_the_device_abi():
