@@ -96,8 +96,9 @@ __device__ __forceinline__ float q_range_scale(float amax, float* up) {
   return __uint_as_float((uint32_t)(127 - e) << 23);
 }
 
-// Same split for a pair of values (|x| below 65504; used for q and for
-// softmax weights in [0, 2^8]):
+// Same split for a pair of values (|x| below 65504, or below 131008 for the
+// softmax weights, which are at most 2^16: round-toward-zero keeps hi finite
+// at 65504 and lo takes the rest):
 // hi = rtz(x) by the packed round-toward-zero conversion, lo = f16(x - hi) by
 // two mixed-precision FMAs (f16 first operand, f32 addend, f16 result written
 // into the low / high half of the register).  x - hi is exact, so hi + lo

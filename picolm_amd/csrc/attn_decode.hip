@@ -23,8 +23,11 @@
 //                                   q split into fp16 hi+lo (two MFMAs each)
 //                                   so the product keeps ~fp32 precision;
 //   online softmax in the log2 domain: maximum over raw scores, scale folded
-//                                   into the exp2 argument, rescale of O only
-//                                   when the maximum grows by more than 2^8;
+//                                   into the exp2 argument (rounded product
+//                                   minus the running maximum: monotone, so
+//                                   weights stay bounded at any score
+//                                   magnitude), rescale of O only when the
+//                                   maximum grows by more than 2^8;
 //   O^T[d][h] += V^T[d][t] P^T[t][h] with P split hi+lo; V goes row-major
 //                                   through a per-wave LDS tile and comes back
 //                                   transposed by ds_read_b64_tr_b16;
@@ -312,8 +315,8 @@ __device__ __forceinline__ void process_tile(const Tile<D>& T, const half8_t (&q
   half8_t ph, pl;
 #pragma unroll
   for (int j = 0; j < 8; j += 2) {
-    const float p0 = fast_exp2(__builtin_fmaf(u[j], sscale, -ms));
-    const float p1 = fast_exp2(__builtin_fmaf(u[j + 1], sscale, -ms));
+    const float p0 = fast_exp2(u[j] * sscale - ms);
+    const float p1 = fast_exp2(u[j + 1] * sscale - ms);
     half2_t hi, lo;
     split_pair_rtz(p0, p1, hi, lo);
     ph[j] = hi[0], ph[j + 1] = hi[1];

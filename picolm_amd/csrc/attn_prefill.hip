@@ -31,7 +31,13 @@
 // scores and the 1/sqrt(D)*log2(e) scale is folded into the exp2 argument;
 // the causal mask is applied only on tiles that cross a column's last row;
 // the running maximum is raised (and O, l rescaled) only when a new score
-// exceeds it by more than 2^kLazy, so weights stay below 2^kLazy.
+// exceeds it by more than 2^kLazy, so weights stay below 2^kLazy.  The exp2
+// argument is the ROUNDED scaled score minus the running maximum (no fused
+// multiply-add): rounding is monotone, so no weight exceeds that of the row
+// that set the maximum test, whatever the magnitude of the scores (a fused
+// product could exceed the margin by its rounding error once the scores
+// pass 2^27 and overflow exp2).  Weights stay at most 2^16 (2^kLazy below
+// scores of 2^26).
 #include <math.h>
 
 #include "attn_common.h"
@@ -373,8 +379,8 @@ void prefill_attn_kernel(PrefillArgs a) {
     half8_t ph, pl;
 #pragma unroll
     for (int j = 0; j < 8; j += 2) {
-      const float p0 = fast_exp2(__builtin_fmaf(u[j], sscale, -ms));
-      const float p1 = fast_exp2(__builtin_fmaf(u[j + 1], sscale, -ms));
+      const float p0 = fast_exp2(u[j] * sscale - ms);
+      const float p1 = fast_exp2(u[j + 1] * sscale - ms);
       half2_t hi, lo;
       split_pair_rtz(p0, p1, hi, lo);
       ph[j] = hi[0], ph[j + 1] = hi[1];
