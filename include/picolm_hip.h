@@ -103,6 +103,24 @@ int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int head_dim,
                     uint16_t *val_cache, const float *rope_cos,
                     const float *rope_sin, float *out);
 
+/* ---- decode attention without allocation -------------------------------- */
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): plh_attn_decode with the same arguments and results,
+ * whose split partials live in a static device array of 16 MiB (each GPU the
+ * library runs on holds it until the process ends) instead of the library
+ * workspace.  It calls no hipMalloc / hipFree.  Returns -1 with a message
+ * when a launch's partials would exceed the 16 MiB (very wide models: the
+ * partials take n_units * min(G,16) * (head_dim+2) * 4 bytes, a few MiB at
+ * the usual shapes).  Every call on a GPU shares that one array: calls that
+ * overlap on one GPU race (the library's own stream serialises its calls). */
+int plh_attn_decode_noalloc(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                            int max_seq_len, int rope_type, int layer0,
+                            int n_launch_layers, int pos, const float *q,
+                            const float *k, const float *v, uint16_t *key_cache,
+                            uint16_t *val_cache, const float *rope_cos,
+                            const float *rope_sin, float *out);
+
 /* ---- prefill attention -------------------------------------------------- */
 /* Replaces model.c:1039-1089 (per prompt token: rope, FP16 append, online-
  * softmax GQA attention) for n_tokens tokens at positions start_pos.. and

@@ -87,6 +87,7 @@ _SIGS = {
     "plh_f16_checksum": (_i, [C.c_uint64, C.c_uint64, C.POINTER(C.c_uint64)]),
     # attention
     "plh_attn_decode": (_i, [_i] * 9 + [_vp] * 8),
+    "plh_attn_decode_noalloc": (_i, [_i] * 9 + [_vp] * 8),
     "plh_attn_prefill": (_i, [_i] * 10 + [_vp] * 8 + [_i]),
     "plh_attn_decode_qknorm": (_i, [_i] * 9 + [_vp] * 10 + [C.c_float]),
     "plh_attn_prefill_qknorm": (_i, [_i] * 10 + [_vp] * 8 + [_i, _vp, _vp, C.c_float]),

@@ -58,6 +58,20 @@
 
 using namespace plh;
 
+// ---- static scratch of the allocation-free entry point ---------------------
+// plh_attn_decode_noalloc keeps its split partials in this file-scope device
+// array instead of the library workspace: each GPU holds its own copy until
+// the process ends, and every call on a GPU shares it (concurrent calls on one
+// GPU would race; the library's single stream serialises its own calls).  No
+// part of it needs clearing: every partial a launch reads was written by the
+// same launch.  In host code `scratch` is a host-side stand-in, not a device
+// address: decode_scratch_setup (called by plh_init with the device current)
+// looks the device address up once per device, and launches use that.
+static constexpr size_t kScratchBytes = 16u << 20;
+static constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+static void* g_scratch_ptr[kMaxDevices];  // its device address, per device
+
 namespace {
 
 constexpr int kTile = 32;
@@ -538,10 +552,10 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
     if (a.n_split == 1) {
       out_base[(size_t)h * D + d] = O * (1.0f / L);
     } else {
-      a.part_o[((size_t)unit * 16 + h) * D + d] = O;
+      a.part_o[((size_t)unit * a.nhm + h) * D + d] = O;
       if (d == 0) {
-        a.part_m[(size_t)unit * 16 + h] = M;
-        a.part_l[(size_t)unit * 16 + h] = L;
+        a.part_m[(size_t)unit * a.nhm + h] = M;
+        a.part_l[(size_t)unit * a.nhm + h] = L;
       }
     }
   }
@@ -577,7 +591,7 @@ __global__ __launch_bounds__(kCombineThreads) void attn_decode_combine_kernel(De
       float mi[CH], li[CH], oi[CH];
 #pragma unroll
       for (int j = 0; j < CH; ++j) {
-        const size_t u = (size_t)(u0 + min(s0 + j, a.n_split - 1)) * 16 + h;
+        const size_t u = (size_t)(u0 + min(s0 + j, a.n_split - 1)) * a.nhm + h;
         mi[j] = a.part_m[u];
         li[j] = a.part_l[u];
         oi[j] = a.part_o[u * D + d];
@@ -611,6 +625,22 @@ int g_target_units = 0;   // 0: four workgroups per CU
 int g_min_split = kDefaultMinSplit;
 
 }  // namespace
+
+namespace plh {
+int decode_scratch_setup(int device) {
+  if (device < 0 || device >= kMaxDevices) {
+    set_error("plh_init: device %d beyond the %d the static scratch table covers", device,
+              kMaxDevices);
+    return -1;
+  }
+  if (g_scratch_ptr[device]) return 0;
+  void* p = nullptr;
+  if (check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"))
+    return -1;
+  g_scratch_ptr[device] = p;
+  return 0;
+}
+}  // namespace plh
 
 extern "C" int plh_set_tuning(int key, int value) {
   if (key == 1) {
@@ -654,7 +684,7 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
                             int pos, const float* q, const float* k, const float* v,
                             uint16_t* key_cache, uint16_t* val_cache, const float* rope_cos,
                             const float* rope_sin, float* out, const float* q_norm,
-                            const float* k_norm, float norm_eps) {
+                            const float* k_norm, float norm_eps, bool noalloc) {
   Context& c = ctx();
   if (!c.stream) {
     set_error("plh_attn_decode: library not initialised");
@@ -694,6 +724,7 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
 
   const int G = n_heads / n_kv_heads;
   const int n_hblk = (G + 15) / 16;
+  const int nhm = G < 16 ? G : 16;  // q heads of the largest head block
   const int n_groups = n_launch_layers * n_kv_heads * n_hblk;
   const int npos = pos + 1;
   // Split plan: contexts of at most g_min_split positions are not split (the
@@ -722,12 +753,25 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
   a.out = out;
   a.part_o = a.part_m = a.part_l = nullptr;
   if (n_split > 1) {
-    const size_t po = (size_t)n_units * 16 * head_dim * sizeof(float);
-    const size_t pm = (size_t)n_units * 16 * sizeof(float);
-    if (ensure_workspace(po + 2 * pm)) return -1;
-    a.part_o = (float*)c.ws;
-    a.part_m = (float*)((char*)c.ws + po);
-    a.part_l = (float*)((char*)c.ws + po + pm);
+    // per unit: (max, sum, acc[D]) of each of the block's q heads
+    const size_t po = (size_t)n_units * nhm * head_dim * sizeof(float);
+    const size_t pm = (size_t)n_units * nhm * sizeof(float);
+    void* base;
+    if (noalloc) {
+      if (po + 2 * pm > kScratchBytes) {
+        set_error("plh_attn_decode_noalloc: this launch needs %zu bytes of split partials, "
+                  "more than the %zu-byte static scratch",
+                  po + 2 * pm, kScratchBytes);
+        return -1;
+      }
+      base = g_scratch_ptr[c.device];
+    } else {
+      if (ensure_workspace(po + 2 * pm)) return -1;
+      base = c.ws;
+    }
+    a.part_o = (float*)base;
+    a.part_m = (float*)((char*)base + po);
+    a.part_l = (float*)((char*)base + po + pm);
   }
   a.layer0 = layer0;
   a.n_launch_layers = n_launch_layers;
@@ -737,6 +781,7 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
   a.pos = pos;
   a.rope_type = rope_type;
   a.n_hblk = n_hblk;
+  a.nhm = nhm;
   a.n_split = n_split;
   a.split_len = split_len;
   a.n_units = n_units;
@@ -785,7 +830,7 @@ extern "C" int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int he
                                const float* rope_sin, float* out) {
   return attn_decode_impl(n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, layer0,
                           n_launch_layers, pos, q, k, v, key_cache, val_cache, rope_cos, rope_sin,
-                          out, nullptr, nullptr, 0.0f);
+                          out, nullptr, nullptr, 0.0f, false);
 }
 
 extern "C" int plh_attn_decode_qknorm(int n_layers, int n_heads, int n_kv_heads, int head_dim,
@@ -797,5 +842,16 @@ extern "C" int plh_attn_decode_qknorm(int n_layers, int n_heads, int n_kv_heads,
                                       const float* k_norm, float norm_eps) {
   return attn_decode_impl(n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, layer0,
                           n_launch_layers, pos, q, k, v, key_cache, val_cache, rope_cos, rope_sin,
-                          out, q_norm, k_norm, norm_eps);
+                          out, q_norm, k_norm, norm_eps, false);
+}
+
+extern "C" int plh_attn_decode_noalloc(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                                       int max_seq_len, int rope_type, int layer0,
+                                       int n_launch_layers, int pos, const float* q,
+                                       const float* k, const float* v, uint16_t* key_cache,
+                                       uint16_t* val_cache, const float* rope_cos,
+                                       const float* rope_sin, float* out) {
+  return attn_decode_impl(n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, layer0,
+                          n_launch_layers, pos, q, k, v, key_cache, val_cache, rope_cos, rope_sin,
+                          out, nullptr, nullptr, 0.0f, true);
 }

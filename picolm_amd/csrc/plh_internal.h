@@ -73,6 +73,10 @@ int gemv_multi_launch(const GemvCall* g, int n);
 // up.out.
 int gemv_pair_launch(const GemvCall& gate, const GemvCall& up);
 
+// Looks up (once per device, with that device current) the device address of
+// the decode kernels' static scratch array; plh_init calls it.  0 or -1.
+int decode_scratch_setup(int device);
+
 // Makes sure the workspace holds at least `bytes` (the outgrown one is
 // retired until plh_shutdown).  Returns 0 or -1.
 int ensure_workspace(size_t bytes);
@@ -87,11 +91,12 @@ struct DecodeArgs {
   const float* cos_t;      // [S][D/2]
   const float* sin_t;
   float* out;              // [n_launch_layers][n_heads*D]
-  float* part_o;           // [n_units][16][D]
-  float* part_m;           // [n_units][16]
-  float* part_l;           // [n_units][16]
+  float* part_o;           // [n_units][nhm][D]
+  float* part_m;           // [n_units][nhm]
+  float* part_l;           // [n_units][nhm]
   int layer0, n_launch_layers, n_heads, n_kv_heads, max_seq_len, pos, rope_type;
   int n_hblk;              // ceil(G / 16): q-head blocks per kv head
+  int nhm;                 // min(G, 16): partial slots per unit
   int n_split, split_len;  // position splits per (layer, kv head, head block)
   int n_units;             // n_groups * n_split
   int per_xcd;             // units per XCD slice of the grid

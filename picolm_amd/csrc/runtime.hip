@@ -91,6 +91,11 @@ int plh_init(int device) {
   // Default-priority stream (no priority games on this hardware).
   if (check_hip(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking), "hipStreamCreate"))
     return -1;
+  if (decode_scratch_setup(device)) {
+    (void)hipStreamDestroy(c.stream);
+    c.stream = nullptr;
+    return -1;
+  }
   c.device = device;
   c.num_cus = prop.multiProcessorCount;
   return 0;
