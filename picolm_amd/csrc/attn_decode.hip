@@ -351,6 +351,86 @@ __device__ __forceinline__ void process_tile(const Tile<D>& T, const half8_t (&q
   }
 }
 
+// Rotates the lane's q elements (after QK-norm when enabled) and splits them
+// into fp16 hi + lo MFMA operands.  The column's range for the split is a
+// power-of-two scale (1 unless some |q| >= 2^15), folded into its score
+// scale: the return value is that column's 2^e.
+template <int D, bool QKN>
+__device__ __forceinline__ float split_q(const DecodeArgs& a, bool valid, int grp, QRaw<D>& qr,
+                                         half8_t (&qhi)[D / 32], half8_t (&qlo)[D / 32]) {
+  constexpr int ND = D / 32;
+  rope_q<D, QKN>(a.rope_type, valid, grp, a.norm_eps, qr);
+  float amax = 0.f;
+#pragma unroll
+  for (int db = 0; db < ND; ++db)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) amax = vmax(amax, fabsf(qr.q[db][j]));
+  amax = max_xor32(max_xor16(amax));
+  float qup;
+  const float qdown = q_range_scale(amax, &qup);
+#pragma unroll
+  for (int db = 0; db < ND; ++db)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      _Float16 hi, lo;
+      split_hi_lo(qr.q[db][j] * qdown, hi, lo);
+      qhi[db][j] = hi;
+      qlo[db][j] = lo;
+    }
+  return qup;
+}
+
+// Row pos of the group's kv head (one wave): k rotated with table row pos
+// (after QK-norm when enabled), both rows rounded with the reference's
+// fp32_to_fp16 and stored to the caches, their fp32 values kept in LDS
+// (knew, vnew) and the row's scaled score against every q head of the block
+// (fp32 q, rotated) in mnew[col].
+template <int D, bool QKN>
+__device__ __forceinline__ void append_new_row(const DecodeArgs& a, int li, int kvh, size_t row0,
+                                               int lane, int col, int grp, const QRaw<D>& qr,
+                                               RowRaw<D>& rr, float* knew, float* vnew,
+                                               float* mnew) {
+  constexpr int ND = D / 32;
+  const int kv_dim = a.n_kv_heads * D;
+  if (QKN) qk_norm_row<D>(grp, a.norm_eps, rr);
+  uint16_t* krow = a.kc + (row0 + a.pos) * kv_dim + (size_t)kvh * D;
+  uint16_t* vrow = a.vc + (row0 + a.pos) * kv_dim + (size_t)kvh * D;
+#pragma unroll
+  for (int u = 0; u < RowRaw<D>::NP; ++u) {
+    const int i = lane + 64 * u;
+    if (i < D / 2) {
+      const int i0 = (a.rope_type == PLH_ROPE_QWEN) ? i : 2 * i;
+      const int i1 = (a.rope_type == PLH_ROPE_QWEN) ? i + D / 2 : 2 * i + 1;
+      float k0 = rr.k0[u], k1 = rr.k1[u];
+      rope_rotate(k0, k1, rr.c[u], rr.s[u]);
+      const uint16_t b0 = f16_bits_rha(k0), b1 = f16_bits_rha(k1);
+      krow[i0] = b0;
+      krow[i1] = b1;
+      knew[i0] = f16_bits_to_f32(b0);
+      knew[i1] = f16_bits_to_f32(b1);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < RowRaw<D>::NV; ++u) {
+    const int d = lane + 64 * u;
+    if (d < D) {
+      const uint16_t b = f16_bits_rha(rr.v[u]);
+      vrow[d] = b;
+      vnew[d] = f16_bits_to_f32(b);
+    }
+  }
+  // knew is written and read by this wave only; order the LDS accesses
+  __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
+  float sc = 0.f;
+#pragma unroll
+  for (int db = 0; db < ND; ++db)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) sc = __builtin_fmaf(qr.q[db][j], knew[32 * db + 8 * grp + j], sc);
+  sc += shfl_xor_f(sc, 16);
+  sc += shfl_xor_f(sc, 32);
+  if (grp == 0) mnew[col] = sc * a.score_scale;
+}
+
 template <int D, bool QKN>
 __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(DecodeArgs a) {
   constexpr int kWaves = DecodeShape<D>::W;
@@ -402,22 +482,21 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
   QRaw<D> qr;
   load_q_raw<D, QKN>(a, li, kvh, G, h0, nh, col, grp, qr);
   RowRaw<D> rr;
-  if (new_row) load_row_raw<D, QKN>(a, li, kvh, lane, rr);
+  load_row_raw<D, QKN>(a, li, kvh, lane, rr);  // used by the owner's wave 0 only
 
   // Rolling prefetch of depth PF: tile i of the wave lives in buffer i % PF,
   // and refilling a buffer with tile i + PF starts as soon as tile i is done.
   // Every load is issued unconditionally (tiles past the range re-read row
-  // tlast and are masked), so the compiler's wait counts stay exact and the
-  // prefetch is never drained early.  A split with no cached rows (te <= tb)
-  // skips the stream as a whole.
+  // tlast, or row 0 when the split has no cached rows, and are masked or
+  // skipped), so the compiler's wait counts stay exact: the q rotation waits
+  // for q alone (issued first), and the prefetch is never drained early.
   constexpr int PF = DecodeShape<D>::PF;
   const bool has_rows = te > tb;
+  const int tclamp = has_rows ? tlast : 0;
   Tile<D> buf[PF];
-  if (has_rows) {
 #pragma unroll
-    for (int j = 0; j < PF; ++j)
-      load_tile<D>(buf[j], kbase, vbase, kv_dim, tw + j * kStride, tlast, lane, col, grp);
-  }
+  for (int j = 0; j < PF; ++j)
+    load_tile<D>(buf[j], kbase, vbase, kv_dim, tw + j * kStride, tclamp, lane, col, grp);
 
   // ---- q operands: rotated, split into fp16 hi + lo ------------------------
   // The owner's wave 0 also appends row pos (k rotated, both rows rounded)
@@ -426,66 +505,8 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
   half8_t qhi[ND], qlo[ND];
   // keep the scheduler from hoisting q's uses (and their waits) above the tiles
   __builtin_amdgcn_sched_barrier(0);
-  rope_q<D, QKN>(a.rope_type, col < nh, grp, a.norm_eps, qr);
-  // the column's range for the fp16 split (a power-of-two scale, folded into
-  // its score scale; 1 unless some |q| >= 2^15)
-  float amax = 0.f;
-#pragma unroll
-  for (int db = 0; db < ND; ++db)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) amax = vmax(amax, fabsf(qr.q[db][j]));
-  amax = max_xor32(max_xor16(amax));
-  float qup;
-  const float qdown = q_range_scale(amax, &qup);
-#pragma unroll
-  for (int db = 0; db < ND; ++db)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      _Float16 hi, lo;
-      split_hi_lo(qr.q[db][j] * qdown, hi, lo);
-      qhi[db][j] = hi;
-      qlo[db][j] = lo;
-    }
-  if (new_row) {
-    if (QKN) qk_norm_row<D>(grp, a.norm_eps, rr);
-    uint16_t* krow = a.kc + (row0 + pos) * kv_dim + (size_t)kvh * D;
-    uint16_t* vrow = a.vc + (row0 + pos) * kv_dim + (size_t)kvh * D;
-#pragma unroll
-    for (int u = 0; u < RowRaw<D>::NP; ++u) {
-      const int i = lane + 64 * u;
-      if (i < D / 2) {
-        const int i0 = (a.rope_type == PLH_ROPE_QWEN) ? i : 2 * i;
-        const int i1 = (a.rope_type == PLH_ROPE_QWEN) ? i + D / 2 : 2 * i + 1;
-        float k0 = rr.k0[u], k1 = rr.k1[u];
-        rope_rotate(k0, k1, rr.c[u], rr.s[u]);
-        const uint16_t b0 = f16_bits_rha(k0), b1 = f16_bits_rha(k1);
-        krow[i0] = b0;
-        krow[i1] = b1;
-        s_knew[i0] = f16_bits_to_f32(b0);
-        s_knew[i1] = f16_bits_to_f32(b1);
-      }
-    }
-#pragma unroll
-    for (int u = 0; u < RowRaw<D>::NV; ++u) {
-      const int d = lane + 64 * u;
-      if (d < D) {
-        const uint16_t b = f16_bits_rha(rr.v[u]);
-        vrow[d] = b;
-        s_vnew[d] = f16_bits_to_f32(b);
-      }
-    }
-    // s_knew is written and read by this wave only; order the LDS accesses
-    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "workgroup");
-    float sc = 0.f;
-#pragma unroll
-    for (int db = 0; db < ND; ++db)
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        sc = __builtin_fmaf(qr.q[db][j], s_knew[32 * db + 8 * grp + j], sc);
-    sc += shfl_xor_f(sc, 16);
-    sc += shfl_xor_f(sc, 32);
-    if (grp == 0) s_mnew[col] = sc * a.score_scale;
-  }
+  const float qup = split_q<D, QKN>(a, col < nh, grp, qr, qhi, qlo);
+  if (new_row) append_new_row<D, QKN>(a, li, kvh, row0, lane, col, grp, qr, rr, s_knew, s_vnew, s_mnew);
 
   // ---- stream the split's cached rows, one tile ahead ----------------------
   _Float16* vt = reinterpret_cast<_Float16*>(smem) + wave * (kTile * VP);
@@ -507,7 +528,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
         if (t0 < te)
           process_tile<D>(buf[j], qhi, qlo, vt, t0, tlast, lane, col, grp, sscale, ones, m, lsum,
                           o);
-        load_tile<D>(buf[j], kbase, vbase, kv_dim, t0 + PF * kStride, tlast, lane, col, grp);
+        load_tile<D>(buf[j], kbase, vbase, kv_dim, t0 + PF * kStride, tclamp, lane, col, grp);
       }
     }
   }
@@ -727,6 +748,7 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
   const int nhm = G < 16 ? G : 16;  // q heads of the largest head block
   const int n_groups = n_launch_layers * n_kv_heads * n_hblk;
   const int npos = pos + 1;
+
   // Split plan: contexts of at most g_min_split positions are not split (the
   // merge launch would cost more than it saves); longer ones are cut into
   // splits of a multiple of 128 rows (one 32-row tile per wave at least),
