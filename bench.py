@@ -1,56 +1,56 @@
 """Benchmark of picolm's attention block on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
 
-A step is one token's decode attention over all layers of the model (one
-plh_attn_decode call covering every layer), with inputs resident in HBM.
-The default workload is TinyLlama-1.1B-shaped decode at position 2047
-(22 layers, 32 q heads, 4 kv heads, head_dim 64, FP16 cache of 2048 rows);
-the same line carries, under "prefill", the TinyLlama-shaped 512-token causal
-prefill (all 22 layers per step) in TFLOP/s of causal-pair flops
-(L * Hq * 4D * sum_i (i+1)) against its binding roof (HBM, for the fp32
-q/k/v/out traffic at these sizes), with the fraction of the fp16 MFMA peak.
+Prints one JSON line.  The headline (the contract keys, `roofline`,
+`cpu_baseline`) is TinyLlama-1.1B-shaped decode at position 2047 (22 layers,
+32 q heads, 4 kv heads, head_dim 64, FP16 cache of 2048 rows): a step is one
+token's decode attention over all 22 layers -- one plh_attn_decode call (main
++ combine kernel) -- with inputs resident in HBM.  The same line carries every
+workload of the attention block's benchmark set, each measured the same way:
 
-Method:
-  * the FP16 caches are rotated over enough copies (>= 512 MiB in total) that
-    the 256 MiB Infinity Cache cannot serve a step from the previous one;
-  * the K timed steps are captured into one HIP graph (no host launch cost
-    between steps); the graph is replayed once untimed and once timed,
-    bracketed by device synchronisation.  ms_per_step is the wall clock of the
-    timed replay / K; roofline.achieved uses hipEvents recorded on the library
-    stream around the timed replay (mean duration per launch);
-  * algorithmic bytes per token (all layers):
-      L * [ (pos+1)*2*Hkv*D*2  (K+V rows read)
-            + Hq*D*4 + 2*Hkv*D*4 (q, k, v in) + 2*Hkv*D*2 (row written)
-            + Hq*D*4 (out) ]
-  * per_layer_launches: the same token as L sequential one-layer calls (how
-    a per-layer forward pass uses the block), also graph-replayed;
-  * cpu_baseline: the reference's own decode attention where oracle/_ref (its
-    sources compiled) exists: its model_forward at position pos minus the same
-    token at position 0, on the forward workload's model (same attention
-    shape), matmuls on the host threads -- the reference runs its attention
-    loop on one thread whatever its -j; cpu_baseline_port (or cpu_baseline
-    without oracle/_ref or with --no-forward): the oracle (the attention
-    restated in C, same op order, out-of-line fp16 widening as in the
-    reference build) on one host thread over a bounded sample;
-    cpu_baseline_head_parallel: the same arithmetic with the q heads split
-    over up to 16 host threads, an upper bound only; "host" records nproc,
-    the CPU model and the C library;
-  * gemv: every weight GEMV of one TinyLlama Q4_K_M-style token (the
-    gpu_try_matmul path: 22 x (q, k, v, o, gate, up, down) + output, 670 MB
-    of GGUF weights), graph-replayed, against the HBM roof; its CPU baseline
-    is the oracle matmul with rows split over the host threads like the
-    reference's matmul pool, and the sampled GPU outputs are checked bit for
-    bit against it;
-  * forward: the whole forward pass on the device (plh_forward) for a
-    TinyLlama-shaped Q4_K_M-style synthetic model: prefill of a 128-token
-    prompt, decode tok/s (tokens queued back to back) and greedy-generation
-    tok/s (logits to the host and argmax every token); its CPU baseline is
-    the reference's own model_forward compiled from its sources
-    (oracle/_ref, the oracle forward pass where that library is absent) on
-    the host threads, and the GPU logits of the sampled tokens are checked
-    against it.
-Prints one JSON line.
+  cfg1  TinyLlama decode at pos 256            HBM-bound
+  cfg2  TinyLlama decode at pos 2047           HBM-bound (the headline)
+  cfg3  TinyLlama causal prefill of 512 tokens MFMA work, HBM roof at fp32 I/O
+  cfg4  Llama-3.2-1B decode at pos 8191        HBM-bound
+  cfg5a Llama-2-7B decode at pos 4095          HBM-bound
+  cfg5b Llama-2-7B causal prefill of 1024      MFMA work, HBM roof at fp32 I/O
+
+Method (device):
+  * inputs rotated over enough copies (>= 512 MiB in all) that the 256 MiB
+    Infinity Cache cannot serve a step from the previous one; K timed steps
+    captured in one HIP graph, replayed once untimed and once timed between
+    device synchronisations; ms_per_step = wall clock / K, roofline.achieved =
+    algorithmic bytes (decode) or causal-pair flops (prefill) / the mean step
+    time from HIP events recorded on the library stream (the stream the
+    kernels run on);
+  * decode bytes per token, all layers: L * [(pos+1)*2*Hkv*D*2 (K+V rows read)
+    + Hq*D*4 + 2*Hkv*D*4 (q, k, v in) + 2*Hkv*D*2 (row written) + Hq*D*4
+    (out)]; prefill flops: L * Hq * 4D * sum_{i<N}(start+i+1) (causal pairs);
+    prefill roof: the HBM roof at its arithmetic intensity (fp32 q/k/v/out),
+    with the fraction of the fp16 MFMA peak beside it;
+  * per_layer: the same token (prompt) as L one-layer calls, how a per-layer
+    forward pass issues them, graph-replayed;
+  * traffic: HBM bytes per launch of the dominant kernel from rocprofv3 --pmc
+    (FETCH_SIZE, WRITE_SIZE, calibrated on a copy kernel), read from
+    profiles/<workload>_traffic.json, null when none was measured;
+  * boundary: the gpu.h-style hooks end to end (tests/c/bench_boundary: host
+    q/k/v in, host output and cache rows back over PCIe) -- the latency
+    picolm's own call sites would see; never the headline value.
+Method (CPU baseline, kind "reference"): picolm's own attention code, i.e.
+its model_forward_ex / model_forward_prefill compiled from its sources into
+oracle/_ref, on the host, median of 5 runs after 1 warm-up, over a bounded
+sample that the `sample` field names:
+  * decode: a 2-layer model of the workload's attention shape with rows
+    0..pos-1 of N(0,1) fp16, the forward at position pos minus the same
+    forward at position 0 (the attention loop is the only part whose cost
+    depends on pos), scaled to L layers; the attention loop runs on one
+    thread whatever picolm's -j (model.c:848-892);
+  * prefill: model_forward_prefill (projections at a small width included)
+    of a 1-layer model with a slice of the workload's q heads (same head_dim,
+    same GQA group), scaled to all heads and layers.
+The oracle (the restatement in C, test infrastructure) checks the GPU outputs
+of a sample layer (parity_normwise_max).
 """
 from __future__ import annotations
 
@@ -58,6 +58,7 @@ import argparse
 import json
 import math
 import os
+import subprocess
 import sys
 import time
 
@@ -69,9 +70,7 @@ sys.path.insert(0, ROOT)
 METRIC = "attn µs/token + KV GB/s (% HBM peak) decode; prefill TFLOP/s (% MFMA)"
 HBM_PEAK_GBS = 8000.0
 MALL_DEFEAT_BYTES = 512 << 20
-
 MFMA_F16_PEAK_TFS = 2516.6
-
 HOST_THREADS_MAX = 16   # host CPU threads available per GPU
 
 WORKLOADS = {
@@ -87,6 +86,15 @@ WORKLOADS = {
     "qwen3_prefill_512": dict(L=28, Hq=16, Hkv=8, D=128, S=2048, theta=1e6, start=0, n=512,
                               rt=1, qkn=1e-6),
 }
+# the benchmark set, in the order of the configs it is quoted on
+BASELINE_SET = [("cfg1", "tinyllama_decode_pos256"), ("cfg2", "tinyllama_decode_pos2047"),
+                ("cfg3", "tinyllama_prefill_512"), ("cfg4", "llama32_decode_pos8191"),
+                ("cfg5a", "llama2_decode_pos4095"), ("cfg5b", "llama2_prefill_1024")]
+HEADLINE = "tinyllama_decode_pos2047"
+# CPU-baseline samples: decode layers; prefill (q heads, kv heads) of a 1-layer model
+CPU_DECODE_LAYERS = 2
+CPU_PREFILL_HEADS = {"tinyllama_prefill_512": (8, 1), "llama2_prefill_1024": (4, 4),
+                     "qwen3_prefill_512": (2, 1)}
 
 
 # The weight GEMVs of one token of a TinyLlama-1.1B Q4_K_M-style model (the
@@ -310,50 +318,22 @@ def cpu_baseline_forward(res):
             "parity_logits_normwise_max": worst, "parity_greedy_token_same": same_argmax}
 
 
-def cpu_reference_attention(h, w, reps=3):
-    """The reference's own decode attention (model.c:828-892) timed inside its
-    model_forward (oracle/_ref): the same TinyLlama-shaped model run at
-    position pos over rows 0..pos-1 of N(0,1) fp16 cache rows, minus the same
-    token at position 0 (everything but the attention loop costs the same at
-    both positions).  The matmuls use the host threads; the attention loop
-    runs on one thread whatever -j is (model.c:848-892).  None without
-    oracle/_ref or when the model's attention shape is not the workload's."""
-    from oracle import oracle as O
-    if not O.ref_available():
-        return None
-    if (h.n_layers, h.n_heads, h.n_kv_heads, h.head_dim, h.max_seq_len) != (
-            w["L"], w["Hq"], w["Hkv"], w["D"], w["S"]) or h.rope_type != w.get("rt", 0):
-        return None
-    pos = w["pos"]
-    n_thr = min(os.cpu_count() or 1, HOST_THREADS_MAX)
-    O.ref().ref_set_threads(n_thr)
-    ref = O.RefForward(h)
+def host_info():
+    """nproc, CPU model and C library of the machine the CPU legs ran on."""
+    model = None
     try:
-        rng = np.random.default_rng(2047)
-        kv = h.n_kv_heads * h.head_dim
-        for cache in (ref.kc, ref.vc):
-            view = cache.reshape(h.n_layers, h.max_seq_len, kv)
-            for layer in range(h.n_layers):
-                view[layer, :pos] = O.f32_to_f16(
-                    rng.standard_normal((pos, kv), dtype=np.float32)).reshape(pos, kv)
-        ref.forward(1, pos)                       # warm-up (writes row pos only)
-        t_long, t_short = [], []
-        for _ in range(reps):
-            t0 = time.perf_counter()
-            ref.forward(1, pos)
-            t_long.append(time.perf_counter() - t0)
-            t0 = time.perf_counter()
-            ref.forward(1, 0)
-            t_short.append(time.perf_counter() - t0)
-    finally:
-        O.ref().ref_set_threads(1)
-        ref.close()
-    attn_s = float(np.median(t_long) - np.median(t_short))
-    return {"value": decode_bytes(w) / attn_s / 1e9, "unit": "GB/s", "cores": 1,
-            "kind": "reference", "us_per_token": attn_s * 1e6,
-            "sample": f"picolm model_forward (oracle/_ref) at pos {pos} minus pos 0, {reps} "
-                      f"runs each, on the forward workload's model (same attention shape); "
-                      f"matmuls on {n_thr} threads, the attention loop on one"}
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    try:
+        libc = os.confstr("CS_GNU_LIBC_VERSION")
+    except (ValueError, OSError):
+        libc = None
+    return {"nproc": os.cpu_count(), "cpu_model": model, "libc": libc}
 
 
 def qkn_bytes(w) -> int:
@@ -382,8 +362,9 @@ def prefill_bytes(w) -> int:
 
 
 def traffic_from_profiles(name: str):
-    """HBM bytes per launch measured by rocprofv3 --pmc (FETCH_SIZE +
-    WRITE_SIZE, calibrated against a copy kernel), if a summary exists."""
+    """HBM bytes per launch of the workload's dominant kernel, measured by
+    rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, calibrated on a copy kernel)
+    and summarised in profiles/<name>_traffic.json; None if not measured."""
     path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
     try:
         with open(path) as f:
@@ -402,29 +383,50 @@ def norm_weights(P, w, rng):
     return P.DeviceBuffer.from_numpy(qn), P.DeviceBuffer.from_numpy(kn)
 
 
-def run_decode(P, w, steps, warmup, name):
+def timed_graph(P, launch, steps):
+    """Captures `steps` calls of launch(i) in one graph, replays it once
+    untimed and once timed; returns (wall seconds, event milliseconds) per
+    step."""
+    with P.Graph() as g:
+        for i in range(steps):
+            launch(i)
+    g.launch()
+    P.synchronize()
+    e0, e1 = P.Event(), P.Event()
+    t0 = time.perf_counter()
+    e0.record()
+    g.launch()
+    e1.record()
+    P.synchronize()
+    wall = (time.perf_counter() - t0) / steps
+    return wall, e0.elapsed_ms(e1) / steps
+
+
+def run_decode(P, w, steps, warmup, name, warm=False):
+    """Decode workload on the device; returns the result dict and what the
+    CPU legs need."""
     rt = w.get("rt", 0)
     cfg = P.AttnConfig(w["L"], w["Hq"], w["Hkv"], w["D"], w["S"], w["theta"], rt)
     cache_bytes = cfg.cache_elems * 2
     n_copies = max(1, math.ceil(MALL_DEFEAT_BYTES / (2 * cache_bytes)))
     rng = np.random.default_rng(2047)
     pos = w["pos"]
-
     # copy 0: rows 0..pos-1 of every layer hold N(0,1) rounded to fp16 on the
     # device with the reference's rounding; other rows are zero
     L, S, kv = cfg.n_layers, cfg.max_seq_len, cfg.kv_dim
     cos_t, sin_t = P.rope_tables(S, cfg.head_dim, cfg.rope_freq_base)
     d_cos, d_sin = P.DeviceBuffer.from_numpy(cos_t), P.DeviceBuffer.from_numpy(sin_t)
-    staging = P.DeviceBuffer(L * S * kv * 4)
+    staging = P.DeviceBuffer(S * kv * 4)
     keys, vals = [], []
     for which in range(2):
-        host = np.zeros((L, S, kv), np.float32)
-        host[:, :pos] = rng.standard_normal((L, pos, kv), dtype=np.float32)
-        staging.upload(host)
         buf = P.DeviceBuffer(cache_bytes)
-        P.f32_to_f16(staging.ptr, buf.ptr, L * S * kv)
+        buf.zero()
+        for layer in range(L):   # one layer at a time keeps host memory small
+            host = np.zeros((S, kv), np.float32)
+            host[:pos] = rng.standard_normal((pos, kv), dtype=np.float32)
+            staging.upload(host)
+            P.f32_to_f16(staging.ptr, buf.ptr + layer * S * kv * 2, S * kv)
         (keys if which == 0 else vals).append(buf)
-        del host
     staging.free()
     for c in range(1, n_copies):
         for lst in (keys, vals):
@@ -458,27 +460,13 @@ def run_decode(P, w, steps, warmup, name):
         q, k, v, o = qkv[c]
         call(0, L, q.ptr, k.ptr, v.ptr, c, o.ptr)
 
-    for i in range(max(1, warmup)):   # also sizes the split-K workspace
+    for i in range(max(1, warmup)):   # also sizes the split workspace
         launch(i)
     P.synchronize()
+    wall, k_ms = timed_graph(P, launch, steps)
 
-    with P.Graph() as g:
-        for i in range(steps):
-            launch(i)
-    g.launch()                     # untimed replay
-    P.synchronize()
-    e0, e1 = P.Event(), P.Event()
-    t0 = time.perf_counter()
-    e0.record()
-    g.launch()
-    e1.record()
-    P.synchronize()
-    wall = time.perf_counter() - t0
-    k_mean = e0.elapsed_ms(e1) / steps
-
-    # the same token as L sequential one-layer launches (how a per-layer
-    # forward pass calls the block), timed the same way over fewer steps
-    pl_steps = max(1, steps // 10)
+    # the same token as L sequential one-layer calls (how a per-layer forward
+    # pass calls the block)
     def launch_per_layer(i):
         c = i % n_copies
         q, k, v, o = qkv[c]
@@ -487,64 +475,42 @@ def run_decode(P, w, steps, warmup, name):
                  o.ptr + l * cfg.q_dim * 4)
     launch_per_layer(0)
     P.synchronize()
-    with P.Graph() as g2:
-        for i in range(pl_steps):
-            launch_per_layer(i)
-    g2.launch()
-    P.synchronize()
-    e0.record()
-    g2.launch()
-    e1.record()
-    P.synchronize()
-    pl_ms = e0.elapsed_ms(e1) / pl_steps
-
-    # warm: every step reuses copy 0, so a cache that fits the 256 MiB
-    # Infinity Cache is served from it (reported apart, never the headline)
-    def launch_warm(i):
-        q, k, v, o = qkv[0]
-        call(0, L, q.ptr, k.ptr, v.ptr, 0, o.ptr)
-    with P.Graph() as g3:
-        for i in range(steps):
-            launch_warm(i)
-    g3.launch()
-    P.synchronize()
-    e0.record()
-    g3.launch()
-    e1.record()
-    P.synchronize()
-    warm_ms = e0.elapsed_ms(e1) / steps
+    _, pl_ms = timed_graph(P, launch_per_layer, max(1, min(steps, 20)))
 
     algo = decode_bytes(w)
-    ms_step = wall * 1e3 / steps
-    achieved = algo / (k_mean * 1e-3) / 1e9
-    result = {
-        "value": algo / (ms_step * 1e-3) / 1e9,
+    achieved = algo / (k_ms * 1e-3) / 1e9
+    res = {
+        "value": algo / wall / 1e9,
         "unit": "GB/s",
-        "ms_per_step": ms_step,
-        "us_per_token": ms_step * 1e3,
-        "kernel_us_mean": k_mean * 1e3,
+        "ms_per_step": wall * 1e3,
+        "us_per_token": wall * 1e6,
+        "kernel_us_mean": k_ms * 1e3,
         "algorithmic_bytes_per_step": algo,
         "cache_copies_rotated": n_copies,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
                      "traffic": traffic_from_profiles(name)},
-        "per_layer_launches": {"us_per_token": pl_ms * 1e3,
-                               "gbs": algo / (pl_ms * 1e-3) / 1e9,
-                               "launches_per_token": L},
-        "warm": {"us_per_token": warm_ms * 1e3,
-                 "gbs": algo / (warm_ms * 1e-3) / 1e9,
-                 "note": "one cache copy reused every step: Infinity-Cache resident when "
-                         "it fits in 256 MiB; not the headline"},
+        "per_layer": {"us_per_token": pl_ms * 1e3, "gbs": algo / (pl_ms * 1e-3) / 1e9,
+                      "launches_per_token": L},
     }
-    # keep what the CPU baseline needs (copy 0 before further appends)
-    result["_cpu_inputs"] = (cfg, keys[0], vals[0], qkv[0], cos_t, sin_t, d_qn, d_kn)
-    return result
+    if warm:
+        # every step reuses copy 0: served from the Infinity Cache when it fits
+        # in 256 MiB (reported apart, never the headline)
+        def launch_warm(i):
+            q, k, v, o = qkv[0]
+            call(0, L, q.ptr, k.ptr, v.ptr, 0, o.ptr)
+        _, warm_ms = timed_graph(P, launch_warm, steps)
+        res["warm"] = {"us_per_token": warm_ms * 1e3, "gbs": algo / (warm_ms * 1e-3) / 1e9,
+                       "note": "one cache copy reused every step: Infinity-Cache resident when "
+                               "it fits in 256 MiB; not the headline"}
+    res["_cpu_inputs"] = (cfg, keys[0], vals[0], qkv[0], d_qn, d_kn)
+    return res
 
 
-def run_prefill(P, w, steps, warmup):
+def run_prefill(P, w, steps, warmup, name):
     """One step = prefill of n prompt tokens over all layers (append kernel +
     causal attention kernel), inputs rotated over enough copies to defeat the
-    Infinity Cache."""
+    Infinity Cache; the per-layer form as L one-layer calls."""
     cfg = P.AttnConfig(w["L"], w["Hq"], w["Hkv"], w["D"], w["S"], w["theta"], w.get("rt", 0))
     L, n, st = cfg.n_layers, w["n"], w["start"]
     per_copy = prefill_bytes(w) + 2 * L * n * cfg.kv_dim * 2
@@ -566,22 +532,23 @@ def run_prefill(P, w, steps, warmup):
         cache, q, k, v, o = copies[i % n_copies]
         P.prefill(cache, 0, st, n, q.ptr, k.ptr, v.ptr, o.ptr, None, L, **norms)
 
+    def launch_per_layer(i):
+        cache, q, k, v, o = copies[i % n_copies]
+        for l in range(L):
+            ln = {} if d_qn is None else dict(q_norm=d_qn.ptr + l * cfg.head_dim * 4,
+                                              k_norm=d_kn.ptr + l * cfg.head_dim * 4,
+                                              norm_eps=w["qkn"])
+            P.prefill(cache, l, st, n, q.ptr + l * n * cfg.q_dim * 4,
+                      k.ptr + l * n * cfg.kv_dim * 4, v.ptr + l * n * cfg.kv_dim * 4,
+                      o.ptr + l * n * cfg.q_dim * 4, None, 1, **ln)
+
     for i in range(max(1, warmup)):
         launch(i)
     P.synchronize()
-    with P.Graph() as g:
-        for i in range(steps):
-            launch(i)
-    g.launch()
+    wall, ms = timed_graph(P, launch, steps)
+    launch_per_layer(0)
     P.synchronize()
-    e0, e1 = P.Event(), P.Event()
-    t0 = time.perf_counter()
-    e0.record()
-    g.launch()
-    e1.record()
-    P.synchronize()
-    wall = time.perf_counter() - t0
-    ms = e0.elapsed_ms(e1) / steps
+    _, pl_ms = timed_graph(P, launch_per_layer, max(1, min(steps, 5)))
     flops = prefill_flops(w)
     algo_bytes = prefill_bytes(w)
     tfs = flops / (ms * 1e-3) / 1e12
@@ -590,13 +557,17 @@ def run_prefill(P, w, steps, warmup):
     hbm_roof = flops / algo_bytes * HBM_PEAK_GBS / 1e3
     roof = min(MFMA_F16_PEAK_TFS, hbm_roof)
     return {
-        "us_per_step": wall * 1e6 / steps,
-        "us_per_token": wall * 1e6 / steps / n,
+        "us_per_step": wall * 1e6,
+        "us_per_token": wall * 1e6 / n,
         "tflops": tfs,
+        "kernel_us_mean": ms * 1e3,
         "roofline": {"bound": "hbm" if hbm_roof < MFMA_F16_PEAK_TFS else "mfma",
                      "achieved": tfs, "peak": roof, "unit": "TFLOP/s", "frac": tfs / roof,
+                     "traffic": traffic_from_profiles(name),
                      "achieved_gbs": algo_bytes / (ms * 1e-3) / 1e9,
                      "mfma_peak": MFMA_F16_PEAK_TFS, "mfma_frac": tfs / MFMA_F16_PEAK_TFS},
+        "per_layer": {"us_per_step": pl_ms * 1e3, "tflops": flops / (pl_ms * 1e-3) / 1e12,
+                      "launches_per_step": L},
         "algorithmic_flops_per_step": flops,
         "algorithmic_bytes_per_step": algo_bytes,
         "copies_rotated": n_copies,
@@ -605,56 +576,98 @@ def run_prefill(P, w, steps, warmup):
     }
 
 
-def cpu_baseline_prefill(P, w, res, budget_s=8.0):
-    """The oracle's prefill on one host thread over a bounded number of layers
-    of the same step, extrapolated to all layers."""
+def n_host_threads():
+    return min(os.cpu_count() or 1, HOST_THREADS_MAX)
+
+
+def cpu_reference_decode(w, reps=5):
+    """picolm's own decode attention (model.c:828-892) timed inside its
+    model_forward_ex (oracle/_ref) on a CPU_DECODE_LAYERS-layer model of the
+    workload's attention shape: the forward at position pos over rows
+    0..pos-1 of N(0,1) fp16, minus the same forward at position 0, median of
+    `reps` after one warm-up each, scaled to all layers."""
     from oracle import oracle as O
-    cache, dq, dk, dv, dout = res.pop("_copies")[0]
-    cfg = cache.cfg
-    L, n, st = cfg.n_layers, w["n"], w["start"]
-    kc, vc = cache.fetch()
-    shp = O.Shape(L, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.max_seq_len,
-                  cfg.rope_freq_base, cfg.rope_type)
-    qn, kn = host_norms(res.pop("_norms"), L, cfg.head_dim)
-    cos_t, sin_t = O.rope_tables(cfg.max_seq_len, cfg.head_dim, cfg.rope_freq_base)
-    q = dq.download(np.float32, (L, n, cfg.q_dim))
-    k = dk.download(np.float32, (L, n, cfg.kv_dim))
-    v = dv.download(np.float32, (L, n, cfg.kv_dim))
-    gpu_out = dout.download(np.float32, (L, n, cfg.q_dim))
-    t_total, layers, worst = 0.0, 0, 0.0
-    while t_total < budget_s and layers < L:
-        t0 = time.perf_counter()
-        ref = O.attn_prefill(shp, layers, st, n, q[layers].copy(), k[layers].copy(), v[layers],
-                             kc, vc, cos_t, sin_t, **norm_args(w, qn, kn, layers))
-        t_total += time.perf_counter() - t0
-        err = np.abs(gpu_out[layers] - ref).reshape(-1, cfg.head_dim).max(1)
-        den = np.abs(ref).reshape(-1, cfg.head_dim).max(1)
-        worst = max(worst, float((err / den).max()))
-        layers += 1
-    step_s = t_total / layers * L
-    return {"cpu_baseline": {"value": prefill_flops(w) / step_s / 1e12, "unit": "TFLOP/s",
-                             "cores": 1, "kind": "port", "us_per_token": step_s * 1e6 / n,
-                             "sample": f"{layers} of {L} layers of the {n}-token prefill, oracle "
-                                       f"on 1 thread, extrapolated"},
-            "parity_normwise_max": worst}
+    if not O.ref_available():
+        return None
+    Ls, pos = CPU_DECODE_LAYERS, w["pos"]
+    shp = O.Shape(Ls, w["Hq"], w["Hkv"], w["D"], w["S"], w["theta"], w.get("rt", 0))
+    R = O.ref()
+    R.ref_set_threads(1)   # the attention loop is single-threaded; idle pool threads would
+    m = O.RefModel(shp, 0, seed=7)   # only compete with it
+    try:
+        rng = np.random.default_rng(4095)
+        kv = w["Hkv"] * w["D"]
+        for cache in (m.kc, m.vc):
+            view = cache.reshape(Ls, w["S"], kv)
+            for layer in range(Ls):
+                view[layer, :pos] = O.f32_to_f16(
+                    rng.standard_normal((pos, kv), dtype=np.float32)).reshape(pos, kv)
+        for layer in range(Ls):
+            q = rng.standard_normal(w["Hq"] * w["D"], dtype=np.float32)
+            k = rng.standard_normal(kv, dtype=np.float32)
+            v = rng.standard_normal(kv, dtype=np.float32)
+            R.ref_set_decode_qkv(m.h, layer, q, k, v)
+        out = np.empty(w["Hq"] * w["D"], np.float32)
+        t_long, t_short = [], []
+        for r in range(reps + 1):
+            t0 = time.perf_counter()
+            R.ref_decode(m.h, pos, Ls, out)
+            t1 = time.perf_counter()
+            R.ref_decode(m.h, 0, Ls, out)
+            t2 = time.perf_counter()
+            if r > 0:
+                t_long.append(t1 - t0)
+                t_short.append(t2 - t1)
+    finally:
+        R.ref_set_threads(1)
+        m.close()
+    attn_s = (float(np.median(t_long)) - float(np.median(t_short))) * w["L"] / Ls
+    return {"value": decode_bytes(w) / attn_s / 1e9, "unit": "GB/s", "cores": 1,
+            "kind": "reference", "us_per_token": attn_s * 1e6,
+            "sample": f"model_forward_ex of a {Ls}-layer model of this attention shape at pos "
+                      f"{pos} minus pos 0, median of {reps} after a warm-up, x{w['L'] // Ls} "
+                      f"layers; 1 thread"}
 
 
-def host_norms(dev, L, D):
-    """Host copies of a QK-norm workload's [L][D] weights (None, None if none)."""
-    if dev[0] is None:
-        return None, None
-    return (dev[0].download(np.float32, (L, D)), dev[1].download(np.float32, (L, D)))
-
-
-def norm_args(w, qn, kn, layer):
-    return {} if qn is None else dict(q_norm=qn[layer], k_norm=kn[layer], eps=w["qkn"])
-
-
-def cpu_baseline(P, w, res, budget_s=12.0):
-    """The oracle on one host thread over a bounded sample of the workload, and
-    a parity spot check of the GPU output of the same step."""
+def cpu_reference_prefill(name, w, reps=5):
+    """picolm's own model_forward_prefill (oracle/_ref) on a 1-layer model with
+    a slice of the workload's q heads (same head_dim and GQA group; its
+    projections at that small width included), median of `reps` after one
+    warm-up, scaled to all heads and layers."""
     from oracle import oracle as O
-    cfg, dkey, dval, (dq, dk, dv, dout), cos_t, sin_t, d_qn, d_kn = res.pop("_cpu_inputs")
+    if not O.ref_available():
+        return None
+    hq, hkv = CPU_PREFILL_HEADS[name]
+    n, st = w["n"], w["start"]
+    shp = O.Shape(1, hq, hkv, w["D"], st + n, w["theta"], w.get("rt", 0))
+    R = O.ref()
+    R.ref_set_threads(1)
+    m = O.RefModel(shp, 1, seed=9, w_scale=0.05)
+    try:
+        toks = (np.arange(n) * 7919 % (hq * w["D"])).astype(np.int32)
+        logits = np.empty(hq * w["D"], np.float32)
+        ts = []
+        for r in range(reps + 1):
+            t0 = time.perf_counter()
+            R.ref_prefill(m.h, toks, n, st, logits)
+            if r > 0:
+                ts.append(time.perf_counter() - t0)
+    finally:
+        R.ref_set_threads(1)
+        m.close()
+    scale = (w["Hq"] / hq) * w["L"]
+    step_s = float(np.median(ts)) * scale
+    return {"value": prefill_flops(w) / step_s / 1e12, "unit": "TFLOP/s", "cores": 1,
+            "kind": "reference", "us_per_token": step_s * 1e6 / n,
+            "sample": f"model_forward_prefill of a 1-layer model with {hq} q / {hkv} kv heads of "
+                      f"head_dim {w['D']} ({n} tokens, projections included), median of {reps} "
+                      f"after a warm-up, x{w['Hq'] // hq} heads x{w['L']} layers; 1 thread"}
+
+
+def decode_parity(P, w, res, layers=(0,)):
+    """Normwise error of the GPU output of sample layers against the oracle."""
+    from oracle import oracle as O
+    cfg, dkey, dval, (dq, dk, dv, dout), d_qn, d_kn = res.pop("_cpu_inputs")
     L, pos = cfg.n_layers, w["pos"]
     kc = dkey.download(np.uint16, (cfg.cache_elems,))
     vc = dval.download(np.uint16, (cfg.cache_elems,))
@@ -664,95 +677,124 @@ def cpu_baseline(P, w, res, budget_s=12.0):
     gpu_out = dout.download(np.float32, (L, cfg.q_dim))
     shp = O.Shape(L, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.max_seq_len,
                   cfg.rope_freq_base, cfg.rope_type)
-    qn, kn = host_norms((d_qn, d_kn), L, cfg.head_dim)
-    tokens, t_total, worst = 0, 0.0, 0.0
-    layers_done = 0
-    while t_total < budget_s and tokens < 50:
-        for l in range(L):
-            qi, ki = q[l].copy(), k[l].copy()
-            t0 = time.perf_counter()
-            ref = O.attn_decode(shp, l, pos, qi, ki, v[l], kc, vc, cos_t, sin_t,
-                                **norm_args(w, qn, kn, l))
-            t_total += time.perf_counter() - t0
-            layers_done += 1
-            if tokens == 0:
-                err = np.abs(gpu_out[l] - ref).reshape(-1, cfg.head_dim).max(1)
-                den = np.abs(ref).reshape(-1, cfg.head_dim).max(1)
-                worst = max(worst, float((err / den).max()))
-            if t_total >= budget_s:
-                break
-        tokens += 1
-    token_s = t_total / layers_done * L
-    algo = decode_bytes(w)
-    # head-parallel upper bound: the same per-head arithmetic over n host
-    # threads (the reference runs its attention on one thread whatever -j)
-    n_thr = min(os.cpu_count() or 1, HOST_THREADS_MAX)
-    t_mt, mt_layers = 0.0, 0
-    while qn is None and t_mt < budget_s / 2 and mt_layers < 4 * L:
-        l = mt_layers % L
-        qi, ki = q[l].copy(), k[l].copy()
-        t0 = time.perf_counter()
-        O.attn_decode_mt(shp, l, pos, qi, ki, v[l], kc, vc, cos_t, sin_t, n_thr)
-        t_mt += time.perf_counter() - t0
-        mt_layers += 1
-    out = {
-        "cpu_baseline": {"value": algo / token_s / 1e9, "unit": "GB/s", "cores": 1,
-                         "kind": "port", "us_per_token": token_s * 1e6,
-                         "sample": f"{layers_done} layer-steps ({layers_done / L:.2f} tokens) of "
-                                   f"{w['L']}-layer decode at pos {pos}, oracle on 1 thread"},
-        "host": host_info(),
-        "parity_normwise_max": worst,
-    }
-    if mt_layers == 0:   # the head-parallel oracle has no QK-norm form
-        return out
-    token_mt = t_mt / mt_layers * L
-    return {
-        "cpu_baseline": {"value": algo / token_s / 1e9, "unit": "GB/s", "cores": 1,
-                         "kind": "port", "us_per_token": token_s * 1e6,
-                         "sample": f"{layers_done} layer-steps ({layers_done / L:.2f} tokens) of "
-                                   f"{w['L']}-layer decode at pos {pos}, oracle on 1 thread"},
-        "cpu_baseline_head_parallel": {
-            "value": algo / token_mt / 1e9, "unit": "GB/s", "cores": n_thr, "kind": "port",
-            "us_per_token": token_mt * 1e6,
-            "sample": f"{mt_layers} layer-steps of the same decode, q heads split over "
-                      f"{n_thr} threads: an upper bound, not the reference's own parallelism"},
-        "host": host_info(),
-        "parity_normwise_max": worst,
-    }
+    cos_t, sin_t = O.rope_tables(cfg.max_seq_len, cfg.head_dim, cfg.rope_freq_base)
+    qn = None if d_qn is None else d_qn.download(np.float32, (L, cfg.head_dim))
+    kn = None if d_kn is None else d_kn.download(np.float32, (L, cfg.head_dim))
+    worst = 0.0
+    for l in layers:
+        extra = {} if qn is None else dict(q_norm=qn[l], k_norm=kn[l], eps=w["qkn"])
+        ref = O.attn_decode(shp, l, pos, q[l].copy(), k[l].copy(), v[l], kc, vc, cos_t, sin_t,
+                            **extra)
+        err = np.abs(gpu_out[l] - ref).reshape(-1, cfg.head_dim).max(1)
+        den = np.abs(ref).reshape(-1, cfg.head_dim).max(1)
+        worst = max(worst, float((err / den).max()))
+    return worst
 
 
-def host_info():
-    """nproc, CPU model and C library of the machine the CPU legs ran on."""
-    model = None
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
-    try:
-        libc = os.confstr("CS_GNU_LIBC_VERSION")
-    except (ValueError, OSError):
-        libc = None
-    return {"nproc": os.cpu_count(), "cpu_model": model, "libc": libc}
+def prefill_parity(P, w, res, layers=(0,)):
+    from oracle import oracle as O
+    cache, dq, dk, dv, dout = res.pop("_copies")[0]
+    d_qn, d_kn = res.pop("_norms")
+    cfg = cache.cfg
+    L, n, st = cfg.n_layers, w["n"], w["start"]
+    kc, vc = cache.fetch()
+    shp = O.Shape(L, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.max_seq_len,
+                  cfg.rope_freq_base, cfg.rope_type)
+    cos_t, sin_t = O.rope_tables(cfg.max_seq_len, cfg.head_dim, cfg.rope_freq_base)
+    qn = None if d_qn is None else d_qn.download(np.float32, (L, cfg.head_dim))
+    kn = None if d_kn is None else d_kn.download(np.float32, (L, cfg.head_dim))
+    worst = 0.0
+    for l in layers:
+        q = dq.download(np.float32, (n, cfg.q_dim), offset=l * n * cfg.q_dim * 4)
+        k = dk.download(np.float32, (n, cfg.kv_dim), offset=l * n * cfg.kv_dim * 4)
+        v = dv.download(np.float32, (n, cfg.kv_dim), offset=l * n * cfg.kv_dim * 4)
+        gpu_out = dout.download(np.float32, (n, cfg.q_dim), offset=l * n * cfg.q_dim * 4)
+        extra = {} if qn is None else dict(q_norm=qn[l], k_norm=kn[l], eps=w["qkn"])
+        ref = O.attn_prefill(shp, l, st, n, q.copy(), k.copy(), v, kc, vc, cos_t, sin_t,
+                             **extra)
+        err = np.abs(gpu_out - ref).reshape(-1, cfg.head_dim).max(1)
+        den = np.abs(ref).reshape(-1, cfg.head_dim).max(1)
+        worst = max(worst, float((err / den).max()))
+    return worst
+
+
+def boundary_latency(w, reps=20):
+    """gpu_try_attention (decode) or gpu_try_attention_prefill end to end,
+    PCIe copies included, from tests/c/bench_boundary; None if not built."""
+    exe = os.path.join(ROOT, "tests", "c", "bench_boundary")
+    if not os.path.exists(exe):
+        return None
+    pos, n = (w["pos"], 0) if "pos" in w else (w["start"], w["n"])
+    args = [exe] + [str(x) for x in (w["L"], w["Hq"], w["Hkv"], w["D"], w["S"], w["theta"], pos,
+                                     n, reps)]
+    r = subprocess.run(args, capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        return {"error": r.stderr.strip()[-200:]}
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
+def measure(P, name, steps, warmup, cpu, warm=False):
+    """One workload: device figures, CPU baseline, parity sample."""
+    w = WORKLOADS[name]
+    if "n" in w:
+        res = run_prefill(P, w, steps, warmup, name)
+        if cpu:
+            res["cpu_baseline"] = cpu_reference_prefill(name, w)
+        res["parity_normwise_max"] = prefill_parity(P, w, res) if w["n"] <= 512 else None
+        res.pop("_copies", None)
+        res.pop("_norms", None)
+    else:
+        res = run_decode(P, w, steps, warmup, name, warm=warm)
+        if cpu:
+            res["cpu_baseline"] = cpu_reference_decode(w)
+        res["parity_normwise_max"] = decode_parity(P, w, res)
+        res.pop("_cpu_inputs", None)
+    return res
+
+
+def workload_config(name):
+    w = WORKLOADS[name]
+    c = {"workload": name, "n_layers": w["L"], "n_heads": w["Hq"], "n_kv_heads": w["Hkv"],
+         "head_dim": w["D"], "max_seq_len": w["S"], "rope_theta": w["theta"],
+         "rope_type": w.get("rt", 0), "qk_norm_eps": w.get("qkn"), "batch": 1}
+    if "pos" in w:
+        c["pos"] = w["pos"]
+    else:
+        c["start_pos"], c["n_tokens"] = w["start"], w["n"]
+    return c
+
+
+def compact(tag, name, res):
+    """The flat summary of one workload (the end of the bench line)."""
+    rf, cb, pl = res["roofline"], res.get("cpu_baseline") or {}, res["per_layer"]
+    out = {"cfg": tag, "w": name}
+    if "tflops" in res:
+        out.update(us_step=round(res["us_per_step"], 1), us_tok=round(res["us_per_token"], 3),
+                   tfs=round(res["tflops"], 1), mfma_frac=round(rf["mfma_frac"], 4),
+                   pl_us_step=round(pl["us_per_step"], 1))
+    else:
+        out.update(us_tok=round(res["us_per_token"], 2), gbs=round(res["value"], 1),
+                   pl_us_tok=round(pl["us_per_token"], 1))
+    out.update(kern_us=round(res["kernel_us_mean"], 2), frac=round(rf["frac"], 4), peak=rf["peak"],
+               traffic=None if rf["traffic"] is None else int(rf["traffic"]),
+               cpu_us_tok=None if not cb else round(cb["us_per_token"], 1),
+               cpu_kind=cb.get("kind"),
+               parity=None if res.get("parity_normwise_max") is None
+               else float(f"{res['parity_normwise_max']:.2e}"))
+    return out
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
-    ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--workload", default="tinyllama_decode_pos2047",
-                    choices=sorted(WORKLOADS) + [GEMV_WORKLOAD, FWD_WORKLOAD])
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default=None,
+                    choices=sorted(WORKLOADS) + [GEMV_WORKLOAD, FWD_WORKLOAD],
+                    help="measure this workload alone (no benchmark set)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline legs")
-    ap.add_argument("--no-prefill", action="store_true",
-                    help="skip the secondary prefill measurement")
-    ap.add_argument("--no-gemv", action="store_true",
-                    help="skip the weight-GEMV measurement")
-    ap.add_argument("--no-forward", action="store_true",
-                    help="skip the whole-forward-pass measurement")
+    ap.add_argument("--no-extras", action="store_true",
+                    help="skip the GEMV, forward-pass and boundary-latency sections")
     ap.add_argument("--prompt", type=int, default=128,
                     help="prompt tokens of the forward-pass workload")
     args = ap.parse_args()
@@ -764,10 +806,11 @@ def main():
         sys.exit(2)
     import picolm_amd as P
     P.init(0)
+    cpu = not args.no_cpu
     if args.workload == GEMV_WORKLOAD:   # the weight GEMVs of one token as the headline
         steps = max(1, args.steps // 50)
         gres = run_gemv(P, steps, min(args.warmup, 3))
-        gextra = {} if args.no_cpu else cpu_baseline_gemv(gres)
+        gextra = cpu_baseline_gemv(gres) if cpu else {}
         gres.pop("_inputs", None)
         line = {"metric": METRIC, "value": gres.pop("gbs"), "unit": "GB/s", "n_gpus": 1,
                 "steps": steps, "warmup": min(args.warmup, 3),
@@ -782,7 +825,7 @@ def main():
     if args.workload == FWD_WORKLOAD:   # the whole forward pass as the headline
         n_decode = max(8, min(args.steps, 256))
         fres = run_forward(P, n_prompt=max(8, args.prompt), n_decode=n_decode)
-        fextra = {} if args.no_cpu else cpu_baseline_forward(fres)
+        fextra = cpu_baseline_forward(fres) if cpu else {}
         fres.pop("_check", None)
         line = {"metric": METRIC, "value": fres.pop("decode_tok_s"), "unit": "tok/s",
                 "n_gpus": 1, "steps": n_decode, "warmup": 4,
@@ -793,84 +836,80 @@ def main():
         line.update(fextra)
         print(json.dumps(line), flush=True)
         return
-    w = WORKLOADS[args.workload]
-    if "n" in w:   # a prefill workload as the headline
-        res = run_prefill(P, w, max(1, args.steps // 10), args.warmup)
-        extra = {} if args.no_cpu else cpu_baseline_prefill(P, w, res)
-        res.pop("_copies", None)
-        res.pop("_norms", None)
-        line = {"metric": METRIC, "value": res.pop("tflops"), "unit": "TFLOP/s", "n_gpus": 1,
-                "steps": max(1, args.steps // 10), "warmup": args.warmup,
-                "ms_per_step": res["us_per_step"] / 1e3, "higher_is_better": True,
-                "scaling": "weak", "vs_baseline": None, "dtype": "f16", "data": "synthetic",
-                "config": {"workload": args.workload, "n_layers": w["L"], "n_heads": w["Hq"],
-                           "n_kv_heads": w["Hkv"], "head_dim": w["D"], "max_seq_len": w["S"],
-                           "start_pos": w["start"], "n_tokens": w["n"],
-                           "rope_theta": w["theta"], "rope_type": w.get("rt", 0),
-                           "qk_norm_eps": w.get("qkn"), "batch": 1}}
-        line.update(res)
-        line.update(extra)
-        print(json.dumps(line), flush=True)
-        return
-    res = run_decode(P, w, args.steps, args.warmup, args.workload)
-    extra = {}
-    if not args.no_cpu:
-        extra = cpu_baseline(P, w, res)
-    else:
-        res.pop("_cpu_inputs", None)
+
+    head = args.workload or HEADLINE
+    w = WORKLOADS[head]
+    hres = measure(P, head, args.steps, args.warmup, cpu, warm=args.workload is None)
+    is_prefill = "n" in w
     line = {
         "metric": METRIC,
-        "value": res.pop("value"),
-        "unit": res.pop("unit"),
+        "value": hres["tflops"] if is_prefill else hres["value"],
+        "unit": "TFLOP/s" if is_prefill else "GB/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": res.pop("ms_per_step"),
+        "ms_per_step": (hres["us_per_step"] / 1e3) if is_prefill else hres["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f16",
         "data": "synthetic",
-        "config": {"workload": args.workload, "n_layers": w["L"], "n_heads": w["Hq"],
-                   "n_kv_heads": w["Hkv"], "head_dim": w["D"], "max_seq_len": w["S"],
-                   "pos": w["pos"], "rope_theta": w["theta"], "rope_type": w.get("rt", 0),
-                   "qk_norm_eps": w.get("qkn"), "batch": 1},
+        "config": workload_config(head),
+        "roofline": hres["roofline"],
+        "cpu_baseline": hres.get("cpu_baseline"),
     }
-    line["hbm_frac"] = res["roofline"]["frac"]
-    line.update(res)
-    line.update(extra)
-    if not args.no_prefill:
-        # the metric's prefill half: TinyLlama-shaped 512-token causal prefill
-        pw = WORKLOADS["tinyllama_prefill_512"]
-        pres = run_prefill(P, pw, 20, 3)
-        pextra = {} if args.no_cpu else cpu_baseline_prefill(P, pw, pres, budget_s=4.0)
-        pres.pop("_copies", None)
-        pres.pop("_norms", None)
-        pres["workload"] = "tinyllama_prefill_512"
-        pres.update(pextra)
-        line["prefill"] = pres
-    if not args.no_gemv:
+    for key in ("us_per_token", "us_per_step", "kernel_us_mean", "algorithmic_bytes_per_step",
+                "algorithmic_flops_per_step", "cache_copies_rotated", "copies_rotated",
+                "per_layer", "warm", "parity_normwise_max"):
+        if key in hres:
+            line[key] = hres[key]
+    if cpu:
+        line["host"] = host_info()
+    if args.workload is not None:   # one workload alone (profiling runs)
+        print(json.dumps(line), flush=True)
+        return
+
+    # the rest of the benchmark set, each measured the same way
+    results = {HEADLINE: hres}
+    for tag, name in BASELINE_SET:
+        if name == HEADLINE:
+            continue
+        # their own step counts (each step is short; the headline keeps --steps)
+        steps = 20 if "n" in WORKLOADS[name] else 200
+        results[name] = measure(P, name, steps, 5, cpu)
+    pres = results["tinyllama_prefill_512"]
+    # the metric's prefill half, flat (cfg3)
+    line["prefill"] = {"workload": "tinyllama_prefill_512",
+                       "us_per_step": pres["us_per_step"], "us_per_token": pres["us_per_token"],
+                       "tflops": pres["tflops"], "roofline_frac": pres["roofline"]["frac"],
+                       "roofline_peak": pres["roofline"]["peak"],
+                       "mfma_frac": pres["roofline"]["mfma_frac"],
+                       "traffic": pres["roofline"]["traffic"],
+                       "per_layer_us_per_step": pres["per_layer"]["us_per_step"],
+                       "cpu_us_per_token": (pres.get("cpu_baseline") or {}).get("us_per_token"),
+                       "cpu_kind": (pres.get("cpu_baseline") or {}).get("kind"),
+                       "parity_normwise_max": pres.get("parity_normwise_max")}
+    if not args.no_extras:
+        # the gpu.h-style hooks end to end (PCIe included), cfg1 / cfg2 decode, cfg3 prefill
+        line["boundary"] = {tag: boundary_latency(WORKLOADS[name])
+                            for tag, name in (("cfg1", "tinyllama_decode_pos256"),
+                                              ("cfg2", "tinyllama_decode_pos2047"),
+                                              ("cfg3", "tinyllama_prefill_512"))}
         # the gpu_try_matmul path: every weight GEMV of one TinyLlama token
         gres = run_gemv(P, 10, 2)
-        gextra = {} if args.no_cpu else cpu_baseline_gemv(gres)
+        gextra = cpu_baseline_gemv(gres) if cpu else {}
         gres.pop("_inputs", None)
         gres["workload"] = GEMV_WORKLOAD
         gres.update(gextra)
         line["gemv"] = gres
-    if not args.no_forward:
         # the whole forward pass on the device (gpu_try_forward's path)
         fres = run_forward(P)
-        h_fwd = fres["_check"][0]
-        fextra = {} if args.no_cpu else cpu_baseline_forward(fres)
-        if not args.no_cpu and "cpu_baseline" in line:
-            # the headline's baseline from the reference itself where it runs
-            refb = cpu_reference_attention(h_fwd, w)
-            if refb is not None:
-                line["cpu_baseline_port"] = line["cpu_baseline"]
-                line["cpu_baseline"] = refb
+        fextra = cpu_baseline_forward(fres) if cpu else {}
         fres.pop("_check", None)
         fres.update(fextra)
         line["forward"] = fres
+    # last, so that a tail of the line holds it: the benchmark set, flat
+    line["workloads"] = [compact(tag, name, results[name]) for tag, name in BASELINE_SET]
     print(json.dumps(line), flush=True)
 
 

@@ -47,6 +47,16 @@ int plh_memcpy2d_dtoh(void *dst, size_t dpitch, const void *src, size_t spitch,
                       size_t width, size_t height);
 int plh_memset(void *dst, int value, size_t bytes);
 int plh_synchronize(void);
+/* Pinned (page-locked) host memory, for staging copies that the DMA engines
+ * run without an intermediate bounce: plh_host_alloc returns NULL on
+ * failure. */
+void *plh_host_alloc(size_t bytes);
+int plh_host_free(void *host);
+/* Copies queued on the library stream without waiting (the host side should
+ * be pinned memory from plh_host_alloc and must stay untouched until a later
+ * plh_synchronize). */
+int plh_memcpy_htod_async(void *dst, const void *src, size_t bytes);
+int plh_memcpy_dtoh_async(void *dst, const void *src, size_t bytes);
 
 /* ---- timing on the library stream (hipEvents) -------------------------- */
 void *plh_event_create(void);

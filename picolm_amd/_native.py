@@ -71,6 +71,10 @@ _SIGS = {
     "plh_memcpy2d_dtoh": (_i, [_vp, _sz, _vp, _sz, _sz, _sz]),
     "plh_memset": (_i, [_vp, _i, _sz]),
     "plh_synchronize": (_i, []),
+    "plh_host_alloc": (_vp, [_sz]),
+    "plh_host_free": (_i, [_vp]),
+    "plh_memcpy_htod_async": (_i, [_vp, _vp, _sz]),
+    "plh_memcpy_dtoh_async": (_i, [_vp, _vp, _sz]),
     # events
     "plh_event_create": (_vp, []),
     "plh_event_record": (_i, [_vp]),

@@ -155,6 +155,31 @@ int plh_memcpy2d_dtoh(void* dst, size_t dpitch, const void* src, size_t spitch, 
   return check_hip(hipStreamSynchronize(g_ctx.stream), "dtoh 2d sync");
 }
 
+void* plh_host_alloc(size_t bytes) {
+  void* p = nullptr;
+  if (check_hip(hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault), "hipHostMalloc"))
+    return nullptr;
+  return p;
+}
+
+int plh_host_free(void* p) {
+  if (!p) return 0;
+  // queued copies may still read or write it
+  if (g_ctx.stream && check_hip(hipStreamSynchronize(g_ctx.stream), "hipStreamSynchronize"))
+    return -1;
+  return check_hip(hipHostFree(p), "hipHostFree");
+}
+
+int plh_memcpy_htod_async(void* dst, const void* src, size_t bytes) {
+  return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, g_ctx.stream),
+                   "htod async");
+}
+
+int plh_memcpy_dtoh_async(void* dst, const void* src, size_t bytes) {
+  return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, g_ctx.stream),
+                   "dtoh async");
+}
+
 int plh_memcpy_dtod(void* dst, const void* src, size_t bytes) {
   return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_ctx.stream), "dtod");
 }

@@ -68,7 +68,12 @@ static struct {
     float *d_cos, *d_sin;
     unsigned char qkn[MAX_LAYERS]; /* layer has QK-norm */
     float *d_qn, *d_kn;            /* [n_layers][head_dim] QK-norm weights, or NULL */
-    float *d_q, *d_k, *d_v, *d_out; /* staging, sized for stage_tokens rows */
+    /* staging, sized for stage_tokens rows: device q|k|v (one block) and out;
+     * pinned host h_in = q|k|v and h_out = out|key rows|val rows, so that a
+     * call is one packed upload, the kernels and queued downloads with a
+     * single synchronisation */
+    float *d_q, *d_k, *d_v, *d_out;
+    unsigned char *h_in, *h_out;
     int stage_tokens;
     gpu_weight_t *weights;          /* GEMV matrices */
     int n_weights, cap_weights;
@@ -128,24 +133,73 @@ static size_t cache_bytes(void) {
            (size_t)gs.head_dim * sizeof(uint16_t);
 }
 
+static void free_stage(void) {
+    plh_free(gs.d_q);
+    plh_free(gs.d_out);
+    plh_host_free(gs.h_in);
+    plh_host_free(gs.h_out);
+    gs.d_q = gs.d_k = gs.d_v = gs.d_out = NULL;
+    gs.h_in = gs.h_out = NULL;
+    gs.stage_tokens = 0;
+}
+
 static int ensure_stage(int n_tokens) {
     if (n_tokens <= gs.stage_tokens) return 0;
-    plh_free(gs.d_q);
-    plh_free(gs.d_k);
-    plh_free(gs.d_v);
-    plh_free(gs.d_out);
-    gs.d_q = gs.d_k = gs.d_v = gs.d_out = NULL;
-    gs.stage_tokens = 0;
+    free_stage();
     size_t q_dim = (size_t)gs.n_heads * gs.head_dim;
     size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
-    size_t stride = (size_t)gs.n_embd > q_dim ? (size_t)gs.n_embd : q_dim;
-    gs.d_q = (float *)plh_malloc((size_t)n_tokens * q_dim * sizeof(float));
-    gs.d_k = (float *)plh_malloc((size_t)n_tokens * kv_dim * sizeof(float));
-    gs.d_v = (float *)plh_malloc((size_t)n_tokens * kv_dim * sizeof(float));
-    gs.d_out = (float *)plh_malloc((size_t)n_tokens * stride * sizeof(float));
-    if (!gs.d_q || !gs.d_k || !gs.d_v || !gs.d_out) return -1;
+    size_t q4 = (q_dim + 3) & ~(size_t)3; /* the device output stride */
+    size_t stride = (size_t)gs.n_embd > q4 ? (size_t)gs.n_embd : q4;
+    size_t in_bytes = (size_t)n_tokens * (q_dim + 2 * kv_dim) * sizeof(float);
+    size_t out_bytes = (size_t)n_tokens * stride * sizeof(float);
+    size_t rows_bytes = 2 * (size_t)n_tokens * kv_dim * sizeof(uint16_t);
+    gs.d_q = (float *)plh_malloc(in_bytes);
+    gs.d_out = (float *)plh_malloc(out_bytes);
+    gs.h_in = (unsigned char *)plh_host_alloc(in_bytes);
+    gs.h_out = (unsigned char *)plh_host_alloc(out_bytes + rows_bytes);
+    if (!gs.d_q || !gs.d_out || !gs.h_in || !gs.h_out) {
+        free_stage();
+        return -1;
+    }
+    gs.d_k = gs.d_q + (size_t)n_tokens * q_dim;
+    gs.d_v = gs.d_k + (size_t)n_tokens * kv_dim;
     gs.stage_tokens = n_tokens;
     return 0;
+}
+
+/* q, k, v of n rows into pinned staging, then one upload to d_q|d_k|d_v
+ * (queued).  The device q block is n rows of q_dim, so k and v follow it. */
+static int stage_in(int n, const float *q, const float *k, const float *v) {
+    const size_t qb = (size_t)n * gs.n_heads * gs.head_dim * sizeof(float);
+    const size_t kvb = (size_t)n * gs.n_kv_heads * gs.head_dim * sizeof(float);
+    memcpy(gs.h_in, q, qb);
+    memcpy(gs.h_in + qb, k, kvb);
+    memcpy(gs.h_in + qb + kvb, v, kvb);
+    gs.d_k = gs.d_q + (size_t)n * gs.n_heads * gs.head_dim;
+    gs.d_v = gs.d_k + (size_t)n * gs.n_kv_heads * gs.head_dim;
+    return plh_memcpy_htod_async(gs.d_q, gs.h_in, qb + 2 * kvb);
+}
+
+/* Queues the downloads of out (out_bytes from d_out) and of rows
+ * [r0, r0+n) of layer `layer` of both device caches into h_out. */
+static int stage_out(size_t out_bytes, int layer, int r0, int n) {
+    const size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
+    const size_t off = ((size_t)layer * gs.max_seq_len + (size_t)r0) * kv_dim;
+    const size_t rb = (size_t)n * kv_dim * sizeof(uint16_t);
+    if (plh_memcpy_dtoh_async(gs.h_out, gs.d_out, out_bytes) != 0 ||
+        plh_memcpy_dtoh_async(gs.h_out + out_bytes, gs.d_key + off, rb) != 0 ||
+        plh_memcpy_dtoh_async(gs.h_out + out_bytes + rb, gs.d_val + off, rb) != 0)
+        return -1;
+    return plh_synchronize();
+}
+
+/* The staged rows of stage_out into the host caches. */
+static void rows_from_stage(const model_t *m, size_t out_bytes, int layer, int r0, int n) {
+    const size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
+    const size_t off = ((size_t)layer * gs.max_seq_len + (size_t)r0) * kv_dim;
+    const size_t rb = (size_t)n * kv_dim * sizeof(uint16_t);
+    memcpy(m->state.key_cache + off, gs.h_out + out_bytes, rb);
+    memcpy(m->state.val_cache + off, gs.h_out + out_bytes + rb, rb);
 }
 
 /* Per-layer QK-norm weights, as the host dequantized them at load
@@ -461,10 +515,7 @@ void gpu_shutdown(void) {
         plh_free(gs.d_sin);
         plh_free(gs.d_qn);
         plh_free(gs.d_kn);
-        plh_free(gs.d_q);
-        plh_free(gs.d_k);
-        plh_free(gs.d_v);
-        plh_free(gs.d_out);
+        free_stage();
         free_forward();
         free_weights();
         plh_shutdown();
@@ -480,26 +531,13 @@ static int same_shape(const model_t *m) {
            c->n_embd == gs.n_embd && c->rms_norm_eps == gs.norm_eps;
 }
 
-/* Copies rows [r0, r0+n) of layer `layer` from the device caches into the
- * host caches. */
-static int rows_to_host(const model_t *m, int layer, int r0, int n) {
-    size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
-    size_t off = ((size_t)layer * gs.max_seq_len + (size_t)r0) * kv_dim;
-    size_t bytes = (size_t)n * kv_dim * sizeof(uint16_t);
-    if (plh_memcpy_dtoh(m->state.key_cache + off, gs.d_key + off, bytes) != 0) return -1;
-    if (plh_memcpy_dtoh(m->state.val_cache + off, gs.d_val + off, bytes) != 0) return -1;
-    return 0;
-}
-
 int gpu_try_attention(model_t *m, int layer, int pos, float *q, float *k, const float *v,
                       float *out) {
     if (!gpu_available() || !same_shape(m)) return -1;
     if (layer < 0 || layer >= gs.n_layers || layer >= gs.gpu_layers) return -1;
     if (pos < 0 || pos >= gs.max_seq_len) return -1;
     size_t q_bytes = (size_t)gs.n_heads * gs.head_dim * sizeof(float);
-    size_t kv_bytes = (size_t)gs.n_kv_heads * gs.head_dim * sizeof(float);
-    if (plh_memcpy_htod(gs.d_q, q, q_bytes) != 0 || plh_memcpy_htod(gs.d_k, k, kv_bytes) != 0 ||
-        plh_memcpy_htod(gs.d_v, v, kv_bytes) != 0) {
+    if (stage_in(1, q, k, v) != 0) {
         /* nothing on the device changed, but the CPU path now appends a row the
          * device cache will not hold: later calls must not use the device */
         backend_lost("staging copy");
@@ -521,10 +559,12 @@ int gpu_try_attention(model_t *m, int layer, int pos, float *q, float *k, const 
         backend_lost("plh_attn_decode");
         return -1;
     }
-    if (plh_memcpy_dtoh(out, gs.d_out, q_bytes) != 0 || rows_to_host(m, layer, pos, 1) != 0) {
+    if (stage_out(q_bytes, layer, pos, 1) != 0) {
         backend_lost("copy back");
         return -1;
     }
+    memcpy(out, gs.h_out, q_bytes);
+    rows_from_stage(m, q_bytes, layer, pos, 1);
     return 0;
 }
 
@@ -540,12 +580,9 @@ int gpu_try_attention_prefill(model_t *m, int layer, int start_pos, int n_tokens
         return -1;
     }
     size_t q_dim = (size_t)gs.n_heads * gs.head_dim;
-    size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
     size_t stride = (size_t)gs.n_embd; /* out row bi at out + bi*n_embd (model.c:1057) */
     if (stride < q_dim) return -1;
-    if (plh_memcpy_htod(gs.d_q, q, (size_t)n_tokens * q_dim * sizeof(float)) != 0 ||
-        plh_memcpy_htod(gs.d_k, k, (size_t)n_tokens * kv_dim * sizeof(float)) != 0 ||
-        plh_memcpy_htod(gs.d_v, v, (size_t)n_tokens * kv_dim * sizeof(float)) != 0) {
+    if (stage_in(n_tokens, q, k, v) != 0) {
         backend_lost("staging copy"); /* as in gpu_try_attention */
         return -1;
     }
@@ -568,17 +605,20 @@ int gpu_try_attention_prefill(model_t *m, int layer, int start_pos, int n_tokens
         backend_lost("plh_attn_prefill");
         return -1;
     }
-    if ((size_t)dev_stride == stride) {
-        rc = plh_memcpy_dtoh(out, gs.d_out, (size_t)n_tokens * stride * sizeof(float));
-    } else {
-        for (int bi = 0; bi < n_tokens && rc == 0; bi++)
-            rc = plh_memcpy_dtoh(out + (size_t)bi * stride, gs.d_out + (size_t)bi * dev_stride,
-                                 q_dim * sizeof(float));
-    }
-    if (rc != 0 || rows_to_host(m, layer, start_pos, n_tokens) != 0) {
+    const size_t out_bytes = (size_t)n_tokens * dev_stride * sizeof(float);
+    if (stage_out(out_bytes, layer, start_pos, n_tokens) != 0) {
         backend_lost("copy back");
         return -1;
     }
+    const float *staged = (const float *)gs.h_out;
+    if ((size_t)dev_stride == stride) {
+        memcpy(out, staged, out_bytes);
+    } else {
+        for (int bi = 0; bi < n_tokens; bi++)
+            memcpy(out + (size_t)bi * stride, staged + (size_t)bi * dev_stride,
+                   q_dim * sizeof(float));
+    }
+    rows_from_stage(m, out_bytes, layer, start_pos, n_tokens);
     return 0;
 }
 
