@@ -245,7 +245,7 @@ void prefill_attn_kernel(PrefillArgs a) {
   // Columns past the prompt (cvalid false) read the last token's row and are
   // never stored; each column's softmax is independent, so they need no mask.
   half8_t qhi[ND], qlo[ND];
-  float qup;  // 2^e of the column's range scale
+  float qup, qdown;  // 2^e and 2^-e of the column's range scale
   {
     const float* qrow = a.q + ((size_t)li * a.n_tokens + tok_c) * q_dim +
                         (size_t)(kvh * G + (cvalid ? hh : 0)) * D;
@@ -298,15 +298,20 @@ void prefill_attn_kernel(PrefillArgs a) {
         rope_rotate_fused(qf[db][6], qf[db][7], c4.w, s4.w);
       }
     }
-    // the column's range for the fp16 split (a power-of-two scale, folded
-    // into its score scale; 1 unless some |q| >= 2^15)
+    // the softmax scale log2(e)/sqrt(D) goes into q, so that the MFMA
+    // produces scores in log2 units; then the column's range for the fp16
+    // split (a power-of-two scale, undone on the scores: 1 unless some
+    // |q| * scale >= 2^15)
     float amax = 0.f;
 #pragma unroll
     for (int db = 0; db < ND; ++db)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) amax = vmax(amax, fabsf(qf[db][j]));
+      for (int j = 0; j < 8; ++j) {
+        qf[db][j] *= a.score_scale;
+        amax = vmax(amax, fabsf(qf[db][j]));
+      }
     amax = max_xor32(max_xor16(amax));
-    const float qdown = q_range_scale(amax, &qup);
+    qdown = q_range_scale(amax, &qup);
 #pragma unroll
     for (int db = 0; db < ND; ++db)
 #pragma unroll
@@ -321,9 +326,15 @@ void prefill_attn_kernel(PrefillArgs a) {
   store_lds(0);
   __syncthreads();
 
-  const float sscale = a.score_scale * qup;  // this lane's column
-  float ms = kNegBig;            // running max (scaled, log2 units)
+  // Running maximum ms (log2 units) and the accumulators.  Each QK MFMA chain
+  // starts from -ms (times the column's 2^-e), so it yields score - ms
+  // directly; the maximum test and the exp2 then read the same values, which
+  // keeps every weight bounded (<= 2^kLazy) whatever the scores' magnitude.
+  // The first tile sets ms to its own maximum (row 0 is never masked).
+  float ms = 0.f;
+  float4_t negm = float4_t{0.f, 0.f, 0.f, 0.f};  // -ms * 2^-e, the QK accumulator start
   float4_t lsum = float4_t{0.f, 0.f, 0.f, 0.f};  // running sum (all 4 entries equal)
+  const bool scaled_cols = __ballot(qup != 1.f) != 0;  // wave-uniform: rare
   half8_t ones;
 #pragma unroll
   for (int j = 0; j < 8; ++j) ones[j] = (_Float16)1.0f;
@@ -332,57 +343,69 @@ void prefill_attn_kernel(PrefillArgs a) {
   for (int ob = 0; ob < NO; ++ob) o[ob] = float4_t{0.f, 0.f, 0.f, 0.f};
   // transposing-read address of this lane: row 8*grp + col/4, chunk col%4
   const int vofs = (8 * grp + (col >> 2)) * VP + 4 * (col & 3);
+  int kofs[2];
+#pragma unroll
+  for (int rb = 0; rb < 2; ++rb) kofs[rb] = (8 * (col >> 2) + 4 * rb + (col & 3)) * KP + 8 * grp;
 
-  for (int it = 0; it < n_tiles; ++it) {
-    const int b = it & 1;
+  // one tile in buffer b (a constant at each call site, so the LDS offsets
+  // fold into the instructions)
+  auto tile = [&](const int b, const int it) {
     const int t0 = it * kKT;
     const bool more = it + 1 < n_tiles;
     if (more) issue_loads(t0 + kKT);
 
-    // S^T for this wave's 16 columns (raw scores)
+    // S^T - ms for this wave's 16 columns
     float4_t s[2];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb) {
-      const int krow = 8 * (col >> 2) + 4 * rb + (col & 3);
-      s[rb] = float4_t{0.f, 0.f, 0.f, 0.f};
+      s[rb] = negm;
 #pragma unroll
       for (int db = 0; db < ND; ++db) {
-        const half8_t kk = *(const half8_t*)&smem[b * KBUF + krow * KP + 32 * db + 8 * grp];
+        const half8_t kk = *(const half8_t*)&smem[b * KBUF + kofs[rb] + 32 * db];
         s[rb] = mfma16x16x32(kk, qhi[db], s[rb]);
         s[rb] = mfma16x16x32(kk, qlo[db], s[rb]);
       }
     }
     // lane holds rows t0 + 8*grp + j, j = 4*rb + r
-    float u[8];
+    float t[8];
 #pragma unroll
     for (int rb = 0; rb < 2; ++rb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) u[4 * rb + r] = s[rb][r];
+      for (int r = 0; r < 4; ++r) t[4 * rb + r] = s[rb][r];
+    if (scaled_cols) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) t[j] *= qup;  // exact: a power of two
+    }
     if (t0 + kKT - 1 > p_min) {
 #pragma unroll
       for (int j = 0; j < 8; ++j)
-        if (t0 + 8 * grp + j > p_col) u[j] = -INFINITY;
+        if (t0 + 8 * grp + j > p_col) t[j] = -INFINITY;
     }
-    float tmax = u[0];
+    float tmax = t[0];
 #pragma unroll
-    for (int j = 1; j < 8; ++j) tmax = vmax(tmax, u[j]);
+    for (int j = 1; j < 8; ++j) tmax = vmax(tmax, t[j]);
     tmax = max_xor32(max_xor16(tmax));
-    const float tms = tmax * sscale;
-    if (__ballot(tms > ms + kLazy)) {
-      const float mnew = fmaxf(ms, tms);
-      const float alpha = fast_exp2(ms - mnew);
-      ms = mnew;
-      lsum *= alpha;
+    if (it == 0 || __ballot(tmax > kLazy)) {
+      // first tile: ms = its maximum (nothing accumulated yet); later, raise
+      // ms by the excess (columns at or below it keep theirs)
+      const float d = it == 0 ? tmax : fmaxf(tmax, 0.f);
+      if (it != 0) {
+        const float alpha = fast_exp2(-d);
+        lsum *= alpha;
 #pragma unroll
-      for (int ob = 0; ob < NO; ++ob) o[ob] *= alpha;
+        for (int ob = 0; ob < NO; ++ob) o[ob] *= alpha;
+      }
+      ms += d;
+      const float nm = -ms * qdown;
+      negm = float4_t{nm, nm, nm, nm};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) t[j] -= d;
     }
     half8_t ph, pl;
 #pragma unroll
     for (int j = 0; j < 8; j += 2) {
-      const float p0 = fast_exp2(u[j] * sscale - ms);
-      const float p1 = fast_exp2(u[j + 1] * sscale - ms);
       half2_t hi, lo;
-      split_pair_rtz(p0, p1, hi, lo);
+      split_pair_rtz(fast_exp2(t[j]), fast_exp2(t[j + 1]), hi, lo);
       ph[j] = hi[0], ph[j + 1] = hi[1];
       pl[j] = lo[0], pl[j + 1] = lo[1];
     }
@@ -401,6 +424,10 @@ void prefill_attn_kernel(PrefillArgs a) {
 
     if (more) store_lds(b ^ 1);
     __syncthreads();
+  };
+  for (int it = 0; it < n_tiles; it += 2) {
+    tile(0, it);
+    if (it + 1 < n_tiles) tile(1, it + 1);
   }
 
   // ---- normalise and write: lane holds d = 16*ob + 4*grp + r of its column ---
