@@ -304,7 +304,9 @@ int plh_forward_prefill(const plh_model *m, const int *tokens, int n_tokens, int
  * not split (multiple of 128, 0 = default); key 3: GEMV rows per thread
  * (1, 2, 4, 8; 0 = default); key 4: plh_forward forms each rmsnorm in a
  * launch of its own (1) instead of inside the GEMVs that read it (0,
- * default). */
+ * default); key 5: prefill launches with fewer q blocks than workgroup slots
+ * split their heavy blocks into chunks of tiles merged afterwards (0
+ * automatic, -1 never, 2, 4, 8 or 16 tiles per chunk). */
 int plh_set_tuning(int key, int value);
 
 #ifdef __cplusplus

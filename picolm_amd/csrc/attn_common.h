@@ -14,6 +14,7 @@ typedef _Float16 half8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 half4_t __attribute__((ext_vector_type(4)));
 typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
 typedef float float4_t __attribute__((ext_vector_type(4)));
+typedef float f32x16_t __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
 
 namespace plh {
@@ -133,6 +134,13 @@ __device__ __forceinline__ float4_t mfma16x16x32(half8_t a, half8_t b, float4_t 
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// v_mfma_f32_32x32x16_f16, lane = 32*h + i: A = row i, k 8*h .. 8*h+7;
+// B = column i, k 8*h .. 8*h+7; C / D = column i, rows 8*(v/4) + 4*h + v%4
+// for v = 0..15.
+__device__ __forceinline__ f32x16_t mfma32x32x16(half8_t a, half8_t b, f32x16_t c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 // Maximum over lanes l and l^16 (resp. l^32) with the gfx950 row-swap
@@ -202,6 +210,30 @@ __device__ __forceinline__ float rms_scale_cols(const float (&x)[D / 32][8], int
         const float sq = x[db][j] * x[db][j];
         acc[j] = acc[j] + __shfl(sq, col + 16 * g, 64);
       }
+  const float l0 = acc[0] + acc[4], l1 = acc[1] + acc[5];
+  const float l2 = acc[2] + acc[6], l3 = acc[3] + acc[7];
+  return 1.0f / sqrtf(((l0 + l2) + (l1 + l3)) / (float)D + eps);
+}
+
+// The same scale for the 32x32 MFMA operand layout: lane (h, col) holds
+// element 16*s + 8*h + j in x[s][j], its partner lane col + 32 - 64*h the
+// other half of the row.  permlane32_swap hands every lane both halves'
+// squares (r[0] from half 0, r[1] from half 1), which are elements 16*s + j
+// and 16*s + 8 + j: added in that order, each running sum a[j] sees the
+// row's elements in increasing order.
+template <int D>
+__device__ __forceinline__ float rms_scale_halves(const float (&x)[D / 16][8], float eps) {
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int s = 0; s < D / 16; ++s)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float sq = x[s][j] * x[s][j];
+      const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(sq), __float_as_uint(sq),
+                                                      false, false);
+      acc[j] = acc[j] + __uint_as_float(r[0]);
+      acc[j] = acc[j] + __uint_as_float(r[1]);
+    }
   const float l0 = acc[0] + acc[4], l1 = acc[1] + acc[5];
   const float l2 = acc[2] + acc[6], l3 = acc[3] + acc[7];
   return 1.0f / sqrtf(((l0 + l2) + (l1 + l3)) / (float)D + eps);

@@ -696,6 +696,14 @@ extern "C" int plh_set_tuning(int key, int value) {
     g_fwd_norm_separate = value;
     return 0;
   }
+  if (key == 5) {
+    if (value != 0 && value != -1 && value != 2 && value != 4 && value != 8 && value != 16) {
+      set_error("plh_set_tuning: prefill chunking must be 0, -1, 2, 4, 8 or 16");
+      return -1;
+    }
+    g_prefill_split = value;
+    return 0;
+  }
   set_error("plh_set_tuning: unknown key %d", key);
   return -1;
 }

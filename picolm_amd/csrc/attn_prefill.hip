@@ -13,31 +13,29 @@
 //   prefill_attn_kernel    flash attention over the cache with fp16 MFMA and
 //                          an fp32 online softmax.
 //
-// Attention workgroup = (layer, kv head, block of bq prompt tokens).  Its 8
-// waves own 16 "columns" each; a column is one (token, q head) pair of the
-// block, so all q heads of the kv head's GQA group share every K/V tile.
-// K/V tiles of 32 rows are staged in LDS (double-buffered, loaded by the
-// whole workgroup), both row-major:
-//   S^T[t][c] = K[t][:] . q_c      A = K rows (ds_read_b128), B = q_c hi/lo
-//   O^T[d][c] += V^T[d][t] P^T[t][c]  A = V^T (two ds_read_b64_tr_b16), B = P hi/lo
-// The two 16-row MFMA blocks of S^T read K rows in the order
-// pi_rb(i) = 8*(i/4) + 4*rb + i%4, which leaves lane group g holding rows
-// 8g..8g+7 of the tile: exactly the K slots of the PV product, so P never
-// leaves registers; the transposing LDS read turns row-major V into the
-// d-major A operand.  q and P are split into fp16 hi + lo parts (two MFMAs
-// each), keeping the products at ~fp32 precision.
+// Attention unit = (layer, kv head, block of bq prompt tokens).  A workgroup
+// of 4 waves runs one unit (or a pair, see prefill_attn_kernel); each wave
+// owns 32 "columns", a column being one (token, q head) pair of the block, so
+// all q heads of the kv head's GQA group share every K/V tile.  K/V tiles of
+// 32 rows are staged in LDS (double-buffered, loaded by the whole workgroup)
+// and both products run on v_mfma_f32_32x32x16_f16:
+//   S^T[t][c] = K[t][:] . q_c           A = K rows (ds_read_b128), B = q_c hi/lo
+//   O^T[d][c] += V^T[d][t] P^T[t][c]    A = V^T (two ds_read_b64_tr_b16), B = P hi/lo
+// K rows are stored in LDS with bits 2 and 3 of the row index swapped, which
+// leaves each lane holding the softmax weights of exactly the keys its PV
+// operand needs, so P never leaves registers.  q and P are split into fp16
+// hi + lo parts (two MFMAs each), keeping the products at ~fp32 precision
+// (one fp16 rounding of either would cost ~2e-4 and, for q, grow with the
+// scores' magnitude).
 //
-// Softmax bookkeeping per tile is kept short: the maximum is taken over raw
-// scores and the 1/sqrt(D)*log2(e) scale is folded into the exp2 argument;
-// the causal mask is applied only on tiles that cross a column's last row;
-// the running maximum is raised (and O, l rescaled) only when a new score
-// exceeds it by more than 2^kLazy, so weights stay below 2^kLazy.  The exp2
-// argument is the ROUNDED scaled score minus the running maximum (no fused
-// multiply-add): rounding is monotone, so no weight exceeds that of the row
-// that set the maximum test, whatever the magnitude of the scores (a fused
-// product could exceed the margin by its rounding error once the scores
-// pass 2^27 and overflow exp2).  Weights stay at most 2^16 (2^kLazy below
-// scores of 2^26).
+// Softmax bookkeeping per tile is kept short: the 1/sqrt(D)*log2(e) scale is
+// folded into q, the QK accumulators start at minus the running maximum (so
+// the MFMA yields score - max), the causal mask is applied only on tiles that
+// cross a column's last row, and the running maximum is raised (and O, l
+// rescaled) only when a new score exceeds it by more than kLazy, so weights
+// stay at most 2^kLazy.  Row sums add the weights as rounded for the MFMA
+// (hi + lo) with v_dot2_f32_f16 in fp32.
+#include <limits.h>
 #include <math.h>
 
 #include "attn_common.h"
@@ -48,8 +46,9 @@ using namespace plh;
 
 namespace {
 
-constexpr int kPW = 8;               // waves per attention workgroup
+constexpr int kPW = 4;               // waves per attention workgroup
 constexpr int kPThreads = 64 * kPW;
+constexpr int kPCols = 32 * kPW;     // (token, q head) columns per workgroup
 constexpr int kKT = 32;              // K/V rows per tile
 constexpr float kLazy = 8.0f;        // rescale threshold (log2 units)
 
@@ -149,42 +148,49 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(PrefillArgs a) {
   }
 }
 
+template <int D>
+struct PrefillLds {
+  static constexpr int KP = D + 8;          // LDS pitch of a K row (halves): KP/8 is odd,
+                                            // so the 8 consecutive rows a ds_read_b128
+                                            // serves at once start in distinct 16-byte
+                                            // bank groups
+  static constexpr int VP = D + 16;         // LDS pitch of a V row: the 4 rows of a
+                                            // transposing read land in disjoint 32-byte
+                                            // bank groups
+  static constexpr int KBUF = kKT * KP;     // one K tile buffer (halves)
+  static constexpr int VBUF = kKT * VP;     // one V tile buffer (halves)
+  static constexpr int VOFF = 2 * KBUF;     // V buffers follow the two K buffers
+  static constexpr int HALVES = 2 * KBUF + 2 * VBUF;
+};
+
+// Tiles of the q block qb of a launch: its last token's causal limit, in
+// 32-row tiles.
+__host__ __device__ inline int prefill_unit_tiles(const PrefillArgs& a, int qb) {
+  const int last = (qb + 1) * a.bq < a.n_tokens ? (qb + 1) * a.bq : a.n_tokens;
+  return (a.start_pos + last + kKT - 1) / kKT;
+}
+
+// One unit: the q block qb (tokens qb*bq ..) of one (layer, kv head) group,
+// over its K/V tiles [tb, min(te, its tile count)).  slot < 0: the whole
+// range, normalised output written to a.out; else one chunk of a split unit,
+// whose unnormalised O, running maximum and sum go to partial slot `slot`
+// (prefill_merge_kernel combines the chunks).
 template <int D, bool QKN>
-__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(D == 64 ? 6 : 4)))
-void prefill_attn_kernel(PrefillArgs a) {
-  constexpr int ND = D / 32;     // 32-wide d blocks of QK
-  constexpr int NO = D / 16;     // 16-wide d blocks of PV
-  constexpr int KP = D + 8;      // LDS pitch of a K row (halves)
-  constexpr int VP = D + 16;     // LDS pitch of a V row (halves): the 4 rows of a
-                                 // transposing read land in disjoint banks
+__device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16* smem, int group,
+                                                  int qb, int tb, int te, int slot) {
+  constexpr int NS = D / 16;        // 16-deep k-steps of QK
+  constexpr int NDB = D / 32;       // 32-row d blocks of O^T
+  constexpr int KP = PrefillLds<D>::KP, VP = PrefillLds<D>::VP;
+  constexpr int KBUF = PrefillLds<D>::KBUF, VBUF = PrefillLds<D>::VBUF;
+  constexpr int VOFF = PrefillLds<D>::VOFF;
   constexpr int KCH = kKT * D / 8;  // 16-byte chunks of a K (or V) tile
-  constexpr int KBUF = kKT * KP;  // one K tile buffer (halves)
-  constexpr int VBUF = kKT * VP;  // one V tile buffer (halves)
-  constexpr int VOFF = 2 * KBUF;  // V buffers follow the two K buffers
-  __shared__ __align__(16) _Float16 smem[2 * KBUF + 2 * VBUF];
+  constexpr int LPT = 2 * KCH / kPThreads;  // chunks per thread: the first LPT/2 are K
+  static_assert(KCH % kPThreads == 0, "tile chunks must split evenly over the workgroup");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int col = lane & 15, grp = lane >> 4;
-
-  // XCD-aware order: each XCD takes whole (layer, kv head) groups, so a
-  // group's K/V tiles, read by all its q blocks, stay in one L2.  When the
-  // slice's K/V fits in L2 its units run heaviest q block first across all
-  // its groups (longest-first keeps the end of the launch even); otherwise
-  // group by group, heaviest first within a group, so that each group's
-  // tiles are reused while still cached.
-  const int nq = a.n_qblk;
-  const int xcd = (int)(blockIdx.x & 7), l = (int)(blockIdx.x >> 3);
-  int group, qb;
-  if (a.qb_major) {
-    group = xcd * a.groups_per_xcd + l % a.groups_per_xcd;
-    qb = nq - 1 - l / a.groups_per_xcd;
-  } else {
-    group = xcd * a.groups_per_xcd + l / nq;
-    qb = nq - 1 - l % nq;
-  }
-  if (group >= a.n_launch_layers * a.n_kv_heads) return;
+  const int col = lane & 31, half = lane >> 5;
   const int kvh = group % a.n_kv_heads;
   const int li = group / a.n_kv_heads;
   const int layer = a.layer0 + li;
@@ -194,132 +200,141 @@ void prefill_attn_kernel(PrefillArgs a) {
   const int i0 = qb * a.bq;
   const int last_tok = min(i0 + a.bq, a.n_tokens) - 1;
   const int n_rows = a.start_pos + last_tok + 1;          // rows [0, n_rows) are needed
-  const int n_tiles = (n_rows + kKT - 1) / kKT;
+  const int n_tiles = min((n_rows + kKT - 1) / kKT, te);
 
   // this lane's column: token i0+tok, q head kvh*G+hh
-  const int c = wave * 16 + col;
+  const int c = wave * 32 + col;
   const int tok = c / G, hh = c - (c / G) * G;
   const bool cvalid = tok < a.bq && i0 + tok < a.n_tokens;
   const int tok_c = cvalid ? i0 + tok : last_tok;          // clamped for addressing
   const int p_col = a.start_pos + tok_c;                  // causal limit of the column
-  // smallest causal limit among the wave's columns (wave-uniform)
+  // smallest and largest causal limits among the wave's columns (wave-uniform)
   const int p_min = __builtin_amdgcn_readfirstlane(
-      a.start_pos + min(i0 + (wave * 16) / G, last_tok));
+      a.start_pos + min(i0 + (wave * 32) / G, last_tok));
+  const int p_max = __builtin_amdgcn_readfirstlane(
+      a.start_pos + min(i0 + (wave * 32 + 31) / G, last_tok));
 
   // ---- cooperative tile loads (issued early; stored to LDS after compute) --
+  // Chunk u of a thread is tile chunk tid + u*kPThreads: row r, 16-byte piece
+  // q8.  K row r goes to LDS row perm(r) (bits 2 and 3 of r swapped), so that
+  // lane m of the QK product reads LDS row m and the MFMA's output rows come
+  // out in the order the PV product takes its k operands (see below); V rows
+  // stay in key order.
   const size_t row0 = (size_t)layer * a.max_seq_len;
   const uint16_t* kbase = a.kc + row0 * kv_dim + (size_t)kvh * D;
   const uint16_t* vbase = a.vc + row0 * kv_dim + (size_t)kvh * D;
-  constexpr int LPT = (2 * KCH + kPThreads - 1) / kPThreads;  // chunks per thread
   half8_t ld[LPT];
   auto issue_loads = [&](int t0) {
 #pragma unroll
     for (int u = 0; u < LPT; ++u) {
-      const int ch = tid + u * kPThreads;
-      const int cc = ch % KCH;                 // chunk within its tile
+      const int cc = (tid + u * kPThreads) % KCH;
       const int r = cc / (D / 8), q8 = cc % (D / 8);
       const int row = min(t0 + r, n_rows - 1);
-      const uint16_t* src = (ch < KCH ? kbase : vbase) + (size_t)row * kv_dim + 8 * q8;
+      const uint16_t* src = (u < LPT / 2 ? kbase : vbase) + (size_t)row * kv_dim + 8 * q8;
       ld[u] = *(const half8_t*)src;
     }
   };
-  // LDS destination of each loaded chunk in buffer 0, and the step to buffer 1
-  int st_off[LPT], st_step[LPT];
+  int st_off[LPT];
 #pragma unroll
   for (int u = 0; u < LPT; ++u) {
-    const int ch = tid + u * kPThreads;
-    const int cc = ch % KCH;
+    const int cc = (tid + u * kPThreads) % KCH;
     const int r = cc / (D / 8), q8 = cc % (D / 8);
-    st_off[u] = ch < KCH ? r * KP + 8 * q8 : VOFF + r * VP + 8 * q8;
-    st_step[u] = ch < KCH ? KBUF : VBUF;
+    const int pr = (r & ~12) | ((r & 4) << 1) | ((r & 8) >> 1);
+    st_off[u] = u < LPT / 2 ? pr * KP + 8 * q8 : VOFF + r * VP + 8 * q8;
   }
   auto store_lds = [&](int b) {
 #pragma unroll
     for (int u = 0; u < LPT; ++u)
-      if (tid + u * kPThreads < 2 * KCH)
-        *(half8_t*)&smem[st_off[u] + b * st_step[u]] = ld[u];
+      *(half8_t*)&smem[st_off[u] + b * (u < LPT / 2 ? KBUF : VBUF)] = ld[u];
   };
-  issue_loads(0);
+  issue_loads(tb * kKT);
 
-  // ---- q operands of this lane's column: rotated, split into fp16 hi + lo --
+  // ---- q operand of this lane's column: element 16*s + 8*half + e of the
+  // rotated head row, split into fp16 hi + lo, in qh[s][e] and ql[s][e].
   // Columns past the prompt (cvalid false) read the last token's row and are
   // never stored; each column's softmax is independent, so they need no mask.
-  half8_t qhi[ND], qlo[ND];
+  half8_t qh[NS], ql[NS];
   float qup, qdown;  // 2^e and 2^-e of the column's range scale
   {
     const float* qrow = a.q + ((size_t)li * a.n_tokens + tok_c) * q_dim +
                         (size_t)(kvh * G + (cvalid ? hh : 0)) * D;
     const float* cr = a.cos_t + (size_t)p_col * (D / 2);
     const float* sr = a.sin_t + (size_t)p_col * (D / 2);
-    float qf[ND][8];
+    float qf[NS][8];
 #pragma unroll
-    for (int db = 0; db < ND; ++db) {
-      const float4 x0 = *(const float4*)(qrow + 32 * db + 8 * grp);
-      const float4 x1 = *(const float4*)(qrow + 32 * db + 8 * grp + 4);
-      qf[db][0] = x0.x, qf[db][1] = x0.y, qf[db][2] = x0.z, qf[db][3] = x0.w;
-      qf[db][4] = x1.x, qf[db][5] = x1.y, qf[db][6] = x1.z, qf[db][7] = x1.w;
+    for (int s = 0; s < NS; ++s) {
+      const float4 x0 = *(const float4*)(qrow + 16 * s + 8 * half);
+      const float4 x1 = *(const float4*)(qrow + 16 * s + 8 * half + 4);
+      qf[s][0] = x0.x, qf[s][1] = x0.y, qf[s][2] = x0.z, qf[s][3] = x0.w;
+      qf[s][4] = x1.x, qf[s][5] = x1.y, qf[s][6] = x1.z, qf[s][7] = x1.w;
     }
     if (QKN) {
       // QK-norm of the column's q head row before the rotation
       const float* wq = a.qn + (size_t)li * D;
-      float w[ND][8];
+      float w[NS][8];
 #pragma unroll
-      for (int db = 0; db < ND; ++db) {
-        const float4 w0 = *(const float4*)(wq + 32 * db + 8 * grp);
-        const float4 w1 = *(const float4*)(wq + 32 * db + 8 * grp + 4);
-        w[db][0] = w0.x, w[db][1] = w0.y, w[db][2] = w0.z, w[db][3] = w0.w;
-        w[db][4] = w1.x, w[db][5] = w1.y, w[db][6] = w1.z, w[db][7] = w1.w;
+      for (int s = 0; s < NS; ++s) {
+        const float4 w0 = *(const float4*)(wq + 16 * s + 8 * half);
+        const float4 w1 = *(const float4*)(wq + 16 * s + 8 * half + 4);
+        w[s][0] = w0.x, w[s][1] = w0.y, w[s][2] = w0.z, w[s][3] = w0.w;
+        w[s][4] = w1.x, w[s][5] = w1.y, w[s][6] = w1.z, w[s][7] = w1.w;
       }
-      const float sc = rms_scale_cols<D>(qf, col, a.norm_eps);
+      const float sc = rms_scale_halves<D>(qf, a.norm_eps);
 #pragma unroll
-      for (int db = 0; db < ND; ++db)
+      for (int s = 0; s < NS; ++s)
 #pragma unroll
         for (int j = 0; j < 8; ++j) {
-          const float t = qf[db][j] * sc;
-          qf[db][j] = t * w[db][j];
+          const float t = qf[s][j] * sc;
+          qf[s][j] = t * w[s][j];
         }
     }
     if (a.rope_type == PLH_ROPE_QWEN) {
+      // pairs (i, i + D/2): elements of k-steps s and s + NS/2
 #pragma unroll
-      for (int db = 0; db < ND / 2; ++db)
+      for (int s = 0; s < NS / 2; ++s) {
+        const float4 c0 = *(const float4*)(cr + 16 * s + 8 * half);
+        const float4 c1 = *(const float4*)(cr + 16 * s + 8 * half + 4);
+        const float4 s0 = *(const float4*)(sr + 16 * s + 8 * half);
+        const float4 s1 = *(const float4*)(sr + 16 * s + 8 * half + 4);
+        const float cc[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+        const float ss[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const int i = 32 * db + 8 * grp + j;
-          rope_rotate_fused(qf[db][j], qf[db + ND / 2][j], cr[i], sr[i]);
-        }
+        for (int j = 0; j < 8; ++j) rope_rotate_fused(qf[s][j], qf[s + NS / 2][j], cc[j], ss[j]);
+      }
     } else {
+      // pairs (2i, 2i+1), i = 8*s + 4*half + j/2
 #pragma unroll
-      for (int db = 0; db < ND; ++db) {
-        const float4 c4 = *(const float4*)(cr + 16 * db + 4 * grp);
-        const float4 s4 = *(const float4*)(sr + 16 * db + 4 * grp);
-        rope_rotate_fused(qf[db][0], qf[db][1], c4.x, s4.x);
-        rope_rotate_fused(qf[db][2], qf[db][3], c4.y, s4.y);
-        rope_rotate_fused(qf[db][4], qf[db][5], c4.z, s4.z);
-        rope_rotate_fused(qf[db][6], qf[db][7], c4.w, s4.w);
+      for (int s = 0; s < NS; ++s) {
+        const float4 c4 = *(const float4*)(cr + 8 * s + 4 * half);
+        const float4 s4 = *(const float4*)(sr + 8 * s + 4 * half);
+        rope_rotate_fused(qf[s][0], qf[s][1], c4.x, s4.x);
+        rope_rotate_fused(qf[s][2], qf[s][3], c4.y, s4.y);
+        rope_rotate_fused(qf[s][4], qf[s][5], c4.z, s4.z);
+        rope_rotate_fused(qf[s][6], qf[s][7], c4.w, s4.w);
       }
     }
     // the softmax scale log2(e)/sqrt(D) goes into q, so that the MFMA
-    // produces scores in log2 units; then the column's range for the fp16
-    // split (a power-of-two scale, undone on the scores: 1 unless some
-    // |q| * scale >= 2^15)
+    // produces scores in log2 units; then the column's range for fp16 (a
+    // power-of-two scale, undone on the scores: 1 unless some |q| * scale >=
+    // 2^15)
     float amax = 0.f;
 #pragma unroll
-    for (int db = 0; db < ND; ++db)
+    for (int s = 0; s < NS; ++s)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        qf[db][j] *= a.score_scale;
-        amax = vmax(amax, fabsf(qf[db][j]));
+        qf[s][j] *= a.score_scale;
+        amax = vmax(amax, fabsf(qf[s][j]));
       }
-    amax = max_xor32(max_xor16(amax));
+    amax = max_xor32(amax);
     qdown = q_range_scale(amax, &qup);
 #pragma unroll
-    for (int db = 0; db < ND; ++db)
+    for (int s = 0; s < NS; ++s)
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
         half2_t hi, lo;
-        split_pair_rtz(qf[db][j] * qdown, qf[db][j + 1] * qdown, hi, lo);
-        qhi[db][j] = hi[0], qhi[db][j + 1] = hi[1];
-        qlo[db][j] = lo[0], qlo[db][j + 1] = lo[1];
+        split_pair_rtz(qf[s][j] * qdown, qf[s][j + 1] * qdown, hi, lo);
+        qh[s][j] = hi[0], qh[s][j + 1] = hi[1];
+        ql[s][j] = lo[0], ql[s][j + 1] = lo[1];
       }
   }
 
@@ -330,22 +345,35 @@ void prefill_attn_kernel(PrefillArgs a) {
   // starts from -ms (times the column's 2^-e), so it yields score - ms
   // directly; the maximum test and the exp2 then read the same values, which
   // keeps every weight bounded (<= 2^kLazy) whatever the scores' magnitude.
-  // The first tile sets ms to its own maximum (row 0 is never masked).
+  // A column is "fresh" until a tile holds one of its unmasked keys; that
+  // tile sets ms to its maximum (a whole unit's first tile does, for every
+  // column: row 0 is never masked; a later chunk's first tiles may be masked
+  // for some columns).
+  //
+  // Layouts (v_mfma_f32_32x32x16_f16, lane = 32*half + col):
+  //   S^T - ms  [32 keys x 32 columns] = K . q^T: A = K rows (LDS row col,
+  //             d 16*s + 8*half ..), B = qh[s]; the lane gets column col and
+  //             output rows 8*(v/4) + 4*half + v%4, v = 0..15, which through
+  //             the K row permutation are keys 16*(v/8) + 8*half + v%8;
+  //   O^T [32 d x 32 columns] += V^T . P^T, per d block and per 16 keys j:
+  //             A = V^T (d = col, keys 16*j + 8*half + 0..7, two transposing
+  //             LDS reads), B = the lane's own weights v = 8*j .. 8*j+7.
+  // So P never leaves registers.  Row sums: each lane adds its 16 weights
+  // (as rounded for the MFMA) with v_dot2_f32_f16 in fp32; the two halves of
+  // a column are added at the end.
   float ms = 0.f;
-  float4_t negm = float4_t{0.f, 0.f, 0.f, 0.f};  // -ms * 2^-e, the QK accumulator start
-  float4_t lsum = float4_t{0.f, 0.f, 0.f, 0.f};  // running sum (all 4 entries equal)
+  bool fresh = true;                // no unmasked key seen yet (ms, lsum, o all 0)
+  f32x16_t negm = {};               // -ms * 2^-e, the QK accumulator start
+  float lsum = 0.f;                 // this lane's half of the running sum
   const bool scaled_cols = __ballot(qup != 1.f) != 0;  // wave-uniform: rare
-  half8_t ones;
+  f32x16_t o[NDB];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) ones[j] = (_Float16)1.0f;
-  float4_t o[NO];
-#pragma unroll
-  for (int ob = 0; ob < NO; ++ob) o[ob] = float4_t{0.f, 0.f, 0.f, 0.f};
-  // transposing-read address of this lane: row 8*grp + col/4, chunk col%4
-  const int vofs = (8 * grp + (col >> 2)) * VP + 4 * (col & 3);
-  int kofs[2];
-#pragma unroll
-  for (int rb = 0; rb < 2; ++rb) kofs[rb] = (8 * (col >> 2) + 4 * rb + (col & 3)) * KP + 8 * grp;
+  for (int db = 0; db < NDB; ++db) o[db] = f32x16_t{};
+  const int kofs = col * KP + 8 * half;
+  // transposing-read address: 16-lane group g reads keys 8*half + (lane%16)/4
+  // (+4 for the second read), d 16*(g%2) + 4*(lane%4) .. of the d block
+  const int vofs = (8 * half + ((lane & 15) >> 2)) * VP + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const half2_t one2 = {(_Float16)1.0f, (_Float16)1.0f};
 
   // one tile in buffer b (a constant at each call site, so the LDS offsets
   // fold into the instructions)
@@ -353,101 +381,240 @@ void prefill_attn_kernel(PrefillArgs a) {
     const int t0 = it * kKT;
     const bool more = it + 1 < n_tiles;
     if (more) issue_loads(t0 + kKT);
-
-    // S^T - ms for this wave's 16 columns
-    float4_t s[2];
+    if (t0 <= p_max) {  // else every column of the wave is masked on this tile
+      f32x16_t s = negm;
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb) {
-      s[rb] = negm;
-#pragma unroll
-      for (int db = 0; db < ND; ++db) {
-        const half8_t kk = *(const half8_t*)&smem[b * KBUF + kofs[rb] + 32 * db];
-        s[rb] = mfma16x16x32(kk, qhi[db], s[rb]);
-        s[rb] = mfma16x16x32(kk, qlo[db], s[rb]);
+      for (int st = 0; st < NS; ++st) {
+        const half8_t kk = *(const half8_t*)&smem[b * KBUF + kofs + 16 * st];
+        s = mfma32x32x16(kk, qh[st], s);
+        s = mfma32x32x16(kk, ql[st], s);
       }
-    }
-    // lane holds rows t0 + 8*grp + j, j = 4*rb + r
-    float t[8];
+      float t[16];
 #pragma unroll
-    for (int rb = 0; rb < 2; ++rb)
+      for (int v = 0; v < 16; ++v) t[v] = s[v];
+      if (scaled_cols) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) t[4 * rb + r] = s[rb][r];
-    if (scaled_cols) {
+        for (int v = 0; v < 16; ++v) t[v] *= qup;  // exact: a power of two
+      }
+      if (t0 + kKT - 1 > p_min) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) t[j] *= qup;  // exact: a power of two
-    }
-    if (t0 + kKT - 1 > p_min) {
+        for (int v = 0; v < 16; ++v)
+          if (t0 + 16 * (v / 8) + 8 * half + v % 8 > p_col) t[v] = -INFINITY;
+      }
+      float tmax = t[0];
 #pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (t0 + 8 * grp + j > p_col) t[j] = -INFINITY;
-    }
-    float tmax = t[0];
-#pragma unroll
-    for (int j = 1; j < 8; ++j) tmax = vmax(tmax, t[j]);
-    tmax = max_xor32(max_xor16(tmax));
-    if (it == 0 || __ballot(tmax > kLazy)) {
-      // first tile: ms = its maximum (nothing accumulated yet); later, raise
-      // ms by the excess (columns at or below it keep theirs)
-      const float d = it == 0 ? tmax : fmaxf(tmax, 0.f);
-      if (it != 0) {
-        const float alpha = fast_exp2(-d);
+      for (int v = 1; v < 16; ++v) tmax = vmax(tmax, t[v]);
+      tmax = max_xor32(tmax);
+      // fresh columns with an unmasked key take its maximum as ms (nothing
+      // accumulated yet); others raise ms by the excess beyond kLazy
+      const bool upd = fresh ? tmax != -INFINITY : tmax > kLazy;
+      if (__ballot(upd)) {
+        const float d = upd ? tmax : 0.f;
+        const float alpha = fresh ? 1.f : fast_exp2(-d);
         lsum *= alpha;
 #pragma unroll
-        for (int ob = 0; ob < NO; ++ob) o[ob] *= alpha;
+        for (int db = 0; db < NDB; ++db) o[db] *= alpha;
+        fresh = fresh && !upd;
+        ms += d;
+        const float nm = -ms * qdown;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) negm[v] = nm;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) t[v] -= d;
       }
-      ms += d;
-      const float nm = -ms * qdown;
-      negm = float4_t{nm, nm, nm, nm};
+      half8_t ph[2], pl[2];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) t[j] -= d;
-    }
-    half8_t ph, pl;
+      for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int j = 0; j < 8; j += 2) {
-      half2_t hi, lo;
-      split_pair_rtz(fast_exp2(t[j]), fast_exp2(t[j + 1]), hi, lo);
-      ph[j] = hi[0], ph[j + 1] = hi[1];
-      pl[j] = lo[0], pl[j + 1] = lo[1];
-    }
-    // row sums on the matrix core: every row of ones . P^T is the column sum
-    lsum = mfma16x16x32(ones, ph, lsum);
-    lsum = mfma16x16x32(ones, pl, lsum);
+        for (int e = 0; e < 8; e += 2) {
+          half2_t hi, lo;
+          split_pair_rtz(fast_exp2(t[8 * j + e]), fast_exp2(t[8 * j + e + 1]), hi, lo);
+          ph[j][e] = hi[0], ph[j][e + 1] = hi[1];
+          pl[j][e] = lo[0], pl[j][e + 1] = lo[1];
+          lsum = __builtin_amdgcn_fdot2(hi, one2, lsum, false);
+          lsum = __builtin_amdgcn_fdot2(lo, one2, lsum, false);
+        }
 #pragma unroll
-    for (int ob = 0; ob < NO; ++ob) {
-      const _Float16* vp = &smem[VOFF + b * VBUF + vofs + 16 * ob];
-      const half4_t v0 = lds_read_tr4(vp);
-      const half4_t v1 = lds_read_tr4(vp + 4 * VP);
-      const half8_t va = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
-      o[ob] = mfma16x16x32(va, ph, o[ob]);
-      o[ob] = mfma16x16x32(va, pl, o[ob]);
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const _Float16* vp = &smem[VOFF + b * VBUF + vofs + 16 * j * VP + 32 * db];
+          const half4_t v0 = lds_read_tr4(vp);
+          const half4_t v1 = lds_read_tr4(vp + 4 * VP);
+          const half8_t va = __builtin_shufflevector(v0, v1, 0, 1, 2, 3, 4, 5, 6, 7);
+          o[db] = mfma32x32x16(va, ph[j], o[db]);
+          o[db] = mfma32x32x16(va, pl[j], o[db]);
+        }
     }
-
     if (more) store_lds(b ^ 1);
     __syncthreads();
   };
-  for (int it = 0; it < n_tiles; it += 2) {
+  for (int it = tb; it < n_tiles; it += 2) {
     tile(0, it);
     if (it + 1 < n_tiles) tile(1, it + 1);
   }
 
-  // ---- normalise and write: lane holds d = 16*ob + 4*grp + r of its column ---
+  // ---- normalise and write: lane holds d = 32*db + 8*(v/4) + 4*half + v%4 --
+  lsum = add_xor32(lsum);
+  if (slot >= 0) {
+    // a chunk's partial: O, ms (-inf for a column with no unmasked key in the
+    // chunk) and the sum, per column of the unit
+    if (cvalid) {
+      const size_t pc = (size_t)slot * kPCols + c;
+      float* po = a.part_o + pc * D;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          *(float4*)(po + 32 * db + 8 * r4 + 4 * half) =
+              make_float4(o[db][4 * r4], o[db][4 * r4 + 1], o[db][4 * r4 + 2], o[db][4 * r4 + 3]);
+      if (half == 0) {
+        a.part_m[pc] = fresh ? -INFINITY : ms;
+        a.part_l[pc] = lsum;
+      }
+    }
+    return;
+  }
   if (cvalid) {
-    const float inv = 1.0f / lsum[0];
+    const float inv = 1.0f / lsum;
     float* orow = a.out + ((size_t)li * a.n_tokens + i0 + tok) * a.out_stride +
                   (size_t)(kvh * G + hh) * D;
 #pragma unroll
-    for (int ob = 0; ob < NO; ++ob) {
-      float4 w;
-      w.x = o[ob][0] * inv;
-      w.y = o[ob][1] * inv;
-      w.z = o[ob][2] * inv;
-      w.w = o[ob][3] * inv;
-      *(float4*)(orow + 16 * ob + 4 * grp) = w;
-    }
+    for (int db = 0; db < NDB; ++db)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        float4 w;
+        w.x = o[db][4 * r4 + 0] * inv;
+        w.y = o[db][4 * r4 + 1] * inv;
+        w.z = o[db][4 * r4 + 2] * inv;
+        w.w = o[db][4 * r4 + 3] * inv;
+        *(float4*)(orow + 32 * db + 8 * r4 + 4 * half) = w;
+      }
   }
 }
 
+// Workgroup = one q block, or (a.paired) a pair of q blocks of one (layer, kv
+// head) group: the heavy block nq-1-p, then its mirror p, whose K/V tiles are
+// a prefix of the heavy block's and still in L2; pairs give every workgroup
+// about the same number of tiles.  Single blocks run heaviest first
+// (longest-first keeps the end of the launch even when there are several
+// workgroups per slot), or (a.split_tiles) as chunks of split_tiles tiles.
+// XCD-aware order with 32 groups or more: each XCD takes whole groups (block
+// b runs on XCD b % 8), so a group's K/V tiles stay in one L2; a slice walks
+// its groups one by one.  Fewer groups run in one linear order over all XCDs.
+template <class T>
+__device__ __forceinline__ void sgpr_ready(T x) {
+  asm volatile("" ::"s"(x));
+}
+
+template <int D, bool QKN>
+__global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) {
+  __shared__ __align__(16) _Float16 smem[PrefillLds<D>::HALVES];
+  // Every launch argument the prologue needs, in scalar registers before
+  // anything else: one batch of kernel-argument loads (one round trip)
+  // instead of batches issued as the code first needs them.
+  sgpr_ready(a.q), sgpr_ready(a.kc), sgpr_ready(a.vc), sgpr_ready(a.cos_t);
+  sgpr_ready(a.sin_t), sgpr_ready(a.layer0), sgpr_ready(a.n_launch_layers);
+  sgpr_ready(a.n_heads), sgpr_ready(a.n_kv_heads), sgpr_ready(a.max_seq_len);
+  sgpr_ready(a.rope_type), sgpr_ready(a.start_pos), sgpr_ready(a.n_tokens), sgpr_ready(a.bq);
+  sgpr_ready(a.n_qblk), sgpr_ready(a.xcd_slices), sgpr_ready(a.groups_per_xcd);
+  sgpr_ready(a.qb_major), sgpr_ready(a.paired), sgpr_ready(a.split_tiles);
+  sgpr_ready(a.chunks_per_group), sgpr_ready(a.score_scale);
+  if (QKN) sgpr_ready(a.qn);
+  const int nq = a.n_qblk;
+  // XCD slices (xcd_slices = 8), or one linear order when there are too few
+  // groups to give every XCD its own (xcd_slices = 1)
+  const int xcd = (int)(blockIdx.x % a.xcd_slices), l = (int)(blockIdx.x / a.xcd_slices);
+  if (a.split_tiles > 0) {
+    // chunks of split_tiles tiles: a group's chunks, heaviest q block first,
+    // are consecutive workgroups of its XCD slice and consecutive slots
+    const int cpg = a.chunks_per_group;
+    const int group = xcd * a.groups_per_xcd + l / cpg;
+    if (group >= a.n_launch_layers * a.n_kv_heads) return;
+    const int r0 = l % cpg;
+    int r = r0, qb = nq - 1;
+    for (;; --qb) {
+      const int nc = (prefill_unit_tiles(a, qb) + a.split_tiles - 1) / a.split_tiles;
+      if (r < nc || qb == 0) {
+        const int slot = nc > 1 ? group * cpg + r0 : -1;
+        prefill_attn_unit<D, QKN>(a, smem, group, qb, r * a.split_tiles, (r + 1) * a.split_tiles,
+                                  slot);
+        return;
+      }
+      r -= nc;
+    }
+  }
+  if (!a.paired) {
+    int group, qb;
+    if (a.qb_major) {
+      group = xcd * a.groups_per_xcd + l % a.groups_per_xcd;
+      qb = nq - 1 - l / a.groups_per_xcd;
+    } else {
+      group = xcd * a.groups_per_xcd + l / nq;
+      qb = nq - 1 - l % nq;
+    }
+    if (group >= a.n_launch_layers * a.n_kv_heads) return;
+    prefill_attn_unit<D, QKN>(a, smem, group, qb, 0, INT_MAX, -1);
+    return;
+  }
+  const int np = (nq + 1) / 2;
+  const int group = xcd * a.groups_per_xcd + l / np;
+  const int p = l % np;
+  if (group >= a.n_launch_layers * a.n_kv_heads) return;
+  prefill_attn_unit<D, QKN>(a, smem, group, nq - 1 - p, 0, INT_MAX, -1);
+  // the unit's last barrier follows every wave's last LDS read: the next
+  // unit may refill the buffers
+  if (p != nq - 1 - p) prefill_attn_unit<D, QKN>(a, smem, group, p, 0, INT_MAX, -1);
+}
+
+// Combines the chunks of split units, one thread per (unit, column, 4 output
+// elements); units with a single chunk wrote their output directly.  Per
+// column: M = max of the chunks' maxima, out = sum 2^(m-M) O / sum 2^(m-M) l
+// (chunk 0 holds row 0, which every column sees, so M is finite).  The
+// chunks' loads are independent, so each thread waits about twice.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
+  constexpr int Q = D / 4;
+  const int nq = a.n_qblk;
+  const long item = (long)blockIdx.x * 256 + threadIdx.x;
+  const int unit = (int)(item / (kPCols * Q));
+  if (unit >= a.n_launch_layers * a.n_kv_heads * nq) return;
+  const int group = unit / nq, qb = unit % nq;
+  const int c = (int)(item / Q % kPCols), q4 = (int)(item % Q);
+  const int G = a.n_heads / a.n_kv_heads;
+  const int tok = c / G, hh = c % G;
+  const int i0 = qb * a.bq;
+  const int T = a.split_tiles;
+  const int nc = (prefill_unit_tiles(a, qb) + T - 1) / T;
+  if (nc <= 1 || tok >= a.bq || i0 + tok >= a.n_tokens) return;
+  int first = 0;  // the unit's first slot within its group's list (heaviest first)
+  for (int q = nq - 1; q > qb; --q) first += (prefill_unit_tiles(a, q) + T - 1) / T;
+  const size_t pc0 = ((size_t)group * a.chunks_per_group + first) * kPCols + c;
+  float M = -INFINITY;
+  for (int k = 0; k < nc; ++k) M = fmaxf(M, a.part_m[pc0 + (size_t)k * kPCols]);
+  float L = 0.f;
+  float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int k = 0; k < nc; ++k) {
+    const size_t pc = pc0 + (size_t)k * kPCols;
+    const float w = fast_exp2(a.part_m[pc] - M);
+    const float4 po = *(const float4*)(a.part_o + pc * D + 4 * q4);
+    L += w * a.part_l[pc];
+    O.x += w * po.x, O.y += w * po.y, O.z += w * po.z, O.w += w * po.w;
+  }
+  const float inv = 1.0f / L;
+  const int kvh = group % a.n_kv_heads, li = group / a.n_kv_heads;
+  float* orow = a.out + ((size_t)li * a.n_tokens + i0 + tok) * a.out_stride +
+                (size_t)(kvh * G + hh) * D;
+  *(float4*)(orow + 4 * q4) = make_float4(O.x * inv, O.y * inv, O.z * inv, O.w * inv);
+}
+
 }  // namespace
+
+namespace plh {
+// plh_set_tuning key 5: prefill chunking of small launches (0 automatic, -1
+// never, or a fixed chunk of 2, 4, 8 or 16 tiles)
+int g_prefill_split = 0;
+}  // namespace plh
 
 static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head_dim,
                              int max_seq_len, int rope_type, int layer0, int n_launch_layers,
@@ -471,8 +638,8 @@ static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head
     return -1;
   }
   const int G = n_heads / n_kv_heads;
-  if (G > 16 * kPW) {
-    set_error("plh_attn_prefill: GQA group %d larger than %d", G, 16 * kPW);
+  if (G > kPCols) {
+    set_error("plh_attn_prefill: GQA group %d larger than %d", G, kPCols);
     return -1;
   }
   if (rope_type != PLH_ROPE_LLAMA && rope_type != PLH_ROPE_QWEN) {
@@ -524,12 +691,49 @@ static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head
   a.start_pos = start_pos;
   a.n_tokens = n_tokens;
   a.out_stride = out_stride;
-  a.bq = (16 * kPW) / G;
+  a.bq = kPCols / G;
   a.n_qblk = (n_tokens + a.bq - 1) / a.bq;
   const int n_groups = n_launch_layers * n_kv_heads;
   a.n_units = n_groups * a.n_qblk;
-  a.groups_per_xcd = (n_groups + 7) / 8;
-  a.per_xcd = a.groups_per_xcd * a.n_qblk;
+  // XCD slices need enough groups to keep all eight XCDs busy
+  a.xcd_slices = n_groups >= 32 ? 8 : 1;
+  a.groups_per_xcd = (n_groups + a.xcd_slices - 1) / a.xcd_slices;
+  // pairs of q blocks when the launch holds many rounds of workgroups (long
+  // prompts, wide models); single blocks, heaviest first, otherwise
+  const long slots = 3L * (c.num_cus > 0 ? c.num_cus : 256);
+  a.paired = a.n_qblk >= 4 && a.n_units >= 8 * slots ? 1 : 0;
+  a.per_xcd = a.groups_per_xcd * (a.paired ? (a.n_qblk + 1) / 2 : a.n_qblk);
+  // Launches with few q blocks (one layer of a prompt chunk, late in the
+  // prompt: at most a quarter as many blocks as CUs) split blocks of more
+  // than 8 tiles into chunks of 8 tiles, merged afterwards: the heaviest
+  // block is the critical path.  Measured on one-layer launches of 128
+  // tokens at start 1024: TinyLlama 32 -> 23 us, Llama-2 51 -> 32 us; launches
+  // with more blocks lose to the extra prologues and the merge.
+  a.split_tiles = 0;
+  a.chunks_per_group = 0;
+  if (!a.paired && g_prefill_split >= 0) {
+    const int max_tiles = prefill_unit_tiles(a, a.n_qblk - 1);
+    const int cus = c.num_cus > 0 ? c.num_cus : 256;
+    int pick = 0, pick_cpg = 0;
+    const int T = g_prefill_split > 0 ? g_prefill_split : 8;
+    if (max_tiles > T && (g_prefill_split > 0 || (long)a.n_units * 4 <= cus)) {
+      int cpg = 0;
+      for (int qb = 0; qb < a.n_qblk; ++qb) cpg += (prefill_unit_tiles(a, qb) + T - 1) / T;
+      pick = T, pick_cpg = cpg;
+    }
+    if (pick) {
+      const size_t n_slots = (size_t)n_groups * pick_cpg;
+      const size_t po = n_slots * kPCols * head_dim * sizeof(float);
+      const size_t pm = n_slots * kPCols * sizeof(float);
+      if (ensure_workspace(po + 2 * pm)) return -1;
+      a.split_tiles = pick;
+      a.chunks_per_group = pick_cpg;
+      a.part_o = (float*)c.ws;
+      a.part_m = (float*)((char*)c.ws + po);
+      a.part_l = (float*)((char*)c.ws + po + pm);
+      a.per_xcd = a.groups_per_xcd * pick_cpg;
+    }
+  }
   // K/V bytes one XCD slice reads: by q-block order when they fit in a
   // comfortable share of the XCD's 4 MB L2
   const double slice_kv = (double)a.groups_per_xcd * (start_pos + n_tokens) * head_dim * 2 * 2;
@@ -542,26 +746,41 @@ static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head
   const long groups = (long)n_launch_layers * n_tokens * n_kv_heads * (head_dim / 8);
   long ab = (groups + 255) / 256;
   if (ab > 16384) ab = 16384;
-  const unsigned grid = (unsigned)(8 * a.per_xcd);
+  const unsigned grid = (unsigned)(a.xcd_slices * a.per_xcd);
   const dim3 ag((unsigned)ab), ab256(256), pg(grid), pb(kPThreads);
-  if (head_dim == 64 && !qkn) {
-    hipLaunchKernelGGL((prefill_append_kernel<64, false>), ag, ab256, 0, c.stream, a);
-    if (check_hip(hipGetLastError(), "prefill_append_kernel")) return -1;
-    hipLaunchKernelGGL((prefill_attn_kernel<64, false>), pg, pb, 0, c.stream, a);
-  } else if (head_dim == 64) {
-    hipLaunchKernelGGL((prefill_append_kernel<64, true>), ag, ab256, 0, c.stream, a);
-    if (check_hip(hipGetLastError(), "prefill_append_kernel")) return -1;
-    hipLaunchKernelGGL((prefill_attn_kernel<64, true>), pg, pb, 0, c.stream, a);
-  } else if (!qkn) {
-    hipLaunchKernelGGL((prefill_append_kernel<128, false>), ag, ab256, 0, c.stream, a);
-    if (check_hip(hipGetLastError(), "prefill_append_kernel")) return -1;
-    hipLaunchKernelGGL((prefill_attn_kernel<128, false>), pg, pb, 0, c.stream, a);
+  if (head_dim == 64) {
+    if (qkn)
+      hipLaunchKernelGGL((prefill_append_kernel<64, true>), ag, ab256, 0, c.stream, a);
+    else
+      hipLaunchKernelGGL((prefill_append_kernel<64, false>), ag, ab256, 0, c.stream, a);
   } else {
-    hipLaunchKernelGGL((prefill_append_kernel<128, true>), ag, ab256, 0, c.stream, a);
-    if (check_hip(hipGetLastError(), "prefill_append_kernel")) return -1;
-    hipLaunchKernelGGL((prefill_attn_kernel<128, true>), pg, pb, 0, c.stream, a);
+    if (qkn)
+      hipLaunchKernelGGL((prefill_append_kernel<128, true>), ag, ab256, 0, c.stream, a);
+    else
+      hipLaunchKernelGGL((prefill_append_kernel<128, false>), ag, ab256, 0, c.stream, a);
   }
-  return check_hip(hipGetLastError(), "prefill_attn_kernel");
+  if (check_hip(hipGetLastError(), "prefill_append_kernel")) return -1;
+  if (head_dim == 64) {
+    if (qkn)
+      hipLaunchKernelGGL((prefill_attn_kernel<64, true>), pg, pb, 0, c.stream, a);
+    else
+      hipLaunchKernelGGL((prefill_attn_kernel<64, false>), pg, pb, 0, c.stream, a);
+  } else {
+    if (qkn)
+      hipLaunchKernelGGL((prefill_attn_kernel<128, true>), pg, pb, 0, c.stream, a);
+    else
+      hipLaunchKernelGGL((prefill_attn_kernel<128, false>), pg, pb, 0, c.stream, a);
+  }
+  if (check_hip(hipGetLastError(), "prefill_attn_kernel")) return -1;
+  if (a.split_tiles > 0) {
+    const dim3 mg((unsigned)(((long)a.n_units * kPCols * (head_dim / 4) + 255) / 256)), mb(256);
+    if (head_dim == 64)
+      hipLaunchKernelGGL((prefill_merge_kernel<64>), mg, mb, 0, c.stream, a);
+    else
+      hipLaunchKernelGGL((prefill_merge_kernel<128>), mg, mb, 0, c.stream, a);
+    return check_hip(hipGetLastError(), "prefill_merge_kernel");
+  }
+  return 0;
 }
 
 extern "C" int plh_attn_prefill(int n_layers, int n_heads, int n_kv_heads, int head_dim,

@@ -37,6 +37,9 @@ int check_hip(hipError_t e, const char* what);
 // GEMV rows per thread forced by plh_set_tuning key 3 (0: the launch's own
 // choice).
 extern int g_gemv_rows_per_thread;
+// plh_set_tuning key 5: prefill chunking of small launches (0 automatic, -1
+// never, 2/4/8/16 a fixed chunk size in tiles).
+extern int g_prefill_split;
 // plh_set_tuning key 4: 1 = the forward pass forms rmsnorm(x) in a launch of
 // its own instead of inside the GEMVs that read it.
 extern int g_fwd_norm_separate;
@@ -125,9 +128,16 @@ struct PrefillArgs {
   int bq;                  // tokens per q block
   int n_qblk;              // q blocks per (layer, kv head)
   int n_units;             // n_launch_layers * n_kv_heads * n_qblk
-  int per_xcd;             // units per XCD slice of the grid
-  int groups_per_xcd;      // (layer, kv head) groups per XCD slice
-  int qb_major;            // 1: order a slice's units by q block, heaviest first
+  int per_xcd;             // workgroups per XCD slice of the grid
+  int xcd_slices;          // 8 (block b runs on XCD b % 8 and takes slice b % 8) or 1
+  int groups_per_xcd;      // (layer, kv head) groups per slice
+  int qb_major;            // single blocks: order a slice's units by q block, heaviest first
+  int paired;              // 1: a workgroup runs a heavy q block and its light mirror
+  int split_tiles;         // > 0: units split into chunks of this many tiles
+  int chunks_per_group;    // chunks of one (layer, kv head) group when split
+  float* part_o;           // split partials [n_groups*chunks_per_group][128 columns][D]
+  float* part_m;           // [..][128] running maxima (log2 units)
+  float* part_l;           // [..][128] running sums
   const float* qn;         // QK-norm weights [n_launch_layers][D], or null
   const float* kn;
   float norm_eps;

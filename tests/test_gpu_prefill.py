@@ -122,6 +122,34 @@ SMALL = [
 ]
 
 
+# launches whose heavy q blocks are split into chunks of tiles (partials merged
+# afterwards): automatic for one-layer launches with few q blocks (a prompt
+# chunk late in the prompt), forced here through plh_set_tuning key 5 for the
+# other chunk sizes
+SPLIT = [
+    # (n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, theta, rope_type, start, n,
+    #  layer, chunk tiles: 0 = automatic)
+    (3, 32, 4, 64, 1024, 1e4, 0, 0, 512, 1, 4),     # TinyLlama heads, one layer of three
+    (2, 32, 4, 64, 1024, 1e4, 0, 300, 333, 0, 2),   # prefix rows, ragged last block
+    (2, 32, 8, 64, 800, 5e5, 0, 17, 700, 1, 16),    # Llama-3.2 heads
+    (2, 32, 32, 128, 1100, 1e4, 0, 0, 1024, 0, 8),  # Llama-2 MHA, D = 128
+    (2, 8, 2, 128, 700, 1e6, 1, 40, 600, 1, 0),     # QWEN rotation, D = 128 (automatic)
+    (2, 32, 4, 64, 1200, 1e4, 0, 1024, 128, 1, 0),  # a 128-token chunk late in the prompt
+]
+
+
+@pytest.mark.parametrize("case", SPLIT)
+def test_prefill_one_layer_split(gpu, oracle_mod, case):
+    L, Hq, Hkv, D, S, theta, rt, start, n, layer, chunk = case
+    cfg = gpu.AttnConfig(L, Hq, Hkv, D, S, theta, rt)
+    gpu.check(gpu.lib.plh_set_tuning(5, chunk), "plh_set_tuning")
+    try:
+        run_prefill(gpu, oracle_mod, cfg, start, n, seed=start + n + layer, check_layers=[0],
+                    layer_range=(layer, 1))
+    finally:
+        gpu.lib.plh_set_tuning(5, 0)
+
+
 @pytest.mark.parametrize("case", SMALL)
 def test_prefill_small(gpu, oracle_mod, case):
     L, Hq, Hkv, D, S, theta, rt, start, n = case
