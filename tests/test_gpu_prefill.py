@@ -172,6 +172,19 @@ def test_prefill_layer_subrange_and_wide_stride(gpu, oracle_mod):
                 out_stride=cfg.q_dim + 64)
 
 
+def test_prefill_split_wide_stride(gpu, oracle_mod):
+    """A split one-layer launch (chunks of 2 tiles, merged) writing output rows
+    strided wider than n_heads*head_dim: the merge kernel honours the stride
+    and writes nothing past each row's heads."""
+    cfg = gpu.AttnConfig(2, 32, 4, 64, 512, 1e4, 0)
+    gpu.check(gpu.lib.plh_set_tuning(5, 2), "plh_set_tuning")
+    try:
+        run_prefill(gpu, oracle_mod, cfg, 60, 200, seed=12, layer_range=(1, 1),
+                    out_stride=cfg.q_dim + 96)
+    finally:
+        gpu.lib.plh_set_tuning(5, 0)
+
+
 def test_prefill_zero_tokens_is_a_no_op(gpu, oracle_mod):
     cfg = gpu.AttnConfig(2, 32, 4, 64, 64, 1e4, 0)
     run_prefill(gpu, oracle_mod, cfg, 10, 0, seed=6)

@@ -127,3 +127,42 @@ def test_qknorm_needs_both_weights(gpu):
                                      cache.sin.ptr, buf.ptr, 16 * 128, None, buf.ptr, 1e-6)
     assert rc == -1 and b"both" in lib.plh_last_error()
     cache.free()
+
+
+@pytest.mark.parametrize("dims", CONFIGS[:2])
+def test_prefill_qknorm_one_layer_split(gpu, oracle_mod, dims):
+    """One layer of a prompt whose heavy q blocks are split into 4-tile chunks
+    (plh_set_tuning key 5) and merged: QK-norm inside every chunk's prologue."""
+    O = oracle_mod
+    L, Hq, Hkv, D, S, theta, rt = dims
+    cfg = gpu.AttnConfig(L, Hq, Hkv, D, S, theta, rt)
+    rng = np.random.default_rng(D + 17)
+    qw, kw = _weights(rng, L, D)
+    dqw = gpu.DeviceBuffer.from_numpy(qw[1].copy())
+    dkw = gpu.DeviceBuffer.from_numpy(kw[1].copy())
+    start, n = 150, 400
+    kc, vc = filled_cache(O, cfg, start, rng)
+    q = normal_f32(rng, (n, cfg.q_dim), 3.0)
+    k = normal_f32(rng, (n, cfg.kv_dim), 3.0)
+    v = normal_f32(rng, (n, cfg.kv_dim))
+    print(f"[case] prefill qknorm split {dims} start {start} n {n}", flush=True)
+    cache = gpu.KVCache(cfg)
+    cache.load(kc, vc)
+    dq, dk, dv = (gpu.DeviceBuffer.from_numpy(x) for x in (q, k, v))
+    dout = gpu.DeviceBuffer(n * cfg.q_dim * 4)
+    gpu.check(gpu.lib.plh_set_tuning(5, 4), "plh_set_tuning")
+    try:
+        gpu.prefill(cache, 1, start, n, dq.ptr, dk.ptr, dv.ptr, dout.ptr, None, 1,
+                    q_norm=dqw.ptr, k_norm=dkw.ptr, norm_eps=EPS)
+        gpu.synchronize()
+    finally:
+        gpu.lib.plh_set_tuning(5, 0)
+    out = dout.download(np.float32, (n, cfg.q_dim))
+    gk, gv = cache.fetch()
+    cache.free()
+    shp = O.Shape(L, Hq, Hkv, D, S, theta, rt)
+    cos_t, sin_t = O.rope_tables(S, D, theta)
+    ref = O.attn_prefill(shp, 1, start, n, q.copy(), k.copy(), v, kc, vc, cos_t, sin_t,
+                         q_norm=qw[1], k_norm=kw[1], eps=EPS)
+    assert_attn_close(out, ref, D, what="prefill qknorm split layer 1")
+    assert np.array_equal(gk, kc) and np.array_equal(gv, vc)
