@@ -65,12 +65,14 @@ float plh_event_elapsed_ms(void *start, void *stop); /* waits for stop */
 void plh_event_destroy(void *ev);
 
 /* ---- HIP graphs of the library stream ------------------------------------ */
-/* Everything queued between begin and end (decode launches, event records) is
- * captured instead of run; plh_graph_launch replays it.  Decode launches need
- * no memset and allocate nothing once the workspace has been sized by one
- * eager call of the same shape, so they can be captured.  A later, larger
- * call moves to a bigger workspace; the old one stays allocated until
- * plh_shutdown, so graphs captured earlier keep replaying correctly. */
+/* Everything queued between begin and end (attention launches, event
+ * records) is captured instead of run; plh_graph_launch replays it.  Decode
+ * and prefill launches need no memset and allocate nothing once the library
+ * workspace has been sized by one eager call of the same shape (decode split
+ * partials; prefill chunk partials of split one-layer launches), so they can
+ * be captured.  A later, larger call moves to a bigger workspace; the old one
+ * stays allocated until plh_shutdown, so graphs captured earlier keep
+ * replaying correctly. */
 int plh_capture_begin(void);
 void *plh_capture_end(void); /* instantiated graph, or NULL */
 int plh_graph_launch(void *graph);

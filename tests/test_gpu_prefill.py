@@ -250,3 +250,44 @@ def test_cfg3_tinyllama_prefill_512(gpu, oracle_mod):
 def test_cfg5b_llama2_prefill_1024(gpu, oracle_mod):
     cfg = gpu.AttnConfig(32, 32, 32, 128, 4096, 1e4, 0)
     run_prefill(gpu, oracle_mod, cfg, 0, 1024, seed=106, check_layers=[0, 31])
+
+
+def test_prefill_split_graph_replays_match_eager(gpu, oracle_mod):
+    """A captured one-layer prefill that splits its heavy q blocks (attention
+    chunks + merge kernel, partials in the library workspace) replayed several
+    times, with eager prefill work in between, gives the eager result each
+    time."""
+    cfg = gpu.AttnConfig(2, 32, 4, 64, 1400, 1e4, 0)
+    rng = np.random.default_rng(31)
+    start, n = 1024, 128
+    kc, vc = filled_cache(oracle_mod, cfg, start, rng)
+    q = normal_f32(rng, (n, cfg.q_dim))
+    k = normal_f32(rng, (n, cfg.kv_dim))
+    v = normal_f32(rng, (n, cfg.kv_dim))
+    cache = gpu.KVCache(cfg)
+    cache.load(kc, vc)
+    dq, dk, dv = (gpu.DeviceBuffer.from_numpy(x) for x in (q, k, v))
+    dout = gpu.DeviceBuffer(n * cfg.q_dim * 4)
+    gpu.prefill(cache, 1, start, n, dq.ptr, dk.ptr, dv.ptr, dout.ptr)
+    gpu.synchronize()
+    eager = dout.download(np.float32, (n, cfg.q_dim))
+    with gpu.Graph() as g:
+        gpu.prefill(cache, 1, start, n, dq.ptr, dk.ptr, dv.ptr, dout.ptr)
+    other = gpu.KVCache(cfg)          # eager work goes to a different cache
+    other.load(kc, vc)
+    scratch = gpu.DeviceBuffer(n * cfg.q_dim * 4)
+    for rep in range(4):
+        dout.zero()
+        gpu.synchronize()
+        g.launch()
+        gpu.synchronize()
+        got = dout.download(np.float32, (n, cfg.q_dim))
+        assert np.array_equal(got, eager), f"replay {rep} differs from eager"
+        # eager split launches between replays reuse the same workspace
+        gpu.prefill(other, 1, start - 200, n, dq.ptr, dk.ptr, dv.ptr, scratch.ptr)
+    shp = oracle_mod.Shape(2, 32, 4, 64, 1400)
+    cos_t, sin_t = oracle_mod.rope_tables(1400, 64, 1e4)
+    ref = oracle_mod.attn_prefill(shp, 1, start, n, q.copy(), k.copy(), v, kc, vc, cos_t, sin_t)
+    assert_attn_close(eager, ref, 64, 1e-3, "eager split prefill")
+    gk, gv = cache.fetch()
+    assert np.array_equal(gk, kc) and np.array_equal(gv, vc)
