@@ -626,7 +626,8 @@ def cpu_reference_decode(w, reps=5):
             "kind": "reference", "us_per_token": attn_s * 1e6,
             "sample": f"model_forward_ex of a {Ls}-layer model of this attention shape at pos "
                       f"{pos} minus pos 0, median of {reps} after a warm-up, x{w['L'] // Ls} "
-                      f"layers; 1 thread"}
+                      f"layers; 1 thread (picolm's pool runs matmul rows only, its attention "
+                      f"loop is serial at any -j)"}
 
 
 def cpu_reference_prefill(name, w, reps=5):
@@ -661,7 +662,9 @@ def cpu_reference_prefill(name, w, reps=5):
             "kind": "reference", "us_per_token": step_s * 1e6 / n,
             "sample": f"model_forward_prefill of a 1-layer model with {hq} q / {hkv} kv heads of "
                       f"head_dim {w['D']} ({n} tokens, projections included), median of {reps} "
-                      f"after a warm-up, x{w['Hq'] // hq} heads x{w['L']} layers; 1 thread"}
+                      f"after a warm-up, x{w['Hq'] // hq} heads x{w['L']} layers; 1 thread "
+                      f"(picolm's pool runs matmul rows only, its attention loop is serial at "
+                      f"any -j)"}
 
 
 def decode_parity(P, w, res, layers=(0,)):
