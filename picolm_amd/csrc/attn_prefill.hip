@@ -141,10 +141,16 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(PrefillArgs a) {
       r.y = (uint32_t)h[2] | ((uint32_t)h[3] << 16);
       return r;
     };
-    *(uint2*)(a.kc + out_row + e0) = pack(kh);
-    *(uint2*)(a.kc + out_row + e1) = pack(kh + 4);
-    *(uint2*)(a.vc + out_row + e0) = pack(vh);
-    *(uint2*)(a.vc + out_row + e1) = pack(vh + 4);
+    if (qwen) {
+      *(uint2*)(a.kc + out_row + e0) = pack(kh);
+      *(uint2*)(a.kc + out_row + e1) = pack(kh + 4);
+      *(uint2*)(a.vc + out_row + e0) = pack(vh);
+      *(uint2*)(a.vc + out_row + e1) = pack(vh + 4);
+    } else {  // e1 = e0 + 4: one 16-byte store each
+      const uint2 k0 = pack(kh), k1 = pack(kh + 4), v0 = pack(vh), v1 = pack(vh + 4);
+      *(uint4*)(a.kc + out_row + e0) = make_uint4(k0.x, k0.y, k1.x, k1.y);
+      *(uint4*)(a.vc + out_row + e0) = make_uint4(v0.x, v0.y, v1.x, v1.y);
+    }
   }
 }
 
@@ -317,15 +323,21 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
     // produces scores in log2 units; then the column's range for fp16 (a
     // power-of-two scale, undone on the scores: 1 unless some |q| * scale >=
     // 2^15)
-    float amax = 0.f;
+    // (the maximum as a tree of independent steps, not one chain)
+    float am[NS];
 #pragma unroll
-    for (int s = 0; s < NS; ++s)
+    for (int s = 0; s < NS; ++s) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        qf[s][j] *= a.score_scale;
-        amax = vmax(amax, fabsf(qf[s][j]));
-      }
-    amax = max_xor32(amax);
+      for (int j = 0; j < 8; ++j) qf[s][j] *= a.score_scale;
+      const float x0 = vmax(vmax(fabsf(qf[s][0]), fabsf(qf[s][1])), fabsf(qf[s][2]));
+      const float x1 = vmax(vmax(fabsf(qf[s][3]), fabsf(qf[s][4])), fabsf(qf[s][5]));
+      am[s] = vmax(vmax(x0, x1), vmax(fabsf(qf[s][6]), fabsf(qf[s][7])));
+    }
+#pragma unroll
+    for (int w = 1; w < NS; w *= 2)
+#pragma unroll
+      for (int s = 0; s + w < NS; s += 2 * w) am[s] = vmax(am[s], am[s + w]);
+    const float amax = max_xor32(am[0]);
     qdown = q_range_scale(amax, &qup);
 #pragma unroll
     for (int s = 0; s < NS; ++s)
@@ -364,7 +376,8 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
   float ms = 0.f;
   bool fresh = true;                // no unmasked key seen yet (ms, lsum, o all 0)
   f32x16_t negm = {};               // -ms * 2^-e, the QK accumulator start
-  float lsum = 0.f;                 // this lane's half of the running sum
+  float ls[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's half of the running sum, in 4
+                                       // partial sums (independent add chains)
   const bool scaled_cols = __ballot(qup != 1.f) != 0;  // wave-uniform: rare
   f32x16_t o[NDB];
 #pragma unroll
@@ -401,17 +414,20 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
         for (int v = 0; v < 16; ++v)
           if (t0 + 16 * (v / 8) + 8 * half + v % 8 > p_col) t[v] = -INFINITY;
       }
-      float tmax = t[0];
-#pragma unroll
-      for (int v = 1; v < 16; ++v) tmax = vmax(tmax, t[v]);
-      tmax = max_xor32(tmax);
+      // the tile maximum as a tree (depth 3, not a chain of 8)
+      const float m0 = vmax(vmax(t[0], t[1]), t[2]), m1 = vmax(vmax(t[3], t[4]), t[5]);
+      const float m2 = vmax(vmax(t[6], t[7]), t[8]), m3 = vmax(vmax(t[9], t[10]), t[11]);
+      const float m4 = vmax(vmax(t[12], t[13]), t[14]);
+      const float tmax =
+          max_xor32(vmax(vmax(vmax(m0, m1), m2), vmax(vmax(m3, m4), t[15])));
       // fresh columns with an unmasked key take its maximum as ms (nothing
       // accumulated yet); others raise ms by the excess beyond kLazy
       const bool upd = fresh ? tmax != -INFINITY : tmax > kLazy;
       if (__ballot(upd)) {
         const float d = upd ? tmax : 0.f;
         const float alpha = fresh ? 1.f : fast_exp2(-d);
-        lsum *= alpha;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) ls[k] *= alpha;
 #pragma unroll
         for (int db = 0; db < NDB; ++db) o[db] *= alpha;
         fresh = fresh && !upd;
@@ -431,8 +447,8 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
           split_pair_rtz(fast_exp2(t[8 * j + e]), fast_exp2(t[8 * j + e + 1]), hi, lo);
           ph[j][e] = hi[0], ph[j][e + 1] = hi[1];
           pl[j][e] = lo[0], pl[j][e + 1] = lo[1];
-          lsum = __builtin_amdgcn_fdot2(hi, one2, lsum, false);
-          lsum = __builtin_amdgcn_fdot2(lo, one2, lsum, false);
+          ls[2 * j] = __builtin_amdgcn_fdot2(hi, one2, ls[2 * j], false);
+          ls[2 * j + 1] = __builtin_amdgcn_fdot2(lo, one2, ls[2 * j + 1], false);
         }
 #pragma unroll
       for (int db = 0; db < NDB; ++db)
@@ -455,7 +471,7 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
   }
 
   // ---- normalise and write: lane holds d = 32*db + 8*(v/4) + 4*half + v%4 --
-  lsum = add_xor32(lsum);
+  const float lsum = add_xor32((ls[0] + ls[1]) + (ls[2] + ls[3]));
   if (slot >= 0) {
     // a chunk's partial: O, ms (-inf for a column with no unmasked key in the
     // chunk) and the sum, per column of the unit
