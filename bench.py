@@ -49,6 +49,11 @@ sample that the `sample` field names:
   * prefill: model_forward_prefill (projections at a small width included)
     of a 1-layer model with a slice of the workload's q heads (same head_dim,
     same GQA group), scaled to all heads and layers.
+Beside it, cpu_baseline.head_parallel_upper_bound (kind "port"): the oracle's
+restatement of the same attention with the q heads split over the host's
+threads (bit-identical output), an upper bound for a parallel CPU attention
+and not the reference's own parallelism (decode: 2 layers at pos; prefill:
+one layer of the prompt; both scaled to all layers).
 The oracle (the restatement in C, test infrastructure) checks the GPU outputs
 of a sample layer (parity_normwise_max).
 """
@@ -667,6 +672,98 @@ def cpu_reference_prefill(name, w, reps=5):
                       f"any -j)"}
 
 
+def cpu_head_parallel_decode(w, reps=7, warm=3):
+    """Upper bound for a parallel CPU attention, not the reference's own
+    parallelism (picolm's -j pool runs matmul rows only): the oracle's
+    restatement of its decode attention (model.c:828-892) with the q heads
+    split over the host's threads (orc_attn_decode_mt, bit-identical to the
+    serial loop), CPU_DECODE_LAYERS layers at pos, median of `reps` after
+    at least `warm` warm-up calls and 0.3 s of them, scaled to all layers
+    (QK-norm, O(D) per head, left out)."""
+    from oracle import oracle as O
+    Ls, pos, S, D = CPU_DECODE_LAYERS, w["pos"], w["S"], w["D"]
+    shp = O.Shape(Ls, w["Hq"], w["Hkv"], D, S, w["theta"], w.get("rt", 0))
+    n_thr = n_host_threads()
+    rng = np.random.default_rng(4096)
+    kv = w["Hkv"] * D
+    kc = np.zeros(Ls * S * kv, np.uint16)
+    vc = np.zeros(Ls * S * kv, np.uint16)
+    for cache in (kc, vc):
+        view = cache.reshape(Ls, S, kv)
+        for layer in range(Ls):
+            view[layer, :pos] = O.f32_to_f16(
+                rng.standard_normal((pos, kv), dtype=np.float32)).reshape(pos, kv)
+    cos_t, sin_t = O.rope_tables(S, D, w["theta"])
+    q = rng.standard_normal((Ls, w["Hq"] * D), dtype=np.float32)
+    k = rng.standard_normal((Ls, kv), dtype=np.float32)
+    v = rng.standard_normal((Ls, kv), dtype=np.float32)
+    def once():
+        qs, ks = q.copy(), k.copy()
+        t0 = time.perf_counter()
+        for layer in range(Ls):
+            O.attn_decode_mt(shp, layer, pos, qs[layer], ks[layer], v[layer], kc, vc, cos_t,
+                             sin_t, n_thr)
+        return time.perf_counter() - t0
+
+    # warm-up: at least `warm` calls and 0.3 s (idle cores take tens of ms to
+    # come up to speed under new threads)
+    t_end = time.perf_counter() + 0.3
+    for r in range(warm):
+        once()
+    while time.perf_counter() < t_end:
+        once()
+    ts = [once() for _ in range(reps)]
+    step_s = float(np.median(ts)) * w["L"] / Ls
+    return {"value": decode_bytes(w) / step_s / 1e9, "unit": "GB/s", "cores": n_thr,
+            "kind": "port", "us_per_token": step_s * 1e6,
+            "sample": f"oracle decode attention at pos {pos} with q heads split over {n_thr} "
+                      f"threads, {Ls} layers, median of {reps} after >= 0.3 s of warm-up, "
+                      f"x{w['L'] // Ls} layers; upper bound, not the reference's own "
+                      f"parallelism"}
+
+
+def cpu_head_parallel_prefill(w, reps=3):
+    """Upper bound for a parallel CPU prefill attention, not the reference's
+    own parallelism: the oracle's restatement of model.c:1019-1090 for one
+    layer with the attention split by q head over the host's threads
+    (orc_attn_prefill_mt, bit-identical to the serial loop), QK-norm
+    included where the workload has it, median of `reps` after a warm-up,
+    scaled to all layers."""
+    from oracle import oracle as O
+    n, st, D = w["n"], w["start"], w["D"]
+    shp = O.Shape(1, w["Hq"], w["Hkv"], D, st + n, w["theta"], w.get("rt", 0))
+    n_thr = n_host_threads()
+    rng = np.random.default_rng(1025)
+    kv = w["Hkv"] * D
+    kc = np.zeros((st + n) * kv, np.uint16)
+    vc = np.zeros((st + n) * kv, np.uint16)
+    if st:
+        kc[: st * kv] = O.f32_to_f16(rng.standard_normal(st * kv, dtype=np.float32))
+        vc[: st * kv] = O.f32_to_f16(rng.standard_normal(st * kv, dtype=np.float32))
+    cos_t, sin_t = O.rope_tables(st + n, D, w["theta"])
+    q = rng.standard_normal((n, w["Hq"] * D), dtype=np.float32)
+    k = rng.standard_normal((n, kv), dtype=np.float32)
+    v = rng.standard_normal((n, kv), dtype=np.float32)
+    qn = kn = None
+    if w.get("qkn"):
+        qn = (rng.standard_normal(D) * 0.5 + 1.0).astype(np.float32)
+        kn = (rng.standard_normal(D) * 0.5 + 1.0).astype(np.float32)
+    ts = []
+    for r in range(reps + 1):
+        qs, ks = q.copy(), k.copy()
+        t0 = time.perf_counter()
+        O.attn_prefill_mt(shp, 0, st, n, qs, ks, v, kc, vc, cos_t, sin_t, n_thr, q_norm=qn,
+                          k_norm=kn, eps=w.get("qkn") or 0.0)
+        if r > 0:
+            ts.append(time.perf_counter() - t0)
+    step_s = float(np.median(ts)) * w["L"]
+    return {"value": prefill_flops(w) / step_s / 1e12, "unit": "TFLOP/s", "cores": n_thr,
+            "kind": "port", "us_per_token": step_s * 1e6 / n,
+            "sample": f"oracle prefill attention of one layer ({n} tokens from {st}) with q heads "
+                      f"split over {n_thr} threads, median of {reps} after a warm-up, "
+                      f"x{w['L']} layers; upper bound, not the reference's own parallelism"}
+
+
 def decode_parity(P, w, res, layers=(0,)):
     """Normwise error of the GPU output of sample layers against the oracle."""
     from oracle import oracle as O
@@ -743,6 +840,8 @@ def measure(P, name, steps, warmup, cpu, warm=False):
         res = run_prefill(P, w, steps, warmup, name)
         if cpu:
             res["cpu_baseline"] = cpu_reference_prefill(name, w)
+            if res["cpu_baseline"] is not None:
+                res["cpu_baseline"]["head_parallel_upper_bound"] = cpu_head_parallel_prefill(w)
         res["parity_normwise_max"] = prefill_parity(P, w, res) if w["n"] <= 512 else None
         res.pop("_copies", None)
         res.pop("_norms", None)
@@ -750,6 +849,8 @@ def measure(P, name, steps, warmup, cpu, warm=False):
         res = run_decode(P, w, steps, warmup, name, warm=warm)
         if cpu:
             res["cpu_baseline"] = cpu_reference_decode(w)
+            if res["cpu_baseline"] is not None:
+                res["cpu_baseline"]["head_parallel_upper_bound"] = cpu_head_parallel_decode(w)
         res["parity_normwise_max"] = decode_parity(P, w, res)
         res.pop("_cpu_inputs", None)
     return res
@@ -782,6 +883,9 @@ def compact(tag, name, res):
                traffic=None if rf["traffic"] is None else int(rf["traffic"]),
                cpu_us_tok=None if not cb else round(cb["us_per_token"], 1),
                cpu_kind=cb.get("kind"),
+               cpu_mt_us_tok=None if not cb.get("head_parallel_upper_bound")
+               else round(cb["head_parallel_upper_bound"]["us_per_token"], 1),
+               cpu_mt_cores=(cb.get("head_parallel_upper_bound") or {}).get("cores"),
                parity=None if res.get("parity_normwise_max") is None
                else float(f"{res['parity_normwise_max']:.2e}"))
     return out

@@ -455,3 +455,71 @@ int orc_attn_prefill_qkn(int n_layers, int n_heads, int n_kv_heads, int head_dim
     }
     return 0;
 }
+
+/* Head-parallel prefill (the CPU baseline's upper bound): the per-token
+ * prologue of orc_attn_prefill_qkn for every row first, then each thread runs
+ * attend_heads for its q heads over all tokens. */
+struct prefill_job {
+    int n_heads, n_kv_heads, head_dim, seq_len, layer, start_pos, n_tokens;
+    const float *q;
+    const uint16_t *kc, *vc;
+    float *out;
+    int out_stride, h_begin, h_end;
+};
+
+static void *prefill_worker(void *arg) {
+    struct prefill_job *j = (struct prefill_job *)arg;
+    size_t q_dim = (size_t)j->n_heads * (size_t)j->head_dim;
+    for (int bi = 0; bi < j->n_tokens; bi++)
+        attend_heads(j->n_heads, j->n_kv_heads, j->head_dim, j->seq_len, j->layer,
+                     j->start_pos + bi, j->q + (size_t)bi * q_dim, j->kc, j->vc,
+                     j->out + (size_t)bi * (size_t)j->out_stride, j->h_begin, j->h_end);
+    return NULL;
+}
+
+int orc_attn_prefill_mt(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                        int max_seq_len, int rope_type, int layer, int start_pos,
+                        int n_tokens, float *q, float *k, const float *v,
+                        uint16_t *key_cache, uint16_t *val_cache,
+                        const float *cos_tab, const float *sin_tab,
+                        float *out, int out_stride,
+                        const float *q_norm, const float *k_norm, float eps,
+                        int n_threads) {
+    if (!dims_ok(n_heads, n_kv_heads, head_dim)) return -1;
+    if (layer < 0 || layer >= n_layers || start_pos < 0 || n_tokens < 0) return -1;
+    if ((q_norm == NULL) != (k_norm == NULL)) return -1;
+    if ((long)start_pos + (long)n_tokens > (long)max_seq_len) return -1;
+    size_t q_dim = (size_t)n_heads * (size_t)head_dim;
+    size_t kv_dim = (size_t)n_kv_heads * (size_t)head_dim;
+    size_t half = (size_t)(head_dim / 2);
+    for (int bi = 0; bi < n_tokens; bi++) {
+        int pos = start_pos + bi;
+        float *qb = q + (size_t)bi * q_dim;
+        float *kb = k + (size_t)bi * kv_dim;
+        if (q_norm) qk_norm(qb, kb, n_heads, n_kv_heads, head_dim, q_norm, k_norm, eps);
+        orc_rope(qb, kb, head_dim, n_heads, n_kv_heads,
+                 cos_tab + (size_t)pos * half, sin_tab + (size_t)pos * half, rope_type);
+        append_row(n_kv_heads, head_dim, max_seq_len, layer, pos, kb,
+                   v + (size_t)bi * kv_dim, key_cache, val_cache);
+    }
+    if (n_threads > n_heads) n_threads = n_heads;
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads > 256) n_threads = 256;
+    pthread_t tid[256];
+    struct prefill_job job[256];
+    int started = 0;
+    for (int t = 0; t < n_threads; t++) {
+        job[t] = (struct prefill_job){n_heads, n_kv_heads, head_dim, max_seq_len, layer,
+                                      start_pos, n_tokens, q, key_cache, val_cache, out,
+                                      out_stride, n_heads * t / n_threads,
+                                      n_heads * (t + 1) / n_threads};
+        if (t == 0) continue;
+        if (pthread_create(&tid[t], NULL, prefill_worker, &job[t]) != 0) break;
+        started = t;
+    }
+    prefill_worker(&job[0]);
+    for (int t = 1; t <= started; t++) pthread_join(tid[t], NULL);
+    /* heads of threads that failed to start run here */
+    for (int t = started + 1; t < n_threads; t++) prefill_worker(&job[t]);
+    return 0;
+}

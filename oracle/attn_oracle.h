@@ -113,6 +113,22 @@ int orc_attn_prefill_qkn(int n_layers, int n_heads, int n_kv_heads, int head_dim
                          float *out, int out_stride,
                          const float *q_norm, const float *k_norm, float eps);
 
+/* orc_attn_prefill_qkn with the attention split over n_threads pthreads by q
+ * head (each thread walks every token for its heads).  QK-norm, rotation and
+ * the appends run first, serially, for all n_tokens rows: each token's
+ * attention reads only rows up to its own position, so the output and caches
+ * are bit-identical to the serial function.  For the CPU baseline's
+ * "head-parallel upper bound" only: the reference runs this loop on one
+ * thread. */
+int orc_attn_prefill_mt(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                        int max_seq_len, int rope_type, int layer, int start_pos,
+                        int n_tokens, float *q, float *k, const float *v,
+                        uint16_t *key_cache, uint16_t *val_cache,
+                        const float *cos_tab, const float *sin_tab,
+                        float *out, int out_stride,
+                        const float *q_norm, const float *k_norm, float eps,
+                        int n_threads);
+
 /* tensor.c:425-492 rmsnorm in the reference's x86-64 AVX2 build order (see
  * the definition).  out may alias x. */
 void orc_rmsnorm(float *out, const float *x, const float *w, int size, float eps);

@@ -106,6 +106,10 @@ def lib() -> C.CDLL:
                                                   _f32p, _f32p, _f32p, C.c_int, _nf, _nf,
                                                   C.c_float]
         L.orc_attn_prefill_qkn.restype = C.c_int
+        L.orc_attn_prefill_mt.argtypes = dims + [C.c_int, _f32p, _f32p, _f32p, _u16p, _u16p,
+                                                 _f32p, _f32p, _f32p, C.c_int, _nf, _nf,
+                                                 C.c_float, C.c_int]
+        L.orc_attn_prefill_mt.restype = C.c_int
         L.orc_rmsnorm.argtypes = [_f32p, _f32p, _f32p, C.c_int, C.c_float]
         L.orc_rmsnorm.restype = None
         for name in ("orc_vec_dot_q4_K", "orc_vec_dot_q6_K", "orc_vec_dot_q8_0",
@@ -313,6 +317,24 @@ def attn_prefill(shp: Shape, layer, start_pos, n_tokens, q, k, v, kc, vc,
                                         out, stride, _nullable(qn), _nullable(kn), eps)
     if rc != 0:
         raise ValueError("orc_attn_prefill rejected its arguments")
+    return out[: n_tokens * stride].reshape(n_tokens, stride)
+
+
+def attn_prefill_mt(shp: Shape, layer, start_pos, n_tokens, q, k, v, kc, vc, cos_t, sin_t,
+                    n_threads, q_norm=None, k_norm=None, eps=0.0):
+    """attn_prefill with the attention split by q head over n_threads host
+    threads (bit-identical output); the CPU baseline's head-parallel upper
+    bound."""
+    stride = shp.q_dim
+    out = np.zeros(max(n_tokens, 1) * stride, dtype=np.float32)
+    qn = None if q_norm is None else np.ascontiguousarray(q_norm, np.float32)
+    kn = None if k_norm is None else np.ascontiguousarray(k_norm, np.float32)
+    rc = lib().orc_attn_prefill_mt(*shp.dims(), layer, start_pos, n_tokens,
+                                   q.reshape(-1), k.reshape(-1), v.reshape(-1),
+                                   kc, vc, cos_t.reshape(-1), sin_t.reshape(-1),
+                                   out, stride, _nullable(qn), _nullable(kn), eps, n_threads)
+    if rc != 0:
+        raise ValueError("orc_attn_prefill_mt rejected its arguments")
     return out[: n_tokens * stride].reshape(n_tokens, stride)
 
 

@@ -227,6 +227,31 @@ def test_head_parallel_decode_is_bit_identical(oracle_mod, threads):
     assert np.array_equal(kc1, kc2) and np.array_equal(vc1, vc2)
 
 
+@pytest.mark.parametrize("threads,qkn", [(1, False), (5, False), (16, True), (40, False)])
+def test_head_parallel_prefill_is_bit_identical(oracle_mod, threads, qkn):
+    """The head-parallel prefill (all prologues first, then each thread's q
+    heads over every token) equals the serial oracle bit for bit: outputs and
+    caches, with a cached prefix, with and without QK-norm."""
+    O = oracle_mod
+    shp = O.Shape(2, 16, 4, 64, 128, rope_type=1 if qkn else 0)
+    rng = np.random.default_rng(31 + threads)
+    c, s = O.rope_tables(128, 64, 1e4)
+    start, n = 20, 37
+    kc1, vc1 = random_cache(O, shp, rng)
+    kc2, vc2 = kc1.copy(), vc1.copy()
+    q = rng.standard_normal((n, shp.q_dim)).astype(np.float32)
+    k = rng.standard_normal((n, shp.kv_dim)).astype(np.float32)
+    v = rng.standard_normal((n, shp.kv_dim)).astype(np.float32)
+    qn = (rng.standard_normal(64) * 0.5 + 1).astype(np.float32) if qkn else None
+    kn = (rng.standard_normal(64) * 0.5 + 1).astype(np.float32) if qkn else None
+    a = O.attn_prefill(shp, 1, start, n, q.copy(), k.copy(), v, kc1, vc1, c, s,
+                       q_norm=qn, k_norm=kn, eps=1e-6)
+    b = O.attn_prefill_mt(shp, 1, start, n, q.copy(), k.copy(), v, kc2, vc2, c, s, threads,
+                          q_norm=qn, k_norm=kn, eps=1e-6)
+    assert np.array_equal(a, b)
+    assert np.array_equal(kc1, kc2) and np.array_equal(vc1, vc2)
+
+
 def test_out_of_range_is_rejected(oracle_mod):
     O = oracle_mod
     shp = O.Shape(1, 4, 2, 64, 16)
