@@ -320,15 +320,15 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
       }
     }
     // the softmax scale log2(e)/sqrt(D) goes into q, so that the MFMA
-    // produces scores in log2 units; then the column's range for fp16 (a
-    // power-of-two scale, undone on the scores: 1 unless some |q| * scale >=
-    // 2^15)
-    // (the maximum as a tree of independent steps, not one chain)
+    // produces scores in log2 units, and the column's range for fp16 (a
+    // power-of-two scale 2^-e, undone on the scores: 1 unless some |q| *
+    // scale >= 2^15), as one factor: scale * 2^-e is exact, and so is x *
+    // (scale * 2^-e) = (x * scale) * 2^-e wherever fp16 can hold the result.
+    // The column's largest |q * scale| is (largest |q|) * scale (rounding is
+    // monotonic); the maximum is a tree of independent steps, not one chain.
     float am[NS];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) qf[s][j] *= a.score_scale;
       const float x0 = vmax(vmax(fabsf(qf[s][0]), fabsf(qf[s][1])), fabsf(qf[s][2]));
       const float x1 = vmax(vmax(fabsf(qf[s][3]), fabsf(qf[s][4])), fabsf(qf[s][5]));
       am[s] = vmax(vmax(x0, x1), vmax(fabsf(qf[s][6]), fabsf(qf[s][7])));
@@ -337,14 +337,15 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
     for (int w = 1; w < NS; w *= 2)
 #pragma unroll
       for (int s = 0; s + w < NS; s += 2 * w) am[s] = vmax(am[s], am[s + w]);
-    const float amax = max_xor32(am[0]);
+    const float amax = max_xor32(am[0]) * a.score_scale;
     qdown = q_range_scale(amax, &qup);
+    const float qmul = a.score_scale * qdown;
 #pragma unroll
     for (int s = 0; s < NS; ++s)
 #pragma unroll
       for (int j = 0; j < 8; j += 2) {
         half2_t hi, lo;
-        split_pair_rtz(qf[s][j] * qdown, qf[s][j + 1] * qdown, hi, lo);
+        split_pair_rtz(qf[s][j] * qmul, qf[s][j + 1] * qmul, hi, lo);
         qh[s][j] = hi[0], qh[s][j + 1] = hi[1];
         ql[s][j] = lo[0], ql[s][j + 1] = lo[1];
       }
@@ -492,7 +493,7 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
     return;
   }
   if (cvalid) {
-    const float inv = 1.0f / lsum;
+    const float inv = __builtin_amdgcn_rcpf(lsum);  // v_rcp_f32: within 1 ulp
     float* orow = a.out + ((size_t)li * a.n_tokens + i0 + tok) * a.out_stride +
                   (size_t)(kvh * G + hh) * D;
 #pragma unroll
