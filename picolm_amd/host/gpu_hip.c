@@ -64,6 +64,8 @@ static struct {
     int n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, n_embd;
     float norm_eps;
     int gpu_layers; /* layers < gpu_layers use the device */
+    int fail_after; /* PICOLM_HIP_FAIL_AFTER: attention hook calls that succeed before an
+                     * injected failure (-1: none) */
     uint16_t *d_key, *d_val;
     float *d_cos, *d_sin;
     unsigned char qkn[MAX_LAYERS]; /* layer has QK-norm */
@@ -101,6 +103,18 @@ static void backend_lost(const char *what) {
     gs.uploaded = 0;
 }
 
+/* Fault injection for the fallback tests (PICOLM_HIP_FAIL_AFTER=N): the
+ * attention hook call after N successful ones fails as a HIP error after its
+ * kernels would: the device cache already holds the new rows, the host cache
+ * does not, and the backend is lost, so the caller's CPU block runs that layer
+ * and every later one.  Returns 1 for the failing call. */
+static int injected_failure(void) {
+    if (gs.fail_after < 0) return 0;
+    if (gs.fail_after-- > 0) return 0;
+    fprintf(stderr, "gpu_hip: injected failure (PICOLM_HIP_FAIL_AFTER)\n");
+    return 1;
+}
+
 int gpu_init(const model_t *m) {
     if (gs.inited) return 0;
     if (env_int("PICOLM_HIP_DISABLE", 0)) return -1;
@@ -125,6 +139,7 @@ int gpu_init(const model_t *m) {
     gs.n_embd = c->n_embd;
     gs.norm_eps = c->rms_norm_eps;
     gs.gpu_layers = env_int("PICOLM_GPU_LAYERS", c->n_layers);
+    gs.fail_after = env_int("PICOLM_HIP_FAIL_AFTER", -1);
     return 0;
 }
 
@@ -555,7 +570,7 @@ int gpu_try_attention(model_t *m, int layer, int pos, float *q, float *k, const 
                              gs.max_seq_len, gs.rope_type, layer, 1, pos, gs.d_q, gs.d_k,
                              gs.d_v, gs.d_key, gs.d_val, gs.d_cos, gs.d_sin, gs.d_out);
     }
-    if (rc != 0) {
+    if (rc != 0 || injected_failure()) {
         backend_lost("plh_attn_decode");
         return -1;
     }
@@ -601,7 +616,7 @@ int gpu_try_attention_prefill(model_t *m, int layer, int start_pos, int n_tokens
                               gs.d_q, gs.d_k, gs.d_v, gs.d_key, gs.d_val, gs.d_cos, gs.d_sin,
                               gs.d_out, dev_stride);
     }
-    if (rc != 0) {
+    if (rc != 0 || injected_failure()) {
         backend_lost("plh_attn_prefill");
         return -1;
     }

@@ -26,6 +26,10 @@
  *               for byte with the CPU model's file; a fresh model loads that
  *               file with kvcache_load, gpu_kv_upload pushes it, and n_resume
  *               more tokens are decoded on the device against the CPU run.
+ *     A hook that returns -1 is answered as picolm's call sites answer it:
+ *     the reference's CPU block runs that layer on the GPU model (counted in
+ *     *_fallback).  With the backend lost (PICOLM_HIP_FAIL_AFTER) the host
+ *     caches are not cleared and restored, they are the only copy.
  *     Writes one line of key=value results.
  *   test_ref_model forward model.bin out.bin
  *     The whole forward pass: model.bin as tests/c/test_gpu_forward reads it
@@ -124,22 +128,30 @@ static int files_equal(const char *p1, const char *p2) {
  * reference's model_forward_ex once per layer (layers 0..l, the appends of
  * earlier layers rewrite identical bits), the GPU model calls
  * gpu_try_attention per layer. */
-static int decode_both(void *hc, model_t *mg, int pos, int L, int q_dim, int kv_dim,
+static int decode_both(void *hc, void *hg, model_t *mg, int pos, int L, int q_dim, int kv_dim,
                        float *q, float *k, float *v, float *outc, float *outg,
-                       double *worst, int *elem_bad) {
+                       double *worst, int *elem_bad, int *fallback) {
     const model_config_t *c = &mg->config;
     int rc = 0;
     fill_normal(q, (size_t)L * q_dim);
     fill_normal(k, (size_t)L * kv_dim);
     fill_normal(v, (size_t)L * kv_dim);
-    for (int l = 0; l < L; l++)
+    for (int l = 0; l < L; l++) {
         ref_set_decode_qkv(hc, l, q + (size_t)l * q_dim, k + (size_t)l * kv_dim,
                            v + (size_t)l * kv_dim);
+        ref_set_decode_qkv(hg, l, q + (size_t)l * q_dim, k + (size_t)l * kv_dim,
+                           v + (size_t)l * kv_dim);
+    }
     for (int l = 0; l < L; l++) {
         ref_decode(hc, pos, l + 1, outc);
         if (gpu_try_attention(mg, l, pos, q + (size_t)l * q_dim, k + (size_t)l * kv_dim,
-                              v + (size_t)l * kv_dim, outg) != 0)
+                              v + (size_t)l * kv_dim, outg) != 0) {
+            /* the CPU block of layer l on the GPU model (earlier layers'
+             * appends rewrite identical bits) */
             rc = -1;
+            ref_decode(hg, pos, l + 1, outg);
+            (*fallback)++;
+        }
         compare(outg, outc, c->n_heads, c->head_dim, worst, elem_bad);
     }
     return rc;
@@ -172,20 +184,29 @@ static int run_attn(int argc, char **argv) {
     fill_normal(pk, (size_t)L * P * kv_dim);
     fill_normal(pv, (size_t)L * P * kv_dim);
     double prefill_err = 0;
-    int prefill_bad = 0, prefill_rc = 0;
+    int prefill_bad = 0, prefill_rc = 0, prefill_fallback = 0;
     for (int l = 0; l < L && P > 0; l++) {
         memset(pout, 0, (size_t)P * E * 4);
+        int fell_back = 0;
         if (gpu_try_attention_prefill(mg, l, 0, P, pq + (size_t)l * P * q_dim,
                                       pk + (size_t)l * P * kv_dim, pv + (size_t)l * P * kv_dim,
-                                      pout) != 0)
+                                      pout) != 0) {
             prefill_rc = -1;
-        /* the reference: the same rows decoded one position at a time */
+            fell_back = 1;
+            prefill_fallback++;
+        }
+        /* the reference: the same rows decoded one position at a time (on the
+         * GPU model too when the hook fell back) */
         for (int p = 0; p < P; p++) {
-            for (int j = 0; j <= l; j++)
-                ref_set_decode_qkv(hc, j, pq + ((size_t)j * P + p) * q_dim,
-                                   pk + ((size_t)j * P + p) * kv_dim,
-                                   pv + ((size_t)j * P + p) * kv_dim);
+            for (int j = 0; j <= l; j++) {
+                const float *qj = pq + ((size_t)j * P + p) * q_dim;
+                const float *kj = pk + ((size_t)j * P + p) * kv_dim;
+                const float *vj = pv + ((size_t)j * P + p) * kv_dim;
+                ref_set_decode_qkv(hc, j, qj, kj, vj);
+                if (fell_back) ref_set_decode_qkv(hg, j, qj, kj, vj);
+            }
             ref_decode(hc, p, l + 1, outc);
+            if (fell_back) ref_decode(hg, p, l + 1, pout + (size_t)p * E);
             compare(pout + (size_t)p * E, outc, Hq, D, &prefill_err, &prefill_bad);
         }
     }
@@ -195,18 +216,21 @@ static int run_attn(int argc, char **argv) {
     float *q = malloc((size_t)L * q_dim * 4), *k = malloc((size_t)L * kv_dim * 4);
     float *v = malloc((size_t)L * kv_dim * 4);
     double decode_err = 0;
-    int decode_bad = 0, decode_rc = 0;
+    int decode_bad = 0, decode_rc = 0, decode_fallback = 0;
     for (int t = 0; t < T; t++)
-        decode_rc |= decode_both(hc, mg, P + t, L, q_dim, kv_dim, q, k, v, outc, outg,
-                                 &decode_err, &decode_bad);
+        decode_rc |= decode_both(hc, hg, mg, P + t, L, q_dim, kv_dim, q, k, v, outc, outg,
+                                 &decode_err, &decode_bad, &decode_fallback);
     const int decode_cache_eq = caches_equal(mc, mg);
 
     /* ---- persistence: gpu_kv_download -> kvcache_save, byte-compared ---- */
     const int n_pos = P + T;
     const size_t cache_n = (size_t)L * S * kv_dim;
-    memset(mg->state.key_cache, 0, cache_n * 2);
-    memset(mg->state.val_cache, 0, cache_n * 2);
-    const int rc_download = gpu_kv_download(mg, n_pos);
+    int rc_download = -1;
+    if (gpu_available()) {
+        memset(mg->state.key_cache, 0, cache_n * 2);
+        memset(mg->state.val_cache, 0, cache_n * 2);
+        rc_download = gpu_kv_download(mg, n_pos);
+    }
     const int download_eq = caches_equal(mc, mg);
     char fc[512], fg[512];
     snprintf(fc, sizeof fc, "%s.cpu.kv", out_path);
@@ -223,10 +247,10 @@ static int run_attn(int argc, char **argv) {
     const int loaded = kvcache_load(mr, fg);
     const int rc_kv_upload = gpu_kv_upload(mr, loaded);
     double resume_err = 0;
-    int resume_bad = 0, resume_rc = 0;
+    int resume_bad = 0, resume_rc = 0, resume_fallback = 0;
     for (int t = 0; t < R; t++)
-        resume_rc |= decode_both(hc, mr, n_pos + t, L, q_dim, kv_dim, q, k, v, outc, outg,
-                                 &resume_err, &resume_bad);
+        resume_rc |= decode_both(hc, hr, mr, n_pos + t, L, q_dim, kv_dim, q, k, v, outc, outg,
+                                 &resume_err, &resume_bad, &resume_fallback);
     const int resume_cache_eq = caches_equal(mc, mr);
     gpu_shutdown();
 
@@ -237,11 +261,11 @@ static int run_attn(int argc, char **argv) {
             "prefill_cache_eq=%d decode_rc=%d decode_err=%.6e decode_bad=%d decode_cache_eq=%d "
             "rc_download=%d download_eq=%d rc_save=%d file_eq=%d rc_reinit=%d rc_reupload=%d "
             "loaded=%d rc_kv_upload=%d resume_rc=%d resume_err=%.6e resume_bad=%d "
-            "resume_cache_eq=%d\n",
+            "resume_cache_eq=%d prefill_fallback=%d decode_fallback=%d resume_fallback=%d\n",
             rc_init, rc_upload, prefill_rc, prefill_err, prefill_bad, prefill_cache_eq, decode_rc,
             decode_err, decode_bad, decode_cache_eq, rc_download, download_eq, rc_save, file_eq,
             rc_reinit, rc_reupload, loaded, rc_kv_upload, resume_rc, resume_err, resume_bad,
-            resume_cache_eq);
+            resume_cache_eq, prefill_fallback, decode_fallback, resume_fallback);
     fclose(fo);
     remove(fc);
     remove(fg);

@@ -38,11 +38,13 @@ needs_exe = pytest.mark.skipif(
 PREC = 5e-5
 
 
-def run_attn(tmp_path, L, Hq, Hkv, D, S_, rt, P, T, R, seed):
+def run_attn(tmp_path, L, Hq, Hkv, D, S_, rt, P, T, R, seed, env_extra=None):
     out = tmp_path / "attn.txt"
     args = [EXE, "attn"] + [str(a) for a in (L, Hq, Hkv, D, S_, rt, P, T, R, seed)] + [str(out)]
-    print(f"[case] ref-model attn {args[2:-1]}", flush=True)
-    r = subprocess.run(args, capture_output=True, text=True, timeout=240)
+    env = dict(os.environ)
+    env.update(env_extra or {})
+    print(f"[case] ref-model attn {args[2:-1]} env {env_extra}", flush=True)
+    r = subprocess.run(args, capture_output=True, text=True, timeout=240, env=env)
     assert r.returncode == 0, r.stderr
     kv = dict(item.split("=") for item in out.read_text().split())
     return {k: float(v) if "err" in k else int(v) for k, v in kv.items()}
@@ -72,6 +74,44 @@ def test_attention_hooks_with_reference_model(tmp_path, case):
     assert r["rc_save"] == 0 and r["file_eq"] == 1
     assert r["rc_reinit"] == 0 and r["rc_reupload"] == 0
     assert r["loaded"] == P + T and r["rc_kv_upload"] == 0
+    assert r["resume_cache_eq"] == 1
+    assert r["prefill_fallback"] == 0 and r["decode_fallback"] == 0 and r["resume_fallback"] == 0
+
+
+@needs_exe
+@pytest.mark.parametrize("fail_after", [1, 3, 8])
+def test_injected_failure_falls_back_to_the_reference(tmp_path, fail_after):
+    """PICOLM_HIP_FAIL_AFTER=N: the attention hook call after N successful
+    ones fails after its kernels ran (device cache ahead of the host's), the
+    backend is lost, and the harness answers every later -1 as picolm's call
+    sites do, with the reference's CPU block on the same model_t.  Outputs stay
+    within the bound and the host caches -- the only copy once the device is
+    lost -- equal the CPU model's bit for bit; kvcache_save writes the same
+    file, and a fresh model (whose own gpu_init re-arms the switch) resumes
+    from it.  Calls: prefill 2 layers, then 4 tokens x 2 layers, then 3 x 2."""
+    L, P, T, R = 2, 9, 4, 3
+    r = run_attn(tmp_path, L, 32, 4, 64, 64, 0, P, T, R, seed=13,
+                 env_extra={"PICOLM_HIP_FAIL_AFTER": str(fail_after)})
+    assert r["rc_init"] == 0 and r["rc_upload"] == 0
+    for phase in ("prefill", "decode", "resume"):
+        assert r[f"{phase}_err"] <= PREC, (phase, r)
+        assert r[f"{phase}_bad"] == 0, (phase, r)
+    # hook calls before the failure succeed; the failing call and all later
+    # ones of the same backend fall back
+    calls = [L] + [T * L]
+    pre_ok = min(fail_after, L)
+    dec_ok = min(max(fail_after - L, 0), T * L)
+    assert r["prefill_fallback"] == L - pre_ok
+    assert r["decode_fallback"] == T * L - dec_ok
+    assert (r["prefill_rc"] == 0) == (pre_ok == L)
+    assert (r["decode_rc"] == 0) == (dec_ok == T * L)
+    assert r["prefill_cache_eq"] == 1 and r["decode_cache_eq"] == 1
+    lost = fail_after < sum(calls)
+    assert r["rc_download"] == (-1 if lost else 0) and r["download_eq"] == 1
+    assert r["rc_save"] == 0 and r["file_eq"] == 1
+    assert r["rc_reinit"] == 0 and r["rc_reupload"] == 0
+    assert r["loaded"] == P + T and r["rc_kv_upload"] == 0
+    assert r["resume_fallback"] == R * L - min(fail_after, R * L)
     assert r["resume_cache_eq"] == 1
 
 
