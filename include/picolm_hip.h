@@ -308,7 +308,10 @@ int plh_forward_prefill(const plh_model *m, const int *tokens, int n_tokens, int
  * launch of its own (1) instead of inside the GEMVs that read it (0,
  * default); key 5: prefill launches with fewer q blocks than workgroup slots
  * split their heavy blocks into chunks of tiles merged afterwards (0
- * automatic, -1 never, 2, 4, 8 or 16 tiles per chunk). */
+ * automatic, -1 never, 2, 4, 8 or 16 tiles per chunk); key 6: prefill
+ * launches of at most one q block per CU run each block in a workgroup of 2
+ * or 3 groups of 4 waves that share its tiles and merge in LDS (0
+ * automatic, -1 never, 2 or 3 groups; head_dim 128 takes at most 2). */
 int plh_set_tuning(int key, int value);
 
 #ifdef __cplusplus

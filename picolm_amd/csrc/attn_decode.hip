@@ -704,6 +704,14 @@ extern "C" int plh_set_tuning(int key, int value) {
     g_prefill_split = value;
     return 0;
   }
+  if (key == 6) {
+    if (value != 0 && value != -1 && value != 2 && value != 3) {
+      set_error("plh_set_tuning: prefill K-split must be 0, -1, 2 or 3");
+      return -1;
+    }
+    g_prefill_ksplit = value;
+    return 0;
+  }
   set_error("plh_set_tuning: unknown key %d", key);
   return -1;
 }

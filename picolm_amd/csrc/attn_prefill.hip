@@ -181,9 +181,16 @@ __host__ __device__ inline int prefill_unit_tiles(const PrefillArgs& a, int qb) 
 // range, normalised output written to a.out; else one chunk of a split unit,
 // whose unnormalised O, running maximum and sum go to partial slot `slot`
 // (prefill_merge_kernel combines the chunks).
-template <int D, bool QKN>
-__device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16* smem, int group,
-                                                  int qb, int tb, int te, int slot) {
+//
+// KS > 1 (prefill_attn_ksplit_kernel, whole units only): the workgroup is KS
+// groups of 4 waves, group g taking tiles tb+g, tb+g+KS, ... with its own LDS
+// tile buffers; every group runs the same number of iterations (a group past
+// the unit's last tile only joins the barrier), and at the end groups 1.. pass
+// their (O, running maximum, sum) through LDS to group 0, which merges them
+// like prefill_merge_kernel and writes the output.
+template <int D, bool QKN, int KS = 1>
+__device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16* smem_wg,
+                                                  int group, int qb, int tb, int te, int slot) {
   constexpr int NS = D / 16;        // 16-deep k-steps of QK
   constexpr int NDB = D / 32;       // 32-row d blocks of O^T
   constexpr int KP = PrefillLds<D>::KP, VP = PrefillLds<D>::VP;
@@ -193,7 +200,9 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
   constexpr int LPT = 2 * KCH / kPThreads;  // chunks per thread: the first LPT/2 are K
   static_assert(KCH % kPThreads == 0, "tile chunks must split evenly over the workgroup");
 
-  const int tid = threadIdx.x;
+  const int tid = (int)threadIdx.x & (kPThreads - 1);    // thread within its wave group
+  const int kg = KS > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x / kPThreads) : 0;
+  _Float16* const smem = smem_wg + kg * PrefillLds<D>::HALVES;  // the group's tile buffers
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 31, half = lane >> 5;
@@ -253,7 +262,7 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
     for (int u = 0; u < LPT; ++u)
       *(half8_t*)&smem[st_off[u] + b * (u < LPT / 2 ? KBUF : VBUF)] = ld[u];
   };
-  issue_loads(tb * kKT);
+  issue_loads((tb + kg) * kKT);
 
   // ---- q operand of this lane's column: element 16*s + 8*half + e of the
   // rotated head row, split into fp16 hi + lo, in qh[s][e] and ql[s][e].
@@ -391,11 +400,11 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
 
   // one tile in buffer b (a constant at each call site, so the LDS offsets
   // fold into the instructions)
-  auto tile = [&](const int b, const int it) {
+  auto tile = [&](const int b, const int it) {   // it: the group's tile, maybe past the end
     const int t0 = it * kKT;
-    const bool more = it + 1 < n_tiles;
-    if (more) issue_loads(t0 + kKT);
-    if (t0 <= p_max) {  // else every column of the wave is masked on this tile
+    const bool more = it + KS < n_tiles;
+    if (more) issue_loads(t0 + KS * kKT);
+    if (it < n_tiles && t0 <= p_max) {  // else every column of the wave is masked here
       f32x16_t s = negm;
 #pragma unroll
       for (int st = 0; st < NS; ++st) {
@@ -466,13 +475,60 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
     if (more) store_lds(b ^ 1);
     __syncthreads();
   };
-  for (int it = tb; it < n_tiles; it += 2) {
-    tile(0, it);
-    if (it + 1 < n_tiles) tile(1, it + 1);
+  const int n_iter = (n_tiles - tb + KS - 1) / KS;  // the same for every group
+  for (int i = 0; i < n_iter; i += 2) {
+    tile(0, tb + i * KS + kg);
+    if (i + 1 < n_iter) tile(1, tb + (i + 1) * KS + kg);
   }
 
   // ---- normalise and write: lane holds d = 32*db + 8*(v/4) + 4*half + v%4 --
-  const float lsum = add_xor32((ls[0] + ls[1]) + (ls[2] + ls[3]));
+  float lsum = add_xor32((ls[0] + ls[1]) + (ls[2] + ls[3]));
+  if (KS > 1) {
+    // groups 1.. hand (O, m, l) of each column to group 0 through LDS (the
+    // tile buffers are dead: the last barrier followed every tile read)
+    constexpr int MP = D + 4;  // floats per column
+    float* mb = reinterpret_cast<float*>(smem_wg);
+    if (kg > 0) {
+      float* dst = mb + ((size_t)(kg - 1) * kPCols + c) * MP;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          *(float4*)(dst + 32 * db + 8 * r4 + 4 * half) =
+              make_float4(o[db][4 * r4], o[db][4 * r4 + 1], o[db][4 * r4 + 2], o[db][4 * r4 + 3]);
+      if (half == 0) {
+        dst[D] = fresh ? -INFINITY : ms;
+        dst[D + 1] = lsum;
+      }
+    }
+    __syncthreads();
+    if (kg > 0) return;
+    // group 0 always holds the unit's first tile (row 0, never masked), so
+    // its maximum is finite
+    float M = ms;
+#pragma unroll
+    for (int g = 1; g < KS; ++g) M = vmax(M, mb[((size_t)(g - 1) * kPCols + c) * MP + D]);
+    const float w0 = fast_exp2(ms - M);
+    lsum *= w0;
+#pragma unroll
+    for (int db = 0; db < NDB; ++db) o[db] *= w0;
+#pragma unroll
+    for (int g = 1; g < KS; ++g) {
+      const float* src = mb + ((size_t)(g - 1) * kPCols + c) * MP;
+      const float wg = fast_exp2(src[D] - M);  // 0 for a group that saw no key
+      lsum = __builtin_fmaf(src[D + 1], wg, lsum);
+#pragma unroll
+      for (int db = 0; db < NDB; ++db)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const float4 x = *(const float4*)(src + 32 * db + 8 * r4 + 4 * half);
+          o[db][4 * r4 + 0] = __builtin_fmaf(x.x, wg, o[db][4 * r4 + 0]);
+          o[db][4 * r4 + 1] = __builtin_fmaf(x.y, wg, o[db][4 * r4 + 1]);
+          o[db][4 * r4 + 2] = __builtin_fmaf(x.z, wg, o[db][4 * r4 + 2]);
+          o[db][4 * r4 + 3] = __builtin_fmaf(x.w, wg, o[db][4 * r4 + 3]);
+        }
+    }
+  }
   if (slot >= 0) {
     // a chunk's partial: O, ms (-inf for a column with no unmasked key in the
     // chunk) and the sum, per column of the unit
@@ -584,6 +640,32 @@ __global__ __launch_bounds__(kPThreads) void prefill_attn_kernel(PrefillArgs a) 
   if (p != nq - 1 - p) prefill_attn_unit<D, QKN>(a, smem, group, p, 0, INT_MAX, -1);
 }
 
+// K-split workgroups for launches of a few units (one layer of a whole
+// prompt: fewer units than CUs): KS groups of 4 waves share each unit's
+// tiles, so a group takes ~1/KS of the heaviest unit's tiles; units in
+// heaviest-first order.  LDS: KS tile buffers, reused for the groups' merge.
+template <int D, int KS>
+struct KsplitLds {
+  static constexpr size_t kTiles = (size_t)KS * PrefillLds<D>::HALVES * 2;
+  static constexpr size_t kMerge = (size_t)(KS - 1) * kPCols * (D + 4) * 4;
+  static constexpr size_t kBytes = kTiles > kMerge ? kTiles : kMerge;
+};
+template <int D, bool QKN, int KS>
+__global__ __launch_bounds__(kPThreads * KS) void prefill_attn_ksplit_kernel(PrefillArgs a) {
+  __shared__ __align__(16) _Float16 smem[KsplitLds<D, KS>::kBytes / 2];
+  sgpr_ready(a.q), sgpr_ready(a.kc), sgpr_ready(a.vc), sgpr_ready(a.cos_t);
+  sgpr_ready(a.sin_t), sgpr_ready(a.layer0), sgpr_ready(a.n_launch_layers);
+  sgpr_ready(a.n_heads), sgpr_ready(a.n_kv_heads), sgpr_ready(a.max_seq_len);
+  sgpr_ready(a.rope_type), sgpr_ready(a.start_pos), sgpr_ready(a.n_tokens), sgpr_ready(a.bq);
+  sgpr_ready(a.n_qblk), sgpr_ready(a.score_scale);
+  if (QKN) sgpr_ready(a.qn);
+  const int n_groups = a.n_launch_layers * a.n_kv_heads;
+  const int l = (int)blockIdx.x;
+  const int qb = a.n_qblk - 1 - l / n_groups, group = l % n_groups;
+  if (qb < 0) return;
+  prefill_attn_unit<D, QKN, KS>(a, smem, group, qb, 0, INT_MAX, -1);
+}
+
 // Combines the chunks of split units, one thread per (unit, column, 4 output
 // elements); units with a single chunk wrote their output directly.  Per
 // column: M = max of the chunks' maxima, out = sum 2^(m-M) O / sum 2^(m-M) l
@@ -631,6 +713,9 @@ namespace plh {
 // plh_set_tuning key 5: prefill chunking of small launches (0 automatic, -1
 // never, or a fixed chunk of 2, 4, 8 or 16 tiles)
 int g_prefill_split = 0;
+// plh_set_tuning key 6: K-split workgroups (0 automatic, -1 never, 2 or 3
+// groups of 4 waves; 3 only for head_dim 64)
+int g_prefill_ksplit = 0;
 }  // namespace plh
 
 static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head_dim,
@@ -751,6 +836,23 @@ static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head
       a.per_xcd = a.groups_per_xcd * pick_cpg;
     }
   }
+  // Launches of more blocks than that but at most one per CU (one layer of a
+  // whole prompt) run each block in one K-split workgroup: 2 groups of 4
+  // waves share its tiles and merge in LDS.  The groups share the CU's
+  // SIMDs, so a tile costs a group more than a lone one: one-layer launches
+  // of 512 tokens measured TinyLlama 16.3 -> 14.8 us (3 groups: 15.3),
+  // Llama-2 1024 tokens 46.1 -> 40.6 us.  3 groups only when forced, and
+  // only for head_dim 64 (head_dim 128 has registers for 2 waves per SIMD).
+  int ksplit = 0;
+  if (!a.paired && a.split_tiles == 0 && g_prefill_ksplit >= 0) {
+    const int cus = c.num_cus > 0 ? c.num_cus : 256;
+    const int kmax = head_dim == 64 ? 3 : 2;
+    if (g_prefill_ksplit > 0)
+      ksplit = g_prefill_ksplit < kmax ? g_prefill_ksplit : kmax;
+    else if ((long)a.n_units * 4 > cus && a.n_units <= cus &&
+             prefill_unit_tiles(a, a.n_qblk - 1) >= 4)
+      ksplit = 2;
+  }
   // K/V bytes one XCD slice reads: by q-block order when they fit in a
   // comfortable share of the XCD's 4 MB L2
   const double slice_kv = (double)a.groups_per_xcd * (start_pos + n_tokens) * head_dim * 2 * 2;
@@ -777,6 +879,26 @@ static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head
       hipLaunchKernelGGL((prefill_append_kernel<128, false>), ag, ab256, 0, c.stream, a);
   }
   if (check_hip(hipGetLastError(), "prefill_append_kernel")) return -1;
+  if (ksplit > 0) {
+    const dim3 kg((unsigned)a.n_units), kb((unsigned)(kPThreads * ksplit));
+    if (head_dim == 64 && ksplit == 3) {
+      if (qkn)
+        hipLaunchKernelGGL((prefill_attn_ksplit_kernel<64, true, 3>), kg, kb, 0, c.stream, a);
+      else
+        hipLaunchKernelGGL((prefill_attn_ksplit_kernel<64, false, 3>), kg, kb, 0, c.stream, a);
+    } else if (head_dim == 64) {
+      if (qkn)
+        hipLaunchKernelGGL((prefill_attn_ksplit_kernel<64, true, 2>), kg, kb, 0, c.stream, a);
+      else
+        hipLaunchKernelGGL((prefill_attn_ksplit_kernel<64, false, 2>), kg, kb, 0, c.stream, a);
+    } else {
+      if (qkn)
+        hipLaunchKernelGGL((prefill_attn_ksplit_kernel<128, true, 2>), kg, kb, 0, c.stream, a);
+      else
+        hipLaunchKernelGGL((prefill_attn_ksplit_kernel<128, false, 2>), kg, kb, 0, c.stream, a);
+    }
+    return check_hip(hipGetLastError(), "prefill_attn_ksplit_kernel");
+  }
   if (head_dim == 64) {
     if (qkn)
       hipLaunchKernelGGL((prefill_attn_kernel<64, true>), pg, pb, 0, c.stream, a);

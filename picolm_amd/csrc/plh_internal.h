@@ -40,6 +40,9 @@ extern int g_gemv_rows_per_thread;
 // plh_set_tuning key 5: prefill chunking of small launches (0 automatic, -1
 // never, 2/4/8/16 a fixed chunk size in tiles).
 extern int g_prefill_split;
+// plh_set_tuning key 6: prefill K-split workgroups (0 automatic, -1 never, 2
+// or 3 groups of 4 waves).
+extern int g_prefill_ksplit;
 // plh_set_tuning key 4: 1 = the forward pass forms rmsnorm(x) in a launch of
 // its own instead of inside the GEMVs that read it.
 extern int g_fwd_norm_separate;

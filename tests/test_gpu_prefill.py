@@ -157,6 +157,48 @@ def test_prefill_small(gpu, oracle_mod, case):
     run_prefill(gpu, oracle_mod, cfg, start, n, seed=start * 7 + n + D)
 
 
+# K-split workgroups (2 or 3 groups of 4 waves share a q block's tiles and
+# merge in LDS): automatic for one-layer launches of a whole prompt (more q
+# blocks than a quarter of the CUs, at most one per CU), forced through
+# plh_set_tuning key 6 otherwise (3 groups only for head_dim 64)
+KSPLIT = [
+    # (n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, theta, rope_type, start, n,
+    #  layer, groups: 0 = automatic)
+    (3, 32, 4, 64, 1024, 1e4, 0, 0, 512, 1, 0),     # TinyLlama heads: 128 q blocks
+    (2, 32, 4, 64, 1024, 1e4, 0, 0, 512, 0, 2),     # the same, 2 groups
+    (2, 32, 8, 64, 800, 5e5, 0, 0, 500, 1, 0),      # Llama-3.2 heads: 128 q blocks
+    (2, 32, 32, 128, 1100, 1e4, 0, 0, 1024, 0, 0),  # Llama-2 MHA, D = 128: 256 q blocks
+    (2, 32, 4, 64, 600, 1e4, 0, 37, 500, 0, 3),     # prefix rows, ragged last block
+    (2, 8, 2, 128, 300, 1e6, 1, 10, 150, 1, 2),     # QWEN rotation, D = 128
+]
+
+
+@pytest.mark.parametrize("case", KSPLIT)
+def test_prefill_one_layer_ksplit(gpu, oracle_mod, case):
+    L, Hq, Hkv, D, S, theta, rt, start, n, layer, groups = case
+    cfg = gpu.AttnConfig(L, Hq, Hkv, D, S, theta, rt)
+    gpu.check(gpu.lib.plh_set_tuning(6, groups), "plh_set_tuning")
+    try:
+        run_prefill(gpu, oracle_mod, cfg, start, n, seed=start + n + layer + 5,
+                    check_layers=[0], layer_range=(layer, 1))
+    finally:
+        gpu.lib.plh_set_tuning(6, 0)
+
+
+@pytest.mark.parametrize("groups", [2, 3])
+@pytest.mark.parametrize("case", SMALL)
+def test_prefill_small_ksplit(gpu, oracle_mod, case, groups):
+    """Every small case through forced K-split workgroups (all layers in one
+    launch; groups without a tile of their own, masked first tiles)."""
+    L, Hq, Hkv, D, S, theta, rt, start, n = case
+    cfg = gpu.AttnConfig(L, Hq, Hkv, D, S, theta, rt)
+    gpu.check(gpu.lib.plh_set_tuning(6, groups), "plh_set_tuning")
+    try:
+        run_prefill(gpu, oracle_mod, cfg, start, n, seed=start * 5 + n + D + groups)
+    finally:
+        gpu.lib.plh_set_tuning(6, 0)
+
+
 def test_prefill_per_layer_and_all_layers(gpu, oracle_mod):
     cfg = gpu.AttnConfig(3, 32, 4, 64, 256, 1e4, 0)
     a = run_prefill(gpu, oracle_mod, cfg, 20, 70, seed=4, per_layer=True)

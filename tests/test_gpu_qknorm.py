@@ -129,10 +129,12 @@ def test_qknorm_needs_both_weights(gpu):
     cache.free()
 
 
+@pytest.mark.parametrize("tuning", [(5, 4), (6, 2), (6, 3)], ids=["chunks4", "ksplit2", "ksplit3"])
 @pytest.mark.parametrize("dims", CONFIGS[:2])
-def test_prefill_qknorm_one_layer_split(gpu, oracle_mod, dims):
+def test_prefill_qknorm_one_layer_split(gpu, oracle_mod, dims, tuning):
     """One layer of a prompt whose heavy q blocks are split into 4-tile chunks
-    (plh_set_tuning key 5) and merged: QK-norm inside every chunk's prologue."""
+    (plh_set_tuning key 5) and merged, or run by K-split workgroups (key 6):
+    QK-norm inside every chunk's or wave group's prologue."""
     O = oracle_mod
     L, Hq, Hkv, D, S, theta, rt = dims
     cfg = gpu.AttnConfig(L, Hq, Hkv, D, S, theta, rt)
@@ -145,18 +147,18 @@ def test_prefill_qknorm_one_layer_split(gpu, oracle_mod, dims):
     q = normal_f32(rng, (n, cfg.q_dim), 3.0)
     k = normal_f32(rng, (n, cfg.kv_dim), 3.0)
     v = normal_f32(rng, (n, cfg.kv_dim))
-    print(f"[case] prefill qknorm split {dims} start {start} n {n}", flush=True)
+    print(f"[case] prefill qknorm split {dims} start {start} n {n} tuning {tuning}", flush=True)
     cache = gpu.KVCache(cfg)
     cache.load(kc, vc)
     dq, dk, dv = (gpu.DeviceBuffer.from_numpy(x) for x in (q, k, v))
     dout = gpu.DeviceBuffer(n * cfg.q_dim * 4)
-    gpu.check(gpu.lib.plh_set_tuning(5, 4), "plh_set_tuning")
+    gpu.check(gpu.lib.plh_set_tuning(*tuning), "plh_set_tuning")
     try:
         gpu.prefill(cache, 1, start, n, dq.ptr, dk.ptr, dv.ptr, dout.ptr, None, 1,
                     q_norm=dqw.ptr, k_norm=dkw.ptr, norm_eps=EPS)
         gpu.synchronize()
     finally:
-        gpu.lib.plh_set_tuning(5, 0)
+        gpu.lib.plh_set_tuning(tuning[0], 0)
     out = dout.download(np.float32, (n, cfg.q_dim))
     gk, gv = cache.fetch()
     cache.free()
