@@ -384,7 +384,9 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
   // (as rounded for the MFMA) with v_dot2_f32_f16 in fp32; the two halves of
   // a column are added at the end.
   float ms = 0.f;
-  bool fresh = true;                // no unmasked key seen yet (ms, lsum, o all 0)
+  // Raise threshold of ms: -inf while the column is fresh (no unmasked key
+  // seen yet; ms, the sums and o all 0), kLazy after (one compare per tile)
+  float thr = -INFINITY;
   f32x16_t negm = {};               // -ms * 2^-e, the QK accumulator start
   float ls[4] = {0.f, 0.f, 0.f, 0.f};  // this lane's half of the running sum, in 4
                                        // partial sums (independent add chains)
@@ -432,15 +434,16 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
           max_xor32(vmax(vmax(vmax(m0, m1), m2), vmax(vmax(m3, m4), t[15])));
       // fresh columns with an unmasked key take its maximum as ms (nothing
       // accumulated yet); others raise ms by the excess beyond kLazy
-      const bool upd = fresh ? tmax != -INFINITY : tmax > kLazy;
+      const bool upd = tmax > thr;
       if (__ballot(upd)) {
         const float d = upd ? tmax : 0.f;
+        const bool fresh = thr == -INFINITY;
         const float alpha = fresh ? 1.f : fast_exp2(-d);
 #pragma unroll
         for (int k = 0; k < 4; ++k) ls[k] *= alpha;
 #pragma unroll
         for (int db = 0; db < NDB; ++db) o[db] *= alpha;
-        fresh = fresh && !upd;
+        thr = upd ? kLazy : thr;
         ms += d;
         const float nm = -ms * qdown;
 #pragma unroll
@@ -497,7 +500,7 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
           *(float4*)(dst + 32 * db + 8 * r4 + 4 * half) =
               make_float4(o[db][4 * r4], o[db][4 * r4 + 1], o[db][4 * r4 + 2], o[db][4 * r4 + 3]);
       if (half == 0) {
-        dst[D] = fresh ? -INFINITY : ms;
+        dst[D] = thr == -INFINITY ? -INFINITY : ms;
         dst[D + 1] = lsum;
       }
     }
@@ -542,7 +545,7 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
           *(float4*)(po + 32 * db + 8 * r4 + 4 * half) =
               make_float4(o[db][4 * r4], o[db][4 * r4 + 1], o[db][4 * r4 + 2], o[db][4 * r4 + 3]);
       if (half == 0) {
-        a.part_m[pc] = fresh ? -INFINITY : ms;
+        a.part_m[pc] = thr == -INFINITY ? -INFINITY : ms;
         a.part_l[pc] = lsum;
       }
     }
