@@ -167,6 +167,7 @@ struct PrefillLds {
   static constexpr int VBUF = kKT * VP;     // one V tile buffer (halves)
   static constexpr int VOFF = 2 * KBUF;     // V buffers follow the two K buffers
   static constexpr int HALVES = 2 * KBUF + 2 * VBUF;
+  static constexpr int QSTAGE = kPCols * (D + 4) * 2;  // the staged q block (halves)
 };
 
 // Tiles of the q block qb of a launch: its last token's causal limit, in
@@ -200,6 +201,10 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
   constexpr int LPT = 2 * KCH / kPThreads;  // chunks per thread: the first LPT/2 are K
   static_assert(KCH % kPThreads == 0, "tile chunks must split evenly over the workgroup");
 
+  // K-split workgroups stage the unit's q block in LDS (their wave groups
+  // share it); one-group workgroups load their columns directly, which keeps
+  // their register peak (and occupancy) where it was
+  constexpr bool kStageQ = KS > 1;
   const int tid = (int)threadIdx.x & (kPThreads - 1);    // thread within its wave group
   const int kg = KS > 1 ? __builtin_amdgcn_readfirstlane((int)threadIdx.x / kPThreads) : 0;
   _Float16* const smem = smem_wg + kg * PrefillLds<D>::HALVES;  // the group's tile buffers
@@ -264,22 +269,55 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
   };
   issue_loads((tb + kg) * kKT);
 
+  // ---- the unit's q block, staged in LDS by coalesced loads.  Token t of
+  // the block holds the G heads of this kv head side by side (G*D floats), so
+  // column c = t*G + hh is element run c*D.. of the token-major block; it
+  // goes to LDS row c (pitch QSP).  Every wave group of a K-split workgroup
+  // reads the same staged block.  The staging overlays the tile buffers,
+  // which are first written after the barrier that follows all reads.
+  constexpr int QSP = D + 4;  // floats per staged column: rows start in distinct banks
+  float* const qs = reinterpret_cast<float*>(smem_wg);
+  if constexpr (kStageQ) {
+    constexpr int kChunks = kPCols * D / 4;  // float4s of a full block
+    constexpr int kPer = (kChunks + kPThreads * KS - 1) / (kPThreads * KS);
+    const int gch = G * D / 4;                // float4s per token
+    const int n_chunks = a.bq * gch;
+    const float* qblk = a.q + (size_t)li * a.n_tokens * q_dim + (size_t)kvh * G * D;
+    // chunks past the block repeat its last one (the same load and store),
+    // so every thread runs the same straight-line code; tokens past the
+    // prompt re-read the last token
+    float4 qv[kPer];
+    uint32_t dst[kPer];
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) {
+      const int j = min((int)threadIdx.x + u * kPThreads * KS, n_chunks - 1);
+      const int t = j / gch, e = 4 * (j - t * gch);  // element of the token's run
+      qv[u] = *(const float4*)(qblk + (uint32_t)min(i0 + t, last_tok) * (uint32_t)q_dim + e);
+      dst[u] = (uint32_t)((t * G + e / D) * QSP + e % D);
+    }
+#pragma unroll
+    for (int u = 0; u < kPer; ++u) *(float4*)(qs + dst[u]) = qv[u];
+    __syncthreads();
+  }
+
   // ---- q operand of this lane's column: element 16*s + 8*half + e of the
   // rotated head row, split into fp16 hi + lo, in qh[s][e] and ql[s][e].
-  // Columns past the prompt (cvalid false) read the last token's row and are
-  // never stored; each column's softmax is independent, so they need no mask.
+  // Columns past the prompt (cvalid false) read column 0 and are never
+  // stored; each column's softmax is independent, so they need no mask.
   half8_t qh[NS], ql[NS];
   float qup, qdown;  // 2^e and 2^-e of the column's range scale
   {
-    const float* qrow = a.q + ((size_t)li * a.n_tokens + tok_c) * q_dim +
-                        (size_t)(kvh * G + (cvalid ? hh : 0)) * D;
+    const float* qcol =
+        kStageQ ? qs + (cvalid ? c : 0) * QSP + 8 * half
+                : a.q + ((size_t)li * a.n_tokens + tok_c) * q_dim +
+                      (size_t)(kvh * G + (cvalid ? hh : 0)) * D + 8 * half;
     const float* cr = a.cos_t + (size_t)p_col * (D / 2);
     const float* sr = a.sin_t + (size_t)p_col * (D / 2);
     float qf[NS][8];
 #pragma unroll
     for (int s = 0; s < NS; ++s) {
-      const float4 x0 = *(const float4*)(qrow + 16 * s + 8 * half);
-      const float4 x1 = *(const float4*)(qrow + 16 * s + 8 * half + 4);
+      const float4 x0 = *(const float4*)(qcol + 16 * s);
+      const float4 x1 = *(const float4*)(qcol + 16 * s + 4);
       qf[s][0] = x0.x, qf[s][1] = x0.y, qf[s][2] = x0.z, qf[s][3] = x0.w;
       qf[s][4] = x1.x, qf[s][5] = x1.y, qf[s][6] = x1.z, qf[s][7] = x1.w;
     }
@@ -360,6 +398,7 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
       }
   }
 
+  if (kStageQ) __syncthreads();  // every lane has read its q column: the tile buffers are free
   store_lds(0);
   __syncthreads();
 
@@ -651,7 +690,9 @@ template <int D, int KS>
 struct KsplitLds {
   static constexpr size_t kTiles = (size_t)KS * PrefillLds<D>::HALVES * 2;
   static constexpr size_t kMerge = (size_t)(KS - 1) * kPCols * (D + 4) * 4;
-  static constexpr size_t kBytes = kTiles > kMerge ? kTiles : kMerge;
+  static constexpr size_t kStage = (size_t)PrefillLds<D>::QSTAGE * 2;
+  static constexpr size_t kTM = kTiles > kMerge ? kTiles : kMerge;
+  static constexpr size_t kBytes = kTM > kStage ? kTM : kStage;
 };
 template <int D, bool QKN, int KS>
 __global__ __launch_bounds__(kPThreads * KS) void prefill_attn_ksplit_kernel(PrefillArgs a) {
