@@ -598,12 +598,19 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) {
-        float4 w;
-        w.x = o[db][4 * r4 + 0] * inv;
-        w.y = o[db][4 * r4 + 1] * inv;
-        w.z = o[db][4 * r4 + 2] * inv;
-        w.w = o[db][4 * r4 + 3] * inv;
-        *(float4*)(orow + 32 * db + 8 * r4 + 4 * half) = w;
+        float4_t w;
+        w[0] = o[db][4 * r4 + 0] * inv;
+        w[1] = o[db][4 * r4 + 1] * inv;
+        w[2] = o[db][4 * r4 + 2] * inv;
+        w[3] = o[db][4 * r4 + 3] * inv;
+        float4_t* dst = (float4_t*)(orow + 32 * db + 8 * r4 + 4 * half);
+        // K-split workgroups run one-layer launches: streaming stores there
+        // leave less in L2 for the end-of-launch write-back (per-layer
+        // TinyLlama 433 -> 420 us); the many-workgroup launches lose with them
+        if constexpr (KS > 1)
+          __builtin_nontemporal_store(w, dst);
+        else
+          *dst = w;
       }
   }
 }
