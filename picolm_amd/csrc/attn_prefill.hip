@@ -856,24 +856,33 @@ static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head
   const long slots = 3L * (c.num_cus > 0 ? c.num_cus : 256);
   a.paired = a.n_qblk >= 4 && a.n_units >= 8 * slots ? 1 : 0;
   a.per_xcd = a.groups_per_xcd * (a.paired ? (a.n_qblk + 1) / 2 : a.n_qblk);
-  // Launches with few q blocks (one layer of a prompt chunk, late in the
-  // prompt: at most a quarter as many blocks as CUs) split blocks of more
-  // than 8 tiles into chunks of 8 tiles, merged afterwards: the heaviest
-  // block is the critical path.  Measured on one-layer launches of 128
-  // tokens at start 1024: TinyLlama 32 -> 23 us, Llama-2 51 -> 32 us; launches
-  // with more blocks lose to the extra prologues and the merge.
+  // Launches with few q blocks (one layer of a prompt chunk, or of a short
+  // or narrow prompt: at most a quarter as many blocks as CUs) split their
+  // blocks into chunks of T tiles, merged afterwards: the heaviest block is
+  // the critical path.  Blocks of more than 8 tiles are split; T is the
+  // smallest of 2, 4, 8 whose chunks still fit one per CU, else 8.  Measured on one-layer launches: 128 tokens at start
+  // 1024 (T = 8), TinyLlama 32 -> 23 us, Llama-2 51 -> 32 us; Qwen3 512
+  // tokens from 0 (T = 4), 820 -> 790 us per 28-layer step against T = 8;
+  // launches with more blocks lose to the extra prologues and the merge.
   a.split_tiles = 0;
   a.chunks_per_group = 0;
   if (!a.paired && g_prefill_split >= 0) {
     const int max_tiles = prefill_unit_tiles(a, a.n_qblk - 1);
     const int cus = c.num_cus > 0 ? c.num_cus : 256;
-    int pick = 0, pick_cpg = 0;
-    const int T = g_prefill_split > 0 ? g_prefill_split : 8;
-    if (max_tiles > T && (g_prefill_split > 0 || (long)a.n_units * 4 <= cus)) {
+    auto chunks_of = [&](int T) {
       int cpg = 0;
       for (int qb = 0; qb < a.n_qblk; ++qb) cpg += (prefill_unit_tiles(a, qb) + T - 1) / T;
-      pick = T, pick_cpg = cpg;
+      return cpg;
+    };
+    int pick = 0, pick_cpg = 0;
+    if (g_prefill_split > 0) {
+      if (max_tiles > g_prefill_split) pick = g_prefill_split;
+    } else if ((long)a.n_units * 4 <= cus && max_tiles > 8) {
+      for (int T = 2; T < 8 && !pick; T *= 2)
+        if ((long)n_groups * chunks_of(T) <= cus) pick = T;
+      if (!pick) pick = 8;
     }
+    if (pick) pick_cpg = chunks_of(pick);
     if (pick) {
       const size_t n_slots = (size_t)n_groups * pick_cpg;
       const size_t po = n_slots * kPCols * head_dim * sizeof(float);
