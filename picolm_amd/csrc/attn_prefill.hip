@@ -302,8 +302,9 @@ __device__ __forceinline__ void prefill_attn_unit(const PrefillArgs& a, _Float16
 
   // ---- q operand of this lane's column: element 16*s + 8*half + e of the
   // rotated head row, split into fp16 hi + lo, in qh[s][e] and ql[s][e].
-  // Columns past the prompt (cvalid false) read column 0 and are never
-  // stored; each column's softmax is independent, so they need no mask.
+  // Columns past the prompt (cvalid false) read a valid row (column 0 of the
+  // staged block, or head 0 of the last token) and are never stored; each
+  // column's softmax is independent, so they need no mask.
   half8_t qh[NS], ql[NS];
   float qup, qdown;  // 2^e and 2^-e of the column's range scale
   {
