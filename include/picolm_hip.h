@@ -115,6 +115,26 @@ int plh_attn_decode(int n_layers, int n_heads, int n_kv_heads, int head_dim,
                     uint16_t *val_cache, const float *rope_cos,
                     const float *rope_sin, float *out);
 
+/* ---- decode attention that also hands back the appended rows ------------- */
+/* plh_attn_decode (q_norm = k_norm = NULL) or plh_attn_decode_qknorm with the
+ * same arguments and results, whose kernel also writes the fp16 bits of the
+ * appended row `pos` of every launched layer to k_rows and v_rows
+ * ([n_launch_layers][n_kv_heads*head_dim] uint16_t each, layer li at
+ * + li*kv_dim).  Every pointer may be any memory the device can access, such
+ * as pinned host memory from plh_host_alloc: the gpu.h decode hook keeps q,
+ * k, v, out and the rows in pinned staging and so needs no copy launches to
+ * return model.c:822-826's cache rows to the host cache (gpu.c:691-699's
+ * synchronous copy-back, for the attention block).  k_rows and v_rows must
+ * not be null. */
+int plh_attn_decode_rows(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                         int max_seq_len, int rope_type, int layer0,
+                         int n_launch_layers, int pos, const float *q,
+                         const float *k, const float *v, uint16_t *key_cache,
+                         uint16_t *val_cache, const float *rope_cos,
+                         const float *rope_sin, float *out, const float *q_norm,
+                         const float *k_norm, float norm_eps, uint16_t *k_rows,
+                         uint16_t *v_rows);
+
 /* ---- decode attention without allocation -------------------------------- */
 /* No counterpart in the reference.  For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that

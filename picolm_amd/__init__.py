@@ -8,7 +8,7 @@ attention operator, `gemv` its weight matmul (the gpu_try_matmul path), `forward
 forward pass (model_forward) and `synth` random models in GGUF layout.
 """
 from ._native import LIB_PATH, PicolmHipError, check, lib  # noqa: F401
-from .attention import (ROPE_LLAMA, ROPE_QWEN, AttnConfig, KVCache, decode,  # noqa: F401
+from .attention import (ROPE_LLAMA, ROPE_QWEN, AttnConfig, KVCache, decode, decode_rows,  # noqa: F401
                         f16_checksum, f32_to_f16, prefill, rope_tables)
 from .device import DeviceBuffer, Event, Graph, init, synchronize  # noqa: F401
 from .forward import DeviceModel  # noqa: F401

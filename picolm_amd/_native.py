@@ -94,6 +94,7 @@ _SIGS = {
     "plh_attn_decode_noalloc": (_i, [_i] * 9 + [_vp] * 8),
     "plh_attn_prefill": (_i, [_i] * 10 + [_vp] * 8 + [_i]),
     "plh_attn_decode_qknorm": (_i, [_i] * 9 + [_vp] * 10 + [C.c_float]),
+    "plh_attn_decode_rows": (_i, [_i] * 9 + [_vp] * 10 + [C.c_float] + [_vp] * 2),
     "plh_attn_prefill_qknorm": (_i, [_i] * 10 + [_vp] * 8 + [_i, _vp, _vp, C.c_float]),
     # weight GEMV
     "plh_gemv_packed_bytes": (_sz, [_i, _i, _i]),

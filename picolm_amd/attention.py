@@ -108,6 +108,20 @@ def decode(cache: KVCache, layer0: int, pos: int, q: int, k: int, v: int, out: i
               "plh_attn_decode_qknorm")
 
 
+def decode_rows(cache: KVCache, layer0: int, pos: int, q: int, k: int, v: int, out: int,
+                k_rows: int, v_rows: int, n_launch_layers: int = 1, q_norm: int | None = None,
+                k_norm: int | None = None, norm_eps: float = 0.0) -> None:
+    """decode() that also writes the appended rows' fp16 bits to k_rows /
+    v_rows ([n_launch_layers][kv_dim] uint16 each; any device-accessible
+    pointers, pinned host memory included)."""
+    c = cache.cfg
+    check(lib.plh_attn_decode_rows(c.n_layers, c.n_heads, c.n_kv_heads, c.head_dim,
+                                   c.max_seq_len, c.rope_type, layer0, n_launch_layers, pos,
+                                   q, k, v, cache.key.ptr, cache.val.ptr, cache.cos.ptr,
+                                   cache.sin.ptr, out, q_norm, k_norm, norm_eps, k_rows, v_rows),
+          "plh_attn_decode_rows")
+
+
 def prefill(cache: KVCache, layer0: int, start_pos: int, n_tokens: int, q: int, k: int, v: int,
             out: int, out_stride: int | None = None, n_launch_layers: int = 1,
             q_norm: int | None = None, k_norm: int | None = None,

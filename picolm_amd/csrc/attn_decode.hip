@@ -406,6 +406,11 @@ __device__ __forceinline__ void append_new_row(const DecodeArgs& a, int li, int 
       const uint16_t b0 = f16_bits_rha(k0), b1 = f16_bits_rha(k1);
       krow[i0] = b0;
       krow[i1] = b1;
+      if (a.k_rows) {
+        uint16_t* kr = a.k_rows + (size_t)li * kv_dim + (size_t)kvh * D;
+        kr[i0] = b0;
+        kr[i1] = b1;
+      }
       knew[i0] = f16_bits_to_f32(b0);
       knew[i1] = f16_bits_to_f32(b1);
     }
@@ -416,6 +421,7 @@ __device__ __forceinline__ void append_new_row(const DecodeArgs& a, int li, int 
     if (d < D) {
       const uint16_t b = f16_bits_rha(rr.v[u]);
       vrow[d] = b;
+      if (a.v_rows) a.v_rows[(size_t)li * kv_dim + (size_t)kvh * D + d] = b;
       vnew[d] = f16_bits_to_f32(b);
     }
   }
@@ -721,7 +727,8 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
                             int pos, const float* q, const float* k, const float* v,
                             uint16_t* key_cache, uint16_t* val_cache, const float* rope_cos,
                             const float* rope_sin, float* out, const float* q_norm,
-                            const float* k_norm, float norm_eps, bool noalloc) {
+                            const float* k_norm, float norm_eps, bool noalloc,
+                            uint16_t* k_rows = nullptr, uint16_t* v_rows = nullptr) {
   Context& c = ctx();
   if (!c.stream) {
     set_error("plh_attn_decode: library not initialised");
@@ -828,6 +835,8 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
   a.kn = k_norm;
   a.norm_eps = norm_eps;
   a.score_scale = kLog2e / sqrtf((float)head_dim);
+  a.k_rows = k_rows;
+  a.v_rows = v_rows;
 
   const dim3 grid((unsigned)(8 * per_xcd)), cblock(kCombineThreads);
   const dim3 b64(64 * DecodeShape<64>::W), b128(64 * DecodeShape<128>::W);
@@ -881,6 +890,22 @@ extern "C" int plh_attn_decode_qknorm(int n_layers, int n_heads, int n_kv_heads,
   return attn_decode_impl(n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, layer0,
                           n_launch_layers, pos, q, k, v, key_cache, val_cache, rope_cos, rope_sin,
                           out, q_norm, k_norm, norm_eps, false);
+}
+
+extern "C" int plh_attn_decode_rows(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                                    int max_seq_len, int rope_type, int layer0,
+                                    int n_launch_layers, int pos, const float* q, const float* k,
+                                    const float* v, uint16_t* key_cache, uint16_t* val_cache,
+                                    const float* rope_cos, const float* rope_sin, float* out,
+                                    const float* q_norm, const float* k_norm, float norm_eps,
+                                    uint16_t* k_rows, uint16_t* v_rows) {
+  if (!k_rows || !v_rows) {
+    set_error("plh_attn_decode_rows: null row buffer");
+    return -1;
+  }
+  return attn_decode_impl(n_layers, n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, layer0,
+                          n_launch_layers, pos, q, k, v, key_cache, val_cache, rope_cos, rope_sin,
+                          out, q_norm, k_norm, norm_eps, false, k_rows, v_rows);
 }
 
 extern "C" int plh_attn_decode_noalloc(int n_layers, int n_heads, int n_kv_heads, int head_dim,

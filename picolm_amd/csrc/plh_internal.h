@@ -110,6 +110,8 @@ struct DecodeArgs {
   const float* kn;
   float norm_eps;
   float score_scale;       // log2(e) / sqrt(D)
+  uint16_t* k_rows;        // the appended rows also here [n_launch_layers][kv_dim], or null
+  uint16_t* v_rows;
 };
 
 }  // namespace plh

@@ -551,31 +551,30 @@ int gpu_try_attention(model_t *m, int layer, int pos, float *q, float *k, const 
     if (!gpu_available() || !same_shape(m)) return -1;
     if (layer < 0 || layer >= gs.n_layers || layer >= gs.gpu_layers) return -1;
     if (pos < 0 || pos >= gs.max_seq_len) return -1;
-    size_t q_bytes = (size_t)gs.n_heads * gs.head_dim * sizeof(float);
-    if (stage_in(1, q, k, v) != 0) {
-        /* nothing on the device changed, but the CPU path now appends a row the
-         * device cache will not hold: later calls must not use the device */
-        backend_lost("staging copy");
-        return -1;
-    }
-    int rc;
-    if (gs.qkn[layer]) {
-        size_t off = (size_t)layer * gs.head_dim;
-        rc = plh_attn_decode_qknorm(gs.n_layers, gs.n_heads, gs.n_kv_heads, gs.head_dim,
-                                    gs.max_seq_len, gs.rope_type, layer, 1, pos, gs.d_q, gs.d_k,
-                                    gs.d_v, gs.d_key, gs.d_val, gs.d_cos, gs.d_sin, gs.d_out,
-                                    gs.d_qn + off, gs.d_kn + off, gs.norm_eps);
-    } else {
-        rc = plh_attn_decode(gs.n_layers, gs.n_heads, gs.n_kv_heads, gs.head_dim,
-                             gs.max_seq_len, gs.rope_type, layer, 1, pos, gs.d_q, gs.d_k,
-                             gs.d_v, gs.d_key, gs.d_val, gs.d_cos, gs.d_sin, gs.d_out);
-    }
+    /* One token's q, k, v, out and cache rows are a few KiB: the kernels read
+     * and write them in the pinned staging itself (pinned host memory is
+     * device-accessible at the same address), so a call is one launch (two
+     * with a split combine) and one synchronisation, no copy commands. */
+    const size_t q_bytes = (size_t)gs.n_heads * gs.head_dim * sizeof(float);
+    const size_t kv_bytes = (size_t)gs.n_kv_heads * gs.head_dim * sizeof(float);
+    const size_t row_bytes = (size_t)gs.n_kv_heads * gs.head_dim * sizeof(uint16_t);
+    memcpy(gs.h_in, q, q_bytes);
+    memcpy(gs.h_in + q_bytes, k, kv_bytes);
+    memcpy(gs.h_in + q_bytes + kv_bytes, v, kv_bytes);
+    const float *hq = (const float *)gs.h_in;
+    const float *hk = (const float *)(gs.h_in + q_bytes);
+    const float *hv = (const float *)(gs.h_in + q_bytes + kv_bytes);
+    const size_t off = (size_t)layer * gs.head_dim;
+    const int qkn = gs.qkn[layer];
+    int rc = plh_attn_decode_rows(gs.n_layers, gs.n_heads, gs.n_kv_heads, gs.head_dim,
+                                  gs.max_seq_len, gs.rope_type, layer, 1, pos, hq, hk, hv,
+                                  gs.d_key, gs.d_val, gs.d_cos, gs.d_sin, (float *)gs.h_out,
+                                  qkn ? gs.d_qn + off : NULL, qkn ? gs.d_kn + off : NULL,
+                                  gs.norm_eps, (uint16_t *)(gs.h_out + q_bytes),
+                                  (uint16_t *)(gs.h_out + q_bytes + row_bytes));
+    if (rc == 0) rc = plh_synchronize();
     if (rc != 0 || injected_failure()) {
-        backend_lost("plh_attn_decode");
-        return -1;
-    }
-    if (stage_out(q_bytes, layer, pos, 1) != 0) {
-        backend_lost("copy back");
+        backend_lost("plh_attn_decode_rows");
         return -1;
     }
     memcpy(out, gs.h_out, q_bytes);
