@@ -36,7 +36,9 @@ Method (device):
     profiles/<workload>_traffic.json, null when none was measured;
   * boundary: the gpu.h-style hooks end to end (tests/c/bench_boundary: host
     q/k/v in, host output and cache rows back over PCIe) -- the latency
-    picolm's own call sites would see; never the headline value.
+    picolm's own call sites would see; never the headline value; with it
+    matmul_hook, gpu_try_matmul for every projection of one TinyLlama token
+    (tests/c/bench_matmul).
 Method (CPU baseline, kind "reference"): picolm's own attention code, i.e.
 its model_forward_ex / model_forward_prefill compiled from its sources into
 oracle/_ref, on the host, median of 5 runs after 1 warm-up, over a bounded
@@ -833,6 +835,19 @@ def boundary_latency(w, reps=20):
     return json.loads(r.stdout.strip().splitlines()[-1])
 
 
+def matmul_hook_latency(reps=10):
+    """gpu_try_matmul over one TinyLlama-shaped token's 155 projections (host
+    x in, host out back), from tests/c/bench_matmul; None if not built."""
+    exe = os.path.join(ROOT, "tests", "c", "bench_matmul")
+    if not os.path.exists(exe):
+        return None
+    args = [exe] + [str(x) for x in (22, 2048, 5632, 32, 4, 32000, reps)]
+    r = subprocess.run(args, capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        return {"error": r.stderr.strip()[-200:]}
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def measure(P, name, steps, warmup, cpu, warm=False):
     """One workload: device figures, CPU baseline, parity sample."""
     w = WORKLOADS[name]
@@ -1002,6 +1017,7 @@ def main():
                             for tag, name in (("cfg1", "tinyllama_decode_pos256"),
                                               ("cfg2", "tinyllama_decode_pos2047"),
                                               ("cfg3", "tinyllama_prefill_512"))}
+        line["matmul_hook"] = matmul_hook_latency()
         # the gpu_try_matmul path: every weight GEMV of one TinyLlama token
         gres = run_gemv(P, 10, 2)
         gextra = cpu_baseline_gemv(gres) if cpu else {}

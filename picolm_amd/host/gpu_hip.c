@@ -79,7 +79,8 @@ static struct {
     int stage_tokens;
     gpu_weight_t *weights;          /* GEMV matrices */
     int n_weights, cap_weights;
-    float *d_mx, *d_mout;           /* GEMV staging: x [mx_cap], out [mout_cap] */
+    float *h_mx, *h_mout;           /* GEMV staging (pinned host memory, which the kernel
+                                     * reads and writes directly): x [mx_cap], out [mout_cap] */
     int mx_cap, mout_cap;
     /* whole forward pass (gpu_try_forward): NULL model when unavailable */
     plh_model fwd;
@@ -296,9 +297,9 @@ static int upload_weights(const model_t *m) {
                       c->n_embd))
         return -1;
     if (gs.n_weights > 0) {
-        gs.d_mx = (float *)plh_malloc((size_t)gs.mx_cap * sizeof(float));
-        gs.d_mout = (float *)plh_malloc((size_t)gs.mout_cap * sizeof(float));
-        if (!gs.d_mx || !gs.d_mout) return -1;
+        gs.h_mx = (float *)plh_host_alloc((size_t)gs.mx_cap * sizeof(float));
+        gs.h_mout = (float *)plh_host_alloc((size_t)gs.mout_cap * sizeof(float));
+        if (!gs.h_mx || !gs.h_mout) return -1;
     }
     return 0;
 }
@@ -306,11 +307,11 @@ static int upload_weights(const model_t *m) {
 static void free_weights(void) {
     for (int i = 0; i < gs.n_weights; i++) plh_free(gs.weights[i].dev);
     free(gs.weights);
-    plh_free(gs.d_mx);
-    plh_free(gs.d_mout);
+    plh_host_free(gs.h_mx);
+    plh_host_free(gs.h_mout);
     gs.weights = NULL;
     gs.n_weights = gs.cap_weights = 0;
-    gs.d_mx = gs.d_mout = NULL;
+    gs.h_mx = gs.h_mout = NULL;
     gs.mx_cap = gs.mout_cap = 0;
 }
 
@@ -514,10 +515,13 @@ int gpu_try_matmul(float *out, const float *x, const void *W, int n, int d,
             break;
         }
     if (!w || w->qtype != (int)qtype || w->n != n || w->d != d) return -1;
-    if (plh_memcpy_htod(gs.d_mx, x, (size_t)n * sizeof(float)) != 0) return -1;
-    if (plh_gemv(w->qtype, n, d, w->dev, gs.d_mx, gs.d_mout) != 0) return -1;
-    /* nothing but staging changed: a failure here leaves the CPU path intact */
-    if (plh_memcpy_dtoh(out, gs.d_mout, (size_t)d * sizeof(float)) != 0) return -1;
+    /* x in and out back through pinned staging that the kernel reads and
+     * writes itself: one launch and one synchronisation, no copy commands
+     * (the Vulkan backend copies through its own staging, gpu.c:606-699) */
+    memcpy(gs.h_mx, x, (size_t)n * sizeof(float));
+    if (plh_gemv(w->qtype, n, d, w->dev, gs.h_mx, gs.h_mout) != 0 || plh_synchronize() != 0)
+        return -1; /* nothing but staging changed: the CPU path stays intact */
+    memcpy(out, gs.h_mout, (size_t)d * sizeof(float));
     return 0;
 }
 
