@@ -38,7 +38,8 @@ Method (device):
     q/k/v in, host output and cache rows back over PCIe) -- the latency
     picolm's own call sites would see; never the headline value; with it
     matmul_hook, gpu_try_matmul for every projection of one TinyLlama token
-    (tests/c/bench_matmul).
+    (tests/c/bench_matmul), and forward_hook, gpu_try_forward and
+    gpu_try_forward_prefill of a TinyLlama-shaped model (tests/c/bench_forward).
 Method (CPU baseline, kind "reference"): picolm's own attention code, i.e.
 its model_forward_ex / model_forward_prefill compiled from its sources into
 oracle/_ref, on the host, median of 5 runs after 1 warm-up, over a bounded
@@ -848,6 +849,21 @@ def matmul_hook_latency(reps=10):
     return json.loads(r.stdout.strip().splitlines()[-1])
 
 
+def forward_hook_latency(reps=10):
+    """gpu_try_forward (a decode token at position 257) and
+    gpu_try_forward_prefill (a 128-token prompt) of a TinyLlama-shaped
+    Q4_K_M model, logits, x and cache rows back in host memory, from
+    tests/c/bench_forward; None if not built."""
+    exe = os.path.join(ROOT, "tests", "c", "bench_forward")
+    if not os.path.exists(exe):
+        return None
+    args = [exe] + [str(x) for x in (22, 2048, 5632, 32, 4, 32000, 2048, 256, reps, 128)]
+    r = subprocess.run(args, capture_output=True, text=True, timeout=300)
+    if r.returncode != 0:
+        return {"error": r.stderr.strip()[-200:]}
+    return json.loads(r.stdout.strip().splitlines()[-1])
+
+
 def measure(P, name, steps, warmup, cpu, warm=False):
     """One workload: device figures, CPU baseline, parity sample."""
     w = WORKLOADS[name]
@@ -1018,6 +1034,7 @@ def main():
                                               ("cfg2", "tinyllama_decode_pos2047"),
                                               ("cfg3", "tinyllama_prefill_512"))}
         line["matmul_hook"] = matmul_hook_latency()
+        line["forward_hook"] = forward_hook_latency()
         # the gpu_try_matmul path: every weight GEMV of one TinyLlama token
         gres = run_gemv(P, 10, 2)
         gextra = cpu_baseline_gemv(gres) if cpu else {}

@@ -57,6 +57,9 @@ int plh_host_free(void *host);
  * plh_synchronize). */
 int plh_memcpy_htod_async(void *dst, const void *src, size_t bytes);
 int plh_memcpy_dtoh_async(void *dst, const void *src, size_t bytes);
+/* plh_memcpy2d_dtoh queued the same way, without waiting. */
+int plh_memcpy2d_dtoh_async(void *dst, size_t dpitch, const void *src, size_t spitch,
+                            size_t width, size_t height);
 
 /* ---- timing on the library stream (hipEvents) -------------------------- */
 void *plh_event_create(void);

@@ -75,6 +75,7 @@ _SIGS = {
     "plh_host_free": (_i, [_vp]),
     "plh_memcpy_htod_async": (_i, [_vp, _vp, _sz]),
     "plh_memcpy_dtoh_async": (_i, [_vp, _vp, _sz]),
+    "plh_memcpy2d_dtoh_async": (_i, [_vp, _sz, _vp, _sz, _sz, _sz]),
     # events
     "plh_event_create": (_vp, []),
     "plh_event_record": (_i, [_vp]),

@@ -180,6 +180,14 @@ int plh_memcpy_dtoh_async(void* dst, const void* src, size_t bytes) {
                    "dtoh async");
 }
 
+int plh_memcpy2d_dtoh_async(void* dst, size_t dpitch, const void* src, size_t spitch,
+                            size_t width, size_t height) {
+  if (height == 0 || width == 0) return 0;
+  return check_hip(hipMemcpy2DAsync(dst, dpitch, src, spitch, width, height,
+                                    hipMemcpyDeviceToHost, g_ctx.stream),
+                   "dtoh 2d async");
+}
+
 int plh_memcpy_dtod(void* dst, const void* src, size_t bytes) {
   return check_hip(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, g_ctx.stream), "dtod");
 }

@@ -88,7 +88,12 @@ static struct {
     float *d_fwd_vecs;              /* norms and biases, one block */
     void *d_embd;                   /* raw token_embd rows */
     void *d_fwd_ws;                 /* plh_forward workspace */
-    float *d_logits, *d_x;
+    float *d_x;
+    /* copy-back staging (pinned host memory): logits [vocab] (the output
+     * GEMV writes them there itself), x [n_embd], then the key rows and the
+     * val rows a call appended, [n_layers][n][kv_dim] each */
+    unsigned char *h_fwd;
+    size_t fwd_cap;
     int fwd_ready;
 } gs;
 
@@ -347,11 +352,13 @@ static void free_forward(void) {
     plh_free(gs.d_fwd_vecs);
     plh_free(gs.d_embd);
     plh_free(gs.d_fwd_ws);
-    plh_free(gs.d_logits);
     plh_free(gs.d_x);
+    plh_host_free(gs.h_fwd);
     gs.d_fwd_vecs = NULL;
     gs.d_embd = gs.d_fwd_ws = NULL;
-    gs.d_logits = gs.d_x = NULL;
+    gs.d_x = NULL;
+    gs.h_fwd = NULL;
+    gs.fwd_cap = 0;
     gs.fwd_ready = 0;
 }
 
@@ -406,9 +413,8 @@ static int upload_forward(const model_t *m) {
     size_t nvec = per_layer * (size_t)c->n_layers + (size_t)E;
     gs.d_fwd_vecs = (float *)plh_malloc(nvec * sizeof(float));
     gs.d_embd = plh_malloc(rb * (size_t)c->vocab_size);
-    gs.d_logits = (float *)plh_malloc((size_t)c->vocab_size * sizeof(float));
     gs.d_x = (float *)plh_malloc((size_t)E * sizeof(float));
-    if (!gs.d_fwd_vecs || !gs.d_embd || !gs.d_logits || !gs.d_x) return -1;
+    if (!gs.d_fwd_vecs || !gs.d_embd || !gs.d_x) return -1;
     if (plh_memcpy_htod(gs.d_embd, w->token_embd, rb * (size_t)c->vocab_size)) return -1;
     float *dv = gs.d_fwd_vecs;
 #define PUT(dst, src, count)                                                   \
@@ -670,27 +676,46 @@ int gpu_kv_download(const model_t *m, int n_pos) { return kv_copy(m, n_pos, 1); 
 
 int gpu_kv_upload(const model_t *m, int n_pos) { return kv_copy(m, n_pos, 0); }
 
-/* The rows of position pos0..pos0+n-1 of every layer, device -> host caches,
- * in one strided copy per cache. */
-static int pos_rows_to_host(const model_t *m, int pos0, int n) {
+/* h_fwd sized for the logits, x and n positions' rows: grown on demand,
+ * NULL (the CPU path runs) when the pinned allocation fails. */
+static float *forward_stage(int n) {
+    const size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
+    const size_t need = ((size_t)gs.fwd.vocab_size + (size_t)gs.n_embd) * sizeof(float) +
+                        (size_t)2 * gs.n_layers * n * kv_dim * sizeof(uint16_t);
+    if (need > gs.fwd_cap) {
+        plh_host_free(gs.h_fwd);
+        gs.h_fwd = (unsigned char *)plh_host_alloc(need);
+        gs.fwd_cap = gs.h_fwd ? need : 0;
+    }
+    return (float *)gs.h_fwd;
+}
+
+/* After plh_forward(_prefill) has written the logits into h_fwd: x and the
+ * rows of positions pos0..pos0+n-1 of every layer queued into h_fwd (one
+ * strided copy per cache), one synchronisation, then the host state and
+ * caches filled from the staging. */
+static int forward_done(model_t *m, int pos0, int n) {
+    const model_config_t *c = &m->config;
     const size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
     const size_t off = (size_t)pos0 * kv_dim;
     const size_t pitch = (size_t)gs.max_seq_len * kv_dim * sizeof(uint16_t);
     const size_t width = (size_t)n * kv_dim * sizeof(uint16_t);
-    if (plh_memcpy2d_dtoh(m->state.key_cache + off, pitch, gs.d_key + off, pitch, width,
-                          (size_t)gs.n_layers) != 0)
-        return -1;
-    return plh_memcpy2d_dtoh(m->state.val_cache + off, pitch, gs.d_val + off, pitch, width,
-                             (size_t)gs.n_layers);
-}
-
-static int forward_done(model_t *m, int pos0, int n) {
-    const model_config_t *c = &m->config;
-    if (plh_memcpy_dtoh(m->state.logits, gs.d_logits, (size_t)c->vocab_size * sizeof(float)) ||
-        plh_memcpy_dtoh(m->state.x, gs.d_x, (size_t)c->n_embd * sizeof(float)) ||
-        pos_rows_to_host(m, pos0, n)) {
+    const size_t lb = (size_t)c->vocab_size * sizeof(float), xb = (size_t)c->n_embd * sizeof(float);
+    const size_t rb = width * (size_t)gs.n_layers;
+    unsigned char *hx = gs.h_fwd + lb, *hk = hx + xb, *hv = hk + rb;
+    if (plh_memcpy_dtoh_async(hx, gs.d_x, xb) ||
+        plh_memcpy2d_dtoh_async(hk, width, gs.d_key + off, pitch, width, (size_t)gs.n_layers) ||
+        plh_memcpy2d_dtoh_async(hv, width, gs.d_val + off, pitch, width, (size_t)gs.n_layers) ||
+        plh_synchronize()) {
         backend_lost("copy back");
         return -1;
+    }
+    memcpy(m->state.logits, gs.h_fwd, lb);
+    memcpy(m->state.x, hx, xb);
+    const size_t lstride = (size_t)gs.max_seq_len * kv_dim;
+    for (int l = 0; l < gs.n_layers; l++) {
+        memcpy(m->state.key_cache + l * lstride + off, hk + l * width, width);
+        memcpy(m->state.val_cache + l * lstride + off, hv + l * width, width);
     }
     return 0;
 }
@@ -698,7 +723,9 @@ static int forward_done(model_t *m, int pos0, int n) {
 int gpu_try_forward(model_t *m, int token, int pos) {
     if (!gpu_available() || !gs.fwd_ready || !same_shape(m)) return -1;
     if (token < 0 || token >= m->config.vocab_size || pos < 0 || pos >= gs.max_seq_len) return -1;
-    if (plh_forward(&gs.fwd, token, pos, gs.d_fwd_ws, gs.d_logits, gs.d_x) != 0) {
+    float *logits = forward_stage(1);
+    if (!logits) return -1;
+    if (plh_forward(&gs.fwd, token, pos, gs.d_fwd_ws, logits, gs.d_x) != 0) {
         backend_lost("plh_forward");
         return -1;
     }
@@ -711,7 +738,9 @@ int gpu_try_forward_prefill(model_t *m, const int *tokens, int n_tokens, int sta
         return -1;
     for (int i = 0; i < n_tokens; i++)
         if (tokens[i] < 0 || tokens[i] >= m->config.vocab_size) return -1;
-    if (plh_forward_prefill(&gs.fwd, tokens, n_tokens, start_pos, gs.d_fwd_ws, gs.d_logits,
+    float *logits = forward_stage(n_tokens);
+    if (!logits) return -1;
+    if (plh_forward_prefill(&gs.fwd, tokens, n_tokens, start_pos, gs.d_fwd_ws, logits,
                             gs.d_x) != 0) {
         backend_lost("plh_forward_prefill");
         return -1;
