@@ -107,7 +107,8 @@ int plh_f16_checksum(uint64_t first, uint64_t count, uint64_t *checksum);
  *   out + li*n_heads*head_dim     fp32 attention output
  * The kernel rotates q and k with table row `pos`, writes f16(k_rot), f16(v)
  * into row `pos` of layer layer0+li of the caches, and attends over rows
- * 0..pos.  Supported: head_dim 64 or 128, n_heads % n_kv_heads == 0.  Any
+ * 0..pos.  Supported: every even head_dim up to 256 (model.c:408, 856; 64 and
+ * 128 run tuned kernels, the others generic ones), n_heads % n_kv_heads == 0.  Any
  * finite q is handled: a q head with some |element| >= 2^15 is scaled by a
  * power of two before its fp16 split and the factor moves into its score
  * scale (exact). */
@@ -308,7 +309,7 @@ size_t plh_forward_workspace_bytes(const plh_model *m);
  * down + residual), the final rmsnorm and the output projection into
  * logits [vocab_size] (device).  x_out (device, may be NULL) receives the
  * final normalised residual (the reference's s->x).  workspace: device,
- * plh_forward_workspace_bytes(m).  Head dims 64 / 128; matrices Q4_K, Q6_K
+ * plh_forward_workspace_bytes(m).  Even head dims up to 256; matrices Q4_K, Q6_K
  * or Q8_0.  Queued on the library stream. */
 int plh_forward(const plh_model *m, int token, int pos, void *workspace, float *logits,
                 float *x_out);

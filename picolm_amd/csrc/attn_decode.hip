@@ -734,8 +734,8 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
     set_error("plh_attn_decode: library not initialised");
     return -1;
   }
-  if (head_dim != 64 && head_dim != 128) {
-    set_error("plh_attn_decode: head_dim %d not supported (64, 128)", head_dim);
+  if (head_dim < 2 || head_dim > 256 || head_dim % 2) {
+    set_error("plh_attn_decode: head_dim %d not supported (even, at most 256)", head_dim);
     return -1;
   }
   if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads) {
@@ -765,6 +765,11 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
     return -1;
   }
   const bool qkn = q_norm != nullptr;
+  if (head_dim != 64 && head_dim != 128)
+    return attn_generic(n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, layer0,
+                        n_launch_layers, pos, 1, q, k, v, key_cache, val_cache, rope_cos,
+                        rope_sin, out, n_heads * head_dim, q_norm, k_norm, norm_eps, k_rows,
+                        v_rows);
 
   const int G = n_heads / n_kv_heads;
   const int n_hblk = (G + 15) / 16;

@@ -782,8 +782,8 @@ static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head
     set_error("plh_attn_prefill: library not initialised");
     return -1;
   }
-  if (head_dim != 64 && head_dim != 128) {
-    set_error("plh_attn_prefill: head_dim %d not supported (64, 128)", head_dim);
+  if (head_dim < 2 || head_dim > 256 || head_dim % 2) {
+    set_error("plh_attn_prefill: head_dim %d not supported (even, at most 256)", head_dim);
     return -1;
   }
   if (n_heads <= 0 || n_kv_heads <= 0 || n_heads % n_kv_heads) {
@@ -826,6 +826,11 @@ static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head
     return -1;
   }
   const bool qkn = q_norm != nullptr;
+  if (head_dim != 64 && head_dim != 128)
+    return attn_generic(n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, layer0,
+                        n_launch_layers, start_pos, n_tokens, q, k, v, key_cache, val_cache,
+                        rope_cos, rope_sin, out, out_stride, q_norm, k_norm, norm_eps, nullptr,
+                        nullptr);
 
   PrefillArgs a;
   a.q = q;

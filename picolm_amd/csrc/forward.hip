@@ -210,7 +210,7 @@ bool model_ok(const plh_model* m) {
   }
   if (m->n_layers < 1 || m->n_embd < 1 || m->n_ffn < 1 || m->vocab_size < 1 ||
       m->max_seq_len < 1 || m->n_heads < 1 || m->n_kv_heads < 1 ||
-      m->n_heads % m->n_kv_heads || (m->head_dim != 64 && m->head_dim != 128) ||
+      m->n_heads % m->n_kv_heads || m->head_dim < 2 || m->head_dim > 256 || m->head_dim % 2 ||
       (m->rope_type != PLH_ROPE_LLAMA && m->rope_type != PLH_ROPE_QWEN)) {
     set_error("plh_forward: unsupported shape (layers %d, embd %d, heads %d/%d, head_dim %d)",
               m->n_layers, m->n_embd, m->n_heads, m->n_kv_heads, m->head_dim);

@@ -87,6 +87,17 @@ int decode_scratch_setup(int device);
 // retired until plh_shutdown).  Returns 0 or -1.
 int ensure_workspace(size_t bytes);
 
+// Attention of the head dims without a tuned kernel (every even head_dim up
+// to 256 but 64 and 128; attn_generic.hip): append and attend n_tokens rows
+// at start_pos.. of layers layer0.. (decode: n_tokens 1, out_stride
+// n_heads*head_dim).  Arguments are checked by the caller.  0 or -1.
+int attn_generic(int n_heads, int n_kv_heads, int head_dim, int max_seq_len, int rope_type,
+                 int layer0, int n_launch_layers, int start_pos, int n_tokens, const float* q,
+                 const float* k, const float* v, uint16_t* key_cache, uint16_t* val_cache,
+                 const float* rope_cos, const float* rope_sin, float* out, int out_stride,
+                 const float* q_norm, const float* k_norm, float norm_eps, uint16_t* k_rows,
+                 uint16_t* v_rows);
+
 // Decode kernel arguments (all device pointers).
 struct DecodeArgs {
   const float* q;          // [n_launch_layers][n_heads*D]

@@ -125,7 +125,9 @@ int gpu_init(const model_t *m) {
     if (gs.inited) return 0;
     if (env_int("PICOLM_HIP_DISABLE", 0)) return -1;
     const model_config_t *c = &m->config;
-    if (c->head_dim != 64 && c->head_dim != 128) {
+    /* every head_dim the reference runs (even, at most 256: its acc[256],
+     * model.c:856); 64 and 128 have tuned kernels, the others a generic one */
+    if (c->head_dim < 2 || c->head_dim > 256 || c->head_dim % 2) {
         fprintf(stderr, "gpu_hip: head_dim %d has no kernel, attention stays on the CPU\n",
                 c->head_dim);
         return -1;

@@ -101,6 +101,7 @@ CASES = [
     ((2, 32, 8, 64, 600, 0), 5e5, 257, 3),     # Llama-3.2 head layout
     ((2, 32, 32, 128, 300, 0), 1e4, 90, 4),    # Llama-2 MHA
     ((2, 16, 2, 64, 128, 1), 1e6, 60, 3),      # QWEN rotation
+    ((2, 8, 2, 96, 300, 0), 1e4, 90, 3),       # head_dim 96 (generic kernels)
 ]
 
 
@@ -122,6 +123,7 @@ def test_boundary_prefill_then_decode(tmp_path, oracle_mod, dims, theta, P, T):
 QKN_CASES = [
     ((3, 16, 8, 128, 400, 1), 1e6, 150, 4, 0b111),  # Qwen3-0.6B head layout, every layer
     ((3, 32, 4, 64, 300, 1), 1e6, 97, 3, 0b101),    # QK-norm layers mixed with plain ones
+    ((2, 8, 4, 80, 200, 1), 1e6, 60, 3, 0b11),      # head_dim 80 (generic kernels)
 ]
 
 

@@ -181,9 +181,9 @@ def test_decode_rejects_bad_arguments_without_side_effects(gpu, oracle_mod):
             gpu.decode(cache, 0, kwargs["pos"], buf.ptr, buf.ptr, buf.ptr, buf.ptr, 1)
     with pytest.raises(gpu.PicolmHipError):
         gpu.decode(cache, 1, 3, buf.ptr, buf.ptr, buf.ptr, buf.ptr, 2)   # layers 1..2 of 2
-    rc = gpu.lib.plh_attn_decode(2, 32, 4, 96, 64, 0, 0, 1, 0, buf.ptr, buf.ptr, buf.ptr,
+    rc = gpu.lib.plh_attn_decode(2, 32, 4, 95, 64, 0, 0, 1, 0, buf.ptr, buf.ptr, buf.ptr,
                                  cache.key.ptr, cache.val.ptr, cache.cos.ptr, cache.sin.ptr,
-                                 buf.ptr)                                 # head_dim 96
+                                 buf.ptr)                                 # odd head_dim
     assert rc == -1 and "head_dim" in gpu._native.last_error()
     gpu.synchronize()
     after = cache.fetch()

@@ -133,6 +133,11 @@ QWEN = dict(n_layers=2, n_embd=512, n_ffn=768, n_heads=4, n_kv_heads=2, head_dim
             vocab_size=700, max_seq_len=128, rope_type=1, rope_base=1e6, eps=1e-6,
             types=dict(embd=Q8, output=Q8, q=Q8, k=Q4K, v=Q6K, o=Q8, gate=Q6K, up=Q4K,
                        down=Q4K), biases=True, qk_norm=True)
+# head dims without a tuned attention kernel (attn_generic.hip)
+HD96 = dict(LLAMA, n_layers=2, n_embd=768, head_dim=96)
+HD80_QKN = dict(QWEN, n_embd=1280, n_heads=16, n_kv_heads=4, head_dim=80)
+MODELS = [LLAMA, QWEN, HD96, HD80_QKN]
+MODEL_IDS = ["llama", "qwen", "llama_hd96", "qwen_hd80"]
 # normwise tolerance of logits and residual (relative to the vector's max);
 # measured differences are ~1e-6
 FWD_TOL = 2e-4
@@ -143,7 +148,7 @@ def normwise(a, b):
     return float(np.max(np.abs(a - b)) / max(np.max(np.abs(b)), 1e-30))
 
 
-@pytest.mark.parametrize("cfg", [LLAMA, QWEN], ids=["llama", "qwen"])
+@pytest.mark.parametrize("cfg", MODELS, ids=MODEL_IDS)
 def test_forward_matches_oracle(gpu, oracle_mod, cfg):
     P, O = gpu, oracle_mod
     h = S.SynthModel(**cfg, seed=11)
@@ -188,7 +193,7 @@ def test_forward_matches_oracle(gpu, oracle_mod, cfg):
         dm.free()
 
 
-@pytest.mark.parametrize("cfg", [LLAMA, QWEN], ids=["llama", "qwen"])
+@pytest.mark.parametrize("cfg", MODELS, ids=MODEL_IDS)
 def test_prefill_matches_oracle(gpu, oracle_mod, cfg):
     """model_forward_prefill: chunks of a prompt over a cached prefix, then a
     decode step; logits of each chunk's last token, layer-0 KV rows exact."""
