@@ -25,6 +25,8 @@
 //                          (scores and v sums each in four partial sums).
 // The softmax is taken per chunk rather than per position, so outputs agree
 // with the reference's within the attention tolerance, not bit for bit.
+#include <algorithm>
+
 #include "picolm_hip.h"
 #include "attn_common.h"
 #include "plh_internal.h"
@@ -247,17 +249,40 @@ int attn_generic(int n_heads, int n_kv_heads, int head_dim, int max_seq_len, int
   a.n_kv_heads = n_kv_heads, a.D = head_dim, a.max_seq_len = max_seq_len;
   a.rope_type = rope_type, a.start_pos = start_pos, a.n_tokens = n_tokens;
   a.out_stride = out_stride;
-  const long rows = (long)n_launch_layers * n_tokens * n_kv_heads;
-  const long heads = (long)n_launch_layers * n_tokens * n_heads;
-  if (heads > 0x7FFFFFFFL) {
-    set_error("attention: %ld (layer, token, head) workgroups in one launch", heads);
+  // A launch holds at most 2^32 - 1 threads: layers go in as many launches
+  // as that takes (each layer is independent); one layer must fit.
+  const long per_layer = (long)n_tokens * n_heads;
+  const long max_wg = 0xFFFFFFFFL / kGThreads;
+  if (per_layer > max_wg) {
+    set_error("attention: %d tokens x %d heads exceed one launch's %ld workgroups", n_tokens,
+              n_heads, max_wg);
     return -1;
   }
+  const int step = (int)std::min<long>(n_launch_layers, max_wg / per_layer);
+  const size_t q_dim = (size_t)n_heads * head_dim, kv_dim = (size_t)n_kv_heads * head_dim;
   hipStream_t st = ctx().stream;
-  hipLaunchKernelGGL(generic_append_kernel, dim3((unsigned)rows), dim3(kGThreads), 0, st, a);
-  if (check_hip(hipGetLastError(), "generic_append_kernel")) return -1;
-  hipLaunchKernelGGL(generic_attn_kernel, dim3((unsigned)heads), dim3(kGThreads), 0, st, a);
-  return check_hip(hipGetLastError(), "generic_attn_kernel");
+  for (int l = 0; l < n_launch_layers; l += step) {
+    GenericArgs b = a;
+    const size_t rows_before = (size_t)l * n_tokens;
+    b.layer0 = layer0 + l;
+    b.n_launch_layers = std::min(step, n_launch_layers - l);
+    b.q = q + rows_before * q_dim;
+    b.k = k + rows_before * kv_dim;
+    b.v = v + rows_before * kv_dim;
+    b.out = out + rows_before * out_stride;
+    if (q_norm) b.qn = q_norm + (size_t)l * head_dim;
+    if (k_norm) b.kn = k_norm + (size_t)l * head_dim;
+    if (k_rows) b.k_rows = k_rows + rows_before * kv_dim;
+    if (v_rows) b.v_rows = v_rows + rows_before * kv_dim;
+    const long nl = b.n_launch_layers;
+    hipLaunchKernelGGL(generic_append_kernel, dim3((unsigned)(nl * n_tokens * n_kv_heads)),
+                       dim3(kGThreads), 0, st, b);
+    if (check_hip(hipGetLastError(), "generic_append_kernel")) return -1;
+    hipLaunchKernelGGL(generic_attn_kernel, dim3((unsigned)(nl * per_layer)), dim3(kGThreads), 0,
+                       st, b);
+    if (check_hip(hipGetLastError(), "generic_attn_kernel")) return -1;
+  }
+  return 0;
 }
 
 }  // namespace plh
