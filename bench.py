@@ -266,6 +266,26 @@ def run_forward(P, n_prompt=128, n_decode=64, n_check=8):
         dm.forward(tok, pos + i)
         tok = int(np.argmax(dm.fetch_logits()))
     gen = (time.perf_counter() - t0) / n_decode
+    # decode at the last cache row: rows 0..2046 of every layer hold N(0,1)
+    # rounded to fp16 (what kvcache_load of a full context brings in), then
+    # n_decode steps at position 2047, each attending over 2048 rows
+    last = h.max_seq_len - 1
+    kv = h.n_kv_heads * h.head_dim
+    kfill = np.zeros((h.n_layers, h.max_seq_len, kv), np.float16)
+    kfill[:, :last] = rng.standard_normal((h.n_layers, last, kv), dtype=np.float32)
+    vfill = np.zeros_like(kfill)
+    vfill[:, :last] = rng.standard_normal((h.n_layers, last, kv), dtype=np.float32)
+    dm.load_cache(kfill.view(np.uint16).reshape(-1), vfill.view(np.uint16).reshape(-1))
+    del kfill, vfill
+    for i in range(4):
+        dm.forward(int(toks[i]), last)
+    P.synchronize()
+    e0.record()
+    for i in range(n_decode):
+        dm.forward(int(toks[4 + i]), last)
+    e1.record()
+    P.synchronize()
+    dev_last_ms = e0.elapsed_ms(e1) / n_decode
     wb = h.weight_bytes_per_token()
     gbs = wb / (dev_ms * 1e-3) / 1e9
     res = {
@@ -275,6 +295,8 @@ def run_forward(P, n_prompt=128, n_decode=64, n_check=8):
         "decode_tok_s": 1.0 / wall,
         "decode_us_per_token": wall * 1e6,
         "decode_device_us_per_token": dev_ms * 1e3,
+        "decode_positions": [n_prompt + 4, n_prompt + 3 + n_decode],
+        "decode_device_us_per_token_pos2047": dev_last_ms * 1e3,
         "generate_tok_s": 1.0 / gen,
         "generate_us_per_token": gen * 1e6,
         "prefill_tok_s": n_prompt / prefill_s,
@@ -370,15 +392,18 @@ def prefill_bytes(w) -> int:
 
 
 def traffic_from_profiles(name: str):
-    """HBM bytes per launch of the workload's dominant kernel, measured by
-    rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, calibrated on a copy kernel)
-    and summarised in profiles/<name>_traffic.json; None if not measured."""
+    """(bytes, commit): HBM bytes per launch of the workload's dominant
+    kernel, measured by rocprofv3 --pmc (FETCH_SIZE + WRITE_SIZE, calibrated
+    on a copy kernel) and summarised in profiles/<name>_traffic.json, and the
+    commit of the tree those counters were read on; (None, None) if not
+    measured."""
     path = os.path.join(ROOT, "profiles", f"{name}_traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get("traffic_bytes")
+            t = json.load(f)
+        return t.get("traffic_bytes"), t.get("commit")
     except (OSError, ValueError):
-        return None
+        return None, None
 
 
 def norm_weights(P, w, rng):
@@ -487,6 +512,7 @@ def run_decode(P, w, steps, warmup, name, warm=False):
 
     algo = decode_bytes(w)
     achieved = algo / (k_ms * 1e-3) / 1e9
+    traffic = traffic_from_profiles(name)
     res = {
         "value": algo / wall / 1e9,
         "unit": "GB/s",
@@ -495,9 +521,12 @@ def run_decode(P, w, steps, warmup, name, warm=False):
         "kernel_us_mean": k_ms * 1e3,
         "algorithmic_bytes_per_step": algo,
         "cache_copies_rotated": n_copies,
+        "gbs_wall": algo / wall / 1e9,
+        "gbs_events": achieved,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": achieved / HBM_PEAK_GBS,
-                     "traffic": traffic_from_profiles(name)},
+                     "achieved_clock": "HIP events on the library stream",
+                     "traffic": traffic[0], "traffic_commit": traffic[1]},
         "per_layer": {"us_per_token": pl_ms * 1e3, "gbs": algo / (pl_ms * 1e-3) / 1e9,
                       "launches_per_token": L},
     }
@@ -564,14 +593,18 @@ def run_prefill(P, w, steps, warmup, name):
     # below the fp16 ridge, else the MFMA peak; MFMA utilisation beside it
     hbm_roof = flops / algo_bytes * HBM_PEAK_GBS / 1e3
     roof = min(MFMA_F16_PEAK_TFS, hbm_roof)
+    traffic = traffic_from_profiles(name)
     return {
         "us_per_step": wall * 1e6,
         "us_per_token": wall * 1e6 / n,
         "tflops": tfs,
+        "tflops_wall": flops / wall / 1e12,
+        "tflops_events": tfs,
         "kernel_us_mean": ms * 1e3,
         "roofline": {"bound": "hbm" if hbm_roof < MFMA_F16_PEAK_TFS else "mfma",
                      "achieved": tfs, "peak": roof, "unit": "TFLOP/s", "frac": tfs / roof,
-                     "traffic": traffic_from_profiles(name),
+                     "achieved_clock": "HIP events on the library stream",
+                     "traffic": traffic[0], "traffic_commit": traffic[1],
                      "achieved_gbs": algo_bytes / (ms * 1e-3) / 1e9,
                      "mfma_peak": MFMA_F16_PEAK_TFS, "mfma_frac": tfs / MFMA_F16_PEAK_TFS},
         "per_layer": {"us_per_step": pl_ms * 1e3, "tflops": flops / (pl_ms * 1e-3) / 1e12,
@@ -632,6 +665,7 @@ def cpu_reference_decode(w, reps=5):
     attn_s = (float(np.median(t_long)) - float(np.median(t_short))) * w["L"] / Ls
     return {"value": decode_bytes(w) / attn_s / 1e9, "unit": "GB/s", "cores": 1,
             "kind": "reference", "us_per_token": attn_s * 1e6,
+            "sample_layers": Ls, "total_layers": w["L"], "scale": w["L"] / Ls,
             "sample": f"model_forward_ex of a {Ls}-layer model of this attention shape at pos "
                       f"{pos} minus pos 0, median of {reps} after a warm-up, x{w['L'] // Ls} "
                       f"layers; 1 thread (picolm's pool runs matmul rows only, its attention "
@@ -668,6 +702,8 @@ def cpu_reference_prefill(name, w, reps=5):
     step_s = float(np.median(ts)) * scale
     return {"value": prefill_flops(w) / step_s / 1e12, "unit": "TFLOP/s", "cores": 1,
             "kind": "reference", "us_per_token": step_s * 1e6 / n,
+            "sample_layers": 1, "total_layers": w["L"], "sample_q_heads": hq,
+            "total_q_heads": w["Hq"], "scale": scale,
             "sample": f"model_forward_prefill of a 1-layer model with {hq} q / {hkv} kv heads of "
                       f"head_dim {w['D']} ({n} tokens, projections included), median of {reps} "
                       f"after a warm-up, x{w['Hq'] // hq} heads x{w['L']} layers; 1 thread "
@@ -719,6 +755,7 @@ def cpu_head_parallel_decode(w, reps=7, warm=3):
     step_s = float(np.median(ts)) * w["L"] / Ls
     return {"value": decode_bytes(w) / step_s / 1e9, "unit": "GB/s", "cores": n_thr,
             "kind": "port", "us_per_token": step_s * 1e6,
+            "sample_layers": Ls, "total_layers": w["L"], "scale": w["L"] / Ls,
             "sample": f"oracle decode attention at pos {pos} with q heads split over {n_thr} "
                       f"threads, {Ls} layers, median of {reps} after >= 0.3 s of warm-up, "
                       f"x{w['L'] // Ls} layers; upper bound, not the reference's own "
@@ -762,6 +799,7 @@ def cpu_head_parallel_prefill(w, reps=3):
     step_s = float(np.median(ts)) * w["L"]
     return {"value": prefill_flops(w) / step_s / 1e12, "unit": "TFLOP/s", "cores": n_thr,
             "kind": "port", "us_per_token": step_s * 1e6 / n,
+            "sample_layers": 1, "total_layers": w["L"], "scale": float(w["L"]),
             "sample": f"oracle prefill attention of one layer ({n} tokens from {st}) with q heads "
                       f"split over {n_thr} threads, median of {reps} after a warm-up, "
                       f"x{w['L']} layers; upper bound, not the reference's own parallelism"}
@@ -912,6 +950,7 @@ def compact(tag, name, res):
                    pl_us_tok=round(pl["us_per_token"], 1))
     out.update(kern_us=round(res["kernel_us_mean"], 2), frac=round(rf["frac"], 4), peak=rf["peak"],
                traffic=None if rf["traffic"] is None else int(rf["traffic"]),
+               traffic_commit=rf.get("traffic_commit"),
                cpu_us_tok=None if not cb else round(cb["us_per_token"], 1),
                cpu_kind=cb.get("kind"),
                cpu_mt_us_tok=None if not cb.get("head_parallel_upper_bound")
@@ -996,7 +1035,10 @@ def main():
         "roofline": hres["roofline"],
         "cpu_baseline": hres.get("cpu_baseline"),
     }
-    for key in ("us_per_token", "us_per_step", "kernel_us_mean", "algorithmic_bytes_per_step",
+    line["value_clock"] = ("HIP events on the library stream" if is_prefill
+                           else "host wall clock around the graph replay")
+    for key in ("gbs_wall", "gbs_events", "tflops_wall", "tflops_events",
+                "us_per_token", "us_per_step", "kernel_us_mean", "algorithmic_bytes_per_step",
                 "algorithmic_flops_per_step", "cache_copies_rotated", "copies_rotated",
                 "per_layer", "warm", "parity_normwise_max"):
         if key in hres:

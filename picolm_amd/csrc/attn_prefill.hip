@@ -792,10 +792,6 @@ static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head
     return -1;
   }
   const int G = n_heads / n_kv_heads;
-  if (G > kPCols) {
-    set_error("plh_attn_prefill: GQA group %d larger than %d", G, kPCols);
-    return -1;
-  }
   if (rope_type != PLH_ROPE_LLAMA && rope_type != PLH_ROPE_QWEN) {
     set_error("plh_attn_prefill: unknown rope_type %d", rope_type);
     return -1;
@@ -811,9 +807,9 @@ static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head
               layer0 + n_launch_layers, n_layers);
     return -1;
   }
-  if (out_stride < n_heads * head_dim || out_stride % 4) {
-    set_error("plh_attn_prefill: out_stride %d must be a multiple of 4 and >= n_heads*head_dim %d",
-              out_stride, n_heads * head_dim);
+  if (out_stride < n_heads * head_dim) {
+    set_error("plh_attn_prefill: out_stride %d must be >= n_heads*head_dim %d", out_stride,
+              n_heads * head_dim);
     return -1;
   }
   if ((q_norm == nullptr) != (k_norm == nullptr)) {
@@ -826,7 +822,10 @@ static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head
     return -1;
   }
   const bool qkn = q_norm != nullptr;
-  if (head_dim != 64 && head_dim != 128)
+  // The tuned kernels take head_dim 64 / 128, a GQA group that fits one
+  // workgroup's columns and 16-byte output rows; everything else the
+  // reference accepts runs on the generic kernels.
+  if ((head_dim != 64 && head_dim != 128) || G > kPCols || out_stride % 4)
     return attn_generic(n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, layer0,
                         n_launch_layers, start_pos, n_tokens, q, k, v, key_cache, val_cache,
                         rope_cos, rope_sin, out, out_stride, q_norm, k_norm, norm_eps, nullptr,

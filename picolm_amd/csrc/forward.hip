@@ -396,7 +396,7 @@ ChunkActs carve_chunk(const plh_model* m, int T, void* base) {
 int ensure_prefill_ws(size_t bytes) {
   Context& c = ctx();
   if (c.pf_ws && c.pf_ws_bytes >= bytes) return 0;
-  return grow_buffer(&c.pf_ws, &c.pf_ws_bytes, bytes, "hipMalloc(prefill workspace)");
+  return grow_buffer(&c.pf_ws, &c.pf_ws_bytes, bytes + bytes / 2, "hipMalloc(prefill workspace)");
 }
 
 int launch_rmsnorm_rows(const float* x, const float* w, float* out, int n, int rows, float eps) {

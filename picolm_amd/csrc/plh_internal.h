@@ -19,15 +19,15 @@ struct Context {
   size_t pf_ws_bytes = 0;
   int num_cus = 0;
   // Workspaces outgrown by a larger call.  A graph captured before the growth
-  // still holds their addresses in its kernel nodes, so they stay allocated
-  // until plh_shutdown.
-  static constexpr int kMaxRetired = 32;
-  void* retired[kMaxRetired] = {};
-  int n_retired = 0;
+  // still holds their addresses in its kernel nodes, so every one of them
+  // stays allocated until plh_shutdown (a host-side list that grows as
+  // needed; both workspaces grow by 1.5x, so it stays short).
+  void** retired = nullptr;
+  int n_retired = 0, cap_retired = 0;
 };
 
 // Replaces the buffer *p of *bytes bytes by a new one of `want` bytes (the
-// old one is retired, not freed).  0 or -1.
+// old one is retired, not freed, until plh_shutdown).  0 or -1.
 int grow_buffer(void** p, size_t* bytes, size_t want, const char* what);
 
 Context& ctx();

@@ -2,6 +2,7 @@
 // behind the C ABI declared in include/picolm_hip.h.
 #include <stdarg.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include "picolm_hip.h"
@@ -31,12 +32,15 @@ int check_hip(hipError_t e, const char* what) {
 int grow_buffer(void** p, size_t* bytes, size_t want, const char* what) {
   Context& c = g_ctx;
   if (*p) {
-    if (c.n_retired == Context::kMaxRetired) {
-      // out of slots: wait for queued work and free the oldest for real
-      if (check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize")) return -1;
-      (void)hipFree(c.retired[0]);
-      memmove(c.retired, c.retired + 1, sizeof(void*) * (Context::kMaxRetired - 1));
-      --c.n_retired;
+    if (c.n_retired == c.cap_retired) {
+      const int cap = c.cap_retired ? 2 * c.cap_retired : 16;
+      void** r = (void**)realloc(c.retired, sizeof(void*) * (size_t)cap);
+      if (!r) {
+        set_error("%s: out of host memory for the retired-buffer list", what);
+        return -1;
+      }
+      c.retired = r;
+      c.cap_retired = cap;
     }
     c.retired[c.n_retired++] = *p;
     *p = nullptr;
@@ -110,6 +114,7 @@ void plh_shutdown(void) {
     for (int i = 0; i < c.n_retired; ++i) (void)hipFree(c.retired[i]);
     (void)hipStreamDestroy(c.stream);
   }
+  free(c.retired);
   c = Context();
 }
 

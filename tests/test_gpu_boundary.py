@@ -86,9 +86,12 @@ def oracle_run(O, dims, theta, inputs, layers_gpu, qkn_mask=0):
     vc = kc.copy()
     pre = np.zeros((L, P, Hq * D), np.float32)
     dec = np.zeros((T, L, Hq * D), np.float32)
+    # the head-parallel form is bit-identical to attn_prefill; long prompts
+    # need its threads to finish in seconds
+    nthr = min(16, os.cpu_count() or 1)
     for l in layers_gpu:
-        pre[l] = O.attn_prefill(shp, l, 0, P, pq[l].copy(), pk[l].copy(), pv[l], kc, vc,
-                                cos_t, sin_t, **norms(l))
+        pre[l] = O.attn_prefill_mt(shp, l, 0, P, pq[l].copy(), pk[l].copy(), pv[l], kc, vc,
+                                   cos_t, sin_t, nthr, **norms(l))
     for t in range(T):
         for l in layers_gpu:
             dec[t, l] = O.attn_decode(shp, l, P + t, dq[t, l].copy(), dk[t, l].copy(), dv[t, l],
@@ -140,6 +143,20 @@ def test_boundary_qk_norm_layers(tmp_path, oracle_mod, dims, theta, P, T, mask):
         for t in range(T):
             assert_attn_close(out_dec[t, l], dec[t, l], D, 1e-3, f"decode t{t} layer {l}")
     assert np.array_equal(kc, okc) and np.array_equal(vc, ovc)
+
+
+# Long contexts: the decode launch splits past 512 positions and its merge
+# writes out into the pinned staging; TinyLlama heads at S 2048, a prompt
+# of P tokens through the prefill hook, then T decode steps from position P.
+LONG_CASES = [
+    ((2, 32, 4, 64, 2048, 0), 1e4, 700, 2),    # decode at 700 and 701
+    ((2, 32, 4, 64, 2048, 0), 1e4, 2047, 1),   # decode at 2047, the last cache row
+]
+
+
+@pytest.mark.parametrize("dims,theta,P,T", LONG_CASES, ids=["pos700", "pos2047"])
+def test_boundary_long_context_decode(tmp_path, oracle_mod, dims, theta, P, T):
+    test_boundary_prefill_then_decode(tmp_path, oracle_mod, dims, theta, P, T)
 
 
 def test_boundary_disabled_falls_back_untouched(tmp_path, oracle_mod):

@@ -141,3 +141,32 @@ def test_forward_fallbacks(tmp_path):
         rcs, res, kc, vc = run(tmp_path, hq, steps)
         assert rcs == (0, 0)
         assert all(rc == -1 and not lg.any() for rc, lg, _ in res)
+
+
+@pytest.mark.parametrize("cfg", [CFG, QWEN], ids=["llama", "qwen"])
+def test_forward_through_boundary_long_context(tmp_path, oracle_mod, cfg):
+    """Decode past 512 cached positions through gpu_try_forward, where the
+    attention launch is split and merged and the logits, state.x and rows
+    come back through pinned staging: a 600-token prompt, decode at 600 and
+    601, the prompt continued to position 2046, decode at 2047 (the last
+    cache row)."""
+    O = oracle_mod
+    h = S.SynthModel(**dict(cfg, max_seq_len=2048), seed=37)
+    rng = np.random.default_rng(38)
+    toks = lambda n: rng.integers(0, h.vocab_size, n).tolist()
+    steps = [(1, 0, toks(600)), (0, 600, toks(1)), (0, 601, toks(1)), (1, 602, toks(1445)),
+             (0, 2047, toks(1))]
+    rcs, res, kc, vc = run(tmp_path, h, steps)
+    assert rcs == (0, 0)
+    orc = O.OracleForward(h)
+    for (kind, start, tk), (rc, lg, x) in zip(steps, res):
+        assert rc == 0, (kind, start)
+        lo, xo = orc.prefill(tk, start, 16) if kind else orc.forward(tk[0], start, 16)
+        assert max(normwise(lg, lo), normwise(x, xo)) <= FWD_TOL, (kind, start)
+    kv_layer = h.max_seq_len * h.kv_dim
+    assert np.array_equal(kc[:kv_layer], orc.kc[:kv_layer])
+    assert np.array_equal(vc[:kv_layer], orc.vc[:kv_layer])
+    for dev_bits, orc_bits in ((kc, orc.kc), (vc, orc.vc)):
+        a, b = O.f16_to_f32(dev_bits[kv_layer:]), O.f16_to_f32(orc_bits[kv_layer:])
+        step = np.spacing(np.maximum(np.abs(a), np.abs(b)).astype(np.float16)).astype(np.float32)
+        assert np.all(np.abs(a - b) <= step + 2e-5 * np.max(np.abs(b)))

@@ -299,3 +299,52 @@ def test_forward_rejects_bad_calls(gpu):
             dm.forward(0, 0)
     finally:
         dm.free()
+
+
+@pytest.mark.parametrize("cfg", [dict(LLAMA, n_layers=2, max_seq_len=2048),
+                                 dict(QWEN, max_seq_len=2048)], ids=["llama", "qwen"])
+def test_forward_long_context_split_decode(gpu, oracle_mod, cfg):
+    """Decode steps past 512 cached positions, where the attention launch is
+    split across workgroups and merged, and the workspace grows: caches
+    pre-filled with N(0,1) rows rounded to fp16 (what kvcache_load would
+    bring in), then model_forward at 600, 601 and 2047 (the last cache row),
+    logits, residual and appended rows against the oracle."""
+    P, O = gpu, oracle_mod
+    h = S.SynthModel(**cfg, seed=61)
+    dm = P.DeviceModel(h)
+    orc = O.OracleForward(h)
+    rng = np.random.default_rng(62)
+    kv_layer = h.max_seq_len * h.kv_dim
+    try:
+        for fill, steps in ((600, (600, 601)), (2047, (2047,))):
+            kc = np.zeros(h.cache_elems(), np.uint16)
+            vc = np.zeros(h.cache_elems(), np.uint16)
+            for l in range(h.n_layers):
+                rows = slice(l * kv_layer, l * kv_layer + fill * h.kv_dim)
+                kc[rows] = O.f32_to_f16(rng.standard_normal(fill * h.kv_dim).astype(np.float32))
+                vc[rows] = O.f32_to_f16(rng.standard_normal(fill * h.kv_dim).astype(np.float32))
+            orc.kc[:] = kc      # the oracle model holds these arrays' addresses
+            orc.vc[:] = vc
+            dm.load_cache(kc, vc)
+            for pos in steps:
+                tok = int(rng.integers(0, h.vocab_size))
+                print(f"[case] long-context forward {h.n_layers}x{h.n_embd} pos {pos} tok {tok}",
+                      flush=True)
+                dm.forward(tok, pos)
+                P.synchronize()
+                lo, xo = orc.forward(tok, pos, n_threads=8)
+                e = max(normwise(dm.fetch_logits(), lo), normwise(dm.fetch_x(), xo))
+                assert e <= FWD_TOL, (pos, e)
+                gk, gv = dm.fetch_cache()
+                assert np.array_equal(gk[:kv_layer], orc.kc[:kv_layer]), pos
+                assert np.array_equal(gv[:kv_layer], orc.vc[:kv_layer]), pos
+                for dev_bits, orc_bits in ((gk, orc.kc), (gv, orc.vc)):
+                    a = O.f16_to_f32(dev_bits[kv_layer:])
+                    b = O.f16_to_f32(orc_bits[kv_layer:])
+                    step = np.spacing(np.maximum(np.abs(a), np.abs(b)).astype(np.float16))
+                    bound = step.astype(np.float32) + KV_TOL * np.max(np.abs(b))
+                    assert np.all(np.abs(a - b) <= bound), pos
+                # keep both caches identical for the next step
+                dm.load_cache(orc.kc, orc.vc)
+    finally:
+        dm.free()

@@ -80,3 +80,17 @@ def test_prefill_qknorm_generic(gpu, oracle_mod, dims):
 def test_decode_rows_generic(gpu, host_rows):
     TR.test_decode_rows_match_plain_decode(gpu, (2, 8, 2, 96, 300, 1, 0, 2, 250, True),
                                            host_rows)
+
+
+# Shapes the tuned prefill kernel does not take, routed to the generic kernels
+# by plh_attn_prefill instead of being refused: an output row of 5 heads x 18
+# floats (q_dim = 90, not a multiple of 4), and a GQA group of 136 q heads
+# (more columns than one tuned workgroup holds) at the tuned head_dim 64.
+@pytest.mark.parametrize("case", [(1, 5, 1, 18, 64, 1e4, 0, 3, 40),
+                                  (1, 5, 5, 18, 64, 1e4, 1, 0, 33),
+                                  (1, 136, 1, 64, 48, 1e4, 0, 2, 20)],
+                         ids=["h5_d18_gqa5", "h5_d18_mha", "g136_d64"])
+def test_prefill_untuned_shapes_use_generic(gpu, oracle_mod, case):
+    L, Hq, Hkv, D, S, theta, rt, start, n = case
+    cfg = gpu.AttnConfig(L, Hq, Hkv, D, S, theta, rt)
+    TP.run_prefill(gpu, oracle_mod, cfg, start, n, seed=start + n + Hq)

@@ -67,6 +67,66 @@ def test_noalloc_matches_decode_twice(gpu, oracle_mod):
             assert_attn_close(out_n[l], ref, cfg.head_dim, 1e-3, f"noalloc call {i} layer {l}")
 
 
+def test_noalloc_captured_in_graph_from_fresh_library(gpu, oracle_mod):
+    """The property the entry point exists for: it queues no allocation.
+    The library is shut down and re-initialised so that no workspace
+    exists, then a split launch (22 layers, pos 2047) is captured in a HIP
+    graph before any allocating decode call (an allocation during capture
+    fails the capture).  The graph is replayed three times with eager work
+    and synchronisations between the replays; every replay's output and
+    cache must equal an eager plh_attn_decode call bit for bit."""
+    O, P = oracle_mod, gpu
+    P.lib.plh_shutdown()
+    P.init(0)
+    cfg = P.AttnConfig(22, 32, 4, 64, 2048, 1e4, 0)
+    pos = 2047
+    rng = np.random.default_rng(300)
+    kc, vc = filled_cache(O, cfg, pos, rng)
+    q = normal_f32(rng, (cfg.n_layers, cfg.q_dim))
+    k = normal_f32(rng, (cfg.n_layers, cfg.kv_dim))
+    v = normal_f32(rng, (cfg.n_layers, cfg.kv_dim))
+    cache = P.KVCache(cfg)
+    cache.load(kc, vc)
+    dq, dk, dv = (P.DeviceBuffer.from_numpy(x) for x in (q, k, v))
+    dout = P.DeviceBuffer(cfg.n_layers * cfg.q_dim * 4)
+    dout.zero()
+    P.synchronize()
+    args = (cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.head_dim, cfg.max_seq_len,
+            cfg.rope_type, 0, cfg.n_layers, pos, dq.ptr, dk.ptr, dv.ptr, cache.key.ptr,
+            cache.val.ptr, cache.cos.ptr, cache.sin.ptr, dout.ptr)
+    print("[case] noalloc captured from a fresh library", flush=True)
+    with P.Graph() as g:
+        P.check(P.lib.plh_attn_decode_noalloc(*args), "plh_attn_decode_noalloc (captured)")
+    try:
+        rc, want, wk, wv = decode_call(P, P.lib.plh_attn_decode, cfg, pos, q, k, v, kc, vc,
+                                       cfg.n_layers)
+        assert rc == 0
+        for rep in range(3):
+            dout.zero()
+            cache.load(kc, vc)
+            P.synchronize()
+            g.launch()
+            P.synchronize()
+            got = dout.download(np.float32, (cfg.n_layers, cfg.q_dim))
+            gk, gv = cache.fetch()
+            assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), rep
+            assert np.array_equal(gk, wk) and np.array_equal(gv, wv), rep
+            # eager work between replays: an allocating call of another shape
+            rc, _, _, _ = decode_call(P, P.lib.plh_attn_decode, P.AttnConfig(*CASES[1][0]),
+                                      CASES[1][1], *small_inputs(O, P, rep), 3)
+            assert rc == 0
+    finally:
+        cache.free()
+
+
+def small_inputs(O, P, seed):
+    cfg = P.AttnConfig(*CASES[1][0])
+    rng = np.random.default_rng(400 + seed)
+    kc, vc = filled_cache(O, cfg, CASES[1][1], rng)
+    return (normal_f32(rng, (cfg.n_layers, cfg.q_dim)), normal_f32(rng, (cfg.n_layers, cfg.kv_dim)),
+            normal_f32(rng, (cfg.n_layers, cfg.kv_dim)), kc, vc)
+
+
 def test_noalloc_refuses_oversized_partials(gpu, oracle_mod):
     """8 layers x 8 kv heads x 16 q heads each, head_dim 128, 4096 rows cut
     into 128-row splits (tuning key 1 asks for that many workgroups):
