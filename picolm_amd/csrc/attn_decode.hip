@@ -68,6 +68,9 @@ using namespace plh;
 // address: decode_scratch_setup (called by plh_init with the device current)
 // looks the device address up once per device, and launches use that.
 static constexpr size_t kScratchBytes = 16u << 20;
+// its first kScratchCounterBytes hold the stream-K kernel's arrival counters,
+// the rest the split partials
+static constexpr size_t kScratchCounterBytes = (size_t)kDecodeCounters * sizeof(unsigned);
 static constexpr int kMaxDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 static void* g_scratch_ptr[kMaxDevices];  // its device address, per device
@@ -644,12 +647,251 @@ __global__ __launch_bounds__(kCombineThreads) void attn_decode_combine_kernel(De
   }
 }
 
+// ---- stream-K decode with the merge inside the kernel --------------------
+//
+// The groups' cached rows, in 16-row blocks, are flattened group-major and
+// cut into sk_W equal ranges, one per workgroup (about one per CU), so every
+// CU streams the same number of bytes whatever the shape.  A range covers
+// the end of one group and the start of the next at most a few times; for
+// each group segment the workgroup's 4 waves take its 32-row tiles in turn
+// with two tiles of loads in flight per wave (a paced stream: the memory
+// queues stay short, so q and the first tiles arrive early), merge through
+// LDS as the split kernel does, and then either write the output (the only
+// producer of the group) or store a partial and count themselves in.  The
+// last producer of a group to arrive merges its partials and writes the
+// output, so one launch does everything.  The partials cross XCDs, whose L2
+// caches are not coherent with each other: they are stored and loaded with
+// device-scope cache policy (sc1: written through, read past the L2), the
+// stores complete before the arrival counter is bumped, and the counter is a
+// device-scope atomic; the merging workgroup resets it to zero for the next
+// launch.
+
+// The T blocks are cut into W ranges of q or q + 1 blocks (q = T / W,
+// r = T % W: the first r ranges take q + 1): range w starts at w*q + min(w,
+// r).  All in 32-bit integers (the host checks T fits): 64-bit division
+// would cost the prologue about a thousand instructions.
+__device__ __forceinline__ int sk_start(int w, int q, int r) { return w * q + min(w, r); }
+__device__ __forceinline__ int sk_owner(int t, int q, int r) {
+  const int big = r * (q + 1);
+  return t < big ? t / (q + 1) : r + (t - big) / q;
+}
+
+constexpr int kSkAux = 16; // buffer cache policy: sc1 (device scope)
+
+template <int D>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const DecodeArgs& a) {
+  return __builtin_amdgcn_make_buffer_rsrc(a.sk_part, 0, (int)a.sk_part_bytes, 0x00020000);
+}
+
+template <int D, bool QKN, int kSkPF>
+__global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
+  constexpr int kWaves = 4;
+  constexpr int kThreads = 64 * kWaves;
+  constexpr int ND = D / 32;
+  constexpr int NO = D / 16;
+  constexpr int VP = D + 16;
+  constexpr int PS = D + 4;  // floats per (slot, head) of a partial: o[D], m, l, pad
+  constexpr int kVtileHalves = kWaves * kTile * VP;
+  constexpr int kCombFloats = kWaves * 16 * (D + 2);
+  constexpr int kSmemBytes =
+      (kVtileHalves * 2 > kCombFloats * 4) ? kVtileHalves * 2 : kCombFloats * 4;
+  __shared__ __align__(16) unsigned char smem[kSmemBytes];
+  __shared__ float s_knew[D], s_vnew[D], s_mnew[16];
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  const int w = blockIdx.x;
+  const int b0 = sk_start(w, a.sk_q, a.sk_r), b1 = sk_start(w + 1, a.sk_q, a.sk_r);
+  const int G = a.n_heads / a.n_kv_heads;
+  const int kv_dim = a.n_kv_heads * D;
+  const int pos = a.pos;
+  const int q_dim = a.n_heads * D;
+  const __amdgpu_buffer_rsrc_t prs = sk_rsrc<D>(a);
+
+  for (int s0 = b0; s0 < b1;) {
+    const int group = s0 / a.sk_nbk;
+    const int gb = group * a.sk_nbk;
+    const int s1 = min(b1, gb + a.sk_nbk);
+    const int hblk = group % a.n_hblk;
+    const int kvh = (group / a.n_hblk) % a.n_kv_heads;
+    const int li = group / (a.n_hblk * a.n_kv_heads);
+    const int layer = a.layer0 + li;
+    const int h0 = hblk * 16;
+    const int nh = min(16, G - h0);
+    const int tb = (s0 - gb) * 16;
+    const int te = min((s1 - gb) * 16, pos);  // cached rows [tb, te); row pos is new
+    const bool owner = s1 == gb + a.sk_nbk;   // covers the group's last block
+
+    const int tlast = te - 1;
+    const size_t row0 = (size_t)layer * a.max_seq_len;
+    const uint16_t* kbase = a.kc + row0 * kv_dim + (size_t)kvh * D;
+    const uint16_t* vbase = a.vc + row0 * kv_dim + (size_t)kvh * D;
+    constexpr int kStride = kWaves * kTile;
+    const int tw = tb + wave * kTile;
+    const bool new_row = owner && wave == 0;
+
+    QRaw<D> qr;
+    load_q_raw<D, QKN>(a, li, kvh, G, h0, nh, col, grp, qr);
+    RowRaw<D> rr;
+    load_row_raw<D, QKN>(a, li, kvh, lane, rr);
+
+    const bool has_rows = te > tb;
+    const int tclamp = has_rows ? tlast : 0;
+    Tile<D> buf[kSkPF];
+#pragma unroll
+    for (int j = 0; j < kSkPF; ++j)
+      load_tile<D>(buf[j], kbase, vbase, kv_dim, tw + j * kStride, tclamp, lane, col, grp);
+
+    half8_t qhi[ND], qlo[ND];
+    __builtin_amdgcn_sched_barrier(0);
+    const float qup = split_q<D, QKN>(a, col < nh, grp, qr, qhi, qlo);
+    if (new_row)
+      append_new_row<D, QKN>(a, li, kvh, row0, lane, col, grp, qr, rr, s_knew, s_vnew, s_mnew);
+
+    _Float16* vt = reinterpret_cast<_Float16*>(smem) + wave * (kTile * VP);
+    const float sscale = a.score_scale * qup;
+    float m = kNegBig;
+    float4_t lsum = float4_t{0.f, 0.f, 0.f, 0.f};
+    half8_t ones;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ones[j] = (_Float16)1.0f;
+    float4_t o[NO];
+#pragma unroll
+    for (int ob = 0; ob < NO; ++ob) o[ob] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    if (has_rows) {
+      for (int base = tw; base < te; base += kSkPF * kStride) {
+#pragma unroll
+        for (int j = 0; j < kSkPF; ++j) {
+          const int t0 = base + j * kStride;
+          if (t0 < te)
+            process_tile<D>(buf[j], qhi, qlo, vt, t0, tlast, lane, col, grp, sscale, ones, m,
+                            lsum, o);
+          load_tile<D>(buf[j], kbase, vbase, kv_dim, t0 + kSkPF * kStride, tclamp, lane, col,
+                       grp);
+        }
+      }
+    }
+    const float l = lsum[0];
+
+    __syncthreads();  // V tiles are dead; the LDS now holds the combine slots
+    float* cm = reinterpret_cast<float*>(smem);
+    float* cl = cm + kWaves * 16;
+    float* co = cl + kWaves * 16;
+    if (grp == 0) {
+      cm[wave * 16 + col] = m;
+      cl[wave * 16 + col] = l;
+    }
+#pragma unroll
+    for (int ob = 0; ob < NO; ++ob)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) co[(wave * 16 + col) * D + 16 * ob + 4 * grp + r] = o[ob][r];
+    __syncthreads();
+
+    // producers of this group: the workgroups owning its first and last block
+    const int p0 = sk_owner(gb, a.sk_q, a.sk_r);
+    const int np = sk_owner(gb + a.sk_nbk - 1, a.sk_q, a.sk_r) - p0 + 1;
+
+    // ---- merge the waves (and the new row); one float4 of d per thread -----
+    float* out_base = a.out + (size_t)li * q_dim + (size_t)(kvh * G + h0) * D;
+    const int slot0 = group * a.sk_maxp;
+    for (int idx = tid; idx < nh * (D / 4); idx += kThreads) {
+      const int h = idx / (D / 4), d = 4 * (idx - h * (D / 4));
+      float M = kNegBig;
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, cm[ww * 16 + h]);
+      if (owner) M = fmaxf(M, s_mnew[h]);
+      float L = 0.f;
+      float4_t O = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) {
+        const float wt = fast_exp2(cm[ww * 16 + h] - M);
+        L = __builtin_fmaf(cl[ww * 16 + h], wt, L);
+        const float4_t x = *reinterpret_cast<const float4_t*>(co + (ww * 16 + h) * D + d);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) O[c] = __builtin_fmaf(x[c], wt, O[c]);
+      }
+      if (owner) {
+        const float wt = fast_exp2(s_mnew[h] - M);
+        L += wt;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) O[c] = __builtin_fmaf(s_vnew[d + c], wt, O[c]);
+      }
+      if (np == 1) {
+        const float inv = 1.0f / L;
+        *reinterpret_cast<float4_t*>(out_base + (size_t)h * D + d) = O * inv;
+      } else {
+        const int off = ((slot0 + (w - p0)) * a.nhm + h) * PS;
+        __builtin_amdgcn_raw_buffer_store_b128(O, prs, (off + d) * 4, 0, kSkAux);
+        if (d == 0)
+          __builtin_amdgcn_raw_buffer_store_b128(float4_t{M, L, 0.f, 0.f}, prs, (off + D) * 4,
+                                                 0, kSkAux);
+      }
+    }
+
+    if (np > 1) {
+      // every partial store has reached memory before the count goes up
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      if (tid == 0)
+        s_last = __hip_atomic_fetch_add(a.sk_ctr + group, 1u, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(np - 1);
+      __syncthreads();
+      if (s_last) {
+        if (tid == 0)
+          __hip_atomic_store(a.sk_ctr + group, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int idx = tid; idx < nh * (D / 4); idx += kThreads) {
+          const int h = idx / (D / 4), d = 4 * (idx - h * (D / 4));
+          float M = kNegBig, L = 0.f;
+          float4_t O = float4_t{0.f, 0.f, 0.f, 0.f};
+          for (int j0 = 0; j0 < np; j0 += 8) {
+            float4_t ml[8], oj[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              const int off = ((slot0 + min(j0 + j, np - 1)) * a.nhm + h) * PS;
+              ml[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, (off + D) * 4, 0, kSkAux);
+              oj[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, (off + d) * 4, 0, kSkAux);
+            }
+            float Mc = M;
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+              if (j0 + j < np) Mc = fmaxf(Mc, ml[j][0]);
+            const float r = fast_exp2(M - Mc);
+            L *= r;
+            O *= r;
+#pragma unroll
+            for (int j = 0; j < 8; ++j) {
+              if (j0 + j < np) {
+                const float wt = fast_exp2(ml[j][0] - Mc);
+                L = __builtin_fmaf(ml[j][1], wt, L);
+#pragma unroll
+                for (int c = 0; c < 4; ++c) O[c] = __builtin_fmaf(oj[j][c], wt, O[c]);
+              }
+            }
+            M = Mc;
+          }
+          const float inv = 1.0f / L;
+          *reinterpret_cast<float4_t*>(out_base + (size_t)h * D + d) = O * inv;
+        }
+      }
+    }
+    s0 = s1;
+    __syncthreads();  // the LDS is reused by the next segment
+  }
+}
+
 // Split plan defaults, from sweeps on MI355X (TinyLlama pos 256 and 2047,
 // Llama-3.2 pos 8191, Llama-2 pos 4095, one-layer launches): about four
 // workgroups per CU; contexts up to 512 positions are not split.
 constexpr int kDefaultMinSplit = 512;
 int g_target_units = 0;   // 0: four workgroups per CU
 int g_min_split = kDefaultMinSplit;
+int g_decode_kernel = 0;  // plh_set_tuning key 7: 0 by shape, 1 split + combine, 2 stream-K
+int g_sk_workgroups = 0;  // key 8: stream-K workgroups (0: the launch's own choice)
+int g_sk_pf = 0;          // key 9: stream-K tiles in flight per wave (0: by head_dim)
 
 }  // namespace
 
@@ -663,6 +905,12 @@ int decode_scratch_setup(int device) {
   if (g_scratch_ptr[device]) return 0;
   void* p = nullptr;
   if (check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)"))
+    return -1;
+  // the stream-K merge counters at the start of the array start at zero
+  // (every launch leaves them zero again)
+  Context& c = ctx();
+  if (check_hip(hipMemsetAsync(p, 0, kScratchCounterBytes, c.stream), "hipMemsetAsync(scratch)") ||
+      check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize"))
     return -1;
   g_scratch_ptr[device] = p;
   return 0;
@@ -718,8 +966,165 @@ extern "C" int plh_set_tuning(int key, int value) {
     g_prefill_ksplit = value;
     return 0;
   }
+  if (key == 7) {
+    if (value != 0 && value != 1 && value != 2) {
+      set_error("plh_set_tuning: decode kernel must be 0 (by shape), 1 (split + combine) or 2 "
+                "(stream-K)");
+      return -1;
+    }
+    g_decode_kernel = value;
+    return 0;
+  }
+  if (key == 8) {
+    if (value < 0) {
+      set_error("plh_set_tuning: stream-K workgroups must be >= 0");
+      return -1;
+    }
+    g_sk_workgroups = value;
+    return 0;
+  }
+  if (key == 9) {
+    if (value != 0 && value != 2 && value != 3 && value != 4) {
+      set_error("plh_set_tuning: stream-K prefetch depth must be 0, 2, 3 or 4");
+      return -1;
+    }
+    g_sk_pf = value;
+    return 0;
+  }
   set_error("plh_set_tuning: unknown key %d", key);
   return -1;
+}
+
+// Which decode kernel a launch gets (plh_set_tuning key 7 overrides).
+// Measured on MI355X with all layers in one launch and with one launch per
+// layer: the stream-K kernel is faster for head_dim 128 (Llama-2 pos 4095:
+// 355 against 379 us per token, per-layer 601 against 778 us) and for
+// head_dim 64 ranges of at most 64 blocks per workgroup (TinyLlama pos
+// 2047: 16.7-17.2 against 17.6-17.9 us); the split kernel is faster for long
+// head_dim 64 streams (Llama-3.2 pos 8191, 256 blocks per workgroup: 54.9
+// against 61.9 us) and for contexts it does not split (TinyLlama pos 256:
+// 6.6 against 8.3 us).
+static bool use_stream_k(int head_dim, int pos, int n_groups, int num_cus) {
+  if (g_decode_kernel) return g_decode_kernel == 2;
+  if (pos + 1 <= g_min_split) return false;
+  if (head_dim == 128) return true;
+  const long T = (long)n_groups * ((pos + 15) / 16);
+  const long cus = num_cus > 0 ? num_cus : 256;
+  long W = T / 8;
+  if (W > cus) W = cus;
+  return W > 0 && T / W <= 64;
+}
+
+// Plans and queues one stream-K launch (attn_decode_sk_kernel).
+static int attn_decode_sk_launch(int n_heads, int n_kv_heads, int head_dim, int max_seq_len,
+                                 int rope_type, int layer0, int n_launch_layers, int pos,
+                                 const float* q, const float* k, const float* v,
+                                 uint16_t* key_cache, uint16_t* val_cache, const float* rope_cos,
+                                 const float* rope_sin, float* out, const float* q_norm,
+                                 const float* k_norm, float norm_eps, bool noalloc,
+                                 uint16_t* k_rows, uint16_t* v_rows) {
+  Context& c = ctx();
+  const int G = n_heads / n_kv_heads;
+  const int n_hblk = (G + 15) / 16;
+  const int nhm = G < 16 ? G : 16;
+  const int n_groups = n_launch_layers * n_kv_heads * n_hblk;
+  // cached rows [0, pos) in 16-row blocks (one empty block at pos 0)
+  const int nbk = pos > 0 ? (pos + 15) / 16 : 1;
+  const long T = (long)n_groups * nbk;
+  if (T > 0x7fffffffL) {
+    set_error("plh_attn_decode: %ld cache blocks in one launch exceed the 32-bit plan", T);
+    return -1;
+  }
+  const int cus = c.num_cus > 0 ? c.num_cus : 256;
+  // about one workgroup per CU, each with at least 8 blocks (one 32-row
+  // tile per wave)
+  long W = g_sk_workgroups > 0 ? g_sk_workgroups : T / 8;
+  if (W > cus && g_sk_workgroups == 0) W = cus;
+  if (W > T) W = T;
+  if (W < 1) W = 1;
+  // producers per group (the partial slots it needs)
+  int maxp = 1;
+  {
+    const long qq = T / W, rr = T % W, big = rr * (qq + 1);
+    auto owner_of = [&](long t) { return t < big ? t / (qq + 1) : rr + (t - big) / qq; };
+    for (int g = 0; g < n_groups; ++g) {
+      const long gb = (long)g * nbk;
+      const long np = owner_of(gb + nbk - 1) - owner_of(gb) + 1;
+      if (np > maxp) maxp = (int)np;
+    }
+  }
+  const size_t part_bytes =
+      maxp > 1 ? (size_t)n_groups * maxp * nhm * (head_dim + 4) * sizeof(float) : 16;
+  float* part;
+  unsigned* ctr;
+  if (noalloc) {
+    if (part_bytes > kScratchBytes - kScratchCounterBytes) {
+      set_error("plh_attn_decode_noalloc: this launch needs %zu bytes of split partials, "
+                "more than the %zu bytes the static scratch holds for them",
+                part_bytes, kScratchBytes - kScratchCounterBytes);
+      return -1;
+    }
+    ctr = (unsigned*)g_scratch_ptr[c.device];
+    part = (float*)((char*)g_scratch_ptr[c.device] + kScratchCounterBytes);
+  } else {
+    if (part_bytes > 0x7fffffffu) {
+      set_error("plh_attn_decode: %zu bytes of split partials exceed the 2 GiB buffer range",
+                part_bytes);
+      return -1;
+    }
+    if (ensure_workspace(part_bytes)) return -1;
+    ctr = c.decode_ctr;
+    part = (float*)c.ws;
+  }
+
+  DecodeArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.kc = key_cache;
+  a.vc = val_cache;
+  a.cos_t = rope_cos;
+  a.sin_t = rope_sin;
+  a.out = out;
+  a.layer0 = layer0;
+  a.n_launch_layers = n_launch_layers;
+  a.n_heads = n_heads;
+  a.n_kv_heads = n_kv_heads;
+  a.max_seq_len = max_seq_len;
+  a.pos = pos;
+  a.rope_type = rope_type;
+  a.n_hblk = n_hblk;
+  a.nhm = nhm;
+  a.qn = q_norm;
+  a.kn = k_norm;
+  a.norm_eps = norm_eps;
+  a.score_scale = kLog2e / sqrtf((float)head_dim);
+  a.k_rows = k_rows;
+  a.v_rows = v_rows;
+  a.sk_q = (int)(T / W);
+  a.sk_r = (int)(T % W);
+  a.sk_nbk = nbk;
+  a.sk_maxp = maxp;
+  a.sk_groups = n_groups;
+  a.sk_part = part;
+  a.sk_part_bytes = (uint32_t)part_bytes;
+  a.sk_ctr = ctr;
+  const dim3 grid((unsigned)W), block(256);
+  const bool qkn = q_norm != nullptr;
+  const int pf = g_sk_pf ? g_sk_pf : 2;
+#define PLH_SK(D, Q, PF) \
+  hipLaunchKernelGGL((attn_decode_sk_kernel<D, Q, PF>), grid, block, 0, c.stream, a)
+  if (head_dim == 64 && !qkn) {
+    if (pf == 2) PLH_SK(64, false, 2); else if (pf == 3) PLH_SK(64, false, 3); else PLH_SK(64, false, 4);
+  } else if (head_dim == 64) {
+    if (pf == 2) PLH_SK(64, true, 2); else if (pf == 3) PLH_SK(64, true, 3); else PLH_SK(64, true, 4);
+  } else if (!qkn) {
+    if (pf == 2) PLH_SK(128, false, 2); else if (pf == 3) PLH_SK(128, false, 3); else PLH_SK(128, false, 4);
+  } else {
+    if (pf == 2) PLH_SK(128, true, 2); else if (pf == 3) PLH_SK(128, true, 3); else PLH_SK(128, true, 4);
+  }
+#undef PLH_SK
+  return check_hip(hipGetLastError(), "attn_decode_sk_kernel");
 }
 
 static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_dim,
@@ -777,6 +1182,13 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
   const int n_groups = n_launch_layers * n_kv_heads * n_hblk;
   const int npos = pos + 1;
 
+  if (use_stream_k(head_dim, pos, n_groups, c.num_cus) && ((uintptr_t)out & 15) == 0 &&
+      n_groups <= kDecodeCounters)
+    return attn_decode_sk_launch(n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, layer0,
+                                 n_launch_layers, pos, q, k, v, key_cache, val_cache, rope_cos,
+                                 rope_sin, out, q_norm, k_norm, norm_eps, noalloc, k_rows,
+                                 v_rows);
+
   // Split plan: contexts of at most g_min_split positions are not split (the
   // merge launch would cost more than it saves); longer ones are cut into
   // splits of a multiple of 128 rows (one 32-row tile per wave at least),
@@ -808,13 +1220,13 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
     const size_t pm = (size_t)n_units * nhm * sizeof(float);
     void* base;
     if (noalloc) {
-      if (po + 2 * pm > kScratchBytes) {
+      if (po + 2 * pm > kScratchBytes - kScratchCounterBytes) {
         set_error("plh_attn_decode_noalloc: this launch needs %zu bytes of split partials, "
-                  "more than the %zu-byte static scratch",
-                  po + 2 * pm, kScratchBytes);
+                  "more than the %zu bytes the static scratch holds for them",
+                  po + 2 * pm, kScratchBytes - kScratchCounterBytes);
         return -1;
       }
-      base = g_scratch_ptr[c.device];
+      base = (char*)g_scratch_ptr[c.device] + kScratchCounterBytes;
     } else {
       if (ensure_workspace(po + 2 * pm)) return -1;
       base = c.ws;

@@ -18,6 +18,9 @@ struct Context {
   void* pf_ws = nullptr;       // prompt-chunk activations of plh_forward_prefill
   size_t pf_ws_bytes = 0;
   int num_cus = 0;
+  // Arrival counters of the decode kernel's in-kernel merge (zeroed once at
+  // plh_init; every launch leaves them zero).
+  unsigned* decode_ctr = nullptr;
   // Workspaces outgrown by a larger call.  A graph captured before the growth
   // still holds their addresses in its kernel nodes, so every one of them
   // stays allocated until plh_shutdown (a host-side list that grows as
@@ -86,6 +89,9 @@ int decode_scratch_setup(int device);
 // Makes sure the workspace holds at least `bytes` (the outgrown one is
 // retired until plh_shutdown).  Returns 0 or -1.
 int ensure_workspace(size_t bytes);
+// Capacity of Context::decode_ctr and of the static scratch's counter region:
+// the most (layer, kv head, q-head block) groups one decode launch may cover.
+constexpr int kDecodeCounters = 1 << 18;
 
 // Attention of the head dims without a tuned kernel (every even head_dim up
 // to 256 but 64 and 128; attn_generic.hip): append and attend n_tokens rows
@@ -123,6 +129,18 @@ struct DecodeArgs {
   float score_scale;       // log2(e) / sqrt(D)
   uint16_t* k_rows;        // the appended rows also here [n_launch_layers][kv_dim], or null
   uint16_t* v_rows;
+  // Stream-K plan (attn_decode_sk_kernel): the groups' cached rows in 16-row
+  // blocks, flattened group-major (sk_nbk blocks per group) and cut into one
+  // range per workgroup, ranges of sk_q or sk_q + 1 blocks (the first sk_r
+  // take sk_q + 1).  A group covered by several
+  // ranges is merged in the kernel by its last-arriving producer through
+  // sk_part (sk_maxp slots per group of nhm x (D + 4) floats) and the
+  // self-resetting arrival counters sk_ctr (one per group, zero between
+  // launches).
+  int sk_q, sk_r, sk_nbk, sk_maxp, sk_groups;
+  float* sk_part;
+  uint32_t sk_part_bytes;
+  unsigned* sk_ctr;
 };
 
 }  // namespace plh

@@ -100,6 +100,16 @@ int plh_init(int device) {
     c.stream = nullptr;
     return -1;
   }
+  if (check_hip(hipMalloc(&c.decode_ctr, kDecodeCounters * sizeof(unsigned)),
+                "hipMalloc(decode counters)") ||
+      check_hip(hipMemsetAsync(c.decode_ctr, 0, kDecodeCounters * sizeof(unsigned), c.stream),
+                "hipMemsetAsync(decode counters)") ||
+      check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize")) {
+    if (c.decode_ctr) (void)hipFree(c.decode_ctr);
+    (void)hipStreamDestroy(c.stream);
+    c = Context();
+    return -1;
+  }
   c.device = device;
   c.num_cus = prop.multiProcessorCount;
   return 0;
@@ -111,6 +121,7 @@ void plh_shutdown(void) {
     (void)hipStreamSynchronize(c.stream);
     if (c.ws) (void)hipFree(c.ws);
     if (c.pf_ws) (void)hipFree(c.pf_ws);
+    if (c.decode_ctr) (void)hipFree(c.decode_ctr);
     for (int i = 0; i < c.n_retired; ++i) (void)hipFree(c.retired[i]);
     (void)hipStreamDestroy(c.stream);
   }

@@ -250,11 +250,36 @@ def test_decode_graph_replays_match_eager(gpu, oracle_mod):
                           kc.reshape(3, -1, cfg.kv_dim)[:, :pos])
 
 
+@pytest.mark.parametrize("workgroups", [1, 3, 7, 64, 256, 1000])
+def test_decode_stream_k_plans(gpu, oracle_mod, workgroups):
+    """Stream-K plans (plh_set_tuning key 8) from one workgroup walking every
+    group whole (several groups per workgroup, no merge) to many short
+    ranges (dozens of producers per group, merged in the kernel in batches
+    of eight): oracle-exact outputs and caches, with ranges that start and
+    end inside tiles, positions 0 and 1 (the new row only), a GQA group of
+    24 q heads (two head blocks) and head_dim 128."""
+    try:
+        gpu.check(gpu.lib.plh_set_tuning(7, 2), "tuning")
+        gpu.check(gpu.lib.plh_set_tuning(8, workgroups), "tuning")
+        cfg = gpu.AttnConfig(4, 32, 4, 64, 2048, 1e4, 0)
+        for pos in (2047, 700, 129, 17, 16, 1, 0):
+            run_decode(gpu, oracle_mod, cfg, pos, seed=pos + workgroups, check_layers=[0, 3])
+        cfg = gpu.AttnConfig(2, 32, 32, 128, 1024, 1e4, 0)
+        run_decode(gpu, oracle_mod, cfg, 1000, seed=5 + workgroups)
+        cfg = gpu.AttnConfig(2, 48, 2, 64, 600, 1e6, 1)
+        run_decode(gpu, oracle_mod, cfg, 555, seed=6 + workgroups)
+    finally:
+        gpu.lib.plh_set_tuning(8, 0)
+        gpu.lib.plh_set_tuning(7, 0)
+
+
 @pytest.mark.parametrize("min_split", [128, 512, 1024, 2048])
 def test_decode_split_lengths(gpu, oracle_mod, min_split):
-    """Several split plans (one split, no combine launch, included) give
-    oracle-exact results."""
+    """The split + combine kernels (plh_set_tuning key 7 = 1) under several
+    split plans (one split, no combine launch, included) give oracle-exact
+    results."""
     try:
+        gpu.check(gpu.lib.plh_set_tuning(7, 1), "tuning")
         gpu.check(gpu.lib.plh_set_tuning(2, min_split), "tuning")
         cfg = gpu.AttnConfig(4, 32, 4, 64, 2048, 1e4, 0)
         for pos in (2047, 700, 129):
@@ -263,3 +288,4 @@ def test_decode_split_lengths(gpu, oracle_mod, min_split):
         run_decode(gpu, oracle_mod, cfg, 1000, seed=5 + min_split)
     finally:
         gpu.lib.plh_set_tuning(2, 0)
+        gpu.lib.plh_set_tuning(7, 0)

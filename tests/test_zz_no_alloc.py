@@ -128,11 +128,13 @@ def small_inputs(O, P, seed):
 
 
 def test_noalloc_refuses_oversized_partials(gpu, oracle_mod):
-    """8 layers x 8 kv heads x 16 q heads each, head_dim 128, 4096 rows cut
-    into 128-row splits (tuning key 1 asks for that many workgroups):
-    2048 units x 16 heads x 130 floats = 17 MB of partials > the 16 MiB
-    scratch.  The call returns -1 with a message and writes nothing; the
-    workspace entry point runs the same launch."""
+    """8 layers x 8 kv heads x 16 q heads each, head_dim 128, 4095 cached
+    rows, with tuning keys 1 and 8 asking for as many workgroups as the
+    rows allow: the stream-K plan gives every 16-row block a workgroup of
+    its own, 64 groups x 257 partial slots x 16 heads x 132 floats = 139 MB
+    of partials (the split plan, 128-row splits, 17 MB), more than the
+    static scratch holds.  The call returns -1 with a message and writes
+    nothing; the workspace entry point runs the same launch."""
     P = gpu
     cfg = P.AttnConfig(8, 128, 8, 128, 4096, 1e4, 0)
     pos = 4095
@@ -142,7 +144,8 @@ def test_noalloc_refuses_oversized_partials(gpu, oracle_mod):
     q = normal_f32(rng, (cfg.n_layers, cfg.q_dim))
     k = normal_f32(rng, (cfg.n_layers, cfg.kv_dim))
     v = normal_f32(rng, (cfg.n_layers, cfg.kv_dim))
-    P.check(P.lib.plh_set_tuning(1, 1 << 20), "plh_set_tuning")
+    P.check(P.lib.plh_set_tuning(1, 1 << 20), "plh_set_tuning")   # split kernel
+    P.check(P.lib.plh_set_tuning(8, 1 << 20), "plh_set_tuning")   # stream-K kernel
     try:
         print("[case] noalloc oversized partials", flush=True)
         rc, out, gk, gv = decode_call(P, P.lib.plh_attn_decode_noalloc, cfg, pos, q, k, v, kc,
@@ -155,3 +158,4 @@ def test_noalloc_refuses_oversized_partials(gpu, oracle_mod):
         assert rc == 0 and np.all(np.isfinite(out))
     finally:
         P.check(P.lib.plh_set_tuning(1, 0), "plh_set_tuning")
+        P.check(P.lib.plh_set_tuning(8, 0), "plh_set_tuning")
