@@ -130,12 +130,24 @@ def gemv_bytes(mats) -> int:
     return total
 
 
-def run_gemv(P, steps, warmup):
+def run_gemv(P, steps, warmup, exact=False, inputs=None):
     """One step = every weight GEMV of one token (155 launches, device
     pointers, graph-replayed); the 670 MB of weights exceed the Infinity
-    Cache, so each step streams them from HBM."""
+    Cache, so each step streams them from HBM.  exact: the reference's AVX2
+    summation order (plh_set_tuning key 10) instead of the default fast one;
+    inputs: the matrices and vectors of an earlier call, reused."""
+    P.check(P.lib.plh_set_tuning(10, 1 if exact else 0), "plh_set_tuning")
+    try:
+        return _run_gemv(P, steps, warmup, inputs)
+    finally:
+        P.check(P.lib.plh_set_tuning(10, 0), "plh_set_tuning")
+
+
+def _run_gemv(P, steps, warmup, inputs):
     from picolm_amd import gemv as G
     from picolm_amd import synth as S
+    if inputs is not None:
+        return _time_gemv(P, steps, warmup, *inputs)
     mats = gemv_matrices()
     rng = np.random.default_rng(155)
     host = {}
@@ -147,6 +159,11 @@ def run_gemv(P, steps, warmup):
         xs.append(P.DeviceBuffer.from_numpy(rng.standard_normal(n).astype(np.float32)))
         outs.append(P.DeviceBuffer(d * 4))
     P.synchronize()
+    return _time_gemv(P, steps, warmup, mats, host, dev, xs, outs)
+
+
+def _time_gemv(P, steps, warmup, mats, host, dev, xs, outs):
+    from picolm_amd import gemv as G
 
     def launch():
         for W, x, o in zip(dev, xs, outs):
@@ -177,7 +194,7 @@ def run_gemv(P, steps, warmup):
         "algorithmic_bytes_per_step": algo,
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": None},
-        "_inputs": (mats, host, xs, outs),
+        "_inputs": (mats, host, dev, xs, outs),
     }
 
 
@@ -185,11 +202,14 @@ def cpu_baseline_gemv(res, budget_s=8.0):
     """The oracle's matmul (bit-identical to the reference's x86-64 AVX2
     vec_dot) on the host's cores, rows split over threads like the
     reference's matmul pool, over a bounded sample of the token's GEMVs;
-    with a bit-exact check of the GPU outputs of the sampled GEMVs."""
+    with the GPU outputs of the sampled GEMVs checked against it (normwise
+    for the fast order, bit for bit for the exact one).  Returns the line's
+    fields and the sampled references."""
     from oracle import oracle as O
-    mats, host, xs, outs = res.pop("_inputs")
+    mats, host, dev, xs, outs = res["_inputs"]
     n_thr = min(os.cpu_count() or 1, HOST_THREADS_MAX)
-    t_total, done_bytes, checked, exact = 0.0, 0, 0, True
+    t_total, done_bytes, checked, exact, worst = 0.0, 0, 0, True, 0.0
+    refs = []
     for i, (qt, n, d) in enumerate(mats):
         if t_total >= budget_s:
             break
@@ -201,13 +221,27 @@ def cpu_baseline_gemv(res, budget_s=8.0):
         done_bytes += d * (n // 256) * (144 if qt == Q4K else 210) + n * 4 + d * 4
         got = outs[i].download(np.float32, (d,))
         exact = exact and bool(np.array_equal(got.view(np.uint32), ref.view(np.uint32)))
+        worst = max(worst, float(np.max(np.abs(got - ref)) / max(np.max(np.abs(ref)), 1e-30)))
+        refs.append((i, ref))
         checked += 1
     return {"cpu_baseline": {"value": done_bytes / t_total / 1e9, "unit": "GB/s",
                              "cores": n_thr, "kind": "port",
                              "us_per_token": t_total / done_bytes * gemv_bytes(mats) * 1e6,
                              "sample": f"the first {checked} of {len(mats)} GEMVs of the token, "
                                        f"oracle rows split over {n_thr} threads"},
-            "parity_bit_exact_sampled": exact, "parity_gemvs_checked": checked}
+            "parity_normwise_max_sampled": worst, "parity_bit_exact_sampled": exact,
+            "parity_gemvs_checked": checked}, refs
+
+
+def gemv_exact_order(P, gres, refs):
+    """The same token's GEMVs in the exact order: timing and a bit-for-bit
+    check of the sampled outputs against the oracle's."""
+    mats, host, dev, xs, outs = gres["_inputs"]
+    ex = run_gemv(P, 10, 2, exact=True, inputs=(mats, host, dev, xs, outs))
+    ok = all(np.array_equal(outs[i].download(np.float32, (mats[i][2],)).view(np.uint32),
+                            ref.view(np.uint32)) for i, ref in refs)
+    return {"us_per_token": ex["us_per_token"], "gbs": ex["gbs"],
+            "roofline_frac": ex["roofline"]["frac"], "parity_bit_exact_sampled": ok}
 
 
 # The whole forward pass (model_forward on the device, plh_forward): a
@@ -286,6 +320,19 @@ def run_forward(P, n_prompt=128, n_decode=64, n_check=8):
     e1.record()
     P.synchronize()
     dev_last_ms = e0.elapsed_ms(e1) / n_decode
+    # the same decode at position 2047 with the GEMVs in the exact order
+    P.check(P.lib.plh_set_tuning(10, 1), "plh_set_tuning")
+    try:
+        dm.forward(int(toks[0]), last)
+        P.synchronize()
+        e0.record()
+        for i in range(n_decode):
+            dm.forward(int(toks[4 + i]), last)
+        e1.record()
+        P.synchronize()
+        dev_last_exact_ms = e0.elapsed_ms(e1) / n_decode
+    finally:
+        P.check(P.lib.plh_set_tuning(10, 0), "plh_set_tuning")
     wb = h.weight_bytes_per_token()
     gbs = wb / (dev_ms * 1e-3) / 1e9
     res = {
@@ -297,6 +344,8 @@ def run_forward(P, n_prompt=128, n_decode=64, n_check=8):
         "decode_device_us_per_token": dev_ms * 1e3,
         "decode_positions": [n_prompt + 4, n_prompt + 3 + n_decode],
         "decode_device_us_per_token_pos2047": dev_last_ms * 1e3,
+        "decode_device_us_per_token_pos2047_exact_gemv": dev_last_exact_ms * 1e3,
+        "gemv_order": "fast (int8 digits of x, integer dot products); prompt GEMVs exact",
         "generate_tok_s": 1.0 / gen,
         "generate_us_per_token": gen * 1e6,
         "prefill_tok_s": n_prompt / prefill_s,
@@ -987,7 +1036,7 @@ def main():
     if args.workload == GEMV_WORKLOAD:   # the weight GEMVs of one token as the headline
         steps = max(1, args.steps // 50)
         gres = run_gemv(P, steps, min(args.warmup, 3))
-        gextra = cpu_baseline_gemv(gres) if cpu else {}
+        gextra = cpu_baseline_gemv(gres)[0] if cpu else {}
         gres.pop("_inputs", None)
         line = {"metric": METRIC, "value": gres.pop("gbs"), "unit": "GB/s", "n_gpus": 1,
                 "steps": steps, "warmup": min(args.warmup, 3),
@@ -1079,9 +1128,11 @@ def main():
         line["forward_hook"] = forward_hook_latency()
         # the gpu_try_matmul path: every weight GEMV of one TinyLlama token
         gres = run_gemv(P, 10, 2)
-        gextra = cpu_baseline_gemv(gres) if cpu else {}
+        gextra, refs = cpu_baseline_gemv(gres) if cpu else ({}, [])
+        gres["exact_order"] = gemv_exact_order(P, gres, refs)
         gres.pop("_inputs", None)
         gres["workload"] = GEMV_WORKLOAD
+        gres["order"] = "fast (int8 digits of x, integer dot products)"
         gres.update(gextra)
         line["gemv"] = gres
         # the whole forward pass on the device (gpu_try_forward's path)

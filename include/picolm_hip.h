@@ -207,10 +207,14 @@ int plh_attn_prefill_qknorm(int n_layers, int n_heads, int n_kv_heads, int head_
 /* ---- weight GEMV (gpu_try_matmul's path) --------------------------------- */
 /* Replaces the reference's matmul row loop (tensor.c:200-215) for GGUF types
  * Q4_K (12), Q6_K (14) and Q8_0 (8) -- the types its Vulkan backend offloads
- * (gpu.c:595-602): out[i] = vec_dot(row i of W, x), bit-identical to the
- * reference's fused dequantize + dot products in its x86-64 (AVX2 + FMA)
- * build (quant.c:390-452, 517-582, 627-659).  W is a d x n matrix, n a
- * multiple of the block (256, 256, 32).
+ * (gpu.c:595-602): out[i] = vec_dot(row i of W, x).  Two summation orders
+ * (plh_set_tuning key 10): the exact one is bit-identical to the reference's
+ * fused dequantize + dot products in its x86-64 (AVX2 + FMA) build
+ * (quant.c:390-452, 517-582, 627-659); the default fast one stages x as
+ * fixed-point int8 digits (30 bits per 32-element block) and uses exact
+ * integer dot products, within ~1e-7 of sum |w x| per output for ordinary
+ * activations.  W is a d x n matrix, n a multiple of the block (256, 256,
+ * 32).
  *
  * plh_gemv_packed_bytes: size of the device copy (0: type or shape has no
  * kernel).  plh_gemv_upload: packs the reference's row-major blocks (HOST
@@ -232,14 +236,16 @@ int plh_gemv(int qtype, int n, int d, const void *dev, const float *x, float *ou
  *     v = v + 0.0f           if bias_zero       (matmul_bias with a zeroed bias)
  *     v = silu(gate[i]) * v  if gate            (hb = silu(hb) * hb2)
  *     out[i] = resid[i] + v  if resid, else v   (x += ...)
- * gate and resid may alias out (read before the row is written).  All but
- * silu's expf are bit-identical to the reference. */
+ * gate and resid may alias out (read before the row is written).  In the
+ * exact order all but silu's expf are bit-identical to the reference; the
+ * fast order also sums the rmsnorm squares as a tree. */
 int plh_gemv_ex(int qtype, int n, int d, const void *dev, const float *x, float *out,
                 const float *norm_w, float norm_eps, const float *bias, int bias_zero,
                 const float *gate, const float *resid);
 
 /* tensor.c:322-366 matmul_batch on the device: out[b*d + i] = vec_dot(row i
- * of W, x + b*n) for b < n_batch, each bit-identical to plh_gemv's. */
+ * of W, x + b*n) for b < n_batch, each bit-identical to plh_gemv's exact
+ * order (n_batch 1 runs plh_gemv itself, in the selected order). */
 int plh_matmul_batch(int qtype, int n, int d, const void *dev, const float *x, int n_batch,
                      float *out);
 
@@ -247,8 +253,8 @@ int plh_matmul_batch(int qtype, int n, int d, const void *dev, const float *x, i
  * projections, silu, elemwise_mul): out[i] = silu(vec_dot(gate row i, xn)) *
  * vec_dot(up row i, xn), xn = rmsnorm(x, norm_w, norm_eps) when norm_w is
  * set (else x).  gate_dev / up_dev: packed copies of two d x n matrices of
- * the same type.  The dot products and the norm are bit-identical to the
- * reference; silu uses the device expf. */
+ * the same type.  In the exact order the dot products and the norm are
+ * bit-identical to the reference; silu uses the device expf. */
 int plh_gemv_swiglu(int qtype, int n, int d, const void *gate_dev, const void *up_dev,
                     const float *x, float *out, const float *norm_w, float norm_eps);
 
@@ -335,7 +341,14 @@ int plh_forward_prefill(const plh_model *m, const int *tokens, int n_tokens, int
  * automatic, -1 never, 2, 4, 8 or 16 tiles per chunk); key 6: prefill
  * launches of at most one q block per CU run each block in a workgroup of 2
  * or 3 groups of 4 waves that share its tiles and merge in LDS (0
- * automatic, -1 never, 2 or 3 groups; head_dim 128 takes at most 2). */
+ * automatic, -1 never, 2 or 3 groups; head_dim 128 takes at most 2); key
+ * 7: decode kernel (0 by shape, 1 split + combine, 2 stream-K with the merge
+ * in the launch); key 8: stream-K workgroups (0 = by shape); key 9:
+ * stream-K tiles in flight per wave (0 = default, 2, 3, 4); key 10: the
+ * single-vector weight GEMVs (plh_gemv*, gpu_try_matmul, plh_forward) keep
+ * the reference's x86 AVX2 summation order bit for bit (1) or use the
+ * faster fixed-point-digit order (0, default: within ~1e-7 of sum |w x| per
+ * output; the batched prompt GEMVs always keep the exact order). */
 int plh_set_tuning(int key, int value);
 
 #ifdef __cplusplus

@@ -983,6 +983,14 @@ extern "C" int plh_set_tuning(int key, int value) {
     g_sk_workgroups = value;
     return 0;
   }
+  if (key == 10) {
+    if (value != 0 && value != 1) {
+      set_error("plh_set_tuning: GEMV order must be 0 (fast) or 1 (exact)");
+      return -1;
+    }
+    g_gemv_exact = value;
+    return 0;
+  }
   if (key == 9) {
     if (value != 0 && value != 2 && value != 3 && value != 4) {
       set_error("plh_set_tuning: stream-K prefetch depth must be 0, 2, 3 or 4");

@@ -30,6 +30,7 @@ using namespace plh;
 
 namespace plh {
 int g_gemv_rows_per_thread = 0;
+int g_gemv_exact = 0;
 }
 
 namespace {
@@ -714,6 +715,323 @@ __global__ __launch_bounds__(kThreads) void gemv_multi_kernel(MultiArgs m) {
   }
 }
 
+// ---- the fast order: x as fixed-point int8 digits, integer dot products --
+//
+// Within the forward pass's tolerance instead of bit-identical to the x86
+// AVX2 order (plh_set_tuning key 10 selects the exact kernels above).  x, or
+// rmsnorm(x) (its sum of squares reduced as a tree), is staged once per
+// workgroup in LDS: each 32-element block b gets a power-of-two scale 2^-k_b
+// with max|x| * 2^k_b < 2^30, and each element the integer
+// X = rint(x * 2^k_b) as four signed base-256 digits X = D3 * 2^24 +
+// D2 * 2^16 + D1 * 2^8 + D0 (each in [-128, 127]) in four byte planes; the
+// sums of x over each 16 elements are kept in fp32.  A quad of quant values
+// against a digit word is one exact v_dot4_i32_i8 per digit; per block the
+// four integer sums become a float once, (S3 * 2^24 + ... + S0) * 2^-k_b.
+// The roundings are that combine, the scale products, the term sums (in any
+// order) and the quantization of x to 30 bits relative to its block's
+// largest element (at most 2^-31 of it per element): measured on random
+// blocks, ~3e-8 of sum |q x| per block, 6e-7 when one element is 1000x the
+// others and meets a zero weight, 7e-6 at 1e4x.  A block spanning more
+// magnitudes than that loses its small elements' precision; the exact order
+// has no such limit.  About 4.5 lane instructions per Q4_K weight saved.
+constexpr int kDigitBlock = 32;
+constexpr int kDigits = 4;
+
+// Word w of a digit plane (4 elements per word), padded by 4 words per 16 so
+// that lanes reading adjacent 64-element units start in different banks.
+__host__ __device__ inline int dg_index(int w) { return w + 4 * (w >> 4); }
+
+struct DigitStage {  // LDS layout of the staged x, in 4-byte words
+  int plane;         // words per digit plane
+  int scales;        // the block scales 2^-k (float)
+  int sums;          // the 16-element sums (float)
+  int words;         // total
+};
+__host__ __device__ inline DigitStage digit_stage(int n) {
+  DigitStage d;
+  d.plane = (dg_index(n / 4 - 1) + 4) / 4 * 4;
+  d.scales = kDigits * d.plane;
+  d.sums = d.scales + n / kDigitBlock;
+  d.words = d.sums + n / 16;
+  return d;
+}
+
+// The staged x of a workgroup, as the digit formats read it.
+struct DigLds {
+  const uint32_t* base;
+  DigitStage st;
+};
+
+// Stages x (NORM: rmsnorm(x, norm_w), the reference's formula with its sum
+// of squares reduced as a tree) into dst.  Thread t takes the 8-element
+// chunks t, t + kThreads, ...: the four chunks of a 32-element block sit on
+// four adjacent lanes.  Workgroup wg 0 also stores rmsnorm(x) to xn_out.
+template <bool NORM>
+__device__ __forceinline__ void stage_digits(const GemvArgs& a, int wg, uint32_t* dst,
+                                             float* red) {
+  const int tid = threadIdx.x;
+  const int n = a.n;
+  const DigitStage st = digit_stage(n);
+  float scale = 1.0f;
+  if constexpr (NORM) {
+    float ss = 0.0f;
+    for (int i = 4 * tid; i < n; i += 4 * kThreads) {
+      const float4 v = ld4(a.x + i);
+      ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    scale = 1.0f / sqrtf(ss / (float)n + a.norm_eps);
+  }
+  const int nch = n / 8;  // a multiple of 4: whole blocks
+  for (int c0 = 0; c0 < nch; c0 += kThreads) {
+    const int c = c0 + tid;
+    const bool ok = c < nch;  // uniform over the four lanes of a block
+    float v[8];
+    if (ok) {
+      const float4 x0 = ld4(a.x + 8 * c), x1 = ld4(a.x + 8 * c + 4);
+      v[0] = x0.x, v[1] = x0.y, v[2] = x0.z, v[3] = x0.w;
+      v[4] = x1.x, v[5] = x1.y, v[6] = x1.z, v[7] = x1.w;
+      if constexpr (NORM) {
+        const float4 w0 = ld4(a.norm_w + 8 * c), w1 = ld4(a.norm_w + 8 * c + 4);
+        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+        for (int j = 0; j < 8; ++j) v[j] = (v[j] * scale) * w[j];
+        if (a.xn_out && wg == 0) {
+          *(float4*)(a.xn_out + 8 * c) = make_float4(v[0], v[1], v[2], v[3]);
+          *(float4*)(a.xn_out + 8 * c + 4) = make_float4(v[4], v[5], v[6], v[7]);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+    }
+    float m = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
+    m = fmaxf(m, __shfl_xor(m, 1, 64));
+    m = fmaxf(m, __shfl_xor(m, 2, 64));
+    // max|x| = f * 2^e, f in [0.5, 1): 2^k = 2^(30 - e) keeps |X| < 2^30.
+    // A block with an infinite or NaN element gets a NaN scale, so its
+    // outputs are NaN (the reference's fp32 products would give inf or NaN).
+    int k = 0;
+    if (m > 0.0f && m <= 3.4028235e38f) k = 30 - __builtin_amdgcn_frexp_expf(m);
+    uint32_t dw[kDigits][2];
+#pragma unroll
+    for (int q = 0; q < 2; ++q) {
+      uint32_t wd[kDigits] = {};
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        int X = (int)rintf(__builtin_amdgcn_ldexpf(v[4 * q + b], k));
+#pragma unroll
+        for (int p = 0; p < kDigits; ++p) {
+          const int dgt = ((X + 128) & 255) - 128;  // balanced digit in [-128, 127]
+          X = (X - dgt) >> 8;                        // exact: X - dgt is a multiple of 256
+          wd[p] |= (uint32_t)(dgt & 255) << (8 * b);
+        }
+      }
+#pragma unroll
+      for (int p = 0; p < kDigits; ++p) dw[p][q] = wd[p];
+    }
+    float s16 = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+    s16 += __shfl_xor(s16, 1, 64);
+    if (ok) {
+#pragma unroll
+      for (int p = 0; p < kDigits; ++p)
+        *(uint2*)(dst + p * st.plane + dg_index(2 * c)) = make_uint2(dw[p][0], dw[p][1]);
+      if ((c & 1) == 0) reinterpret_cast<float*>(dst)[st.sums + c / 2] = s16;
+      if ((c & 3) == 0) {
+        const bool fin = m <= 3.4028235e38f;
+        reinterpret_cast<float*>(dst)[st.scales + c / 4] =
+            fin ? __builtin_amdgcn_ldexpf(1.0f, -k) : __builtin_nanf("");
+      }
+    }
+  }
+}
+
+// x of one unit: NW digit words per plane (4 elements each), the scales of
+// its 32-element blocks and the sums of its 16-element groups.
+template <int NW>
+struct XDig {
+  uint32_t d[kDigits][NW];
+  float sc[NW / 8];
+  float sx[NW / 4];
+};
+template <int NW>
+__device__ __forceinline__ void load_xdig(const DigLds& src, int u, XDig<NW>& U) {
+  const int w0 = NW * u;  // first word of the unit
+#pragma unroll
+  for (int p = 0; p < kDigits; ++p)
+#pragma unroll
+    for (int i = 0; i < NW; i += 4) {
+      const uint4 v = *(const uint4*)(src.base + p * src.st.plane + dg_index(w0 + i));
+      U.d[p][i] = v.x, U.d[p][i + 1] = v.y, U.d[p][i + 2] = v.z, U.d[p][i + 3] = v.w;
+    }
+  const float* f = reinterpret_cast<const float*>(src.base);
+#pragma unroll
+  for (int b = 0; b < NW / 8; ++b) U.sc[b] = f[src.st.scales + NW / 8 * u + b];
+#pragma unroll
+  for (int g = 0; g < NW / 4; ++g) U.sx[g] = f[src.st.sums + NW / 4 * u + g];
+}
+
+// (S3 * 2^24 + S2 * 2^16 + S1 * 2^8 + S0) of the digit sums
+__device__ __forceinline__ float digit_value(const int (&s)[kDigits]) {
+  return __builtin_fmaf(
+      (float)s[3], 16777216.0f,
+      __builtin_fmaf((float)s[2], 65536.0f, __builtin_fmaf((float)s[1], 256.0f, (float)s[0])));
+}
+
+// Q4_K: the unit is one 64-element sub-block pair (low nibbles: sub-block
+// 2j, elements 0-31; high nibbles: 2j + 1, elements 32-63)
+struct Q4KD : Q4K {
+  using X = XDig<16>;
+  template <class XS>
+  static __device__ __forceinline__ void load_x(const XS& x, int u, X& U) {
+    load_xdig<16>(x, u, U);
+  }
+  static __device__ __forceinline__ void terms(int u, const Raw& r, const X& U, float* t) {
+    const int j = u & 3;
+    const uint32_t w[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    int s1[kDigits] = {}, s2[kDigits] = {};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t lo = w[i] & 0x0F0F0F0Fu, hi = (w[i] >> 4) & 0x0F0F0F0Fu;
+#pragma unroll
+      for (int p = 0; p < kDigits; ++p) {
+        s1[p] = __builtin_amdgcn_sdot4((int)lo, (int)U.d[p][i], s1[p], false);
+        s2[p] = __builtin_amdgcn_sdot4((int)hi, (int)U.d[p][8 + i], s2[p], false);
+      }
+    }
+    const float qx1 = digit_value(s1) * U.sc[0], qx2 = digit_value(s2) * U.sc[1];
+    const float sx1 = U.sx[0] + U.sx[1], sx2 = U.sx[2] + U.sx[3];
+    const float dd = f16_bits_to_f32((uint16_t)(r.hdr.x & 0xFFFFu));
+    const float dmin = f16_bits_to_f32((uint16_t)(r.hdr.x >> 16));
+    int sc, mn;
+    scale_min(2 * j, r.hdr, sc, mn);
+    const float d1 = dd * (float)sc, m1 = dmin * (float)mn;
+    scale_min(2 * j + 1, r.hdr, sc, mn);
+    const float d2 = dd * (float)sc, m2 = dmin * (float)mn;
+    t[0] = (d1 * qx1 - m1 * sx1) + (d2 * qx2 - m2 * sx2);
+  }
+};
+
+// Q6_K: the unit is four 16-element groups; value v - 32 times d * scale
+struct Q6KD : Q6K<4> {
+  using X = XDig<16>;
+  template <class XS>
+  static __device__ __forceinline__ void load_x(const XS& x, int u, X& U) {
+    load_xdig<16>(x, u, U);
+  }
+  static __device__ __forceinline__ void terms(int, const Raw& r, const X& U, float* t) {
+    const float dd = f16_bits_to_f32((uint16_t)(r.d & 0xFFFFu));
+    const uint32_t m4 = 0x0F0F0F0Fu, m30 = 0x30303030u;
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const uint32_t L0 = r.q[0][g], L1 = r.q[1][g], H = r.q[2][g];
+      const uint32_t v[4] = {(L0 & m4) | ((H << 4) & m30), ((L0 >> 4) & m4) | ((H << 2) & m30),
+                             (L1 & m4) | (H & m30), ((L1 >> 4) & m4) | ((H >> 2) & m30)};
+      int s[kDigits] = {};
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int p = 0; p < kDigits; ++p)
+          s[p] = __builtin_amdgcn_sdot4((int)v[i], (int)U.d[p][4 * g + i], s[p], false);
+      const float vx = digit_value(s) * U.sc[g / 2];
+      t[g] = (dd * sbyte(r.sc, g)) * (vx - 32.0f * U.sx[g]);
+    }
+  }
+};
+
+// Q8_0: the unit is one 32-element block of signed quants
+struct Q80D : Q80 {
+  using X = XDig<8>;
+  template <class XS>
+  static __device__ __forceinline__ void load_x(const XS& x, int u, X& U) {
+    load_xdig<8>(x, u, U);
+  }
+  static __device__ __forceinline__ void terms(int, const Raw& r, const X& U, float* t) {
+    const uint32_t qw[8] = {r.q0.x, r.q0.y, r.q0.z, r.q0.w, r.q1.x, r.q1.y, r.q1.z, r.q1.w};
+    int s[kDigits] = {};
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+      for (int p = 0; p < kDigits; ++p)
+        s[p] = __builtin_amdgcn_sdot4((int)qw[i], (int)U.d[p][i], s[p], false);
+    t[0] = f16_bits_to_f32((uint16_t)(r.d & 0xFFFFu)) * (digit_value(s) * U.sc[0]);
+  }
+};
+
+// One workgroup of the fast order: rows [r0, r0 + rows_per_wg).  The first
+// pass's weight loads are issued, x is staged as digits (after rmsnorm for
+// NORM), then each thread computes its units' terms; phase 2 adds a row's
+// terms in four independent partial sums.
+template <class F, int RB, bool NORM, bool PAIR>
+__device__ __forceinline__ void gemv_body_fast(const GemvArgs& a, int wg, float* terms) {
+  __shared__ float red[kThreads / 64];
+  const int tid = threadIdx.x;
+  const int r0 = wg * a.rows_per_wg;
+  const int rows = min(a.rows_per_wg, (PAIR ? 2 * a.d : a.d) - r0);
+  const int rlane = tid / a.uspan;
+  const bool active = rlane < a.row_par;
+  const int u = tid % a.uspan;
+  const bool first = active && u < a.units;
+  typename F::Raw raw[RB];
+  if (first) load_rows<F, RB, PAIR>(a, r0, rows, rlane, u, raw);
+  uint32_t* xd = reinterpret_cast<uint32_t*>(terms + a.xs_off);
+  stage_digits<NORM>(a, wg, xd, red);
+  __syncthreads();
+  const DigLds src{xd, digit_stage(a.n)};
+  if (first) {
+    unit_terms<F, RB>(a, src, terms, rows, rlane, u, raw);
+    unit_passes<F, RB, PAIR>(a, src, terms, r0, rows, rlane, 1);
+  }
+  __syncthreads();
+  for (int rr = tid; rr < rows; rr += kThreads) {
+    const float* t = terms + rr * a.tpitch;  // 16-byte aligned rows
+    float p4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+    const int full = a.terms / 4 * 4;
+    for (int s0 = 0; s0 < full; s0 += 4) {
+      const float4 v = *(const float4*)(t + s0);
+      p4[0] += v.x, p4[1] += v.y, p4[2] += v.z, p4[3] += v.w;
+    }
+    for (int s0 = full; s0 < a.terms; ++s0) p4[s0 - full] += t[s0];
+    float sumf = (p4[0] + p4[1]) + (p4[2] + p4[3]);
+    const int r = r0 + rr;
+    if constexpr (PAIR) {
+      const float g = __shfl_xor(sumf, 1);
+      if (r & 1) a.out[r >> 1] = silu(g) * sumf;
+    } else {
+      if (a.bias_mode == 1) sumf = sumf + a.bias[r];
+      if (a.bias_mode == 2) sumf = sumf + 0.0f;
+      if (a.gate) sumf = silu(a.gate[r]) * sumf;
+      if (a.resid) sumf = a.resid[r] + sumf;
+      a.out[r] = sumf;
+    }
+  }
+}
+
+template <class F, int RB, bool NORM, bool PAIR>
+__global__ __launch_bounds__(kThreads) void gemv_fast_kernel(GemvArgs a) {
+  extern __shared__ __align__(16) float terms[];
+  gemv_body_fast<F, RB, NORM, PAIR>(a, blockIdx.x, terms);
+}
+
+template <int RB, bool NORM>
+__global__ __launch_bounds__(kThreads) void gemv_fast_multi_kernel(MultiArgs m) {
+  extern __shared__ __align__(16) float terms[];
+  int s = 0;
+  while (s + 1 < m.nseg && (int)blockIdx.x >= m.wg0[s + 1]) ++s;
+  const int wg = blockIdx.x - m.wg0[s];
+  switch (m.qtype[s]) {
+    case kTypeQ4K: gemv_body_fast<Q4KD, RB, NORM, false>(m.seg[s], wg, terms); break;
+    case kTypeQ8_0: gemv_body_fast<Q80D, RB, NORM, false>(m.seg[s], wg, terms); break;
+    default: gemv_body_fast<Q6KD, RB, NORM, false>(m.seg[s], wg, terms); break;
+  }
+}
+
 template <class F, bool NORM, bool PAIR>
 void launch_rb(int rb, int grid, size_t lds, hipStream_t st, const GemvArgs& a) {
   switch (rb) {
@@ -743,6 +1061,59 @@ void launch_fmt(bool norm, bool pair, int rb, int grid, size_t lds, hipStream_t 
     launch_rb<F, true, false>(rb, grid, lds, st, a);
   else
     launch_rb<F, false, false>(rb, grid, lds, st, a);
+}
+
+template <class F, bool NORM, bool PAIR>
+void launch_rb_fast(int rb, int grid, size_t lds, hipStream_t st, const GemvArgs& a) {
+  switch (rb) {
+    case 1:
+      hipLaunchKernelGGL((gemv_fast_kernel<F, 1, NORM, PAIR>), dim3(grid), dim3(kThreads), lds, st,
+                         a);
+      break;
+    case 2:
+      hipLaunchKernelGGL((gemv_fast_kernel<F, 2, NORM, PAIR>), dim3(grid), dim3(kThreads), lds, st,
+                         a);
+      break;
+    case 4:
+      hipLaunchKernelGGL((gemv_fast_kernel<F, 4, NORM, PAIR>), dim3(grid), dim3(kThreads), lds, st,
+                         a);
+      break;
+    default:
+      hipLaunchKernelGGL((gemv_fast_kernel<F, 8, NORM, PAIR>), dim3(grid), dim3(kThreads), lds, st,
+                         a);
+      break;
+  }
+}
+
+template <class F>
+void launch_fmt_fast(bool norm, bool pair, int rb, int grid, size_t lds, hipStream_t st,
+                     const GemvArgs& a) {
+  if (pair && norm)
+    launch_rb_fast<F, true, true>(rb, grid, lds, st, a);
+  else if (pair)
+    launch_rb_fast<F, false, true>(rb, grid, lds, st, a);
+  else if (norm)
+    launch_rb_fast<F, true, false>(rb, grid, lds, st, a);
+  else
+    launch_rb_fast<F, false, false>(rb, grid, lds, st, a);
+}
+
+template <bool NORM>
+void launch_multi_fast(int rb, int grid, size_t lds, hipStream_t st, const MultiArgs& m) {
+  switch (rb) {
+    case 1:
+      hipLaunchKernelGGL((gemv_fast_multi_kernel<1, NORM>), dim3(grid), dim3(kThreads), lds, st,
+                         m);
+      break;
+    case 2:
+      hipLaunchKernelGGL((gemv_fast_multi_kernel<2, NORM>), dim3(grid), dim3(kThreads), lds, st,
+                         m);
+      break;
+    default:
+      hipLaunchKernelGGL((gemv_fast_multi_kernel<4, NORM>), dim3(grid), dim3(kThreads), lds, st,
+                         m);
+      break;
+  }
 }
 
 template <bool NORM>
@@ -866,15 +1237,33 @@ size_t lds_bytes(GemvArgs& a) {
   return lds;
 }
 
+// LDS of a fast-order launch: the terms, then x's digits.
+size_t lds_bytes_fast(GemvArgs& a) {
+  size_t lds = sizeof(float) * (size_t)a.rows_per_wg * a.tpitch;
+  lds = (lds + 15) / 16 * 16;
+  a.xs_off = (int)(lds / sizeof(float));
+  return lds + sizeof(uint32_t) * (size_t)digit_stage(a.n).words;
+}
+
 int launch_single(int qtype, bool pair, const GemvArgs& a0, int rows) {
   GemvArgs a = a0;
   const int rb = pick_rb(&a, &rows, 1, pair, 8);
   if (rb < 0) return -1;
   a.rows_per_wg = a.row_par * rb;
   const int grid = (rows + a.rows_per_wg - 1) / a.rows_per_wg;
-  const size_t lds = lds_bytes(a);
   hipStream_t st = ctx().stream;
   const bool norm = a.norm_w != nullptr;
+  if (!g_gemv_exact) {
+    const size_t lds = lds_bytes_fast(a);
+    if (qtype == kTypeQ4K)
+      launch_fmt_fast<Q4KD>(norm, pair, rb, grid, lds, st, a);
+    else if (qtype == kTypeQ8_0)
+      launch_fmt_fast<Q80D>(norm, pair, rb, grid, lds, st, a);
+    else
+      launch_fmt_fast<Q6KD>(norm, pair, rb, grid, lds, st, a);
+    return check_hip(hipGetLastError(), "gemv_fast_kernel launch");
+  }
+  const size_t lds = lds_bytes(a);
   if (qtype == kTypeQ4K)
     launch_fmt<Q4K>(norm, pair, rb, grid, lds, st, a);
   else if (qtype == kTypeQ8_0)
@@ -1067,8 +1456,15 @@ int gemv_multi_launch(const GemvCall* g, int n) {
   for (int s = 0; s < n; ++s) {
     m.seg[s].rows_per_wg = m.seg[s].row_par * rb;
     m.wg0[s + 1] = m.wg0[s] + (rows[s] + m.seg[s].rows_per_wg - 1) / m.seg[s].rows_per_wg;
-    const size_t b = lds_bytes(m.seg[s]);
+    const size_t b = g_gemv_exact ? lds_bytes(m.seg[s]) : lds_bytes_fast(m.seg[s]);
     if (b > lds) lds = b;
+  }
+  if (!g_gemv_exact) {
+    if (g[0].norm_w)
+      launch_multi_fast<true>(rb, m.wg0[n], lds, ctx().stream, m);
+    else
+      launch_multi_fast<false>(rb, m.wg0[n], lds, ctx().stream, m);
+    return check_hip(hipGetLastError(), "gemv_fast_multi_kernel launch");
   }
   if (g[0].norm_w)
     launch_multi<true>(rb, m.wg0[n], lds, ctx().stream, m);

@@ -40,6 +40,10 @@ int check_hip(hipError_t e, const char* what);
 // GEMV rows per thread forced by plh_set_tuning key 3 (0: the launch's own
 // choice).
 extern int g_gemv_rows_per_thread;
+// plh_set_tuning key 10: 1 = the single-vector GEMVs keep the reference's x86
+// AVX2 summation order bit for bit; 0 (default) = the fast order (x as int8
+// digits, integer dot products), within the forward tolerance.
+extern int g_gemv_exact;
 // plh_set_tuning key 5: prefill chunking of small launches (0 automatic, -1
 // never, 2/4/8/16 a fixed chunk size in tiles).
 extern int g_prefill_split;

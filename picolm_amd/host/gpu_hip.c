@@ -137,6 +137,14 @@ int gpu_init(const model_t *m) {
         fprintf(stderr, "gpu_hip: %s\n", plh_last_error());
         return -1;
     }
+    /* PICOLM_HIP_GEMV_EXACT=1: the weight GEMVs keep the reference's x86 AVX2
+     * summation order bit for bit (gpu_try_matmul then equals the CPU matmul
+     * exactly); by default they use the faster order, within the forward
+     * pass's tolerance. */
+    if (plh_set_tuning(10, env_int("PICOLM_HIP_GEMV_EXACT", 0) ? 1 : 0) != 0) {
+        fprintf(stderr, "gpu_hip: %s\n", plh_last_error());
+        return -1;
+    }
     gs.inited = 1;
     gs.n_layers = c->n_layers;
     gs.n_heads = c->n_heads;

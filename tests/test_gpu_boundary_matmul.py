@@ -47,6 +47,7 @@ def run(tmp_path, O, dims, types, type_out, seed, env_extra=None):
             x.tofile(f)
             data.append((W, x))
     env = dict(os.environ)
+    env["PICOLM_HIP_GEMV_EXACT"] = "1"   # bit-exact order unless a test asks otherwise
     env.update(env_extra or {})
     print(f"[case] matmul dims {dims} types {types} out {type_out} env {env_extra}", flush=True)
     r = subprocess.run([EXE, str(fin), str(fout)], env=env, capture_output=True, text=True,
@@ -91,6 +92,22 @@ def test_matmul_offload_bit_exact(tmp_path, oracle_mod, dims):
         assert rc == 0, (qt, n, d)
         want = O.matmul(W, x, n, d, qt)
         assert np.array_equal(out.view(np.uint32), want.view(np.uint32)), (qt, n, d)
+    assert list(neg) == [-1, -1, -1]
+
+
+def test_matmul_offload_fast_order(tmp_path, oracle_mod):
+    """The default GEMV order through gpu_try_matmul: every output within 64
+    fp32 ulps of sum |w x| of the float64 dequantize-then-dot."""
+    from test_gpu_gemv import assert_fast_close, decode64
+    rcs, mats, data, res, neg = run(tmp_path, oracle_mod, DIMS, TYPES, Q6K, seed=4,
+                                    env_extra={"PICOLM_HIP_GEMV_EXACT": "0"})
+    assert rcs == (0, 0)
+    for (qt, n, d), (W, x), (rc, out) in zip(mats, data, res):
+        if qt in (F32, F16):
+            assert rc == -1 and not out.any()
+            continue
+        assert rc == 0, (qt, n, d)
+        assert_fast_close(out, decode64(qt, W, n, d), x, (qt, n, d))
     assert list(neg) == [-1, -1, -1]
 
 

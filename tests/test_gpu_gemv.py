@@ -1,7 +1,11 @@
 """Weight GEMV on the GPU (plh_gemv, the gpu_try_matmul path) against the
-oracle, bit for bit: every output of every row equals the reference's
-vec_dot in its x86-64 AVX2 build (the oracle is pinned to it in
-tests/test_oracle_gemv.py).
+oracle.  The exact order (plh_set_tuning key 10 = 1), bit for bit: every
+output of every row equals the reference's vec_dot in its x86-64 AVX2 build
+(the oracle is pinned to it in tests/test_oracle_gemv.py).  The default fast
+order (x as fixed-point int8 digits, integer dot products): every output
+within 64 fp32 ulps of sum |w x| of the float64 dequantize-then-dot, the
+bound the oracle's own AVX2 order meets (tests/test_oracle_gemv.py), for
+plain, tiny, large and outlier-heavy x.
 
 Shapes: the TinyLlama projections (q/o 2048x2048, k/v 256x2048, gate/up
 5632x2048, down 2048x5632), a Llama-2 MLP row length (11008) whose term
@@ -16,6 +20,30 @@ from picolm_amd import synth as S
 
 pytestmark = pytest.mark.gpu
 
+
+@pytest.fixture
+def exact_order(gpu):
+    """The bit-exact GEMV order for one test."""
+    gpu.check(gpu.lib.plh_set_tuning(10, 1), "plh_set_tuning")
+    yield
+    gpu.check(gpu.lib.plh_set_tuning(10, 0), "plh_set_tuning")
+
+
+def decode64(qtype, W, n, d):
+    from test_oracle_gemv import _decode64
+    name = {G.TYPE_Q4_K: "q4_K", G.TYPE_Q6_K: "q6_K", G.TYPE_Q8_0: "q8_0"}[qtype]
+    return _decode64(name, W, n, d)
+
+
+def assert_fast_close(got, W64, x, what):
+    """|got - float64 dot| <= 64 ulps of sum |w x| (the AVX2 order's bound)."""
+    x64 = x.astype(np.float64)
+    exact = W64 @ x64
+    bound = 64 * np.finfo(np.float32).eps * (np.abs(W64) @ np.abs(x64)) + 1e-30
+    err = np.abs(got.astype(np.float64) - exact)
+    assert np.all(err <= bound), (what, float(np.max(err / bound)))
+    return float(np.max(err / bound))
+
 SHAPES = [  # (qtype, n, d)
     (G.TYPE_Q4_K, 2048, 2048), (G.TYPE_Q4_K, 2048, 256), (G.TYPE_Q4_K, 2048, 5632),
     (G.TYPE_Q4_K, 5632, 2048), (G.TYPE_Q4_K, 256, 77), (G.TYPE_Q4_K, 11008, 129),
@@ -27,7 +55,7 @@ SHAPES = [  # (qtype, n, d)
 
 
 @pytest.mark.parametrize("qtype,n,d", SHAPES)
-def test_gemv_bit_exact(gpu, oracle_mod, qtype, n, d):
+def test_gemv_bit_exact(gpu, oracle_mod, exact_order, qtype, n, d):
     O = oracle_mod
     rng = np.random.default_rng(n * 7 + d + qtype)
     print(f"[case] gemv type {qtype} n {n} d {d}", flush=True)
@@ -47,8 +75,47 @@ def test_gemv_bit_exact(gpu, oracle_mod, qtype, n, d):
     Wd.free()
 
 
-def test_gemv_repeat_and_special_blocks(gpu, oracle_mod):
-    """Zero scales, all-zero x and repeated calls (no state between calls)."""
+@pytest.mark.parametrize("qtype,n,d", SHAPES)
+def test_gemv_fast_order(gpu, qtype, n, d):
+    rng = np.random.default_rng(n * 7 + d + qtype)
+    print(f"[case] fast gemv type {qtype} n {n} d {d}", flush=True)
+    W = S.random_weights(rng, qtype, n, d)
+    W64 = decode64(qtype, W, n, d)
+    Wd = G.QMatrix(qtype, n, d, W)
+    worst = 0.0
+    for trial, xs in enumerate((1.0, 1e-3, 40.0, "outliers")):
+        if xs == "outliers":
+            # one element in every 32-element block 300x the rest, and blocks
+            # of zeros and of tiny values
+            x = rng.standard_normal(n).astype(np.float32)
+            x[rng.integers(0, 32) + 32 * np.arange(n // 32)] *= 300.0
+            x[: n // 4] = 0.0
+            x[n // 4: n // 2] *= 1e-30
+        else:
+            x = (rng.standard_normal(n) * xs).astype(np.float32)
+        dx = P.DeviceBuffer.from_numpy(x)
+        dout = P.DeviceBuffer(d * 4)
+        G.matmul(dout.ptr, dx.ptr, Wd)
+        got = dout.download(np.float32, (d,))
+        worst = max(worst, assert_fast_close(got, W64, x, (qtype, n, d, trial)))
+        dx.free()
+        dout.free()
+    print(f"[fast] type {qtype} n {n} d {d}: worst error / bound {worst:.3f}")
+    Wd.free()
+
+
+@pytest.mark.parametrize("order", ["exact", "fast"])
+def test_gemv_repeat_and_special_blocks(gpu, oracle_mod, order):
+    """Zero scales, all-zero x and repeated calls (no state between calls):
+    bit-exact in the exact order, within the bound in the fast one."""
+    gpu.check(gpu.lib.plh_set_tuning(10, 1 if order == "exact" else 0), "plh_set_tuning")
+    try:
+        _repeat_and_special_blocks(gpu, oracle_mod, order == "exact")
+    finally:
+        gpu.check(gpu.lib.plh_set_tuning(10, 0), "plh_set_tuning")
+
+
+def _repeat_and_special_blocks(gpu, oracle_mod, exact):
     O = oracle_mod
     rng = np.random.default_rng(5)
     n, d = 512, 64
@@ -71,7 +138,10 @@ def test_gemv_repeat_and_special_blocks(gpu, oracle_mod):
             for _ in range(2):
                 G.matmul(dout.ptr, dx.ptr, Wd)
                 got = dout.download(np.float32, (d,))
-                assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+                if exact:
+                    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+                else:
+                    assert_fast_close(got, decode64(qtype, W, n, d), x, qtype)
             assert not got[::3].any()
             dx.free()
             dout.free()

@@ -42,6 +42,7 @@ def run_attn(tmp_path, L, Hq, Hkv, D, S_, rt, P, T, R, seed, env_extra=None):
     out = tmp_path / "attn.txt"
     args = [EXE, "attn"] + [str(a) for a in (L, Hq, Hkv, D, S_, rt, P, T, R, seed)] + [str(out)]
     env = dict(os.environ)
+    env["PICOLM_HIP_GEMV_EXACT"] = "1"   # gpu_try_matmul bit-exact against the reference
     env.update(env_extra or {})
     print(f"[case] ref-model attn {args[2:-1]} env {env_extra}", flush=True)
     r = subprocess.run(args, capture_output=True, text=True, timeout=240, env=env)
@@ -123,8 +124,10 @@ def run_forward(tmp_path, h, steps):
         for kind, start, toks in steps:
             np.array([kind, start, len(toks)] + list(toks), np.int32).tofile(f)
     print(f"[case] ref-model forward {h.n_layers}x{h.n_embd} steps {len(steps)}", flush=True)
+    env = dict(os.environ)
+    env["PICOLM_HIP_GEMV_EXACT"] = "1"   # gpu_try_matmul bit-exact against the reference
     r = subprocess.run([EXE, "forward", str(fin), str(fout)], capture_output=True, text=True,
-                       timeout=240)
+                       timeout=240, env=env)
     assert r.returncode == 0, r.stderr
     buf = open(fout, "rb").read()
     off = 0
