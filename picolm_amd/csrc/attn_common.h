@@ -143,6 +143,15 @@ __device__ __forceinline__ f32x16_t mfma32x32x16(half8_t a, half8_t b, f32x16_t 
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Kernel arguments in scalar registers at one point: an empty asm statement
+// that takes them all as scalar operands makes the compiler issue their
+// loads together, behind one wait.  Left alone, it loads an argument just
+// before its first use, and every load that sits behind a branch or a
+// computed index then costs a memory round trip of its own before the
+// kernel's first real load is issued.  (One statement: a chain of them gets
+// one load and one wait each.)
+#define PLH_ARGS_NOW(...) __asm__ volatile("" ::__VA_ARGS__)
+
 // Maximum over lanes l and l^16 (resp. l^32) with the gfx950 row-swap
 // permutes: permlane16_swap(x, x) returns rows {0,0,2,2} and {1,1,3,3} of x
 // (rows of 16 lanes), permlane32_swap(x, x) returns halves {0,0} and {1,1}, so

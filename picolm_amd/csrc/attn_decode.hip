@@ -454,6 +454,12 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
       (kVtileHalves * 2 > kCombFloats * 4) ? kVtileHalves * 2 : kCombFloats * 4;
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
 
+  PLH_ARGS_NOW("s"(a.q), "s"(a.k), "s"(a.v), "s"(a.kc), "s"(a.vc), "s"(a.cos_t), "s"(a.sin_t),
+               "s"(a.out), "s"(a.part_o), "s"(a.part_m), "s"(a.part_l), "s"(a.layer0),
+               "s"(a.n_heads), "s"(a.n_kv_heads), "s"(a.max_seq_len), "s"(a.pos),
+               "s"(a.rope_type), "s"(a.n_hblk), "s"(a.nhm), "s"(a.n_split), "s"(a.split_len),
+               "s"(a.n_units), "s"(a.per_xcd), "s"(a.score_scale), "s"(a.k_rows),
+               "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps));
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -699,6 +705,12 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
   __shared__ float s_knew[D], s_vnew[D], s_mnew[16];
   __shared__ int s_last;
 
+  PLH_ARGS_NOW("s"(a.q), "s"(a.k), "s"(a.v), "s"(a.kc), "s"(a.vc), "s"(a.cos_t), "s"(a.sin_t),
+               "s"(a.out), "s"(a.layer0), "s"(a.n_heads), "s"(a.n_kv_heads),
+               "s"(a.max_seq_len), "s"(a.pos), "s"(a.rope_type), "s"(a.n_hblk), "s"(a.nhm),
+               "s"(a.score_scale), "s"(a.sk_q), "s"(a.sk_r), "s"(a.sk_nbk), "s"(a.sk_maxp),
+               "s"(a.sk_part), "s"(a.sk_part_bytes), "s"(a.sk_ctr), "s"(a.k_rows),
+               "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps));
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);

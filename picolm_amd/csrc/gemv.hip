@@ -964,12 +964,31 @@ struct Q80D : Q80 {
   }
 };
 
+// Unit u's terms of this thread's RB rows, added to its per-row sums.
+template <class F, int RB>
+__device__ __forceinline__ void unit_acc(const DigLds& xs, int u, const typename F::Raw (&raw)[RB],
+                                         float (&acc)[RB]) {
+  typename F::X U;
+  F::load_x(xs, u, U);
+#pragma unroll
+  for (int k = 0; k < RB; ++k) {
+    float t[F::kTerms];
+    F::terms(u, raw[k], U, t);
+    float s = t[0];
+#pragma unroll
+    for (int g = 1; g < F::kTerms; ++g) s += t[g];
+    acc[k] += s;
+  }
+}
+
 // One workgroup of the fast order: rows [r0, r0 + rows_per_wg).  The first
 // pass's weight loads are issued, x is staged as digits (after rmsnorm for
-// NORM), then each thread computes its units' terms; phase 2 adds a row's
-// terms in four independent partial sums.
+// NORM), then each thread adds its units' terms per row in registers (later
+// passes load and add more units); the uspan sums of a row go through LDS
+// and are added by a power-of-two group of lanes (a shuffle tree), which
+// applies the epilogue.
 template <class F, int RB, bool NORM, bool PAIR>
-__device__ __forceinline__ void gemv_body_fast(const GemvArgs& a, int wg, float* terms) {
+__device__ __forceinline__ void gemv_body_fast(const GemvArgs& a, int wg, float* lds) {
   __shared__ float red[kThreads / 64];
   const int tid = threadIdx.x;
   const int r0 = wg * a.rows_per_wg;
@@ -980,35 +999,55 @@ __device__ __forceinline__ void gemv_body_fast(const GemvArgs& a, int wg, float*
   const bool first = active && u < a.units;
   typename F::Raw raw[RB];
   if (first) load_rows<F, RB, PAIR>(a, r0, rows, rlane, u, raw);
-  uint32_t* xd = reinterpret_cast<uint32_t*>(terms + a.xs_off);
+  uint32_t* xd = reinterpret_cast<uint32_t*>(lds + a.xs_off);
   stage_digits<NORM>(a, wg, xd, red);
   __syncthreads();
   const DigLds src{xd, digit_stage(a.n)};
+  float acc[RB];
+#pragma unroll
+  for (int k = 0; k < RB; ++k) acc[k] = 0.0f;
   if (first) {
-    unit_terms<F, RB>(a, src, terms, rows, rlane, u, raw);
-    unit_passes<F, RB, PAIR>(a, src, terms, r0, rows, rlane, 1);
+    unit_acc<F, RB>(src, u, raw, acc);
+    for (int it = 1; it < a.unit_iters; ++it) {
+      const int uu = u + it * a.uspan;
+      if (uu >= a.units) break;
+      load_rows<F, RB, PAIR>(a, r0, rows, rlane, uu, raw);
+      unit_acc<F, RB>(src, uu, raw, acc);
+    }
+  }
+  // row rr's per-thread sums at lds[rr * uspan + u] (the term buffer's space)
+  if (first) {
+#pragma unroll
+    for (int k = 0; k < RB; ++k) {
+      const int rr = rlane + a.row_par * k;
+      if (rr < rows) lds[rr * a.uspan + u] = acc[k];
+    }
   }
   __syncthreads();
-  for (int rr = tid; rr < rows; rr += kThreads) {
-    const float* t = terms + rr * a.tpitch;  // 16-byte aligned rows
-    float p4[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    const int full = a.terms / 4 * 4;
-    for (int s0 = 0; s0 < full; s0 += 4) {
-      const float4 v = *(const float4*)(t + s0);
-      p4[0] += v.x, p4[1] += v.y, p4[2] += v.z, p4[3] += v.w;
-    }
-    for (int s0 = full; s0 < a.terms; ++s0) p4[s0 - full] += t[s0];
-    float sumf = (p4[0] + p4[1]) + (p4[2] + p4[3]);
+  // tpr lanes per row (a power of two, at most 32 so that a gate/up pair's
+  // two rows share a wave)
+  int tpr = 1;
+  while (tpr < 32 && 2 * tpr * a.rows_per_wg <= kThreads) tpr *= 2;
+  const int j = tid & (tpr - 1);
+  const int nsum = min(a.units, a.uspan);
+  for (int rr0 = 0; rr0 < rows; rr0 += kThreads / tpr) {
+    const int rr = rr0 + tid / tpr;  // uniform over the tpr lanes
+    float sumf = 0.0f;
+    if (rr < rows)
+      for (int i = j; i < nsum; i += tpr) sumf += lds[rr * a.uspan + i];
+    for (int m = tpr / 2; m >= 1; m >>= 1) sumf += __shfl_xor(sumf, m, 64);
     const int r = r0 + rr;
     if constexpr (PAIR) {
-      const float g = __shfl_xor(sumf, 1);
-      if (r & 1) a.out[r >> 1] = silu(g) * sumf;
+      const float g = __shfl_xor(sumf, tpr, 64);  // the gate row's sum
+      if (rr < rows && j == 0 && (r & 1)) a.out[r >> 1] = silu(g) * sumf;
     } else {
-      if (a.bias_mode == 1) sumf = sumf + a.bias[r];
-      if (a.bias_mode == 2) sumf = sumf + 0.0f;
-      if (a.gate) sumf = silu(a.gate[r]) * sumf;
-      if (a.resid) sumf = a.resid[r] + sumf;
-      a.out[r] = sumf;
+      if (rr < rows && j == 0) {
+        if (a.bias_mode == 1) sumf = sumf + a.bias[r];
+        if (a.bias_mode == 2) sumf = sumf + 0.0f;
+        if (a.gate) sumf = silu(a.gate[r]) * sumf;
+        if (a.resid) sumf = a.resid[r] + sumf;
+        a.out[r] = sumf;
+      }
     }
   }
 }
@@ -1022,10 +1061,23 @@ __global__ __launch_bounds__(kThreads) void gemv_fast_kernel(GemvArgs a) {
 template <int RB, bool NORM>
 __global__ __launch_bounds__(kThreads) void gemv_fast_multi_kernel(MultiArgs m) {
   extern __shared__ __align__(16) float terms[];
-  int s = 0;
-  while (s + 1 < m.nseg && (int)blockIdx.x >= m.wg0[s + 1]) ++s;
-  const int wg = blockIdx.x - m.wg0[s];
-  switch (m.qtype[s]) {
+  static_assert(kMaxSeg == 3, "the segment choice below covers three segments");
+  // the segment from one batch of argument loads (a search loop would chain
+  // one memory round trip per step)
+  PLH_ARGS_NOW("s"(m.nseg), "s"(m.wg0[1]), "s"(m.wg0[2]), "s"(m.qtype[0]), "s"(m.qtype[1]),
+               "s"(m.qtype[2]));
+  const int b = blockIdx.x;
+  const int s = (m.nseg > 1 && b >= m.wg0[1]) + (m.nseg > 2 && b >= m.wg0[2]);
+  const int wg = b - (s == 2 ? m.wg0[2] : s == 1 ? m.wg0[1] : 0);
+  const int qtype = s == 2 ? m.qtype[2] : s == 1 ? m.qtype[1] : m.qtype[0];
+  // the segment's arguments: a second (and last) batch
+  const GemvArgs& g = m.seg[s];
+  PLH_ARGS_NOW("s"(g.w), "s"(g.x), "s"(g.out), "s"(g.d), "s"(g.nb), "s"(g.units), "s"(g.uspan),
+               "s"(g.row_par), "s"(g.unit_iters), "s"(g.rows_per_wg), "s"(g.off0), "s"(g.off1),
+               "s"(g.off2), "s"(g.scales_off), "s"(g.d_off), "s"(g.n), "s"(g.xs_off),
+               "s"(g.bias), "s"(g.gate), "s"(g.resid), "s"(g.bias_mode), "s"(g.norm_w),
+               "s"(g.norm_eps), "s"(g.xn_out));
+  switch (qtype) {
     case kTypeQ4K: gemv_body_fast<Q4KD, RB, NORM, false>(m.seg[s], wg, terms); break;
     case kTypeQ8_0: gemv_body_fast<Q80D, RB, NORM, false>(m.seg[s], wg, terms); break;
     default: gemv_body_fast<Q6KD, RB, NORM, false>(m.seg[s], wg, terms); break;
