@@ -5,8 +5,9 @@
 Prints one JSON line.  The headline (the contract keys, `roofline`,
 `cpu_baseline`) is TinyLlama-1.1B-shaped decode at position 2047 (22 layers,
 32 q heads, 4 kv heads, head_dim 64, FP16 cache of 2048 rows): a step is one
-token's decode attention over all 22 layers -- one plh_attn_decode call (main
-+ combine kernel) -- with inputs resident in HBM.  The same line carries every
+token's decode attention over all 22 layers -- one plh_attn_decode call (one
+stream-K launch at this shape, the split merge inside it) -- with inputs
+resident in HBM.  The same line carries every
 workload of the attention block's benchmark set, each measured the same way:
 
   cfg1  TinyLlama decode at pos 256            HBM-bound
