@@ -819,22 +819,28 @@ __device__ __forceinline__ void stage_digits(const GemvArgs& a, int wg, uint32_t
     // outputs are NaN (the reference's fp32 products would give inf or NaN).
     int k = 0;
     if (m > 0.0f && m <= 3.4028235e38f) k = 30 - __builtin_amdgcn_frexp_expf(m);
+    // Balanced base-256 digits of X (|X| < 2^30): the bytes of
+    // Z = (X + 0x80808080) ^ 0x80808080 read as signed bytes (byte p of
+    // X + 0x80808080 is D_p + 128).  A 4 x 4 byte transpose of four elements'
+    // Z then gives the digit words (word p: byte p of each element).
     uint32_t dw[kDigits][2];
 #pragma unroll
     for (int q = 0; q < 2; ++q) {
-      uint32_t wd[kDigits] = {};
+      uint32_t z[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        int X = (int)rintf(__builtin_amdgcn_ldexpf(v[4 * q + b], k));
-#pragma unroll
-        for (int p = 0; p < kDigits; ++p) {
-          const int dgt = ((X + 128) & 255) - 128;  // balanced digit in [-128, 127]
-          X = (X - dgt) >> 8;                        // exact: X - dgt is a multiple of 256
-          wd[p] |= (uint32_t)(dgt & 255) << (8 * b);
-        }
+        const int X = (int)rintf(__builtin_amdgcn_ldexpf(v[4 * q + b], k));
+        z[b] = ((uint32_t)X + 0x80808080u) ^ 0x80808080u;
       }
-#pragma unroll
-      for (int p = 0; p < kDigits; ++p) dw[p][q] = wd[p];
+      // perm(hi, lo, sel): byte i of the result is byte sel_i of {hi:lo}
+      const uint32_t t0 = __builtin_amdgcn_perm(z[1], z[0], 0x05010400u);  // z0.0 z1.0 z0.1 z1.1
+      const uint32_t t1 = __builtin_amdgcn_perm(z[1], z[0], 0x07030602u);  // z0.2 z1.2 z0.3 z1.3
+      const uint32_t t2 = __builtin_amdgcn_perm(z[3], z[2], 0x05010400u);
+      const uint32_t t3 = __builtin_amdgcn_perm(z[3], z[2], 0x07030602u);
+      dw[0][q] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+      dw[1][q] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+      dw[2][q] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+      dw[3][q] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
     }
     float s16 = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
     s16 += __shfl_xor(s16, 1, 64);
@@ -1259,11 +1265,23 @@ int pick_rb(const GemvArgs* seg, const int* rows, int nseg, bool pair, int max_r
     return true;
   };
   int rb = 4;
-  while (rb > 1 && (grid_of(rb) * 10 < 6L * cus || !lds_ok(rb))) rb /= 2;
-  // with the rmsnorm prologue every workgroup pays the norm's latency, and
-  // workgroups sharing a CU measured to pay it one after the other: 8 rows
-  // per thread when 4 would need more than one workgroup per CU
-  if (seg[0].norm_w && rb == 4 && max_rb >= 8 && grid_of(4) > cus && lds_ok(8)) rb = 8;
+  if (g_gemv_exact) {
+    while (rb > 1 && (grid_of(rb) * 10 < 6L * cus || !lds_ok(rb))) rb /= 2;
+    // with the rmsnorm prologue every workgroup pays the norm's latency, and
+    // workgroups sharing a CU measured to pay it one after the other: 8 rows
+    // per thread when 4 would need more than one workgroup per CU
+    if (seg[0].norm_w && rb == 4 && max_rb >= 8 && grid_of(4) > cus && lds_ok(8)) rb = 8;
+  } else {
+    // the fast order: the most rows per thread that still leaves ~2
+    // workgroups per CU (swept on the TinyLlama shapes with cold weights:
+    // gate/up pair 2, output projection 8, q and o 1), else 1
+    rb = 1;
+    for (int c = max_rb; c >= 1; c /= 2)
+      if (grid_of(c) * 10 >= 19L * cus && lds_ok(c)) {
+        rb = c;
+        break;
+      }
+  }
   if (g_gemv_rows_per_thread > 0) rb = g_gemv_rows_per_thread;
   if (rb > max_rb) rb = max_rb;
   if (pair && (seg[0].row_par * rb) % 2) rb *= 2;
