@@ -762,22 +762,49 @@ struct DigLds {
   DigitStage st;
 };
 
+// This thread's first 8-element chunk of x (and of the norm weights), loaded
+// before the workgroup's weight loads: loads complete in issue order, so x
+// loaded after them would wait for all of them and the staging below could
+// not overlap the weight stream.
+struct XFirst {
+  float4 x0, x1, w0, w1;
+};
+template <bool NORM>
+__device__ __forceinline__ void load_x_first(const GemvArgs& a, XFirst& f) {
+  const int c = threadIdx.x;
+  f.x0 = f.x1 = f.w0 = f.w1 = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (c < a.n / 8) {
+    f.x0 = ld4(a.x + 8 * c);
+    f.x1 = ld4(a.x + 8 * c + 4);
+    if constexpr (NORM) {
+      f.w0 = ld4(a.norm_w + 8 * c);
+      f.w1 = ld4(a.norm_w + 8 * c + 4);
+    }
+  }
+}
+
 // Stages x (NORM: rmsnorm(x, norm_w), the reference's formula with its sum
 // of squares reduced as a tree) into dst.  Thread t takes the 8-element
 // chunks t, t + kThreads, ...: the four chunks of a 32-element block sit on
 // four adjacent lanes.  Workgroup wg 0 also stores rmsnorm(x) to xn_out.
 template <bool NORM>
-__device__ __forceinline__ void stage_digits(const GemvArgs& a, int wg, uint32_t* dst,
-                                             float* red) {
+__device__ __forceinline__ void stage_digits(const GemvArgs& a, int wg, const XFirst& xf,
+                                             uint32_t* dst, float* red) {
   const int tid = threadIdx.x;
   const int n = a.n;
   const DigitStage st = digit_stage(n);
+  const int nch = n / 8;  // a multiple of 4: whole blocks
   float scale = 1.0f;
   if constexpr (NORM) {
+    // sum of squares over this thread's chunks tid, tid + kThreads, ...
     float ss = 0.0f;
-    for (int i = 4 * tid; i < n; i += 4 * kThreads) {
-      const float4 v = ld4(a.x + i);
-      ss += (v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w);
+    if (tid < nch)
+      ss = ((xf.x0.x * xf.x0.x + xf.x0.y * xf.x0.y) + (xf.x0.z * xf.x0.z + xf.x0.w * xf.x0.w)) +
+           ((xf.x1.x * xf.x1.x + xf.x1.y * xf.x1.y) + (xf.x1.z * xf.x1.z + xf.x1.w * xf.x1.w));
+    for (int c = tid + kThreads; c < nch; c += kThreads) {
+      const float4 v = ld4(a.x + 8 * c), u = ld4(a.x + 8 * c + 4);
+      ss += ((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w)) +
+            ((u.x * u.x + u.y * u.y) + (u.z * u.z + u.w * u.w));
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) ss += __shfl_xor(ss, m, 64);
@@ -786,17 +813,18 @@ __device__ __forceinline__ void stage_digits(const GemvArgs& a, int wg, uint32_t
     ss = (red[0] + red[1]) + (red[2] + red[3]);
     scale = 1.0f / sqrtf(ss / (float)n + a.norm_eps);
   }
-  const int nch = n / 8;  // a multiple of 4: whole blocks
   for (int c0 = 0; c0 < nch; c0 += kThreads) {
     const int c = c0 + tid;
     const bool ok = c < nch;  // uniform over the four lanes of a block
     float v[8];
     if (ok) {
-      const float4 x0 = ld4(a.x + 8 * c), x1 = ld4(a.x + 8 * c + 4);
+      const float4 x0 = c0 == 0 ? xf.x0 : ld4(a.x + 8 * c);
+      const float4 x1 = c0 == 0 ? xf.x1 : ld4(a.x + 8 * c + 4);
       v[0] = x0.x, v[1] = x0.y, v[2] = x0.z, v[3] = x0.w;
       v[4] = x1.x, v[5] = x1.y, v[6] = x1.z, v[7] = x1.w;
       if constexpr (NORM) {
-        const float4 w0 = ld4(a.norm_w + 8 * c), w1 = ld4(a.norm_w + 8 * c + 4);
+        const float4 w0 = c0 == 0 ? xf.w0 : ld4(a.norm_w + 8 * c);
+        const float4 w1 = c0 == 0 ? xf.w1 : ld4(a.norm_w + 8 * c + 4);
         const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
 #pragma unroll
         for (int j = 0; j < 8; ++j) v[j] = (v[j] * scale) * w[j];
@@ -1003,10 +1031,12 @@ __device__ __forceinline__ void gemv_body_fast(const GemvArgs& a, int wg, float*
   const bool active = rlane < a.row_par;
   const int u = tid % a.uspan;
   const bool first = active && u < a.units;
+  XFirst xf;
+  load_x_first<NORM>(a, xf);
   typename F::Raw raw[RB];
   if (first) load_rows<F, RB, PAIR>(a, r0, rows, rlane, u, raw);
   uint32_t* xd = reinterpret_cast<uint32_t*>(lds + a.xs_off);
-  stage_digits<NORM>(a, wg, xd, red);
+  stage_digits<NORM>(a, wg, xf, xd, red);
   __syncthreads();
   const DigLds src{xd, digit_stage(a.n)};
   float acc[RB];
@@ -1272,12 +1302,16 @@ int pick_rb(const GemvArgs* seg, const int* rows, int nseg, bool pair, int max_r
     // per thread when 4 would need more than one workgroup per CU
     if (seg[0].norm_w && rb == 4 && max_rb >= 8 && grid_of(4) > cus && lds_ok(8)) rb = 8;
   } else {
-    // the fast order: the most rows per thread that still leaves ~2
-    // workgroups per CU (swept on the TinyLlama shapes with cold weights:
-    // gate/up pair 2, output projection 8, q and o 1), else 1
+    // the fast order: the most rows per thread that still leaves ~2.5
+    // workgroups per CU, fewer when x is long (every workgroup stages all of
+    // x): swept on the TinyLlama shapes with cold weights, the best were
+    // gate/up pair 2, output projection 4, down projection (n 5632) 4, q and
+    // o 1; else 1
+    const double per_cu = fmin(2.5, fmax(1.0, 2.5 * 2048.0 / (double)seg[0].n));
+    const long target = (long)(per_cu * cus + 0.5);
     rb = 1;
     for (int c = max_rb; c >= 1; c /= 2)
-      if (grid_of(c) * 10 >= 19L * cus && lds_ok(c)) {
+      if (grid_of(c) >= target && lds_ok(c)) {
         rb = c;
         break;
       }
