@@ -766,17 +766,29 @@ struct DigLds {
 // before the workgroup's weight loads: loads complete in issue order, so x
 // loaded after them would wait for all of them and the staging below could
 // not overlap the weight stream.
+// Without the norm prologue the first three chunks (x up to 6144
+// elements); with it the first chunk and its norm weights.
+template <bool NORM>
 struct XFirst {
-  float4 x0, x1, w0, w1;
+  static constexpr int N = NORM ? 1 : 3;
+  float4 x0[N], x1[N], w0, w1;
 };
 template <bool NORM>
-__device__ __forceinline__ void load_x_first(const GemvArgs& a, XFirst& f) {
-  const int c = threadIdx.x;
-  f.x0 = f.x1 = f.w0 = f.w1 = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (c < a.n / 8) {
-    f.x0 = ld4(a.x + 8 * c);
-    f.x1 = ld4(a.x + 8 * c + 4);
-    if constexpr (NORM) {
+__device__ __forceinline__ void load_x_first(const GemvArgs& a, XFirst<NORM>& f) {
+  const int nch = a.n / 8;
+  f.w0 = f.w1 = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int j = 0; j < XFirst<NORM>::N; ++j) {
+    const int c = threadIdx.x + j * kThreads;
+    f.x0[j] = f.x1[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c < nch) {
+      f.x0[j] = ld4(a.x + 8 * c);
+      f.x1[j] = ld4(a.x + 8 * c + 4);
+    }
+  }
+  if constexpr (NORM) {
+    const int c = threadIdx.x;
+    if (c < nch) {
       f.w0 = ld4(a.norm_w + 8 * c);
       f.w1 = ld4(a.norm_w + 8 * c + 4);
     }
@@ -787,8 +799,80 @@ __device__ __forceinline__ void load_x_first(const GemvArgs& a, XFirst& f) {
 // of squares reduced as a tree) into dst.  Thread t takes the 8-element
 // chunks t, t + kThreads, ...: the four chunks of a 32-element block sit on
 // four adjacent lanes.  Workgroup wg 0 also stores rmsnorm(x) to xn_out.
+// One 8-element chunk c of x (x0, x1; w0, w1 its norm weights for NORM)
+// scaled and staged as digits.  Every lane calls it (the shuffles need all
+// of them), ok false past the end of x.
 template <bool NORM>
-__device__ __forceinline__ void stage_digits(const GemvArgs& a, int wg, const XFirst& xf,
+__device__ __forceinline__ void stage_chunk(const GemvArgs& a, int wg, int c, bool ok,
+                                            float4 x0, float4 x1, float4 w0, float4 w1,
+                                            float scale, uint32_t* dst, const DigitStage& st) {
+  float v[8];
+  if (ok) {
+    v[0] = x0.x, v[1] = x0.y, v[2] = x0.z, v[3] = x0.w;
+    v[4] = x1.x, v[5] = x1.y, v[6] = x1.z, v[7] = x1.w;
+    if constexpr (NORM) {
+      const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = (v[j] * scale) * w[j];
+      if (a.xn_out && wg == 0) {
+        *(float4*)(a.xn_out + 8 * c) = make_float4(v[0], v[1], v[2], v[3]);
+        *(float4*)(a.xn_out + 8 * c + 4) = make_float4(v[4], v[5], v[6], v[7]);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = 0.0f;
+  }
+  float m = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
+  m = fmaxf(m, __shfl_xor(m, 1, 64));
+  m = fmaxf(m, __shfl_xor(m, 2, 64));
+  // max|x| = f * 2^e, f in [0.5, 1): 2^k = 2^(30 - e) keeps |X| < 2^30.
+  // A block with an infinite or NaN element gets a NaN scale, so its
+  // outputs are NaN (the reference's fp32 products would give inf or NaN).
+  int k = 0;
+  if (m > 0.0f && m <= 3.4028235e38f) k = 30 - __builtin_amdgcn_frexp_expf(m);
+  // Balanced base-256 digits of X (|X| < 2^30): the bytes of
+  // Z = (X + 0x80808080) ^ 0x80808080 read as signed bytes (byte p of
+  // X + 0x80808080 is D_p + 128).  A 4 x 4 byte transpose of four elements'
+  // Z then gives the digit words (word p: byte p of each element).
+  uint32_t dw[kDigits][2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    uint32_t z[4];
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int X = (int)rintf(__builtin_amdgcn_ldexpf(v[4 * q + b], k));
+      z[b] = ((uint32_t)X + 0x80808080u) ^ 0x80808080u;
+    }
+    // perm(hi, lo, sel): byte i of the result is byte sel_i of {hi:lo}
+    const uint32_t t0 = __builtin_amdgcn_perm(z[1], z[0], 0x05010400u);  // z0.0 z1.0 z0.1 z1.1
+    const uint32_t t1 = __builtin_amdgcn_perm(z[1], z[0], 0x07030602u);  // z0.2 z1.2 z0.3 z1.3
+    const uint32_t t2 = __builtin_amdgcn_perm(z[3], z[2], 0x05010400u);
+    const uint32_t t3 = __builtin_amdgcn_perm(z[3], z[2], 0x07030602u);
+    dw[0][q] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
+    dw[1][q] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
+    dw[2][q] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
+    dw[3][q] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
+  }
+  float s16 = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
+  s16 += __shfl_xor(s16, 1, 64);
+  if (ok) {
+#pragma unroll
+    for (int p = 0; p < kDigits; ++p)
+      *(uint2*)(dst + p * st.plane + dg_index(2 * c)) = make_uint2(dw[p][0], dw[p][1]);
+    if ((c & 1) == 0) reinterpret_cast<float*>(dst)[st.sums + c / 2] = s16;
+    if ((c & 3) == 0) {
+      const bool fin = m <= 3.4028235e38f;
+      reinterpret_cast<float*>(dst)[st.scales + c / 4] =
+          fin ? __builtin_amdgcn_ldexpf(1.0f, -k) : __builtin_nanf("");
+    }
+  }
+}
+
+template <bool NORM>
+__device__ __forceinline__ void stage_digits(const GemvArgs& a, int wg, const XFirst<NORM>& xf,
                                              uint32_t* dst, float* red) {
   const int tid = threadIdx.x;
   const int n = a.n;
@@ -798,9 +882,11 @@ __device__ __forceinline__ void stage_digits(const GemvArgs& a, int wg, const XF
   if constexpr (NORM) {
     // sum of squares over this thread's chunks tid, tid + kThreads, ...
     float ss = 0.0f;
-    if (tid < nch)
-      ss = ((xf.x0.x * xf.x0.x + xf.x0.y * xf.x0.y) + (xf.x0.z * xf.x0.z + xf.x0.w * xf.x0.w)) +
-           ((xf.x1.x * xf.x1.x + xf.x1.y * xf.x1.y) + (xf.x1.z * xf.x1.z + xf.x1.w * xf.x1.w));
+    if (tid < nch) {
+      const float4 v = xf.x0[0], u = xf.x1[0];
+      ss = ((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w)) +
+           ((u.x * u.x + u.y * u.y) + (u.z * u.z + u.w * u.w));
+    }
     for (int c = tid + kThreads; c < nch; c += kThreads) {
       const float4 v = ld4(a.x + 8 * c), u = ld4(a.x + 8 * c + 4);
       ss += ((v.x * v.x + v.y * v.y) + (v.z * v.z + v.w * v.w)) +
@@ -813,76 +899,27 @@ __device__ __forceinline__ void stage_digits(const GemvArgs& a, int wg, const XF
     ss = (red[0] + red[1]) + (red[2] + red[3]);
     scale = 1.0f / sqrtf(ss / (float)n + a.norm_eps);
   }
-  for (int c0 = 0; c0 < nch; c0 += kThreads) {
+  // the chunks already in registers, then the rest
+#pragma unroll
+  for (int j = 0; j < XFirst<NORM>::N; ++j) {
+    const int c0 = j * kThreads;  // uniform
+    if (c0 < nch)
+      stage_chunk<NORM>(a, wg, c0 + tid, c0 + tid < nch, xf.x0[j], xf.x1[j], xf.w0, xf.w1, scale,
+                        dst, st);
+  }
+  for (int c0 = XFirst<NORM>::N * kThreads; c0 < nch; c0 += kThreads) {
     const int c = c0 + tid;
     const bool ok = c < nch;  // uniform over the four lanes of a block
-    float v[8];
+    float4 x0 = make_float4(0.f, 0.f, 0.f, 0.f), x1 = x0, w0 = x0, w1 = x0;
     if (ok) {
-      const float4 x0 = c0 == 0 ? xf.x0 : ld4(a.x + 8 * c);
-      const float4 x1 = c0 == 0 ? xf.x1 : ld4(a.x + 8 * c + 4);
-      v[0] = x0.x, v[1] = x0.y, v[2] = x0.z, v[3] = x0.w;
-      v[4] = x1.x, v[5] = x1.y, v[6] = x1.z, v[7] = x1.w;
+      x0 = ld4(a.x + 8 * c);
+      x1 = ld4(a.x + 8 * c + 4);
       if constexpr (NORM) {
-        const float4 w0 = c0 == 0 ? xf.w0 : ld4(a.norm_w + 8 * c);
-        const float4 w1 = c0 == 0 ? xf.w1 : ld4(a.norm_w + 8 * c + 4);
-        const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-        for (int j = 0; j < 8; ++j) v[j] = (v[j] * scale) * w[j];
-        if (a.xn_out && wg == 0) {
-          *(float4*)(a.xn_out + 8 * c) = make_float4(v[0], v[1], v[2], v[3]);
-          *(float4*)(a.xn_out + 8 * c + 4) = make_float4(v[4], v[5], v[6], v[7]);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = 0.0f;
-    }
-    float m = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) m = fmaxf(m, fabsf(v[j]));
-    m = fmaxf(m, __shfl_xor(m, 1, 64));
-    m = fmaxf(m, __shfl_xor(m, 2, 64));
-    // max|x| = f * 2^e, f in [0.5, 1): 2^k = 2^(30 - e) keeps |X| < 2^30.
-    // A block with an infinite or NaN element gets a NaN scale, so its
-    // outputs are NaN (the reference's fp32 products would give inf or NaN).
-    int k = 0;
-    if (m > 0.0f && m <= 3.4028235e38f) k = 30 - __builtin_amdgcn_frexp_expf(m);
-    // Balanced base-256 digits of X (|X| < 2^30): the bytes of
-    // Z = (X + 0x80808080) ^ 0x80808080 read as signed bytes (byte p of
-    // X + 0x80808080 is D_p + 128).  A 4 x 4 byte transpose of four elements'
-    // Z then gives the digit words (word p: byte p of each element).
-    uint32_t dw[kDigits][2];
-#pragma unroll
-    for (int q = 0; q < 2; ++q) {
-      uint32_t z[4];
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int X = (int)rintf(__builtin_amdgcn_ldexpf(v[4 * q + b], k));
-        z[b] = ((uint32_t)X + 0x80808080u) ^ 0x80808080u;
-      }
-      // perm(hi, lo, sel): byte i of the result is byte sel_i of {hi:lo}
-      const uint32_t t0 = __builtin_amdgcn_perm(z[1], z[0], 0x05010400u);  // z0.0 z1.0 z0.1 z1.1
-      const uint32_t t1 = __builtin_amdgcn_perm(z[1], z[0], 0x07030602u);  // z0.2 z1.2 z0.3 z1.3
-      const uint32_t t2 = __builtin_amdgcn_perm(z[3], z[2], 0x05010400u);
-      const uint32_t t3 = __builtin_amdgcn_perm(z[3], z[2], 0x07030602u);
-      dw[0][q] = __builtin_amdgcn_perm(t2, t0, 0x05040100u);
-      dw[1][q] = __builtin_amdgcn_perm(t2, t0, 0x07060302u);
-      dw[2][q] = __builtin_amdgcn_perm(t3, t1, 0x05040100u);
-      dw[3][q] = __builtin_amdgcn_perm(t3, t1, 0x07060302u);
-    }
-    float s16 = ((v[0] + v[1]) + (v[2] + v[3])) + ((v[4] + v[5]) + (v[6] + v[7]));
-    s16 += __shfl_xor(s16, 1, 64);
-    if (ok) {
-#pragma unroll
-      for (int p = 0; p < kDigits; ++p)
-        *(uint2*)(dst + p * st.plane + dg_index(2 * c)) = make_uint2(dw[p][0], dw[p][1]);
-      if ((c & 1) == 0) reinterpret_cast<float*>(dst)[st.sums + c / 2] = s16;
-      if ((c & 3) == 0) {
-        const bool fin = m <= 3.4028235e38f;
-        reinterpret_cast<float*>(dst)[st.scales + c / 4] =
-            fin ? __builtin_amdgcn_ldexpf(1.0f, -k) : __builtin_nanf("");
+        w0 = ld4(a.norm_w + 8 * c);
+        w1 = ld4(a.norm_w + 8 * c + 4);
       }
     }
+    stage_chunk<NORM>(a, wg, c, ok, x0, x1, w0, w1, scale, dst, st);
   }
 }
 
@@ -1031,7 +1068,7 @@ __device__ __forceinline__ void gemv_body_fast(const GemvArgs& a, int wg, float*
   const bool active = rlane < a.row_par;
   const int u = tid % a.uspan;
   const bool first = active && u < a.units;
-  XFirst xf;
+  XFirst<NORM> xf;
   load_x_first<NORM>(a, xf);
   typename F::Raw raw[RB];
   if (first) load_rows<F, RB, PAIR>(a, r0, rows, rlane, u, raw);
