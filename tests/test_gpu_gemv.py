@@ -177,3 +177,50 @@ def test_matmul_batch_bit_exact(gpu, oracle_mod, qtype, n, d, nb):
     for b in range(nb):
         want = O.matmul(W, X[b], n, d, qtype)
         assert np.array_equal(got[b].view(np.uint32), want.view(np.uint32)), b
+
+
+@pytest.mark.parametrize("rb", [1, 2, 4, 8])
+def test_gemv_fast_order_rows_per_thread(gpu, rb):
+    """Every rows-per-thread variant of the fast order (tuning key 3), as a
+    single GEMV with the rmsnorm prologue and as a gate/up pair (whose second
+    rows are issued after the x staging), within the fast order's bound of
+    the float64 product; the pair's silu(gate) * up within that bound carried
+    through silu and the product."""
+    import ctypes as C
+    rng = np.random.default_rng(900 + rb)
+    qt, n, d = G.TYPE_Q4_K, 2048, 1000
+    Wg = S.random_weights(rng, qt, n, d, S.unit_scale_exp(qt, n))
+    Wu = S.random_weights(rng, qt, n, d, S.unit_scale_exp(qt, n))
+    g64, u64 = decode64(qt, Wg, n, d), decode64(qt, Wu, n, d)
+    x = rng.standard_normal(n).astype(np.float32)
+    nw = rng.uniform(0.5, 1.5, n).astype(np.float32)
+    xs = x.astype(np.float64)
+    xn = xs / np.sqrt(np.mean(xs * xs) + 1e-5) * nw
+    Gd, Ud = G.QMatrix(qt, n, d, Wg), G.QMatrix(qt, n, d, Wu)
+    dx, dnw = P.DeviceBuffer.from_numpy(x), P.DeviceBuffer.from_numpy(nw)
+    out = P.DeviceBuffer(4 * d)
+    vp = C.c_void_p
+    eps32 = np.finfo(np.float32).eps
+    P.check(P.lib.plh_set_tuning(3, rb), "plh_set_tuning")
+    try:
+        print(f"[case] fast gemv rows per thread {rb}", flush=True)
+        P.check(P.lib.plh_gemv_ex(qt, n, d, vp(Gd.ptr), vp(dx.ptr), vp(out.ptr), vp(dnw.ptr),
+                                  C.c_float(1e-5), None, 0, None, None), "plh_gemv_ex")
+        got = out.download(np.float32, (d,)).astype(np.float64)
+        want = g64 @ xn
+        mag = np.abs(g64) @ np.abs(xn)
+        assert np.all(np.abs(got - want) <= 128 * eps32 * mag + 1e-30), rb
+        P.check(P.lib.plh_gemv_swiglu(qt, n, d, vp(Gd.ptr), vp(Ud.ptr), vp(dx.ptr), vp(out.ptr),
+                                      vp(dnw.ptr), C.c_float(1e-5)), "plh_gemv_swiglu")
+        got = out.download(np.float32, (d,)).astype(np.float64)
+        g, u = g64 @ xn, u64 @ xn
+        want = g / (1.0 + np.exp(-g)) * u
+        dg = 128 * eps32 * (np.abs(g64) @ np.abs(xn))
+        du = 128 * eps32 * (np.abs(u64) @ np.abs(xn))
+        # |d silu(g)/dg| <= 1.1; silu's own rounding a few ulps of the result
+        tol = 1.1 * dg * np.abs(u) + np.abs(g) * du + 1.1 * dg * du + 8 * eps32 * np.abs(want)
+        assert np.all(np.abs(got - want) <= tol + 1e-30), (rb, float(np.max(np.abs(got - want) / (tol + 1e-30))))
+    finally:
+        P.check(P.lib.plh_set_tuning(3, 0), "plh_set_tuning")
+        for b in (Gd, Ud, dx, dnw, out):
+            b.free()
