@@ -459,7 +459,9 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
                "s"(a.n_heads), "s"(a.n_kv_heads), "s"(a.max_seq_len), "s"(a.pos),
                "s"(a.rope_type), "s"(a.n_hblk), "s"(a.nhm), "s"(a.n_split), "s"(a.split_len),
                "s"(a.n_units), "s"(a.per_xcd), "s"(a.score_scale), "s"(a.k_rows),
-               "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps));
+               "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps), "s"(a.G),
+               "s"(a.fd_split.m), "s"(a.fd_split.sh), "s"(a.fd_hblk.m), "s"(a.fd_hblk.sh),
+               "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh));
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -470,13 +472,14 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
   // multiple of n_split) and a group's splits share one L2.
   const int unit = (int)(blockIdx.x & 7) * a.per_xcd + (int)(blockIdx.x >> 3);
   if (unit >= a.n_units) return;
-  const int split = unit % a.n_split;
-  const int group = unit / a.n_split;
-  const int hblk = group % a.n_hblk;
-  const int kvh = (group / a.n_hblk) % a.n_kv_heads;
-  const int li = group / (a.n_hblk * a.n_kv_heads);
+  const int group = (int)fdiv(unit, a.fd_split);
+  const int split = unit - group * a.n_split;
+  const int gh = (int)fdiv(group, a.fd_hblk);  // group / n_hblk
+  const int hblk = group - gh * a.n_hblk;
+  const int li = (int)fdiv(gh, a.fd_kvh);
+  const int kvh = gh - li * a.n_kv_heads;
   const int layer = a.layer0 + li;
-  const int G = a.n_heads / a.n_kv_heads;
+  const int G = a.G;
   const int h0 = hblk * 16;
   const int nh = min(16, G - h0);
   const int kv_dim = a.n_kv_heads * D;
@@ -607,11 +610,12 @@ __global__ __launch_bounds__(kCombineThreads) void attn_decode_combine_kernel(De
   // workgroup ids go to consecutive XCDs
   const int gpx = a.per_xcd / a.n_split;
   const int group = (int)(blockIdx.x & 7) * gpx + (int)(blockIdx.x >> 3);
-  if (group >= a.n_units / a.n_split) return;
-  const int hblk = group % a.n_hblk;
-  const int kvh = (group / a.n_hblk) % a.n_kv_heads;
-  const int li = group / (a.n_hblk * a.n_kv_heads);
-  const int G = a.n_heads / a.n_kv_heads;
+  if (group * a.n_split >= a.n_units) return;
+  const int gh = (int)fdiv(group, a.fd_hblk);  // group / n_hblk
+  const int hblk = group - gh * a.n_hblk;
+  const int li = (int)fdiv(gh, a.fd_kvh);
+  const int kvh = gh - li * a.n_kv_heads;
+  const int G = a.G;
   const int h0 = hblk * 16;
   const int nh = min(16, G - h0);
   float* out_base = a.out + (size_t)li * a.n_heads * D + (size_t)(kvh * G + h0) * D;
@@ -677,9 +681,9 @@ __global__ __launch_bounds__(kCombineThreads) void attn_decode_combine_kernel(De
 // r).  All in 32-bit integers (the host checks T fits): 64-bit division
 // would cost the prologue about a thousand instructions.
 __device__ __forceinline__ int sk_start(int w, int q, int r) { return w * q + min(w, r); }
-__device__ __forceinline__ int sk_owner(int t, int q, int r) {
-  const int big = r * (q + 1);
-  return t < big ? t / (q + 1) : r + (t - big) / q;
+__device__ __forceinline__ int sk_owner(int t, const DecodeArgs& a) {
+  const int big = a.sk_r * (a.sk_q + 1);
+  return t < big ? (int)fdiv(t, a.fd_q1) : a.sk_r + (int)fdiv(t - big, a.fd_q);
 }
 
 constexpr int kSkAux = 16; // buffer cache policy: sc1 (device scope)
@@ -710,26 +714,30 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
                "s"(a.max_seq_len), "s"(a.pos), "s"(a.rope_type), "s"(a.n_hblk), "s"(a.nhm),
                "s"(a.score_scale), "s"(a.sk_q), "s"(a.sk_r), "s"(a.sk_nbk), "s"(a.sk_maxp),
                "s"(a.sk_part), "s"(a.sk_part_bytes), "s"(a.sk_ctr), "s"(a.k_rows),
-               "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps));
+               "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps), "s"(a.G),
+               "s"(a.fd_hblk.m), "s"(a.fd_hblk.sh), "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh),
+               "s"(a.fd_nbk.m), "s"(a.fd_nbk.sh), "s"(a.fd_q.m), "s"(a.fd_q.sh),
+               "s"(a.fd_q1.m), "s"(a.fd_q1.sh));
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
   const int w = blockIdx.x;
   const int b0 = sk_start(w, a.sk_q, a.sk_r), b1 = sk_start(w + 1, a.sk_q, a.sk_r);
-  const int G = a.n_heads / a.n_kv_heads;
+  const int G = a.G;
   const int kv_dim = a.n_kv_heads * D;
   const int pos = a.pos;
   const int q_dim = a.n_heads * D;
   const __amdgpu_buffer_rsrc_t prs = sk_rsrc<D>(a);
 
   for (int s0 = b0; s0 < b1;) {
-    const int group = s0 / a.sk_nbk;
+    const int group = (int)fdiv(s0, a.fd_nbk);
     const int gb = group * a.sk_nbk;
     const int s1 = min(b1, gb + a.sk_nbk);
-    const int hblk = group % a.n_hblk;
-    const int kvh = (group / a.n_hblk) % a.n_kv_heads;
-    const int li = group / (a.n_hblk * a.n_kv_heads);
+    const int gh = (int)fdiv(group, a.fd_hblk);  // group / n_hblk
+    const int hblk = group - gh * a.n_hblk;
+    const int li = (int)fdiv(gh, a.fd_kvh);
+    const int kvh = gh - li * a.n_kv_heads;
     const int layer = a.layer0 + li;
     const int h0 = hblk * 16;
     const int nh = min(16, G - h0);
@@ -804,8 +812,8 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
     __syncthreads();
 
     // producers of this group: the workgroups owning its first and last block
-    const int p0 = sk_owner(gb, a.sk_q, a.sk_r);
-    const int np = sk_owner(gb + a.sk_nbk - 1, a.sk_q, a.sk_r) - p0 + 1;
+    const int p0 = sk_owner(gb, a);
+    const int np = sk_owner(gb + a.sk_nbk - 1, a) - p0 + 1;
 
     // ---- merge the waves (and the new row); one float4 of d per thread -----
     float* out_base = a.out + (size_t)li * q_dim + (size_t)(kvh * G + h0) * D;
@@ -1124,6 +1132,14 @@ static int attn_decode_sk_launch(int n_heads, int n_kv_heads, int head_dim, int 
   a.sk_q = (int)(T / W);
   a.sk_r = (int)(T % W);
   a.sk_nbk = nbk;
+  a.G = G;
+  a.fd_hblk = make_fastdiv((uint32_t)n_hblk);
+  a.fd_kvh = make_fastdiv((uint32_t)n_kv_heads);
+  a.fd_nbk = make_fastdiv((uint32_t)nbk);
+  // q = 0 (fewer blocks than workgroups) never divides by q: every block
+  // then lies in the first r ranges
+  a.fd_q = make_fastdiv((uint32_t)(a.sk_q > 0 ? a.sk_q : 1));
+  a.fd_q1 = make_fastdiv((uint32_t)(a.sk_q + 1));
   a.sk_maxp = maxp;
   a.sk_groups = n_groups;
   a.sk_part = part;
@@ -1268,6 +1284,10 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
   a.split_len = split_len;
   a.n_units = n_units;
   a.per_xcd = per_xcd;
+  a.G = G;
+  a.fd_split = make_fastdiv((uint32_t)n_split);
+  a.fd_hblk = make_fastdiv((uint32_t)n_hblk);
+  a.fd_kvh = make_fastdiv((uint32_t)n_kv_heads);
   a.qn = q_norm;
   a.kn = k_norm;
   a.norm_eps = norm_eps;

@@ -5,6 +5,8 @@
 #include <stddef.h>
 #include <stdint.h>
 
+#include "fastdiv.h"
+
 namespace plh {
 
 // One device, one stream, one growable workspace: the library follows the
@@ -145,6 +147,10 @@ struct DecodeArgs {
   float* sk_part;
   uint32_t sk_part_bytes;
   unsigned* sk_ctr;
+  // n_heads / n_kv_heads, and divisions by the launch's constants
+  int G;
+  FastDiv fd_split, fd_hblk, fd_kvh;  // n_split, n_hblk, n_kv_heads
+  FastDiv fd_nbk, fd_q, fd_q1;         // sk_nbk, sk_q, sk_q + 1
 };
 
 }  // namespace plh
