@@ -20,8 +20,12 @@ workload of the attention block's benchmark set, each measured the same way:
 Method (device):
   * inputs rotated over enough copies (>= 512 MiB in all) that the 256 MiB
     Infinity Cache cannot serve a step from the previous one; K timed steps
-    captured in one HIP graph, replayed once untimed and once timed between
-    device synchronisations; ms_per_step = wall clock / K, roofline.achieved =
+    captured in one HIP graph, replayed untimed until SETTLE_S of device work
+    has run, then once timed between device synchronisations (MFMA-heavy
+    prefill runs up to 25% slower for the first ~30 ms after the GPU idles,
+    a clock transient that settles whatever the kernel; the memory- and
+    latency-bound decode, GEMV and forward steps show none);
+    ms_per_step = wall clock / K, roofline.achieved =
     algorithmic bytes (decode) or causal-pair flops (prefill) / the mean step
     time from HIP events recorded on the library stream (the stream the
     kernels run on);
@@ -79,6 +83,8 @@ sys.path.insert(0, ROOT)
 METRIC = "attn µs/token + KV GB/s (% HBM peak) decode; prefill TFLOP/s (% MFMA)"
 HBM_PEAK_GBS = 8000.0
 MALL_DEFEAT_BYTES = 512 << 20
+# untimed replays before each timed one, in seconds of device work
+SETTLE_S = 0.1
 MFMA_F16_PEAK_TFS = 2516.6
 HOST_THREADS_MAX = 16   # host CPU threads available per GPU
 
@@ -467,14 +473,18 @@ def norm_weights(P, w, rng):
 
 
 def timed_graph(P, launch, steps):
-    """Captures `steps` calls of launch(i) in one graph, replays it once
-    untimed and once timed; returns (wall seconds, event milliseconds) per
-    step."""
+    """Captures `steps` calls of launch(i) in one graph, replays it untimed
+    until SETTLE_S seconds have passed (at least once), then once timed;
+    returns (wall seconds, event milliseconds) per step."""
     with P.Graph() as g:
         for i in range(steps):
             launch(i)
-    g.launch()
-    P.synchronize()
+    t_end = time.perf_counter() + SETTLE_S
+    while True:
+        g.launch()
+        P.synchronize()
+        if time.perf_counter() >= t_end:
+            break
     e0, e1 = P.Event(), P.Event()
     t0 = time.perf_counter()
     e0.record()

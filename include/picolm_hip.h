@@ -348,7 +348,9 @@ int plh_forward_prefill(const plh_model *m, const int *tokens, int n_tokens, int
  * single-vector weight GEMVs (plh_gemv*, gpu_try_matmul, plh_forward) keep
  * the reference's x86 AVX2 summation order bit for bit (1) or use the
  * faster fixed-point-digit order (0, default: within ~1e-7 of sum |w x| per
- * output; the batched prompt GEMVs always keep the exact order). */
+ * output; the batched prompt GEMVs always keep the exact order); key 11:
+ * stream-K groups whose producers share an XCD merge through its L2 (0 by
+ * shape, 1 wherever the plan allows, -1 never: every merge device-wide). */
 int plh_set_tuning(int key, int value);
 
 #ifdef __cplusplus

@@ -686,7 +686,49 @@ __device__ __forceinline__ int sk_owner(int t, const DecodeArgs& a) {
   return t < big ? (int)fdiv(t, a.fd_q1) : a.sk_r + (int)fdiv(t - big, a.fd_q);
 }
 
-constexpr int kSkAux = 16; // buffer cache policy: sc1 (device scope)
+constexpr int kSkAux = 16;   // buffer cache policy: sc1 (device scope)
+constexpr int kSkLocal = 1;  // sc0: past the CU's L1, served by the XCD's L2
+// local arrival counters sit one 128-byte L2 line apart
+constexpr int kSkLocalPitch = 32;
+
+// The last producer's merge of a group's np partials (slots slot0..): POL is
+// the cache policy the producers stored them with.
+template <int D, int POL>
+__device__ __forceinline__ void sk_merge_partials(const DecodeArgs& a,
+                                                  __amdgpu_buffer_rsrc_t prs, int slot0, int np,
+                                                  int h, int d, float* dst) {
+  constexpr int PS = D + 4;
+  float M = kNegBig, L = 0.f;
+  float4_t O = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < np; j0 += 8) {
+    float4_t ml[8], oj[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int off = ((slot0 + min(j0 + j, np - 1)) * a.nhm + h) * PS;
+      ml[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, (off + D) * 4, 0, POL);
+      oj[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, (off + d) * 4, 0, POL);
+    }
+    float Mc = M;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j0 + j < np) Mc = fmaxf(Mc, ml[j][0]);
+    const float r = fast_exp2(M - Mc);
+    L *= r;
+    O *= r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j0 + j < np) {
+        const float wt = fast_exp2(ml[j][0] - Mc);
+        L = __builtin_fmaf(ml[j][1], wt, L);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) O[c] = __builtin_fmaf(oj[j][c], wt, O[c]);
+      }
+    }
+    M = Mc;
+  }
+  const float inv = 1.0f / L;
+  *reinterpret_cast<float4_t*>(dst) = O * inv;
+}
 
 template <int D>
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const DecodeArgs& a) {
@@ -717,12 +759,17 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
                "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps), "s"(a.G),
                "s"(a.fd_hblk.m), "s"(a.fd_hblk.sh), "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh),
                "s"(a.fd_nbk.m), "s"(a.fd_nbk.sh), "s"(a.fd_q.m), "s"(a.fd_q.sh),
-               "s"(a.fd_q1.m), "s"(a.fd_q1.sh));
+               "s"(a.fd_q1.m), "s"(a.fd_q1.sh), "s"(a.sk_wx), "s"(a.fd_wx.m), "s"(a.fd_wx.sh),
+               "s"(a.sk_ctr_local));
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int col = lane & 15, grp = lane >> 4;
-  const int w = blockIdx.x;
+  // sk_wx > 0: ranges x*wx .. x*wx + wx - 1 run on XCD x (workgroup ids x,
+  // x + 8, ...: the dispatcher deals workgroups to the XCDs in turn), so
+  // most groups' producers share one L2
+  const int w = a.sk_wx ? (int)(blockIdx.x & 7) * a.sk_wx + (int)(blockIdx.x >> 3)
+                        : (int)blockIdx.x;
   const int b0 = sk_start(w, a.sk_q, a.sk_r), b1 = sk_start(w + 1, a.sk_q, a.sk_r);
   const int G = a.G;
   const int kv_dim = a.n_kv_heads * D;
@@ -814,6 +861,8 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
     // producers of this group: the workgroups owning its first and last block
     const int p0 = sk_owner(gb, a);
     const int np = sk_owner(gb + a.sk_nbk - 1, a) - p0 + 1;
+    // all producers on one XCD: partials and the count stay in its L2
+    const bool local = a.sk_wx && fdiv(p0, a.fd_wx) == fdiv(p0 + np - 1, a.fd_wx);
 
     // ---- merge the waves (and the new row); one float4 of d per thread -----
     float* out_base = a.out + (size_t)li * q_dim + (size_t)(kvh * G + h0) * D;
@@ -845,10 +894,14 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
         *reinterpret_cast<float4_t*>(out_base + (size_t)h * D + d) = O * inv;
       } else {
         const int off = ((slot0 + (w - p0)) * a.nhm + h) * PS;
-        __builtin_amdgcn_raw_buffer_store_b128(O, prs, (off + d) * 4, 0, kSkAux);
-        if (d == 0)
-          __builtin_amdgcn_raw_buffer_store_b128(float4_t{M, L, 0.f, 0.f}, prs, (off + D) * 4,
-                                                 0, kSkAux);
+        const float4_t ml = float4_t{M, L, 0.f, 0.f};
+        if (local) {
+          __builtin_amdgcn_raw_buffer_store_b128(O, prs, (off + d) * 4, 0, kSkLocal);
+          if (d == 0) __builtin_amdgcn_raw_buffer_store_b128(ml, prs, (off + D) * 4, 0, kSkLocal);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b128(O, prs, (off + d) * 4, 0, kSkAux);
+          if (d == 0) __builtin_amdgcn_raw_buffer_store_b128(ml, prs, (off + D) * 4, 0, kSkAux);
+        }
       }
     }
 
@@ -856,45 +909,29 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
       // every partial store has reached memory before the count goes up
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
+      // a local count is an L2 atomic of the XCD (no sc1); a cross-XCD one
+      // a device-scope atomic
+      unsigned* ctr = local ? a.sk_ctr_local + group * kSkLocalPitch : a.sk_ctr + group;
       if (tid == 0)
-        s_last = __hip_atomic_fetch_add(a.sk_ctr + group, 1u, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT) == (unsigned)(np - 1);
+        s_last = (local ? __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_WORKGROUP)
+                        : __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED,
+                                                 __HIP_MEMORY_SCOPE_AGENT)) == (unsigned)(np - 1);
       __syncthreads();
       if (s_last) {
-        if (tid == 0)
-          __hip_atomic_store(a.sk_ctr + group, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (tid == 0) {
+          if (local)
+            __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+          else
+            __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         for (int idx = tid; idx < nh * (D / 4); idx += kThreads) {
           const int h = idx / (D / 4), d = 4 * (idx - h * (D / 4));
-          float M = kNegBig, L = 0.f;
-          float4_t O = float4_t{0.f, 0.f, 0.f, 0.f};
-          for (int j0 = 0; j0 < np; j0 += 8) {
-            float4_t ml[8], oj[8];
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              const int off = ((slot0 + min(j0 + j, np - 1)) * a.nhm + h) * PS;
-              ml[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, (off + D) * 4, 0, kSkAux);
-              oj[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, (off + d) * 4, 0, kSkAux);
-            }
-            float Mc = M;
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-              if (j0 + j < np) Mc = fmaxf(Mc, ml[j][0]);
-            const float r = fast_exp2(M - Mc);
-            L *= r;
-            O *= r;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) {
-              if (j0 + j < np) {
-                const float wt = fast_exp2(ml[j][0] - Mc);
-                L = __builtin_fmaf(ml[j][1], wt, L);
-#pragma unroll
-                for (int c = 0; c < 4; ++c) O[c] = __builtin_fmaf(oj[j][c], wt, O[c]);
-              }
-            }
-            M = Mc;
-          }
-          const float inv = 1.0f / L;
-          *reinterpret_cast<float4_t*>(out_base + (size_t)h * D + d) = O * inv;
+          float* dst = out_base + (size_t)h * D + d;
+          if (local)
+            sk_merge_partials<D, kSkLocal>(a, prs, slot0, np, h, d, dst);
+          else
+            sk_merge_partials<D, kSkAux>(a, prs, slot0, np, h, d, dst);
         }
       }
     }
@@ -912,6 +949,18 @@ int g_min_split = kDefaultMinSplit;
 int g_decode_kernel = 0;  // plh_set_tuning key 7: 0 by shape, 1 split + combine, 2 stream-K
 int g_sk_workgroups = 0;  // key 8: stream-K workgroups (0: the launch's own choice)
 int g_sk_pf = 0;          // key 9: stream-K tiles in flight per wave (0: by head_dim)
+int g_sk_xcd_local = 0;   // key 11: XCD-local stream-K merges (0 by shape, 1 always, -1 never)
+// per device: 1 when workgroup ids congruent mod 8 ran on one XCD at
+// plh_init, -1 when they did not, 0 before the check
+int g_xcd_ok[kMaxDevices] = {};
+
+// Each workgroup's XCD (the hardware XCC_ID register) by workgroup id.
+constexpr int kXcdProbeGroups = 2048;
+__global__ __launch_bounds__(64) void xcd_probe_kernel(unsigned* out) {
+  unsigned x;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(x));
+  if (threadIdx.x == 0) out[blockIdx.x] = x;
+}
 
 }  // namespace
 
@@ -932,6 +981,21 @@ int decode_scratch_setup(int device) {
   if (check_hip(hipMemsetAsync(p, 0, kScratchCounterBytes, c.stream), "hipMemsetAsync(scratch)") ||
       check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize"))
     return -1;
+  // The stream-K kernel's XCD-local merges need every workgroup id
+  // congruent mod 8 to run on one XCD (the dispatcher deals workgroups to
+  // the XCDs in turn); the ids' XCDs are read back once per device, through
+  // the scratch's partial region, and the merges stay device-wide otherwise.
+  unsigned* probe = (unsigned*)((char*)p + kScratchCounterBytes);
+  unsigned xcc[kXcdProbeGroups];
+  hipLaunchKernelGGL(xcd_probe_kernel, dim3(kXcdProbeGroups), dim3(64), 0, c.stream, probe);
+  if (check_hip(hipGetLastError(), "xcd_probe_kernel") ||
+      check_hip(hipMemcpyAsync(xcc, probe, sizeof(xcc), hipMemcpyDeviceToHost, c.stream),
+                "hipMemcpyAsync(xcd probe)") ||
+      check_hip(hipStreamSynchronize(c.stream), "hipStreamSynchronize"))
+    return -1;
+  bool same = true;
+  for (int b = 8; b < kXcdProbeGroups; ++b) same = same && xcc[b] == xcc[b & 7];
+  g_xcd_ok[device] = same ? 1 : -1;
   g_scratch_ptr[device] = p;
   return 0;
 }
@@ -1009,6 +1073,14 @@ extern "C" int plh_set_tuning(int key, int value) {
       return -1;
     }
     g_gemv_exact = value;
+    return 0;
+  }
+  if (key == 11) {
+    if (value < -1 || value > 1) {
+      set_error("plh_set_tuning: XCD-local stream-K merges must be 0 (by shape), 1 or -1");
+      return -1;
+    }
+    g_sk_xcd_local = value;
     return 0;
   }
   if (key == 9) {
@@ -1140,6 +1212,26 @@ static int attn_decode_sk_launch(int n_heads, int n_kv_heads, int head_dim, int 
   // then lies in the first r ranges
   a.fd_q = make_fastdiv((uint32_t)(a.sk_q > 0 ? a.sk_q : 1));
   a.fd_q1 = make_fastdiv((uint32_t)(a.sk_q + 1));
+  // Ranges dealt to the XCDs in blocks, so that groups whose producers all
+  // land on one XCD merge through its L2: needs workgroups that split evenly
+  // over the eight XCDs, the local counters to fit, and plh_init's check
+  // that workgroup ids congruent mod 8 share an XCD.  By shape (measured on
+  // MI355X, one launch per layer and all layers in one): head_dim 64 always
+  // (TinyLlama pos 1024 14.3 -> 13.3 us, pos 2047 16.5 -> 16.1 us, per layer
+  // 190.6 -> 185.9 us per token; Llama-3.2 pos 8191 per layer 218 -> 162
+  // us); head_dim 128 only with 16 or more workgroups per group, where the
+  // merge dominates (Qwen3 pos 2047 per layer 341 -> 313 us, a 16-layer
+  // 8-kv-head model at pos 8191 per layer 289 -> 268 us).  Fewer producers
+  // per group at head_dim 128 lose more to the XCD-major placement of the
+  // ranges than the L2 merge saves (Llama-2 pos 4095: 355 -> 361 us, per
+  // layer 594 -> 640 us).
+  const bool xcd_shape = g_sk_xcd_local > 0 || head_dim == 64 || W >= 16L * n_groups;
+  const bool xcd_local = g_sk_xcd_local >= 0 && xcd_shape && g_xcd_ok[c.device] == 1 &&
+                         W % 8 == 0 && W >= 16 &&
+                         (long)n_groups * kSkLocalPitch <= kDecodeCounters / 2;
+  a.sk_wx = xcd_local ? (int)(W / 8) : 0;
+  a.fd_wx = make_fastdiv((uint32_t)(xcd_local ? W / 8 : 1));
+  a.sk_ctr_local = ctr + kDecodeCounters / 2;
   a.sk_maxp = maxp;
   a.sk_groups = n_groups;
   a.sk_part = part;
@@ -1219,7 +1311,7 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
   const int npos = pos + 1;
 
   if (use_stream_k(head_dim, pos, n_groups, c.num_cus) && ((uintptr_t)out & 15) == 0 &&
-      n_groups <= kDecodeCounters)
+      n_groups <= kDecodeCounters / 2)
     return attn_decode_sk_launch(n_heads, n_kv_heads, head_dim, max_seq_len, rope_type, layer0,
                                  n_launch_layers, pos, q, k, v, key_cache, val_cache, rope_cos,
                                  rope_sin, out, q_norm, k_norm, norm_eps, noalloc, k_rows,
