@@ -1104,10 +1104,42 @@ extern "C" int plh_set_tuning(int key, int value) {
 // head_dim 64 streams (Llama-3.2 pos 8191, 256 blocks per workgroup: 54.9
 // against 61.9 us) and for contexts it does not split (TinyLlama pos 256:
 // 6.6 against 8.3 us).
+// Stream-K workgroups of a launch (tuning key 8 overrides).  Head_dim 64
+// launches whose groups split evenly over the XCDs take an aligned plan:
+// W = k * n_groups, so each workgroup streams 1/k of one group and a
+// group's k producers sit on one XCD (merged through its L2), with k the
+// smallest power of two that gives about 0.6 workgroups per CU or more and
+// at most 384 KB of K and V rows per workgroup (W at most 4 per CU, else
+// the general plan).  Measured on MI355X, all-layer TinyLlama launches (88
+// groups): pos 512 / 600 / 1024 / 2047 took 8.2 / 8.7 / 10.0 / 15.6 us with
+// k = 2 against 12.0 / 11.9 / 13.4 / 16.4 us for the general plan;
+// Llama-3.2 (128 groups) pos 4095 / 8191 33.2 / 56.1 us with k = 4 / 8
+// against 33.9 / 63.8 us (those launches run the split kernel, 31.5 / 55.2
+// us).  Otherwise about one workgroup per CU, each with at least 8
+// blocks (one 32-row tile per wave): head_dim 128 launches gain nothing
+// from the aligned plan (Qwen3 pos 2047: 50.1-51.3 us with k = 1 and
+// 52.9-59.8 us with k = 2 or 4, against 51.5 us).
+static long sk_plan_workgroups(int head_dim, int n_groups, int nbk, int num_cus, int device) {
+  const long T = (long)n_groups * nbk;
+  const long cus = num_cus > 0 ? num_cus : 256;
+  if (g_sk_workgroups > 0) return g_sk_workgroups;
+  if (head_dim == 64 && n_groups % 8 == 0 && g_sk_xcd_local >= 0 && g_xcd_ok[device] == 1) {
+    const double bytes = (double)T * 16 * 64 * 2 * 2;  // K and V rows the launch reads
+    for (long k = 1; k <= nbk && k * n_groups <= 4 * cus; k *= 2)
+      if (k * n_groups * 10 >= 6 * cus && bytes / (double)(k * n_groups) <= 384.0 * 1024)
+        return k * n_groups;
+  }
+  long W = T / 8;
+  if (W > cus) W = cus;
+  return W;
+}
+
 static bool use_stream_k(int head_dim, int pos, int n_groups, int num_cus) {
   if (g_decode_kernel) return g_decode_kernel == 2;
   if (pos + 1 <= g_min_split) return false;
   if (head_dim == 128) return true;
+  // by the general plan's range length (the aligned plan's would send
+  // Llama-3.2 pos 4095 to stream-K: 32.5 us against 31.5 us split)
   const long T = (long)n_groups * ((pos + 15) / 16);
   const long cus = num_cus > 0 ? num_cus : 256;
   long W = T / 8;
@@ -1136,10 +1168,7 @@ static int attn_decode_sk_launch(int n_heads, int n_kv_heads, int head_dim, int 
     return -1;
   }
   const int cus = c.num_cus > 0 ? c.num_cus : 256;
-  // about one workgroup per CU, each with at least 8 blocks (one 32-row
-  // tile per wave)
-  long W = g_sk_workgroups > 0 ? g_sk_workgroups : T / 8;
-  if (W > cus && g_sk_workgroups == 0) W = cus;
+  long W = sk_plan_workgroups(head_dim, n_groups, nbk, cus, c.device);
   if (W > T) W = T;
   if (W < 1) W = 1;
   // producers per group (the partial slots it needs)

@@ -274,23 +274,24 @@ def test_decode_stream_k_plans(gpu, oracle_mod, workgroups):
 
 
 @pytest.mark.parametrize("shape", [
-    ((1, 32, 8, 64, 8192, 5e5, 0), 8191, None),      # one Llama-3.2 layer: 32 producers a group
-    ((2, 16, 8, 128, 4096, 1e6, 1), 2047, None),     # head_dim 128, 8 producers a group
-    ((22, 32, 4, 64, 2048, 1e4, 0), 2047, None),     # TinyLlama, groups across XCD boundaries
+    ((1, 32, 8, 64, 8192, 5e5, 0), 8191, 256),       # one Llama-3.2 layer: 32 producers a group
+    ((2, 16, 8, 128, 4096, 1e6, 1), 2047, 256),      # head_dim 128, 16 producers a group
+    ((22, 32, 4, 64, 2048, 1e4, 0), 2047, 256),      # TinyLlama, groups across XCD boundaries
+    ((22, 32, 4, 64, 2048, 1e4, 0), 1024, 176),      # TinyLlama, two ranges a group (aligned)
     ((3, 48, 2, 64, 600, 1e4, 0), 599, 1000),        # two head blocks, 1000 workgroups
-], ids=["llama32-layer", "d128", "tinyllama", "hblk2-w1000"])
+], ids=["llama32-layer", "d128", "tinyllama", "tinyllama-aligned", "hblk2-w1000"])
 def test_decode_xcd_local_merges(gpu, oracle_mod, shape):
     """Stream-K merges inside one XCD's L2 (plh_set_tuning key 11 = 1) give
     oracle-exact outputs and caches, and the same bits as device-wide merges
-    (key 11 = -1): the partials are merged in the same order either way."""
+    (key 11 = -1) under the same plan (workgroups fixed by key 8): the
+    partials are merged in the same order either way."""
     dims, pos, workgroups = shape
     cfg = gpu.AttnConfig(*dims)
     check = None if cfg.n_layers <= 3 else [0, cfg.n_layers - 1]
     outs = {}
     try:
         gpu.check(gpu.lib.plh_set_tuning(7, 2), "tuning")
-        if workgroups:
-            gpu.check(gpu.lib.plh_set_tuning(8, workgroups), "tuning")
+        gpu.check(gpu.lib.plh_set_tuning(8, workgroups), "tuning")
         for mode in (1, -1):
             gpu.check(gpu.lib.plh_set_tuning(11, mode), "tuning")
             outs[mode] = run_decode(gpu, oracle_mod, cfg, pos, seed=77, check_layers=check)
