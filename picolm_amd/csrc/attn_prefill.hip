@@ -68,12 +68,27 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(PrefillArgs a) {
   __shared__ __align__(16) float ksq[QKN ? (256 / NG) * kSqPitch : 1];
   for (long idx = (long)blockIdx.x * 256 + threadIdx.x; idx < total;
        idx += (long)gridDim.x * 256) {
+    // item idx = ((layer * n_tokens + token) * n_kv_heads + kv head) * NG + g;
+    // below 2^31 items the divisions are multiplies (a 64-bit division by a
+    // runtime value costs hundreds of instructions)
     const int g = (int)(idx % NG);
-    const long rest = idx / NG;
-    const int kvh = (int)(rest % a.n_kv_heads);
-    const long lt = rest / a.n_kv_heads;
-    const int tok = (int)(lt % a.n_tokens);
-    const int li = (int)(lt / a.n_tokens);
+    int kvh, tok, li;
+    long lt;
+    if (a.app32) {
+      const uint32_t rest = (uint32_t)idx / NG;
+      const uint32_t lt32 = fdiv(rest, a.fd_app_kvh);
+      const uint32_t li32 = fdiv(lt32, a.fd_app_tok);
+      kvh = (int)(rest - lt32 * (uint32_t)a.n_kv_heads);
+      tok = (int)(lt32 - li32 * (uint32_t)a.n_tokens);
+      li = (int)li32;
+      lt = lt32;
+    } else {
+      const long rest = idx / NG;
+      kvh = (int)(rest % a.n_kv_heads);
+      lt = rest / a.n_kv_heads;
+      tok = (int)(lt % a.n_tokens);
+      li = (int)(lt / a.n_tokens);
+    }
     const int pos = a.start_pos + tok;
     const float* kin = a.k + (size_t)lt * kv_dim + (size_t)kvh * D;
     const float* vin = a.v + (size_t)lt * kv_dim + (size_t)kvh * D;
@@ -928,6 +943,9 @@ static int attn_prefill_impl(int n_layers, int n_heads, int n_kv_heads, int head
   a.score_scale = kLog2e / sqrtf((float)head_dim);
 
   const long groups = (long)n_launch_layers * n_tokens * n_kv_heads * (head_dim / 8);
+  a.app32 = groups < (1L << 31) ? 1 : 0;
+  a.fd_app_kvh = make_fastdiv((uint32_t)n_kv_heads);
+  a.fd_app_tok = make_fastdiv((uint32_t)n_tokens);
   long ab = (groups + 255) / 256;
   if (ab > 16384) ab = 16384;
   const unsigned grid = (unsigned)(a.xcd_slices * a.per_xcd);

@@ -193,6 +193,10 @@ struct PrefillArgs {
   const float* kn;
   float norm_eps;
   float score_scale;       // log2(e) / sqrt(D)
+  // the append's item decomposition: division by n_kv_heads and n_tokens
+  // (items fit 32 bits when app32 is set)
+  int app32;
+  FastDiv fd_app_kvh, fd_app_tok;
 };
 
 }  // namespace plh
