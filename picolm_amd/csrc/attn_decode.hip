@@ -669,12 +669,14 @@ __global__ __launch_bounds__(kCombineThreads) void attn_decode_combine_kernel(De
 // LDS as the split kernel does, and then either write the output (the only
 // producer of the group) or store a partial and count themselves in.  The
 // last producer of a group to arrive merges its partials and writes the
-// output, so one launch does everything.  The partials cross XCDs, whose L2
-// caches are not coherent with each other: they are stored and loaded with
-// device-scope cache policy (sc1: written through, read past the L2), the
-// stores complete before the arrival counter is bumped, and the counter is a
-// device-scope atomic; the merging workgroup resets it to zero for the next
-// launch.
+// output, so one launch does everything.  Partials that cross XCDs, whose L2
+// caches are not coherent with each other, are stored and loaded with
+// device-scope cache policy (sc1: written through, read past the L2); when
+// every producer of a group runs on one XCD (sk_wx > 0 places the ranges so,
+// see the launch) they go through that XCD's L2 instead (sc0: past the CU's
+// L1 only).  Either way the stores complete before the arrival counter is
+// bumped, the counter is an atomic at device scope, and the merging
+// workgroup resets it to zero for the next launch.
 
 // The T blocks are cut into W ranges of q or q + 1 blocks (q = T / W,
 // r = T % W: the first r ranges take q + 1): range w starts at w*q + min(w,
