@@ -95,10 +95,10 @@ int decode_scratch_setup(int device);
 // Makes sure the workspace holds at least `bytes` (the outgrown one is
 // retired until plh_shutdown).  Returns 0 or -1.
 int ensure_workspace(size_t bytes);
-// Capacity of Context::decode_ctr and of the static scratch's counter region.
-// The stream-K kernel's device-scope counters take the lower half (the most
-// (layer, kv head, q-head block) groups one stream-K launch may cover), its
-// XCD-local counters the upper half.
+// Capacity of Context::decode_ctr and of the static scratch's counter region,
+// in counters; the stream-K kernel keeps one per 32 (a 128-byte line), so a
+// launch of at most kDecodeCounters / 32 (layer, kv head, q-head block)
+// groups runs it.
 constexpr int kDecodeCounters = 1 << 18;
 
 // Attention of the head dims without a tuned kernel (every even head_dim up
@@ -153,11 +153,9 @@ struct DecodeArgs {
   int G;
   FastDiv fd_split, fd_hblk, fd_kvh;  // n_split, n_hblk, n_kv_heads
   FastDiv fd_nbk, fd_q, fd_q1;         // sk_nbk, sk_q, sk_q + 1
-  // stream-K ranges per XCD (0: ranges in workgroup order), its division,
-  // and the arrival counters of groups merged inside one XCD's L2
+  // stream-K ranges per XCD (0: ranges in workgroup order) and its division
   int sk_wx;
   FastDiv fd_wx;
-  unsigned* sk_ctr_local;
 };
 
 }  // namespace plh
