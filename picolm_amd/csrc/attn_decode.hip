@@ -764,7 +764,8 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
                "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps), "s"(a.G),
                "s"(a.fd_hblk.m), "s"(a.fd_hblk.sh), "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh),
                "s"(a.fd_nbk.m), "s"(a.fd_nbk.sh), "s"(a.fd_q.m), "s"(a.fd_q.sh),
-               "s"(a.fd_q1.m), "s"(a.fd_q1.sh), "s"(a.sk_wx), "s"(a.fd_wx.m), "s"(a.fd_wx.sh));
+               "s"(a.fd_q1.m), "s"(a.fd_q1.sh), "s"(a.sk_wx), "s"(a.fd_wx.m), "s"(a.fd_wx.sh),
+               "s"(a.sk_k), "s"(a.sk_kshift));
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -774,7 +775,16 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
   // most groups' producers share one L2
   const int w = a.sk_wx ? (int)(blockIdx.x & 7) * a.sk_wx + (int)(blockIdx.x >> 3)
                         : (int)blockIdx.x;
-  const int b0 = sk_start(w, a.sk_q, a.sk_r), b1 = sk_start(w + 1, a.sk_q, a.sk_r);
+  int b0, b1;
+  if (a.sk_k) {
+    // range j of group g: blocks [j * nbk / k, (j + 1) * nbk / k) of the group
+    const int g = w >> a.sk_kshift, j = w & (a.sk_k - 1);
+    b0 = g * a.sk_nbk + ((j * a.sk_nbk) >> a.sk_kshift);
+    b1 = g * a.sk_nbk + (((j + 1) * a.sk_nbk) >> a.sk_kshift);
+  } else {
+    b0 = sk_start(w, a.sk_q, a.sk_r);
+    b1 = sk_start(w + 1, a.sk_q, a.sk_r);
+  }
   const int G = a.G;
   const int kv_dim = a.n_kv_heads * D;
   const int pos = a.pos;
@@ -863,8 +873,8 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
     __syncthreads();
 
     // producers of this group: the workgroups owning its first and last block
-    const int p0 = sk_owner(gb, a);
-    const int np = sk_owner(gb + a.sk_nbk - 1, a) - p0 + 1;
+    const int p0 = a.sk_k ? group << a.sk_kshift : sk_owner(gb, a);
+    const int np = a.sk_k ? a.sk_k : sk_owner(gb + a.sk_nbk - 1, a) - p0 + 1;
     // all producers on one XCD: partials and the count stay in its L2
     const bool local = a.sk_wx && fdiv(p0, a.fd_wx) == fdiv(p0 + np - 1, a.fd_wx);
 
@@ -1105,8 +1115,8 @@ extern "C" int plh_set_tuning(int key, int value) {
 // W = k * n_groups, so each workgroup streams 1/k of one group and a
 // group's k producers sit on one XCD (merged through its L2), with k the
 // smallest power of two that gives about 0.6 workgroups per CU or more and
-// at most 384 KB of K and V rows per workgroup (W at most 4 per CU, else
-// the general plan).  Measured on MI355X, all-layer TinyLlama launches (88
+// at most 384 KB of K and V rows per workgroup (W at most 4 per CU and at
+// least 8 blocks a range, else the general plan).  Measured on MI355X, all-layer TinyLlama launches (88
 // groups): pos 512 / 600 / 1024 / 2047 took 8.2 / 8.7 / 10.0 / 15.6 us with
 // k = 2 against 12.0 / 11.9 / 13.4 / 16.4 us for the general plan;
 // Llama-3.2 (128 groups) pos 4095 / 8191 33.2 / 56.1 us with k = 4 / 8
@@ -1115,15 +1125,39 @@ extern "C" int plh_set_tuning(int key, int value) {
 // blocks (one 32-row tile per wave): head_dim 128 launches gain nothing
 // from the aligned plan (Qwen3 pos 2047: 50.1-51.3 us with k = 1 and
 // 52.9-59.8 us with k = 2 or 4, against 51.5 us).
-static long sk_plan_workgroups(int head_dim, int n_groups, int nbk, int num_cus, int device) {
+//
+// Launches whose groups do not split evenly over the XCDs (one TinyLlama
+// layer: 4 groups) take an aligned plan too, merged device-wide: k at most 8
+// ranges a group (one round of partial loads) of at least 8 blocks each,
+// the fewest that give ~0.6 workgroups per CU, else the most allowed.  One
+// TinyLlama layer at pos 700 / 1024 / 2047: 168 / 163 / 179 us per token
+// with k = 4 / 8 / 8, against 243 / 162 / 184 us for the general plan.
+//
+// Aligned plans give every group its own k ranges (*k_out = k); the
+// general plan cuts the flattened blocks (*k_out = 0).
+static long sk_plan_workgroups(int head_dim, int n_groups, int nbk, int num_cus, int device,
+                               int* k_out) {
   const long T = (long)n_groups * nbk;
   const long cus = num_cus > 0 ? num_cus : 256;
+  *k_out = 0;
   if (g_sk_workgroups > 0) return g_sk_workgroups;
   if (head_dim == 64 && n_groups % 8 == 0 && g_sk_xcd_local >= 0 && g_xcd_ok[device] == 1) {
     const double bytes = (double)T * 16 * 64 * 2 * 2;  // K and V rows the launch reads
-    for (long k = 1; k <= nbk && k * n_groups <= 4 * cus; k *= 2)
-      if (k * n_groups * 10 >= 6 * cus && bytes / (double)(k * n_groups) <= 384.0 * 1024)
+    for (long k = 1; k <= nbk / 8 && k * n_groups <= 4 * cus; k *= 2)
+      if (k * n_groups * 10 >= 6 * cus && bytes / (double)(k * n_groups) <= 384.0 * 1024) {
+        *k_out = (int)k;
         return k * n_groups;
+      }
+  }
+  if (head_dim == 64 && n_groups % 8 != 0) {
+    int cap = 0;
+    for (int k = 2; k <= 8 && nbk / k >= 8; k *= 2) cap = k;
+    if (cap >= 2) {
+      int k = 2;
+      while (k < cap && (long)k * n_groups * 10 < 6 * cus) k *= 2;
+      *k_out = k;
+      return (long)k * n_groups;
+    }
   }
   long W = T / 8;
   if (W > cus) W = cus;
@@ -1164,12 +1198,14 @@ static int attn_decode_sk_launch(int n_heads, int n_kv_heads, int head_dim, int 
     return -1;
   }
   const int cus = c.num_cus > 0 ? c.num_cus : 256;
-  long W = sk_plan_workgroups(head_dim, n_groups, nbk, cus, c.device);
+  int k_aligned = 0;
+  long W = sk_plan_workgroups(head_dim, n_groups, nbk, cus, c.device, &k_aligned);
   if (W > T) W = T;
   if (W < 1) W = 1;
   // producers per group (the partial slots it needs)
-  int maxp = 1;
-  {
+  int maxp = k_aligned;
+  if (!k_aligned) {
+    maxp = 1;
     const long qq = T / W, rr = T % W, big = rr * (qq + 1);
     auto owner_of = [&](long t) { return t < big ? t / (qq + 1) : rr + (t - big) / qq; };
     for (int g = 0; g < n_groups; ++g) {
@@ -1255,6 +1291,9 @@ static int attn_decode_sk_launch(int n_heads, int n_kv_heads, int head_dim, int 
                          W % 8 == 0 && W >= 16;
   a.sk_wx = xcd_local ? (int)(W / 8) : 0;
   a.fd_wx = make_fastdiv((uint32_t)(xcd_local ? W / 8 : 1));
+  a.sk_k = k_aligned;
+  a.sk_kshift = 0;
+  while ((1 << a.sk_kshift) < k_aligned) ++a.sk_kshift;
   a.sk_maxp = maxp;
   a.sk_groups = n_groups;
   a.sk_part = part;

@@ -156,6 +156,10 @@ struct DecodeArgs {
   // stream-K ranges per XCD (0: ranges in workgroup order) and its division
   int sk_wx;
   FastDiv fd_wx;
+  // sk_k > 0: W = sk_k * n_groups ranges, sk_k (a power of two, 1 << sk_kshift,
+  // at most sk_nbk) to a group, each group's blocks split evenly among its own
+  // (else the flattened blocks cut into W ranges)
+  int sk_k, sk_kshift;
 };
 
 }  // namespace plh

@@ -302,6 +302,25 @@ def test_decode_xcd_local_merges(gpu, oracle_mod, shape):
     assert np.array_equal(outs[1].view(np.uint32), outs[-1].view(np.uint32))
 
 
+@pytest.mark.parametrize("shape", [
+    ((1, 32, 4, 64, 2048, 1e4, 0), 530),    # one TinyLlama layer: 4 ranges a group, uneven
+    ((1, 32, 4, 64, 2048, 1e4, 0), 700),    # 4 ranges of 11 blocks
+    ((1, 32, 4, 64, 2048, 1e4, 0), 2047),   # 8 ranges of 16 blocks
+    ((1, 24, 3, 64, 1024, 1e4, 0), 1000),   # 3 groups, 4 ranges of 15-16 blocks
+    ((22, 32, 4, 64, 1024, 1e4, 0), 1000),  # 88 groups: the XCD-local aligned plan, uneven
+], ids=["tl-530", "tl-700", "tl-2047", "3groups", "88groups"])
+def test_decode_aligned_plans(gpu, oracle_mod, shape):
+    """The default stream-K plans that give every group its own ranges
+    (including group block counts the ranges do not divide evenly): oracle-
+    exact outputs and caches."""
+    dims, pos = shape
+    try:
+        gpu.check(gpu.lib.plh_set_tuning(7, 2), "tuning")
+        run_decode(gpu, oracle_mod, gpu.AttnConfig(*dims), pos, seed=pos + dims[2])
+    finally:
+        gpu.lib.plh_set_tuning(7, 0)
+
+
 @pytest.mark.parametrize("min_split", [128, 512, 1024, 2048])
 def test_decode_split_lengths(gpu, oracle_mod, min_split):
     """The split + combine kernels (plh_set_tuning key 7 = 1) under several
