@@ -350,7 +350,10 @@ int plh_forward_prefill(const plh_model *m, const int *tokens, int n_tokens, int
  * faster fixed-point-digit order (0, default: within ~1e-7 of sum |w x| per
  * output; the batched prompt GEMVs always keep the exact order); key 11:
  * stream-K groups whose producers share an XCD merge through its L2 (0 by
- * shape, 1 wherever the plan allows, -1 never: every merge device-wide). */
+ * shape, 1 wherever the plan allows, -1 never: every merge device-wide);
+ * key 14: the split decode kernel's partials are merged by each group's last
+ * split inside the launch (0, default, where its splits share an XCD) or by
+ * a combine launch (-1). */
 int plh_set_tuning(int key, int value);
 
 #ifdef __cplusplus

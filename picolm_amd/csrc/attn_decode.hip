@@ -94,6 +94,15 @@ struct DecodeShape<128> {
   static constexpr int W = 4, PF = 1;
 };
 constexpr int kCombineChunk = 16;  // most split partials loaded together by the combine
+constexpr int kSplitLocal = 1;     // buffer cache policy sc0: past the CU's L1, from the L2
+constexpr int kSplitCtrPitch = 32; // in-kernel split merge: one counter per 128-byte line
+
+// A buffer over one of the split partial arrays: n_units * nhm * per floats
+// (under 2 GiB: the launch checks).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t split_rsrc(float* base, const DecodeArgs& a,
+                                                             int per) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, 0, a.n_units * a.nhm * per * 4, 0x00020000);
+}
 
 template <int D>
 struct Tile {
@@ -453,6 +462,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
   constexpr int kSmemBytes =
       (kVtileHalves * 2 > kCombFloats * 4) ? kVtileHalves * 2 : kCombFloats * 4;
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
+  __shared__ int s_merge;
 
   PLH_ARGS_NOW("s"(a.q), "s"(a.k), "s"(a.v), "s"(a.kc), "s"(a.vc), "s"(a.cos_t), "s"(a.sin_t),
                "s"(a.out), "s"(a.part_o), "s"(a.part_m), "s"(a.part_l), "s"(a.layer0),
@@ -461,7 +471,7 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
                "s"(a.n_units), "s"(a.per_xcd), "s"(a.score_scale), "s"(a.k_rows),
                "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps), "s"(a.G),
                "s"(a.fd_split.m), "s"(a.fd_split.sh), "s"(a.fd_hblk.m), "s"(a.fd_hblk.sh),
-               "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh));
+               "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh), "s"(a.split_merge), "s"(a.split_ctr));
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -590,6 +600,18 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
     }
     if (a.n_split == 1) {
       out_base[(size_t)h * D + d] = O * (1.0f / L);
+    } else if (a.split_merge) {
+      // sc0 stores: in the L2 (the merging split's) when they complete; the
+      // 32-bit buffer builtins move raw bits
+      const int u = unit * a.nhm + h;
+      __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(O), split_rsrc(a.part_o, a, D),
+                                            (u * D + d) * 4, 0, kSplitLocal);
+      if (d == 0) {
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(M), split_rsrc(a.part_m, a, 1),
+                                              u * 4, 0, kSplitLocal);
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(L), split_rsrc(a.part_l, a, 1),
+                                              u * 4, 0, kSplitLocal);
+      }
     } else {
       a.part_o[((size_t)unit * a.nhm + h) * D + d] = O;
       if (d == 0) {
@@ -597,6 +619,57 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
         a.part_l[(size_t)unit * a.nhm + h] = L;
       }
     }
+  }
+  if (a.n_split == 1 || !a.split_merge) return;
+
+  // ---- the group's last split merges (its splits share this XCD's L2) -----
+  // The partials' sc0 stores complete in the L2 before the count goes up;
+  // the merger reads them with sc0 (past its L1) and resets the count for
+  // the next launch.
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  unsigned* ctr = a.split_ctr + group * kSplitCtrPitch;
+  if (tid == 0)
+    s_merge = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+              (unsigned)(a.n_split - 1);
+  __syncthreads();
+  if (!s_merge) return;
+  if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  const int u0 = group * a.n_split;
+  const __amdgpu_buffer_rsrc_t ro = split_rsrc(a.part_o, a, D);
+  const __amdgpu_buffer_rsrc_t rm = split_rsrc(a.part_m, a, 1);
+  const __amdgpu_buffer_rsrc_t rl = split_rsrc(a.part_l, a, 1);
+  for (int idx = tid; idx < nh * D; idx += kThreads) {
+    const int h = idx / D, d = idx - (idx / D) * D;
+    float M = kNegBig, L = 0.f, O = 0.f;
+    for (int s0 = 0; s0 < a.n_split; s0 += 8) {
+      float mi[8], li[8], oi[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int u = (u0 + min(s0 + j, a.n_split - 1)) * a.nhm + h;
+        mi[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rm, u * 4, 0, kSplitLocal));
+        li[j] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(rl, u * 4, 0, kSplitLocal));
+        oi[j] = __uint_as_float(
+            __builtin_amdgcn_raw_buffer_load_b32(ro, (u * D + d) * 4, 0, kSplitLocal));
+      }
+      float Mc = M;
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (s0 + j < a.n_split) Mc = fmaxf(Mc, mi[j]);
+      const float r = fast_exp2(M - Mc);
+      L *= r;
+      O *= r;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        if (s0 + j < a.n_split) {
+          const float w = fast_exp2(mi[j] - Mc);
+          L = __builtin_fmaf(li[j], w, L);
+          O = __builtin_fmaf(oi[j], w, O);
+        }
+      }
+      M = Mc;
+    }
+    out_base[(size_t)h * D + d] = O * (1.0f / L);
   }
 }
 
@@ -956,6 +1029,7 @@ int g_decode_kernel = 0;  // plh_set_tuning key 7: 0 by shape, 1 split + combine
 int g_sk_workgroups = 0;  // key 8: stream-K workgroups (0: the launch's own choice)
 int g_sk_pf = 0;          // key 9: stream-K tiles in flight per wave (0: by head_dim)
 int g_sk_xcd_local = 0;   // key 11: XCD-local stream-K merges (0 by shape, 1 always, -1 never)
+int g_split_merge = 0;    // key 14: the split kernel merges in the launch (0) or a combine launch (-1)
 // per device: 1 when workgroup ids congruent mod 8 ran on one XCD at
 // plh_init, -1 when they did not, 0 before the check
 int g_xcd_ok[kMaxDevices] = {};
@@ -1079,6 +1153,14 @@ extern "C" int plh_set_tuning(int key, int value) {
       return -1;
     }
     g_gemv_exact = value;
+    return 0;
+  }
+  if (key == 14) {
+    if (value != 0 && value != -1) {
+      set_error("plh_set_tuning: split merge must be 0 (in the launch) or -1 (combine launch)");
+      return -1;
+    }
+    g_split_merge = value;
     return 0;
   }
   if (key == 11) {
@@ -1460,6 +1542,13 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
   a.score_scale = kLog2e / sqrtf((float)head_dim);
   a.k_rows = k_rows;
   a.v_rows = v_rows;
+  // The group's last split merges in the launch when its splits share an
+  // XCD (plh_init's check of the workgroup-to-XCD deal) and the counters fit
+  // (tuning key 14 = -1: a combine launch instead).
+  a.split_merge = n_split > 1 && g_split_merge >= 0 && g_xcd_ok[c.device] == 1 &&
+                  (long)n_groups * kSplitCtrPitch <= kDecodeCounters &&
+                  (size_t)n_units * nhm * head_dim * sizeof(float) < (1u << 31);
+  a.split_ctr = noalloc ? (unsigned*)g_scratch_ptr[c.device] : c.decode_ctr;
 
   const dim3 grid((unsigned)(8 * per_xcd)), cblock(kCombineThreads);
   const dim3 b64(64 * DecodeShape<64>::W), b128(64 * DecodeShape<128>::W);
@@ -1472,7 +1561,7 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
   else
     hipLaunchKernelGGL((attn_decode_kernel<128, true>), grid, b128, 0, c.stream, a);
   if (check_hip(hipGetLastError(), "attn_decode_kernel")) return -1;
-  if (n_split == 1) return 0;
+  if (n_split == 1 || a.split_merge) return 0;
   // one thread per (q head of the block, d): no workgroup without work
   const int nh_max = G < 16 ? G : 16;
   const dim3 cgrid64((unsigned)(8 * groups_per_xcd),

@@ -153,6 +153,10 @@ struct DecodeArgs {
   int G;
   FastDiv fd_split, fd_hblk, fd_kvh;  // n_split, n_hblk, n_kv_heads
   FastDiv fd_nbk, fd_q, fd_q1;         // sk_nbk, sk_q, sk_q + 1
+  // split kernel: a group's last split to finish merges the partials itself
+  // (through its XCD's L2, counting on split_ctr) instead of a combine launch
+  int split_merge;
+  unsigned* split_ctr;
   // stream-K ranges per XCD (0: ranges in workgroup order) and its division
   int sk_wx;
   FastDiv fd_wx;

@@ -321,19 +321,23 @@ def test_decode_aligned_plans(gpu, oracle_mod, shape):
         gpu.lib.plh_set_tuning(7, 0)
 
 
+@pytest.mark.parametrize("merge", [0, -1], ids=["in-launch", "combine"])
 @pytest.mark.parametrize("min_split", [128, 512, 1024, 2048])
-def test_decode_split_lengths(gpu, oracle_mod, min_split):
-    """The split + combine kernels (plh_set_tuning key 7 = 1) under several
-    split plans (one split, no combine launch, included) give oracle-exact
-    results."""
+def test_decode_split_lengths(gpu, oracle_mod, min_split, merge):
+    """The split kernel (plh_set_tuning key 7 = 1) under several split plans
+    (one split included), its partials merged by the group's last split in
+    the launch (key 14 = 0) or by the combine launch (key 14 = -1): oracle-
+    exact results."""
     try:
         gpu.check(gpu.lib.plh_set_tuning(7, 1), "tuning")
         gpu.check(gpu.lib.plh_set_tuning(2, min_split), "tuning")
+        gpu.check(gpu.lib.plh_set_tuning(14, merge), "tuning")
         cfg = gpu.AttnConfig(4, 32, 4, 64, 2048, 1e4, 0)
         for pos in (2047, 700, 129):
             run_decode(gpu, oracle_mod, cfg, pos, seed=pos + min_split, check_layers=[0, 3])
         cfg = gpu.AttnConfig(2, 32, 32, 128, 1024, 1e4, 0)
         run_decode(gpu, oracle_mod, cfg, 1000, seed=5 + min_split)
     finally:
+        gpu.lib.plh_set_tuning(14, 0)
         gpu.lib.plh_set_tuning(2, 0)
         gpu.lib.plh_set_tuning(7, 0)
