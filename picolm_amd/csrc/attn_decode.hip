@@ -472,6 +472,8 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
                "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps), "s"(a.G),
                "s"(a.fd_split.m), "s"(a.fd_split.sh), "s"(a.fd_hblk.m), "s"(a.fd_hblk.sh),
                "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh), "s"(a.split_merge), "s"(a.split_ctr));
+  static_assert(kSmemBytes >= kPfLdsBytes, "prefetch workgroups use the kernel's LDS");
+  if (l2_prefetch_role(a.pf, a.n_main, kWaves, smem)) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -828,6 +830,8 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
   __shared__ float s_knew[D], s_vnew[D], s_mnew[16];
   __shared__ int s_last;
+  static_assert(kSmemBytes >= kPfLdsBytes, "prefetch workgroups use the kernel's LDS");
+  if (l2_prefetch_role(a.pf, a.n_main, kWaves, smem)) return;
 
   PLH_ARGS_NOW("s"(a.q), "s"(a.k), "s"(a.v), "s"(a.kc), "s"(a.vc), "s"(a.cos_t), "s"(a.sin_t),
                "s"(a.out), "s"(a.layer0), "s"(a.n_heads), "s"(a.n_kv_heads),
@@ -1030,9 +1034,6 @@ int g_sk_workgroups = 0;  // key 8: stream-K workgroups (0: the launch's own cho
 int g_sk_pf = 0;          // key 9: stream-K tiles in flight per wave (0: by head_dim)
 int g_sk_xcd_local = 0;   // key 11: XCD-local stream-K merges (0 by shape, 1 always, -1 never)
 int g_split_merge = 0;    // key 14: the split kernel merges in the launch (0) or a combine launch (-1)
-// per device: 1 when workgroup ids congruent mod 8 ran on one XCD at
-// plh_init, -1 when they did not, 0 before the check
-int g_xcd_ok[kMaxDevices] = {};
 
 // Each workgroup's XCD (the hardware XCC_ID register) by workgroup id.
 constexpr int kXcdProbeGroups = 2048;
@@ -1045,6 +1046,13 @@ __global__ __launch_bounds__(64) void xcd_probe_kernel(unsigned* out) {
 }  // namespace
 
 namespace plh {
+// key 15: the forward's attention launches prefetch the o-projection's and
+// the gate/up pair's weights, and the down projection's unless the launch is
+// an unsplit one (0); all three always (1); never the down projection's (2);
+// none (-1)
+int g_fwd_prefetch = 0;
+int g_xcd_ok[kMaxDevices] = {};
+
 int decode_scratch_setup(int device) {
   if (device < 0 || device >= kMaxDevices) {
     set_error("plh_init: device %d beyond the %d the static scratch table covers", device,
@@ -1161,6 +1169,14 @@ extern "C" int plh_set_tuning(int key, int value) {
       return -1;
     }
     g_split_merge = value;
+    return 0;
+  }
+  if (key == 15) {
+    if (value < -1 || value > 2) {
+      set_error("plh_set_tuning: forward weight prefetch must be 0, 1, 2 or -1 (off)");
+      return -1;
+    }
+    g_fwd_prefetch = value;
     return 0;
   }
   if (key == 11) {
@@ -1393,7 +1409,12 @@ static int attn_decode_sk_launch(int n_heads, int n_kv_heads, int head_dim, int 
   a.sk_part = part;
   a.sk_part_bytes = (uint32_t)part_bytes;
   a.sk_ctr = ctr;
-  const dim3 grid((unsigned)W), block(256);
+  // the forward pass's pending prefetch rides on this launch's spare CUs
+  a.n_main = (int)W;
+  a.pf = c.pf_next;
+  if (g_xcd_ok[c.device] != 1 || W > (c.num_cus > 0 ? c.num_cus : 256) / 4) a.pf.n = 0;
+  const int n_pf = a.pf.n > 0 ? 8 * kPfWorkgroupsPerXcd : 0;
+  const dim3 grid((unsigned)(W + n_pf)), block(256);
   const bool qkn = q_norm != nullptr;
   const int pf = g_sk_pf ? g_sk_pf : 2;
 #define PLH_SK(D, Q, PF) \
@@ -1549,8 +1570,16 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
                   (long)n_groups * kSplitCtrPitch <= kDecodeCounters &&
                   (size_t)n_units * nhm * head_dim * sizeof(float) < (1u << 31);
   a.split_ctr = noalloc ? (unsigned*)g_scratch_ptr[c.device] : c.decode_ctr;
+  // the forward pass's pending prefetch rides on this launch's spare CUs
+  a.n_main = 8 * per_xcd;
+  a.pf = c.pf_next;
+  if (n_split == 1) a.pf.n = a.pf.n_short;
+  // only a launch that leaves most CUs idle takes them
+  if (g_xcd_ok[c.device] != 1 || 8 * per_xcd > (c.num_cus > 0 ? c.num_cus : 256) / 4)
+    a.pf.n = 0;
+  const int n_pf = a.pf.n > 0 ? 8 * kPfWorkgroupsPerXcd : 0;
 
-  const dim3 grid((unsigned)(8 * per_xcd)), cblock(kCombineThreads);
+  const dim3 grid((unsigned)(8 * per_xcd + n_pf)), cblock(kCombineThreads);
   const dim3 b64(64 * DecodeShape<64>::W), b128(64 * DecodeShape<128>::W);
   if (head_dim == 64 && !qkn)
     hipLaunchKernelGGL((attn_decode_kernel<64, false>), grid, b64, 0, c.stream, a);

@@ -1666,4 +1666,52 @@ int gemv_pair_launch(const GemvCall& gate, const GemvCall& up) {
   return launch_single(up.qtype, true, a, 2 * up.d);
 }
 
+// Appends the plane streams of one matrix, read wg_rows rows per workgroup
+// by workgroups wg0, wg0 + 1, ...; planes whose chunks are not whole 16-byte
+// units are left out.
+static int prefetch_matrix(int qtype, int n, int d, const void* w, int wg_rows, int wg0,
+                           PfPlan& pf) {
+  Layout L;
+  if (!w || !make_layout(qtype, n, d, L)) return -1;
+  // per-row bytes of each plane (the packed layouts of make_layout)
+  const size_t nb = (size_t)L.nb;
+  size_t off[5], bpr[5];
+  int np = 0;
+  if (qtype == kTypeQ4K) {
+    off[0] = L.off[0], bpr[0] = nb * 16;
+    off[1] = L.off[1], bpr[1] = nb * 64;
+    off[2] = L.off[2], bpr[2] = nb * 64;
+    np = 3;
+  } else if (qtype == kTypeQ6K) {
+    for (int p = 0; p < 3; ++p) off[p] = L.off[p], bpr[p] = nb * 64;
+    off[3] = L.scales_off, bpr[3] = nb * 16;
+    off[4] = L.d_off, bpr[4] = nb * 2;
+    np = 5;
+  } else {
+    off[0] = L.off[0], bpr[0] = nb * 16;
+    off[1] = L.off[1], bpr[1] = nb * 16;
+    off[2] = L.d_off, bpr[2] = nb * 2;
+    np = 3;
+  }
+  if (pf.n + np > kPfStreams) return -1;
+  for (int p = 0; p < np; ++p)
+    if (make_pf_stream((const uint8_t*)w + off[p], bpr[p] * (size_t)wg_rows, bpr[p] * (size_t)d,
+                       wg0, pf.s[pf.n]))
+      ++pf.n;
+  return 0;
+}
+
+int gemv_prefetch_plan(const GemvCall& g, const GemvCall* up, PfPlan& pf) {
+  GemvArgs a;
+  if (g.n_tok > 1 || prepare(g, a)) return -1;
+  // the rows per workgroup launch_single picks for this call
+  const bool pair = up != nullptr;
+  const int rows = pair ? 2 * g.d : g.d;
+  const int rb = pick_rb(&a, &rows, 1, pair, 8);
+  if (rb < 0) return -1;
+  const int wg_rows = pair ? a.row_par * rb / 2 : a.row_par * rb;  // matrix rows
+  if (prefetch_matrix(g.qtype, g.n, g.d, g.w, wg_rows, 0, pf)) return -1;
+  return pair ? prefetch_matrix(up->qtype, up->n, up->d, up->w, wg_rows, 0, pf) : 0;
+}
+
 }  // namespace plh

@@ -6,6 +6,7 @@
 #include <stdint.h>
 
 #include "fastdiv.h"
+#include "l2_prefetch.h"
 
 namespace plh {
 
@@ -29,6 +30,9 @@ struct Context {
   // needed; both workspaces grow by 1.5x, so it stays short).
   void** retired = nullptr;
   int n_retired = 0, cap_retired = 0;
+  // Operands the next decode launch warms the L2 with (set by the forward
+  // pass around its attention launches; n = 0 otherwise).
+  PfPlan pf_next{};
 };
 
 // Replaces the buffer *p of *bytes bytes by a new one of `want` bytes (the
@@ -60,6 +64,15 @@ extern int g_fwd_norm_separate;
 // normalised x share 64 KiB of LDS).
 constexpr int kGemvNormMax = 7680;
 
+// plh_set_tuning key 15: the forward pass's attention launches warm the L2
+// with the o-projection's and gate/up pair's weights, and the down
+// projection's unless the launch is an unsplit one (0); with all three (1);
+// never the down projection's (2); not at all (-1).
+extern int g_fwd_prefetch;
+// per device: 1 when workgroup c of a launch runs on XCD c % 8 (checked at
+// plh_init), -1 when not, 0 before the check
+extern int g_xcd_ok[64];
+
 // One weight GEMV with the forward pass's prologue and epilogues (the
 // arguments of plh_gemv_ex).
 struct GemvCall {
@@ -87,6 +100,10 @@ int gemv_multi_launch(const GemvCall* g, int n);
 // the same type and shape and the same rmsnorm prologue (or none); out =
 // up.out.
 int gemv_pair_launch(const GemvCall& gate, const GemvCall& up);
+// Appends to pf the weight streams a later gemv_launch(g) (up == null) or
+// gemv_pair_launch(g, *up) reads, chunked as its workgroups read them; -1
+// (pf unchanged) when the call is not a single-vector GEMV or pf is full.
+int gemv_prefetch_plan(const GemvCall& g, const GemvCall* up, PfPlan& pf);
 
 // Looks up (once per device, with that device current) the device address of
 // the decode kernels' static scratch array; plh_init calls it.  0 or -1.
@@ -164,6 +181,10 @@ struct DecodeArgs {
   // at most sk_nbk) to a group, each group's blocks split evenly among its own
   // (else the flattened blocks cut into W ranges)
   int sk_k, sk_kshift;
+  // Workgroups n_main .. of attn_decode_kernel's grid only prefetch pf
+  // (8 * kPfWorkgroupsPerXcd of them when pf.n > 0).
+  int n_main;
+  PfPlan pf;
 };
 
 }  // namespace plh

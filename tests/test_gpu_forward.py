@@ -369,6 +369,44 @@ def test_forward_rejects_bad_calls(gpu):
         dm.free()
 
 
+# gate and up of one type, so that they run (and are prefetched) as a pair
+PF_LLAMA = dict(LLAMA, n_layers=2, max_seq_len=2048, types=dict(LLAMA["types"], up=Q4K))
+PF_QWEN = dict(QWEN, max_seq_len=2048, types=dict(QWEN["types"], up=Q6K))
+
+
+@pytest.mark.parametrize("cfg", [PF_LLAMA, PF_QWEN], ids=["llama", "qwen"])
+def test_forward_weight_prefetch_changes_nothing(gpu, cfg):
+    """Tuning key 15: the attention launch's spare workgroups that load the
+    next GEMVs' weights into the L2 (every setting) leave every result
+    bit-identical to no prefetch: logits, residual and both caches, at a
+    short position (unsplit attention launch) and past 512 positions (split
+    or stream-K launch)."""
+    P = gpu
+    h = S.SynthModel(**cfg, seed=71)
+    dm = P.DeviceModel(h)
+    rng = np.random.default_rng(72)
+    fill = rng.standard_normal((2, h.cache_elems()), dtype=np.float32).astype(np.float16)
+    kc, vc = fill[0].view(np.uint16), fill[1].view(np.uint16)
+    try:
+        for pos in (100, 1500, 2047):
+            ref = None
+            for key in (-1, 0, 1, 2):
+                P.check(P.lib.plh_set_tuning(15, key), "plh_set_tuning")
+                dm.load_cache(kc, vc)
+                print(f"[case] forward prefetch setting {key} pos {pos}", flush=True)
+                dm.forward(7, pos)
+                P.synchronize()
+                got = (bits(dm.fetch_logits()), bits(dm.fetch_x())) + tuple(dm.fetch_cache())
+                if ref is None:
+                    ref = got
+                    continue
+                for a, b in zip(ref, got):
+                    assert np.array_equal(a, b), (pos, key)
+    finally:
+        P.check(P.lib.plh_set_tuning(15, 0), "plh_set_tuning")
+        dm.free()
+
+
 @pytest.mark.parametrize("cfg", [dict(LLAMA, n_layers=2, max_seq_len=2048),
                                  dict(QWEN, max_seq_len=2048)], ids=["llama", "qwen"])
 def test_forward_long_context_split_decode(gpu, oracle_mod, cfg):
