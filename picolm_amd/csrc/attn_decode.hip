@@ -471,7 +471,8 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
                "s"(a.n_units), "s"(a.per_xcd), "s"(a.score_scale), "s"(a.k_rows),
                "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps), "s"(a.G),
                "s"(a.fd_split.m), "s"(a.fd_split.sh), "s"(a.fd_hblk.m), "s"(a.fd_hblk.sh),
-               "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh), "s"(a.split_merge), "s"(a.split_ctr));
+               "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh), "s"(a.split_merge), "s"(a.split_ctr),
+               "s"(a.n_main));
   static_assert(kSmemBytes >= kPfLdsBytes, "prefetch workgroups use the kernel's LDS");
   if (l2_prefetch_role(a.pf, a.n_main, kWaves, smem)) return;
   const int tid = threadIdx.x;
@@ -830,8 +831,6 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
   __shared__ float s_knew[D], s_vnew[D], s_mnew[16];
   __shared__ int s_last;
-  static_assert(kSmemBytes >= kPfLdsBytes, "prefetch workgroups use the kernel's LDS");
-  if (l2_prefetch_role(a.pf, a.n_main, kWaves, smem)) return;
 
   PLH_ARGS_NOW("s"(a.q), "s"(a.k), "s"(a.v), "s"(a.kc), "s"(a.vc), "s"(a.cos_t), "s"(a.sin_t),
                "s"(a.out), "s"(a.layer0), "s"(a.n_heads), "s"(a.n_kv_heads),
@@ -842,7 +841,10 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
                "s"(a.fd_hblk.m), "s"(a.fd_hblk.sh), "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh),
                "s"(a.fd_nbk.m), "s"(a.fd_nbk.sh), "s"(a.fd_q.m), "s"(a.fd_q.sh),
                "s"(a.fd_q1.m), "s"(a.fd_q1.sh), "s"(a.sk_wx), "s"(a.fd_wx.m), "s"(a.fd_wx.sh),
-               "s"(a.sk_k), "s"(a.sk_kshift));
+               "s"(a.sk_k), "s"(a.sk_kshift), "s"(a.n_main));
+  // (the prefetch split from the same batch of argument loads)
+  static_assert(kSmemBytes >= kPfLdsBytes, "prefetch workgroups use the kernel's LDS");
+  if (l2_prefetch_role(a.pf, a.n_main, kWaves, smem)) return;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
