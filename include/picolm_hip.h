@@ -354,11 +354,10 @@ int plh_forward_prefill(const plh_model *m, const int *tokens, int n_tokens, int
  * key 14: the split decode kernel's partials are merged by each group's last
  * split inside the launch (0, default, where its splits share an XCD) or by
  * a combine launch (-1); key 15: plh_forward's attention launches add
- * workgroups that load the weights of the layer's o-projection and gate/up
- * pair, and of its down projection unless the attention launch is an
- * unsplit one, into the L2 of the XCDs whose GEMV workgroups read them (0,
- * default), all three always (1), never the down projection's (2), or none
- * (-1); results are the same bits in every setting. */
+ * workgroups, one per CU they leave idle, that load the weights of the
+ * layer's o-projection, gate/up pair and down projection into the L2 of the
+ * XCDs whose GEMV workgroups read them (0, default), of the first two only
+ * (1), or none (-1); results are the same bits in every setting. */
 int plh_set_tuning(int key, int value);
 
 #ifdef __cplusplus

@@ -1048,10 +1048,9 @@ __global__ __launch_bounds__(64) void xcd_probe_kernel(unsigned* out) {
 }  // namespace
 
 namespace plh {
-// key 15: the forward's attention launches prefetch the o-projection's and
-// the gate/up pair's weights, and the down projection's unless the launch is
-// an unsplit one (0); all three always (1); never the down projection's (2);
-// none (-1)
+// key 15: the forward's attention launches prefetch the o-projection's, the
+// gate/up pair's and the down projection's weights (0), the first two only
+// (1), or none (-1)
 int g_fwd_prefetch = 0;
 int g_xcd_ok[kMaxDevices] = {};
 
@@ -1174,8 +1173,8 @@ extern "C" int plh_set_tuning(int key, int value) {
     return 0;
   }
   if (key == 15) {
-    if (value < -1 || value > 2) {
-      set_error("plh_set_tuning: forward weight prefetch must be 0, 1, 2 or -1 (off)");
+    if (value < -1 || value > 1) {
+      set_error("plh_set_tuning: forward weight prefetch must be 0, 1 or -1 (off)");
       return -1;
     }
     g_fwd_prefetch = value;
@@ -1414,8 +1413,10 @@ static int attn_decode_sk_launch(int n_heads, int n_kv_heads, int head_dim, int 
   // the forward pass's pending prefetch rides on this launch's spare CUs
   a.n_main = (int)W;
   a.pf = c.pf_next;
-  if (g_xcd_ok[c.device] != 1 || W > (c.num_cus > 0 ? c.num_cus : 256) / 4) a.pf.n = 0;
-  const int n_pf = a.pf.n > 0 ? 8 * kPfWorkgroupsPerXcd : 0;
+  a.pf.per_xcd = pf_per_xcd(c.num_cus > 0 ? c.num_cus : 256, W);
+  if (g_xcd_ok[c.device] != 1 || W > (c.num_cus > 0 ? c.num_cus : 256) / 4 || a.pf.per_xcd == 0)
+    a.pf.n = 0;
+  const int n_pf = a.pf.n > 0 ? 8 * a.pf.per_xcd : 0;
   const dim3 grid((unsigned)(W + n_pf)), block(256);
   const bool qkn = q_norm != nullptr;
   const int pf = g_sk_pf ? g_sk_pf : 2;
@@ -1575,11 +1576,12 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
   // the forward pass's pending prefetch rides on this launch's spare CUs
   a.n_main = 8 * per_xcd;
   a.pf = c.pf_next;
-  if (n_split == 1) a.pf.n = a.pf.n_short;
-  // only a launch that leaves most CUs idle takes them
-  if (g_xcd_ok[c.device] != 1 || 8 * per_xcd > (c.num_cus > 0 ? c.num_cus : 256) / 4)
+  // only a launch that leaves most CUs idle takes them, one workgroup each
+  a.pf.per_xcd = pf_per_xcd(c.num_cus > 0 ? c.num_cus : 256, 8L * per_xcd);
+  if (g_xcd_ok[c.device] != 1 || 8 * per_xcd > (c.num_cus > 0 ? c.num_cus : 256) / 4 ||
+      a.pf.per_xcd == 0)
     a.pf.n = 0;
-  const int n_pf = a.pf.n > 0 ? 8 * kPfWorkgroupsPerXcd : 0;
+  const int n_pf = a.pf.n > 0 ? 8 * a.pf.per_xcd : 0;
 
   const dim3 grid((unsigned)(8 * per_xcd + n_pf)), cblock(kCombineThreads);
   const dim3 b64(64 * DecodeShape<64>::W), b128(64 * DecodeShape<128>::W);

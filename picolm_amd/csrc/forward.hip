@@ -329,11 +329,11 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, float
         call(L.k, E, KV, xin, a.k, nw, L.k_bias, 0, nullptr, nullptr),
         call(L.v, E, KV, xin, a.v, nw, L.v_bias, 0, nullptr, nullptr)};
     if (gemv_multi_launch(qkv, 3)) return -1;
-    // The attention launch leaves most CUs idle at short context: its spare
-    // workgroups bring the o-projection's and the gate/up pair's weights into
-    // the L2 of the XCDs whose GEMV workgroups will read them.
+    // The attention launch leaves most CUs idle: its spare workgroups bring
+    // the o-projection's, the gate/up pair's and the down projection's
+    // weights into the L2 of the XCDs whose GEMV workgroups will read them.
     PfPlan& pf = ctx().pf_next;
-    pf.n = pf.n_short = 0;
+    pf.n = 0;
     if (g_fwd_prefetch >= 0) {
       const float* ffn_nw = separate ? nullptr : L.ffn_norm;
       const float* ffn_x = separate ? a.xb : a.x;
@@ -342,13 +342,9 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, float
       const GemvCall u = call(L.up, E, F, ffn_x, a.hb, ffn_nw, nullptr, 0, nullptr, nullptr);
       gemv_prefetch_plan(o, nullptr, pf);
       if (L.gate.qtype == L.up.qtype) gemv_prefetch_plan(g, &u, pf);
-      // an unsplit attention launch (short context) ends before it could also
-      // bring in the down projection's weights; longer ones take them too
-      pf.n_short = pf.n;
-      if (g_fwd_prefetch != 2)
+      if (g_fwd_prefetch == 0)
         gemv_prefetch_plan(call(L.down, F, E, a.hb, a.x, nullptr, nullptr, 0, nullptr, a.x),
                            nullptr, pf);
-      if (g_fwd_prefetch == 1) pf.n_short = pf.n;
     }
     const int rc = L.q_norm ? plh_attn_decode_qknorm(m->n_layers, m->n_heads, m->n_kv_heads,
                                                      m->head_dim, m->max_seq_len, m->rope_type, l,
@@ -359,7 +355,7 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, float
                                               m->head_dim, m->max_seq_len, m->rope_type, l, 1,
                                               pos, a.q, a.k, a.v, m->key_cache, m->val_cache,
                                               m->rope_cos, m->rope_sin, a.att);
-    pf.n = pf.n_short = 0;
+    pf.n = 0;
     if (rc) return -1;
     // x = x + (Wo att + o_bias)
     if (gemv_launch(call(L.o, Q, E, a.att, a.x, nullptr, L.o_bias, !L.o_bias, nullptr, a.x)))

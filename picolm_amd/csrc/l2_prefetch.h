@@ -18,7 +18,7 @@
 namespace plh {
 
 constexpr int kPfStreams = 16;           // byte streams of one plan
-constexpr int kPfWorkgroupsPerXcd = 24;  // prefetch workgroups a launch adds per XCD
+constexpr int kPfMaxPerXcd = 31;         // prefetch workgroups a launch adds per XCD, at most
 constexpr int kPfUnit = 16;              // bytes per lane and load
 
 // The later launch's workgroup wg0 + c reads bytes [c * chunk, min((c + 1) *
@@ -32,9 +32,19 @@ struct PfStream {
 };
 struct PfPlan {
   int n;        // streams in use (0: no prefetch)
-  int n_short;  // the first streams, all a short launch takes (n_short <= n)
+  int per_xcd;  // prefetch workgroups per XCD (set by the launch)
   PfStream s[kPfStreams];
 };
+
+// Prefetch workgroups per XCD for a launch of n_main workgroups of its own:
+// the CUs it leaves idle, one workgroup each (a CU shared with the launch's
+// own workgroups slows them), at most kPfMaxPerXcd; 0 when fewer than 8
+// would be left.
+inline int pf_per_xcd(int num_cus, long n_main) {
+  const long free_cus = (long)num_cus - n_main;
+  const long per = free_cus / 8 < kPfMaxPerXcd ? free_cus / 8 : kPfMaxPerXcd;
+  return per >= 8 ? (int)per : 0;
+}
 
 // LDS a prefetch workgroup needs: 1 KB that the loads land in, then the
 // plan's stream descriptors.
@@ -52,7 +62,7 @@ inline bool make_pf_stream(const uint8_t* base, size_t chunk, size_t len, int wg
   return true;
 }
 
-// A prefetch workgroup of rank `rank` (below kPfWorkgroupsPerXcd) on XCD x,
+// A prefetch workgroup of rank `rank` (below pf.per_xcd) on XCD x,
 // with `waves` waves, called by all of the workgroup's threads (it has a
 // barrier).  The stream
 // descriptors are first copied to the LDS in one round of loads (fetched one
@@ -75,7 +85,7 @@ __device__ __forceinline__ void l2_prefetch(const PfPlan& pf, uint32_t x, uint32
   __syncthreads();
   const uint32_t lane = threadIdx.x & 63u;
   const uint32_t r = rank * (uint32_t)waves + (threadIdx.x >> 6);
-  const uint32_t step = (uint32_t)(kPfWorkgroupsPerXcd * waves) * 64u;
+  const uint32_t step = (uint32_t)(pf.per_xcd * waves) * 64u;
   for (int s = 0; s < pf.n; ++s) {
     const PfStream st = desc[s];
     const uint32_t c0 = (x - st.xoff) & 7u;
@@ -92,8 +102,8 @@ __device__ __forceinline__ void l2_prefetch(const PfPlan& pf, uint32_t x, uint32
 }
 
 // The prefetch role of a launch whose workgroups n_main .. n_main + 8 *
-// kPfWorkgroupsPerXcd - 1 prefetch: each XCD gets kPfWorkgroupsPerXcd of
-// them, whatever n_main is.  True for the workgroups that took it.
+// pf.per_xcd - 1 prefetch: each XCD gets pf.per_xcd of them, whatever
+// n_main is.  True for the workgroups that took it.
 __device__ __forceinline__ bool l2_prefetch_role(const PfPlan& pf, int n_main, int waves,
                                                  void* lds) {
   if ((int)blockIdx.x < n_main) return false;

@@ -65,9 +65,8 @@ extern int g_fwd_norm_separate;
 constexpr int kGemvNormMax = 7680;
 
 // plh_set_tuning key 15: the forward pass's attention launches warm the L2
-// with the o-projection's and gate/up pair's weights, and the down
-// projection's unless the launch is an unsplit one (0); with all three (1);
-// never the down projection's (2); not at all (-1).
+// with the o-projection's, gate/up pair's and down projection's weights (0),
+// the first two only (1), or not at all (-1).
 extern int g_fwd_prefetch;
 // per device: 1 when workgroup c of a launch runs on XCD c % 8 (checked at
 // plh_init), -1 when not, 0 before the check
@@ -182,7 +181,7 @@ struct DecodeArgs {
   // (else the flattened blocks cut into W ranges)
   int sk_k, sk_kshift;
   // Workgroups n_main .. of attn_decode_kernel's grid only prefetch pf
-  // (8 * kPfWorkgroupsPerXcd of them when pf.n > 0).
+  // (8 * pf.per_xcd of them when pf.n > 0).
   int n_main;
   PfPlan pf;
 };

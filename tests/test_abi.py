@@ -141,12 +141,12 @@ int main(void) {
 
 def test_set_tuning_checks_prefetch_setting():
     """plh_set_tuning needs no device: key 15 (the forward pass's L2 weight
-    prefetch) takes -1, 0, 1 and 2 and refuses anything else, and an unknown
-    key is refused."""
+    prefetch) takes -1, 0 and 1 and refuses anything else, and an unknown key
+    is refused."""
     import picolm_amd as P
-    for v in (-1, 1, 2, 0):
+    for v in (-1, 1, 0):
         assert P.lib.plh_set_tuning(15, v) == 0
-    for v in (-2, 3):
+    for v in (-2, 2):
         assert P.lib.plh_set_tuning(15, v) == -1
         assert "forward weight prefetch" in P._native.last_error()
     assert P.lib.plh_set_tuning(99, 0) == -1
