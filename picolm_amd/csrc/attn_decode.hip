@@ -449,8 +449,11 @@ __device__ __forceinline__ void append_new_row(const DecodeArgs& a, int li, int 
   if (grp == 0) mnew[col] = sc * a.score_scale;
 }
 
-template <int D, bool QKN>
-__global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(DecodeArgs a) {
+// The split kernel's body.  PFR: the launch also carries the prefetch
+// workgroups of pl (attn_decode_pf_kernel); launches without them take the
+// smaller argument block of attn_decode_kernel.
+template <int D, bool QKN, bool PFR>
+__device__ __forceinline__ void attn_decode_body(const DecodeArgs& a, const PfLaunch& pl) {
   constexpr int kWaves = DecodeShape<D>::W;
   constexpr int kThreads = 64 * kWaves;
   constexpr int ND = D / 32;          // 32-wide d blocks of QK
@@ -464,17 +467,23 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
   __shared__ __align__(16) unsigned char smem[kSmemBytes];
   __shared__ int s_merge;
 
-  PLH_ARGS_NOW("s"(a.q), "s"(a.k), "s"(a.v), "s"(a.kc), "s"(a.vc), "s"(a.cos_t), "s"(a.sin_t),
-               "s"(a.out), "s"(a.part_o), "s"(a.part_m), "s"(a.part_l), "s"(a.layer0),
-               "s"(a.n_heads), "s"(a.n_kv_heads), "s"(a.max_seq_len), "s"(a.pos),
-               "s"(a.rope_type), "s"(a.n_hblk), "s"(a.nhm), "s"(a.n_split), "s"(a.split_len),
-               "s"(a.n_units), "s"(a.per_xcd), "s"(a.score_scale), "s"(a.k_rows),
-               "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps), "s"(a.G),
-               "s"(a.fd_split.m), "s"(a.fd_split.sh), "s"(a.fd_hblk.m), "s"(a.fd_hblk.sh),
-               "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh), "s"(a.split_merge), "s"(a.split_ctr),
-               "s"(a.n_main));
-  static_assert(kSmemBytes >= kPfLdsBytes, "prefetch workgroups use the kernel's LDS");
-  if (l2_prefetch_role(a.pf, a.n_main, kWaves, smem)) return;
+#define PLH_SPLIT_ARGS(a)                                                                        \
+  "s"(a.q), "s"(a.k), "s"(a.v), "s"(a.kc), "s"(a.vc), "s"(a.cos_t), "s"(a.sin_t), "s"(a.out),   \
+      "s"(a.part_o), "s"(a.part_m), "s"(a.part_l), "s"(a.layer0), "s"(a.n_heads),               \
+      "s"(a.n_kv_heads), "s"(a.max_seq_len), "s"(a.pos), "s"(a.rope_type), "s"(a.n_hblk),       \
+      "s"(a.nhm), "s"(a.n_split), "s"(a.split_len), "s"(a.n_units), "s"(a.per_xcd),            \
+      "s"(a.score_scale), "s"(a.k_rows), "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps),  \
+      "s"(a.G), "s"(a.fd_split.m), "s"(a.fd_split.sh), "s"(a.fd_hblk.m), "s"(a.fd_hblk.sh),     \
+      "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh), "s"(a.split_merge), "s"(a.split_ctr)
+  if constexpr (PFR) {
+    // the prefetch split from the same batch of argument loads
+    PLH_ARGS_NOW(PLH_SPLIT_ARGS(a), "s"(pl.n_main));
+    static_assert(kSmemBytes >= kPfLdsBytes, "prefetch workgroups use the kernel's LDS");
+    if (l2_prefetch_role(pl.plan, pl.n_main, kWaves, smem)) return;
+  } else {
+    PLH_ARGS_NOW(PLH_SPLIT_ARGS(a));
+  }
+#undef PLH_SPLIT_ARGS
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -676,6 +685,16 @@ __global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(Dec
   }
 }
 
+template <int D, bool QKN>
+__global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_kernel(DecodeArgs a) {
+  attn_decode_body<D, QKN, false>(a, PfLaunch{});
+}
+template <int D, bool QKN>
+__global__ __launch_bounds__(64 * DecodeShape<D>::W) void attn_decode_pf_kernel(DecodeArgs a,
+                                                                               PfLaunch pl) {
+  attn_decode_body<D, QKN, true>(a, pl);
+}
+
 // Merges the n_split partials of one group: out = sum_s O_s 2^(m_s-M) /
 // sum_s l_s 2^(m_s-M) with M the largest m_s.  CH partials are loaded
 // together (8 when there are at most 8 splits, else kCombineChunk).
@@ -816,8 +835,9 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const DecodeArgs& a) {
   return __builtin_amdgcn_make_buffer_rsrc(a.sk_part, 0, (int)a.sk_part_bytes, 0x00020000);
 }
 
-template <int D, bool QKN, int kSkPF>
-__global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
+// The stream-K kernel's body; PFR as for attn_decode_body.
+template <int D, bool QKN, int kSkPF, bool PFR>
+__device__ __forceinline__ void attn_decode_sk_body(const DecodeArgs& a, const PfLaunch& pl) {
   constexpr int kWaves = 4;
   constexpr int kThreads = 64 * kWaves;
   constexpr int ND = D / 32;
@@ -832,19 +852,25 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
   __shared__ float s_knew[D], s_vnew[D], s_mnew[16];
   __shared__ int s_last;
 
-  PLH_ARGS_NOW("s"(a.q), "s"(a.k), "s"(a.v), "s"(a.kc), "s"(a.vc), "s"(a.cos_t), "s"(a.sin_t),
-               "s"(a.out), "s"(a.layer0), "s"(a.n_heads), "s"(a.n_kv_heads),
-               "s"(a.max_seq_len), "s"(a.pos), "s"(a.rope_type), "s"(a.n_hblk), "s"(a.nhm),
-               "s"(a.score_scale), "s"(a.sk_q), "s"(a.sk_r), "s"(a.sk_nbk), "s"(a.sk_maxp),
-               "s"(a.sk_part), "s"(a.sk_part_bytes), "s"(a.sk_ctr), "s"(a.k_rows),
-               "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps), "s"(a.G),
-               "s"(a.fd_hblk.m), "s"(a.fd_hblk.sh), "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh),
-               "s"(a.fd_nbk.m), "s"(a.fd_nbk.sh), "s"(a.fd_q.m), "s"(a.fd_q.sh),
-               "s"(a.fd_q1.m), "s"(a.fd_q1.sh), "s"(a.sk_wx), "s"(a.fd_wx.m), "s"(a.fd_wx.sh),
-               "s"(a.sk_k), "s"(a.sk_kshift), "s"(a.n_main));
-  // (the prefetch split from the same batch of argument loads)
-  static_assert(kSmemBytes >= kPfLdsBytes, "prefetch workgroups use the kernel's LDS");
-  if (l2_prefetch_role(a.pf, a.n_main, kWaves, smem)) return;
+#define PLH_SK_ARGS(a)                                                                           \
+  "s"(a.q), "s"(a.k), "s"(a.v), "s"(a.kc), "s"(a.vc), "s"(a.cos_t), "s"(a.sin_t), "s"(a.out),   \
+      "s"(a.layer0), "s"(a.n_heads), "s"(a.n_kv_heads), "s"(a.max_seq_len), "s"(a.pos),        \
+      "s"(a.rope_type), "s"(a.n_hblk), "s"(a.nhm), "s"(a.score_scale), "s"(a.sk_q),             \
+      "s"(a.sk_r), "s"(a.sk_nbk), "s"(a.sk_maxp), "s"(a.sk_part), "s"(a.sk_part_bytes),         \
+      "s"(a.sk_ctr), "s"(a.k_rows), "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps),       \
+      "s"(a.G), "s"(a.fd_hblk.m), "s"(a.fd_hblk.sh), "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh),         \
+      "s"(a.fd_nbk.m), "s"(a.fd_nbk.sh), "s"(a.fd_q.m), "s"(a.fd_q.sh), "s"(a.fd_q1.m),         \
+      "s"(a.fd_q1.sh), "s"(a.sk_wx), "s"(a.fd_wx.m), "s"(a.fd_wx.sh), "s"(a.sk_k),              \
+      "s"(a.sk_kshift)
+  if constexpr (PFR) {
+    // the prefetch split from the same batch of argument loads
+    PLH_ARGS_NOW(PLH_SK_ARGS(a), "s"(pl.n_main));
+    static_assert(kSmemBytes >= kPfLdsBytes, "prefetch workgroups use the kernel's LDS");
+    if (l2_prefetch_role(pl.plan, pl.n_main, kWaves, smem)) return;
+  } else {
+    PLH_ARGS_NOW(PLH_SK_ARGS(a));
+  }
+#undef PLH_SK_ARGS
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -1023,6 +1049,16 @@ __global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
     s0 = s1;
     __syncthreads();  // the LDS is reused by the next segment
   }
+}
+
+template <int D, bool QKN, int kSkPF>
+__global__ __launch_bounds__(256) void attn_decode_sk_kernel(DecodeArgs a) {
+  attn_decode_sk_body<D, QKN, kSkPF, false>(a, PfLaunch{});
+}
+// with prefetch workgroups: the default two tiles in flight only
+template <int D, bool QKN>
+__global__ __launch_bounds__(256) void attn_decode_sk_pf_kernel(DecodeArgs a, PfLaunch pl) {
+  attn_decode_sk_body<D, QKN, 2, true>(a, pl);
 }
 
 // Split plan defaults, from sweeps on MI355X (TinyLlama pos 256 and 2047,
@@ -1410,16 +1446,32 @@ static int attn_decode_sk_launch(int n_heads, int n_kv_heads, int head_dim, int 
   a.sk_part = part;
   a.sk_part_bytes = (uint32_t)part_bytes;
   a.sk_ctr = ctr;
-  // the forward pass's pending prefetch rides on this launch's spare CUs
-  a.n_main = (int)W;
-  a.pf = c.pf_next;
-  a.pf.per_xcd = pf_per_xcd(c.num_cus > 0 ? c.num_cus : 256, W);
-  if (g_xcd_ok[c.device] != 1 || W > (c.num_cus > 0 ? c.num_cus : 256) / 4 || a.pf.per_xcd == 0)
-    a.pf.n = 0;
-  const int n_pf = a.pf.n > 0 ? 8 * a.pf.per_xcd : 0;
-  const dim3 grid((unsigned)(W + n_pf)), block(256);
   const bool qkn = q_norm != nullptr;
   const int pf = g_sk_pf ? g_sk_pf : 2;
+  // the forward pass's pending prefetch rides on this launch's spare CUs
+  // (with the default two tiles in flight)
+  PfLaunch pl;
+  pl.n_main = (int)W;
+  pl.plan = c.pf_next;
+  pl.plan.per_xcd = pf_per_xcd(c.num_cus > 0 ? c.num_cus : 256, W);
+  if (g_xcd_ok[c.device] != 1 || W > (c.num_cus > 0 ? c.num_cus : 256) / 4 ||
+      pl.plan.per_xcd == 0 || pf != 2)
+    pl.plan.n = 0;
+  if (pl.plan.n > 0) {
+    const dim3 pgrid((unsigned)(W + 8 * pl.plan.per_xcd)), pblock(256);
+    if (head_dim == 64 && !qkn)
+      hipLaunchKernelGGL((attn_decode_sk_pf_kernel<64, false>), pgrid, pblock, 0, c.stream, a, pl);
+    else if (head_dim == 64)
+      hipLaunchKernelGGL((attn_decode_sk_pf_kernel<64, true>), pgrid, pblock, 0, c.stream, a, pl);
+    else if (!qkn)
+      hipLaunchKernelGGL((attn_decode_sk_pf_kernel<128, false>), pgrid, pblock, 0, c.stream, a,
+                         pl);
+    else
+      hipLaunchKernelGGL((attn_decode_sk_pf_kernel<128, true>), pgrid, pblock, 0, c.stream, a,
+                         pl);
+    return check_hip(hipGetLastError(), "attn_decode_sk_pf_kernel");
+  }
+  const dim3 grid((unsigned)W), block(256);
 #define PLH_SK(D, Q, PF) \
   hipLaunchKernelGGL((attn_decode_sk_kernel<D, Q, PF>), grid, block, 0, c.stream, a)
   if (head_dim == 64 && !qkn) {
@@ -1573,26 +1625,37 @@ static int attn_decode_impl(int n_layers, int n_heads, int n_kv_heads, int head_
                   (long)n_groups * kSplitCtrPitch <= kDecodeCounters &&
                   (size_t)n_units * nhm * head_dim * sizeof(float) < (1u << 31);
   a.split_ctr = noalloc ? (unsigned*)g_scratch_ptr[c.device] : c.decode_ctr;
-  // the forward pass's pending prefetch rides on this launch's spare CUs
-  a.n_main = 8 * per_xcd;
-  a.pf = c.pf_next;
+  // the forward pass's pending prefetch rides on this launch's spare CUs:
   // only a launch that leaves most CUs idle takes them, one workgroup each
-  a.pf.per_xcd = pf_per_xcd(c.num_cus > 0 ? c.num_cus : 256, 8L * per_xcd);
+  PfLaunch pl;
+  pl.n_main = 8 * per_xcd;
+  pl.plan = c.pf_next;
+  pl.plan.per_xcd = pf_per_xcd(c.num_cus > 0 ? c.num_cus : 256, 8L * per_xcd);
   if (g_xcd_ok[c.device] != 1 || 8 * per_xcd > (c.num_cus > 0 ? c.num_cus : 256) / 4 ||
-      a.pf.per_xcd == 0)
-    a.pf.n = 0;
-  const int n_pf = a.pf.n > 0 ? 8 * a.pf.per_xcd : 0;
+      pl.plan.per_xcd == 0)
+    pl.plan.n = 0;
 
-  const dim3 grid((unsigned)(8 * per_xcd + n_pf)), cblock(kCombineThreads);
+  const dim3 grid((unsigned)(8 * per_xcd)), cblock(kCombineThreads);
   const dim3 b64(64 * DecodeShape<64>::W), b128(64 * DecodeShape<128>::W);
-  if (head_dim == 64 && !qkn)
+  if (pl.plan.n > 0) {
+    const dim3 pgrid((unsigned)(8 * per_xcd + 8 * pl.plan.per_xcd));
+    if (head_dim == 64 && !qkn)
+      hipLaunchKernelGGL((attn_decode_pf_kernel<64, false>), pgrid, b64, 0, c.stream, a, pl);
+    else if (head_dim == 64)
+      hipLaunchKernelGGL((attn_decode_pf_kernel<64, true>), pgrid, b64, 0, c.stream, a, pl);
+    else if (!qkn)
+      hipLaunchKernelGGL((attn_decode_pf_kernel<128, false>), pgrid, b128, 0, c.stream, a, pl);
+    else
+      hipLaunchKernelGGL((attn_decode_pf_kernel<128, true>), pgrid, b128, 0, c.stream, a, pl);
+  } else if (head_dim == 64 && !qkn) {
     hipLaunchKernelGGL((attn_decode_kernel<64, false>), grid, b64, 0, c.stream, a);
-  else if (head_dim == 64)
+  } else if (head_dim == 64) {
     hipLaunchKernelGGL((attn_decode_kernel<64, true>), grid, b64, 0, c.stream, a);
-  else if (!qkn)
+  } else if (!qkn) {
     hipLaunchKernelGGL((attn_decode_kernel<128, false>), grid, b128, 0, c.stream, a);
-  else
+  } else {
     hipLaunchKernelGGL((attn_decode_kernel<128, true>), grid, b128, 0, c.stream, a);
+  }
   if (check_hip(hipGetLastError(), "attn_decode_kernel")) return -1;
   if (n_split == 1 || a.split_merge) return 0;
   // one thread per (q head of the block, d): no workgroup without work

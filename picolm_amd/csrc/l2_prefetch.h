@@ -46,6 +46,14 @@ inline int pf_per_xcd(int num_cus, long n_main) {
   return per >= 8 ? (int)per : 0;
 }
 
+// A launch's prefetch: its workgroups n_main .. n_main + 8 * plan.per_xcd - 1
+// take plan.  A kernel argument of its own, so that launches without a plan
+// keep the smaller argument block.
+struct PfLaunch {
+  int n_main;
+  PfPlan plan;
+};
+
 // LDS a prefetch workgroup needs: 1 KB that the loads land in, then the
 // plan's stream descriptors.
 constexpr int kPfLdsBytes = 1024 + kPfStreams * (int)sizeof(PfStream);

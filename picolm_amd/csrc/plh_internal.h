@@ -180,10 +180,6 @@ struct DecodeArgs {
   // at most sk_nbk) to a group, each group's blocks split evenly among its own
   // (else the flattened blocks cut into W ranges)
   int sk_k, sk_kshift;
-  // Workgroups n_main .. of attn_decode_kernel's grid only prefetch pf
-  // (8 * pf.per_xcd of them when pf.n > 0).
-  int n_main;
-  PfPlan pf;
 };
 
 }  // namespace plh
