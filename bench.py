@@ -1,6 +1,7 @@
 """Benchmark of picolm's attention block on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME] [--no-cpu]
+                    [--tune KEY=VALUE ...]   (plh_set_tuning before the run, for sweeps)
 
 Prints one JSON line.  The headline (the contract keys, `roofline`,
 `cpu_baseline`) is TinyLlama-1.1B-shaped decode at position 2047 (22 layers,
@@ -257,6 +258,8 @@ def gemv_exact_order(P, gres, refs):
 FWD_MODEL = dict(n_layers=22, n_embd=2048, n_ffn=5632, n_heads=32, n_kv_heads=4, head_dim=64,
                  vocab_size=32000, max_seq_len=2048)
 FWD_WORKLOAD = "tinyllama_q4km_forward"
+# plh_set_tuning settings from --tune (key -> value), reported in the line
+TUNING = {}
 
 
 def run_forward(P, n_prompt=128, n_decode=64, n_check=8):
@@ -300,6 +303,21 @@ def run_forward(P, n_prompt=128, n_decode=64, n_check=8):
     P.synchronize()
     wall = (time.perf_counter() - t0) / n_decode
     dev_ms = e0.elapsed_ms(e1) / n_decode
+    # the same tokens with the attention launches' L2 weight prefetch off
+    # (tuning key 15), for comparison
+    P.check(P.lib.plh_set_tuning(15, -1), "plh_set_tuning")
+    try:
+        for i in range(4):
+            dm.forward(int(toks[i]), n_prompt + i)
+        P.synchronize()
+        e0.record()
+        for i in range(n_decode):
+            dm.forward(int(toks[4 + i]), n_prompt + 4 + i)
+        e1.record()
+        P.synchronize()
+        dev_nopf_ms = e0.elapsed_ms(e1) / n_decode
+    finally:
+        P.check(P.lib.plh_set_tuning(15, TUNING.get(15, 0)), "plh_set_tuning")
     pos = n_prompt + 4 + n_decode
     tok = int(toks[-1])
     t0 = time.perf_counter()
@@ -349,6 +367,7 @@ def run_forward(P, n_prompt=128, n_decode=64, n_check=8):
         "decode_tok_s": 1.0 / wall,
         "decode_us_per_token": wall * 1e6,
         "decode_device_us_per_token": dev_ms * 1e3,
+        "decode_device_us_per_token_no_l2_prefetch": dev_nopf_ms * 1e3,
         "decode_positions": [n_prompt + 4, n_prompt + 3 + n_decode],
         "decode_device_us_per_token_pos2047": dev_last_ms * 1e3,
         "decode_device_us_per_token_pos2047_exact_gemv": dev_last_exact_ms * 1e3,
@@ -1034,7 +1053,12 @@ def main():
                     help="skip the GEMV, forward-pass and boundary-latency sections")
     ap.add_argument("--prompt", type=int, default=128,
                     help="prompt tokens of the forward-pass workload")
+    ap.add_argument("--tune", action="append", default=[], metavar="KEY=VALUE",
+                    help="plh_set_tuning(KEY, VALUE) before the run (repeatable)")
     args = ap.parse_args()
+    for t in args.tune:
+        k, _, v = t.partition("=")
+        TUNING[int(k)] = int(v)
     if args.gpus != 1:
         print(json.dumps({"error": "one GPU only: the attention block would shard by kv head "
                                    "(no exchange) or by sequence (one merge of the split "
@@ -1043,6 +1067,8 @@ def main():
         sys.exit(2)
     import picolm_amd as P
     P.init(0)
+    for k, v in TUNING.items():
+        P.check(P.lib.plh_set_tuning(k, v), f"plh_set_tuning({k}, {v})")
     cpu = not args.no_cpu
     if args.workload == GEMV_WORKLOAD:   # the weight GEMVs of one token as the headline
         steps = max(1, args.steps // 50)
@@ -1057,6 +1083,8 @@ def main():
                            **GEMV_TOKEN, "types": "Q4_K (q,k,o,gate,up), Q6_K (v,down,output)"}}
         line.update(gres)
         line.update(gextra)
+        if TUNING:
+            line["tuning"] = {str(k): v for k, v in TUNING.items()}
         print(json.dumps(line), flush=True)
         return
     if args.workload == FWD_WORKLOAD:   # the whole forward pass as the headline
@@ -1071,6 +1099,8 @@ def main():
                 "config": {"workload": FWD_WORKLOAD, **fres.pop("config")}}
         line.update(fres)
         line.update(fextra)
+        if TUNING:
+            line["tuning"] = {str(k): v for k, v in TUNING.items()}
         print(json.dumps(line), flush=True)
         return
 
@@ -1106,6 +1136,8 @@ def main():
     if cpu:
         line["host"] = host_info()
     if args.workload is not None:   # one workload alone (profiling runs)
+        if TUNING:
+            line["tuning"] = {str(k): v for k, v in TUNING.items()}
         print(json.dumps(line), flush=True)
         return
 
@@ -1154,6 +1186,8 @@ def main():
         line["forward"] = fres
     # last, so that a tail of the line holds it: the benchmark set, flat
     line["workloads"] = [compact(tag, name, results[name]) for tag, name in BASELINE_SET]
+    if TUNING:
+        line["tuning"] = {str(k): v for k, v in TUNING.items()}
     print(json.dumps(line), flush=True)
 
 
