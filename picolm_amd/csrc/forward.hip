@@ -328,7 +328,17 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, float
         call(L.q, E, Q, xin, a.q, nw, L.q_bias, !L.q_bias, nullptr, nullptr),
         call(L.k, E, KV, xin, a.k, nw, L.k_bias, 0, nullptr, nullptr),
         call(L.v, E, KV, xin, a.v, nw, L.v_bias, 0, nullptr, nullptr)};
-    if (gemv_multi_launch(qkv, 3)) return -1;
+    // At short context q, k, v and the attention run in one launch (tuning
+    // key 17): the attention workgroups wait for their group's rows instead
+    // of a launch boundary (qkv_attention_launch).
+    DecodeArgs fd;
+    unsigned* fctr = nullptr;
+    const bool fuse = g_fwd_fuse >= 0 && !L.q_norm && nw != nullptr && !g_gemv_exact &&
+                      decode_args_fused(m->n_layers, m->n_heads, m->n_kv_heads, m->head_dim,
+                                        m->max_seq_len, m->rope_type, l, pos, a.q, a.k, a.v,
+                                        m->key_cache, m->val_cache, m->rope_cos, m->rope_sin,
+                                        a.att, fd, &fctr);
+    if (!fuse && gemv_multi_launch(qkv, 3)) return -1;
     // The attention launch leaves most CUs idle: its spare workgroups bring
     // the o-projection's, the gate/up pair's and the down projection's
     // weights into the L2 of the XCDs whose GEMV workgroups will read them.
@@ -346,15 +356,19 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, float
         gemv_prefetch_plan(call(L.down, F, E, a.hb, a.x, nullptr, nullptr, 0, nullptr, a.x),
                            nullptr, pf);
     }
-    const int rc = L.q_norm ? plh_attn_decode_qknorm(m->n_layers, m->n_heads, m->n_kv_heads,
-                                                     m->head_dim, m->max_seq_len, m->rope_type, l,
-                                                     1, pos, a.q, a.k, a.v, m->key_cache,
-                                                     m->val_cache, m->rope_cos, m->rope_sin,
-                                                     a.att, L.q_norm, L.k_norm, eps)
-                            : plh_attn_decode(m->n_layers, m->n_heads, m->n_kv_heads,
-                                              m->head_dim, m->max_seq_len, m->rope_type, l, 1,
-                                              pos, a.q, a.k, a.v, m->key_cache, m->val_cache,
-                                              m->rope_cos, m->rope_sin, a.att);
+    int rc;
+    if (fuse)
+      rc = qkv_attention_launch(qkv, fd, m->head_dim, fctr, pf,
+                                g_fwd_fuse >= 8 ? g_fwd_fuse : kFusePrefetchPerXcd);
+    else if (L.q_norm)
+      rc = plh_attn_decode_qknorm(m->n_layers, m->n_heads, m->n_kv_heads, m->head_dim,
+                                  m->max_seq_len, m->rope_type, l, 1, pos, a.q, a.k, a.v,
+                                  m->key_cache, m->val_cache, m->rope_cos, m->rope_sin, a.att,
+                                  L.q_norm, L.k_norm, eps);
+    else
+      rc = plh_attn_decode(m->n_layers, m->n_heads, m->n_kv_heads, m->head_dim,
+                           m->max_seq_len, m->rope_type, l, 1, pos, a.q, a.k, a.v, m->key_cache,
+                           m->val_cache, m->rope_cos, m->rope_sin, a.att);
     pf.n = 0;
     if (rc) return -1;
     // x = x + (Wo att + o_bias)

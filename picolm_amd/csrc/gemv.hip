@@ -23,6 +23,7 @@
 #include <vector>
 
 #include "attn_common.h"
+#include "attn_decode_dev.h"
 #include "picolm_hip.h"
 #include "plh_internal.h"
 
@@ -1072,7 +1073,9 @@ __device__ __forceinline__ void unit_acc(const DigLds& xs, int u, const typename
 // passes load and add more units); the uspan sums of a row go through LDS
 // and are added by a power-of-two group of lanes (a shuffle tree), which
 // applies the epilogue.
-template <class F, int RB, bool NORM, bool PAIR>
+// COH: the outputs are read by other workgroups of the same launch (the fused
+// q/k/v + attention launch): stored at device scope.
+template <class F, int RB, bool NORM, bool PAIR, bool COH = false>
 __device__ __forceinline__ void gemv_body_fast(const GemvArgs& a, int wg, float* lds) {
   __shared__ float red[kThreads / 64];
   const int tid = threadIdx.x;
@@ -1145,7 +1148,10 @@ __device__ __forceinline__ void gemv_body_fast(const GemvArgs& a, int wg, float*
         if (a.bias_mode == 2) sumf = sumf + 0.0f;
         if (a.gate) sumf = silu(a.gate[r]) * sumf;
         if (a.resid) sumf = a.resid[r] + sumf;
-        a.out[r] = sumf;
+        if constexpr (COH)
+          __hip_atomic_store(a.out + r, sumf, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        else
+          a.out[r] = sumf;
       }
     }
   }
@@ -1180,6 +1186,62 @@ __global__ __launch_bounds__(kThreads) void gemv_fast_multi_kernel(MultiArgs m) 
     case kTypeQ4K: gemv_body_fast<Q4KD, RB, NORM, false>(m.seg[s], wg, terms); break;
     case kTypeQ8_0: gemv_body_fast<Q80D, RB, NORM, false>(m.seg[s], wg, terms); break;
     default: gemv_body_fast<Q6KD, RB, NORM, false>(m.seg[s], wg, terms); break;
+  }
+}
+
+// ---- q/k/v projections and the attention in one launch (plh_forward) ------
+//
+// Workgroups 0 .. n_att - 1 are the layer's attention (one unsplit group
+// each, attn_decode_body's fused form); the rest are gemv_fast_multi_kernel's
+// q, k and v workgroups, which store their rows at device scope and then
+// count themselves in on the counter of every group their rows belong to.
+// The attention workgroups issue their first cached tiles, wait for their
+// group's count, and go on as the split kernel does: one launch instead of
+// two, and the attention's cache loads overlap the projections.
+struct FusedArgs {
+  MultiArgs m;   // q, k, v (segments 0, 1, 2); wg0 counts from workgroup n_att
+  DecodeArgs d;  // the layer's unsplit attention
+  FuseWait fw;
+  int n_att;
+  PfLaunch pl;   // workgroups pl.n_main.. prefetch the next GEMVs' weights
+};
+
+template <int D, int RB>
+__global__ __launch_bounds__(kThreads) void qkv_attn_fused_kernel(FusedArgs f) {
+  extern __shared__ __align__(16) float terms[];
+  static_assert(64 * DecodeShape<D>::W == kThreads, "one workgroup shape for both roles");
+  if ((int)blockIdx.x < f.n_att) {
+    attn_decode_body<D, false, false, true>(f.d, PfLaunch{}, f.fw);
+    return;
+  }
+  const MultiArgs& m = f.m;
+  PLH_ARGS_NOW("s"(f.n_att), "s"(m.wg0[1]), "s"(m.wg0[2]), "s"(m.qtype[0]), "s"(m.qtype[1]),
+               "s"(m.qtype[2]), "s"(f.pl.n_main));
+  if (l2_prefetch_role(f.pl.plan, f.pl.n_main, kThreads / 64, terms)) return;
+  const int b = (int)blockIdx.x - f.n_att;
+  const int s = (b >= m.wg0[1]) + (b >= m.wg0[2]);
+  const int wg = b - (s == 2 ? m.wg0[2] : s == 1 ? m.wg0[1] : 0);
+  const int qtype = s == 2 ? m.qtype[2] : s == 1 ? m.qtype[1] : m.qtype[0];
+  const GemvArgs& g = m.seg[s];
+  PLH_ARGS_NOW("s"(g.w), "s"(g.x), "s"(g.out), "s"(g.d), "s"(g.nb), "s"(g.units), "s"(g.uspan),
+               "s"(g.row_par), "s"(g.unit_iters), "s"(g.rows_per_wg), "s"(g.off0), "s"(g.off1),
+               "s"(g.off2), "s"(g.scales_off), "s"(g.d_off), "s"(g.n), "s"(g.xs_off),
+               "s"(g.bias), "s"(g.bias_mode), "s"(g.norm_w), "s"(g.norm_eps));
+  switch (qtype) {
+    case kTypeQ4K: gemv_body_fast<Q4KD, RB, true, false, true>(g, wg, terms); break;
+    case kTypeQ8_0: gemv_body_fast<Q80D, RB, true, false, true>(g, wg, terms); break;
+    default: gemv_body_fast<Q6KD, RB, true, false, true>(g, wg, terms); break;
+  }
+  // every row stored before the counts go up
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    const int r0 = wg * g.rows_per_wg;
+    const int r1 = min(r0 + g.rows_per_wg, g.d);
+    const int per = f.fw.group_rows[s];
+    for (int grp = r0 / per; grp <= (r1 - 1) / per; ++grp)
+      __hip_atomic_fetch_add(f.fw.ctr + grp * kFuseCtrPitch, 1u, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
@@ -1638,6 +1700,69 @@ int gemv_multi_launch(const GemvCall* g, int n) {
   else
     launch_multi<false>(rb, m.wg0[n], lds, ctx().stream, m);
   return check_hip(hipGetLastError(), "gemv_multi_kernel launch");
+}
+
+int qkv_attention_launch(const GemvCall* g, const DecodeArgs& d, int head_dim, unsigned* ctr,
+                         const PfPlan& pf, int pf_per_xcd) {
+  if (!ctx().stream) {
+    set_error("plh_gemv: plh_init has not been called");
+    return -1;
+  }
+  if (g_gemv_exact || (head_dim != 64 && head_dim != 128) || !g[0].norm_w || !ctr) {
+    set_error("qkv_attention_launch: needs the fast GEMV order, the rmsnorm prologue and "
+              "head_dim 64 or 128");
+    return -1;
+  }
+  MultiArgs m{};
+  int rows[kMaxSeg];
+  for (int s = 0; s < kMaxSeg; ++s) {
+    if (g[s].x != g[0].x || g[s].norm_w != g[0].norm_w || g[s].n_tok > 1) {
+      set_error("qkv_attention_launch: segments must share x and the rmsnorm prologue");
+      return -1;
+    }
+    if (prepare(g[s], m.seg[s])) return -1;
+    m.qtype[s] = g[s].qtype;
+    rows[s] = g[s].d;
+  }
+  // the rows per thread gemv_multi_launch would pick, so the projections
+  // are the same sums
+  const int rb = pick_rb(m.seg, rows, kMaxSeg, false, 4);
+  if (rb < 0) return -1;
+  size_t lds = 0;
+  m.nseg = kMaxSeg;
+  m.wg0[0] = 0;
+  FusedArgs f{};
+  for (int s = 0; s < kMaxSeg; ++s) {
+    m.seg[s].rows_per_wg = m.seg[s].row_par * rb;
+    m.wg0[s + 1] = m.wg0[s] + (rows[s] + m.seg[s].rows_per_wg - 1) / m.seg[s].rows_per_wg;
+    const size_t b = lds_bytes_fast(m.seg[s]);
+    if (b > lds) lds = b;
+    f.fw.wg_rows[s] = m.seg[s].rows_per_wg;
+  }
+  f.m = m;
+  f.d = d;
+  f.fw.ctr = ctr;
+  f.fw.group_rows[0] = d.G * head_dim;  // q rows of one kv head's q heads
+  f.fw.group_rows[1] = head_dim;        // k rows of one kv head
+  f.fw.group_rows[2] = head_dim;
+  f.n_att = d.n_units;
+  f.pl.n_main = f.n_att + m.wg0[kMaxSeg];
+  f.pl.plan = pf;
+  f.pl.plan.per_xcd = pf_per_xcd;
+  if (g_xcd_ok[ctx().device] != 1 || pf_per_xcd <= 0) f.pl.plan.n = 0;
+  const int n_pf = f.pl.plan.n > 0 ? 8 * pf_per_xcd : 0;
+  if (n_pf && lds < (size_t)kPfLdsBytes) lds = kPfLdsBytes;
+  const dim3 grid((unsigned)(f.pl.n_main + n_pf)), block(kThreads);
+  hipStream_t st = ctx().stream;
+#define PLH_FUSED(D, RB) \
+  hipLaunchKernelGGL((qkv_attn_fused_kernel<D, RB>), grid, block, lds, st, f)
+  if (head_dim == 64) {
+    if (rb == 1) PLH_FUSED(64, 1); else if (rb == 2) PLH_FUSED(64, 2); else PLH_FUSED(64, 4);
+  } else {
+    if (rb == 1) PLH_FUSED(128, 1); else if (rb == 2) PLH_FUSED(128, 2); else PLH_FUSED(128, 4);
+  }
+#undef PLH_FUSED
+  return check_hip(hipGetLastError(), "qkv_attn_fused_kernel launch");
 }
 
 int gemv_pair_launch(const GemvCall& gate, const GemvCall& up) {

@@ -68,6 +68,14 @@ constexpr int kGemvNormMax = 7680;
 // with the o-projection's, gate/up pair's and down projection's weights (0),
 // the first two only (1), or not at all (-1).
 extern int g_fwd_prefetch;
+// plh_set_tuning key 17: plh_forward runs q, k, v and an unsplit attention in
+// one launch, with kFusePrefetchPerXcd prefetch workgroups per XCD (0) or
+// with 8..31 of them, or in two launches (-1).
+extern int g_fwd_fuse;
+// Prefetch workgroups per XCD of a fused q/k/v + attention launch (they share
+// the CUs with its GEMV workgroups; 8, 16 and 24 measured 675, 678 and 679 us
+// per TinyLlama token).
+constexpr int kFusePrefetchPerXcd = 8;
 // per device: 1 when workgroup c of a launch runs on XCD c % 8 (checked at
 // plh_init), -1 when not, 0 before the check
 extern int g_xcd_ok[64];
@@ -181,6 +189,22 @@ struct DecodeArgs {
   // (else the flattened blocks cut into W ranges)
   int sk_k, sk_kshift;
 };
+
+// The fused q/k/v + attention launch of plh_forward (short contexts): the
+// arguments of the unsplit one-layer decode launch plh_attn_decode would
+// queue for this call, and the counters the attention workgroups wait on;
+// false (nothing set) when that call would take another kernel or split.
+bool decode_args_fused(int n_layers, int n_heads, int n_kv_heads, int head_dim,
+                       int max_seq_len, int rope_type, int layer, int pos, const float* q,
+                       const float* k, const float* v, uint16_t* key_cache, uint16_t* val_cache,
+                       const float* rope_cos, const float* rope_sin, float* out, DecodeArgs& a,
+                       unsigned** ctr);
+// q, k and v (g[0..2], the rmsnorm prologue, fast order) and the attention of
+// d in one launch: d's groups' attention workgroups first, then the q/k/v
+// GEMV workgroups, which count themselves in on ctr, then pf_per_xcd
+// workgroups per XCD prefetching pf (none when pf.n is 0).  -1 on error.
+int qkv_attention_launch(const GemvCall* g, const DecodeArgs& d, int head_dim, unsigned* ctr,
+                         const PfPlan& pf, int pf_per_xcd);
 
 }  // namespace plh
 

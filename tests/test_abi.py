@@ -149,5 +149,10 @@ def test_set_tuning_checks_prefetch_setting():
     for v in (-2, 2):
         assert P.lib.plh_set_tuning(15, v) == -1
         assert "forward weight prefetch" in P._native.last_error()
+    for v in (-1, 8, 31, 0):
+        assert P.lib.plh_set_tuning(17, v) == 0
+    for v in (-2, 1, 7, 32):
+        assert P.lib.plh_set_tuning(17, v) == -1
+        assert "fusion" in P._native.last_error()
     assert P.lib.plh_set_tuning(99, 0) == -1
     assert "unknown key" in P._native.last_error()

@@ -407,6 +407,44 @@ def test_forward_weight_prefetch_changes_nothing(gpu, cfg):
         dm.free()
 
 
+# head_dim 128 without QK-norm: the fused q/k/v + attention launch's other shape
+PF_LLAMA128 = dict(PF_LLAMA, n_heads=4, n_kv_heads=2, head_dim=128)
+
+
+@pytest.mark.parametrize("cfg", [PF_LLAMA, PF_LLAMA128], ids=["hd64", "hd128"])
+def test_forward_fused_qkv_attention_changes_nothing(gpu, cfg):
+    """Tuning key 17: q, k, v and the attention in one launch (the attention
+    workgroups wait on per-group counts of the GEMV workgroups that stored
+    their rows) give the bits of the two launches -- logits, residual and
+    both caches -- with every prefetch count, at a short position (fused)
+    and past 512 positions (not fused), several tokens in a row."""
+    P = gpu
+    h = S.SynthModel(**cfg, seed=73)
+    dm = P.DeviceModel(h)
+    rng = np.random.default_rng(74)
+    fill = rng.standard_normal((2, h.cache_elems()), dtype=np.float32).astype(np.float16)
+    kc, vc = fill[0].view(np.uint16), fill[1].view(np.uint16)
+    try:
+        for pos in (100, 511, 1500):
+            ref = None
+            for key in (-1, 0, 8, 31):
+                P.check(P.lib.plh_set_tuning(17, key), "plh_set_tuning")
+                dm.load_cache(kc, vc)
+                print(f"[case] forward fusion setting {key} pos {pos}", flush=True)
+                for i in range(3):
+                    dm.forward(7 + i, pos + i if pos + i < h.max_seq_len else pos)
+                P.synchronize()
+                got = (bits(dm.fetch_logits()), bits(dm.fetch_x())) + tuple(dm.fetch_cache())
+                if ref is None:
+                    ref = got
+                    continue
+                for a, b in zip(ref, got):
+                    assert np.array_equal(a, b), (pos, key)
+    finally:
+        P.check(P.lib.plh_set_tuning(17, 0), "plh_set_tuning")
+        dm.free()
+
+
 @pytest.mark.parametrize("cfg", [dict(LLAMA, n_layers=2, max_seq_len=2048),
                                  dict(QWEN, max_seq_len=2048)], ids=["llama", "qwen"])
 def test_forward_long_context_split_decode(gpu, oracle_mod, cfg):
