@@ -357,7 +357,11 @@ int plh_forward_prefill(const plh_model *m, const int *tokens, int n_tokens, int
  * workgroups, one per CU they leave idle, that load the weights of the
  * layer's o-projection, gate/up pair and down projection into the L2 of the
  * XCDs whose GEMV workgroups read them (0, default), of the first two only
- * (1), or none (-1); results are the same bits in every setting. */
+ * (1), or none (-1); results are the same bits in every setting; key 17:
+ * plh_forward runs a layer's q/k/v projections and its unsplit (short
+ * context, no QK-norm, head_dim 64 or 128) attention in one launch, with 8
+ * prefetch workgroups per XCD (0, default) or 8..31 of them, or in two
+ * launches (-1); the same bits either way. */
 int plh_set_tuning(int key, int value);
 
 #ifdef __cplusplus
