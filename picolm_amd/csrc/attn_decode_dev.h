@@ -527,7 +527,7 @@ __device__ __forceinline__ void attn_decode_body(const DecodeArgs& a, const PfLa
   // skipped), so the compiler's wait counts stay exact: the q rotation waits
   // for q alone (issued first), and the prefetch is never drained early.
   // A fused launch issues its first tiles (cached rows, ready) before it
-  // waits for q, k and v.
+  // waits for q, k and v (two tiles in flight there measured the same).
   constexpr int PF = DecodeShape<D>::PF;
   const bool has_rows = te > tb;
   const int tclamp = has_rows ? tlast : 0;
@@ -538,6 +538,23 @@ __device__ __forceinline__ void attn_decode_body(const DecodeArgs& a, const PfLa
 #pragma unroll
     for (int j = 0; j < PF; ++j)
       load_tile<D>(buf[j], kbase, vbase, kv_dim, tw + j * kStride, tclamp, lane, col, grp);
+    // The projections take microseconds: meanwhile the group's other cached
+    // rows come into this XCD's L2 (one 16-byte load per 128-byte line of each
+    // K and V row, straight into a scratch LDS buffer), so the tiles after the
+    // first are read from the L2.  Waited for here: the waves only wait next.
+    {
+      typedef __attribute__((address_space(3))) void* lds_ptr;
+      typedef __attribute__((address_space(1))) void* global_ptr;
+      __shared__ __align__(16) unsigned char s_warm[1024];
+      constexpr int kLines = D / 64;  // 128-byte lines per fp16 row
+      for (int i = tid; i < (te - tb) * kLines; i += kThreads) {
+        const int t = tb + i / kLines, part = i - (i / kLines) * kLines;
+        const size_t off = (size_t)t * kv_dim + 64 * part;
+        __builtin_amdgcn_global_load_lds((global_ptr)(kbase + off), (lds_ptr)s_warm, 16, 0, 0);
+        __builtin_amdgcn_global_load_lds((global_ptr)(vbase + off), (lds_ptr)s_warm, 16, 0, 0);
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+    }
     if (tid == 0) {
       // the producers of this group's rows of q, k and v
       const int g = kvh;
