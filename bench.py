@@ -103,9 +103,9 @@ WORKLOADS = {
                               rt=1, qkn=1e-6),
 }
 # the benchmark set, in the order of the configs it is quoted on
-BASELINE_SET = [("cfg1", "tinyllama_decode_pos256"), ("cfg2", "tinyllama_decode_pos2047"),
-                ("cfg3", "tinyllama_prefill_512"), ("cfg4", "llama32_decode_pos8191"),
-                ("cfg5a", "llama2_decode_pos4095"), ("cfg5b", "llama2_prefill_1024")]
+CFG_SET = [("cfg1", "tinyllama_decode_pos256"), ("cfg2", "tinyllama_decode_pos2047"),
+           ("cfg3", "tinyllama_prefill_512"), ("cfg4", "llama32_decode_pos8191"),
+           ("cfg5a", "llama2_decode_pos4095"), ("cfg5b", "llama2_prefill_1024")]
 HEADLINE = "tinyllama_decode_pos2047"
 # CPU-baseline samples: decode layers; prefill (q heads, kv heads) of a 1-layer model
 CPU_DECODE_LAYERS = 2
@@ -1143,7 +1143,7 @@ def main():
 
     # the rest of the benchmark set, each measured the same way
     results = {HEADLINE: hres}
-    for tag, name in BASELINE_SET:
+    for tag, name in CFG_SET:
         if name == HEADLINE:
             continue
         # their own step counts (each step is short; the headline keeps --steps)
@@ -1185,7 +1185,7 @@ def main():
         fres.update(fextra)
         line["forward"] = fres
     # last, so that a tail of the line holds it: the benchmark set, flat
-    line["workloads"] = [compact(tag, name, results[name]) for tag, name in BASELINE_SET]
+    line["workloads"] = [compact(tag, name, results[name]) for tag, name in CFG_SET]
     if TUNING:
         line["tuning"] = {str(k): v for k, v in TUNING.items()}
     print(json.dumps(line), flush=True)
