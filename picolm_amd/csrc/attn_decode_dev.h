@@ -445,6 +445,48 @@ __device__ __forceinline__ int fuse_span(int a, int b, int wg_rows) {
   return (b - 1) / wg_rows - a / wg_rows + 1;
 }
 
+// Thread 0 of an attention workgroup: returns once every producer of group
+// g's rows of q, k and v has counted in.  They are all dispatched eventually
+// (the launch's attention workgroups come first and take one slot each), so
+// the wait ends; the poll count only bounds it outright.  The poll is an
+// atomic, read where the counts are kept.
+__device__ __forceinline__ void fuse_wait(const FuseWait& fw, int g) {
+  const int want = fuse_span(g * fw.group_rows[0], (g + 1) * fw.group_rows[0], fw.wg_rows[0]) +
+                   fuse_span(g * fw.group_rows[1], (g + 1) * fw.group_rows[1], fw.wg_rows[1]) +
+                   fuse_span(g * fw.group_rows[2], (g + 1) * fw.group_rows[2], fw.wg_rows[2]);
+  unsigned* c = fw.ctr + g * kFuseCtrPitch;
+  for (int it = 0; it < (1 << 22); ++it) {
+    if (__hip_atomic_fetch_add(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
+        (unsigned)want)
+      break;
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+// Zeroes group g's count for the next launch, once no workgroup of this
+// launch waits on it any more.
+__device__ __forceinline__ void fuse_reset(const FuseWait& fw, int g) {
+  __hip_atomic_store(fw.ctr + g * kFuseCtrPitch, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// While the projections run: the cached rows [tb, te) of a group come into
+// this XCD's L2 (one 16-byte load per 128-byte line of each K and V row,
+// straight into a scratch LDS buffer), so the tiles after the first are read
+// from the L2.  Waited for here: the waves only wait next.
+template <int D>
+__device__ __forceinline__ void fuse_warm_rows(const uint16_t* kbase, const uint16_t* vbase,
+                                               int kv_dim, int tb, int te, int nthreads) {
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  typedef __attribute__((address_space(1))) void* global_ptr;
+  __shared__ __align__(16) unsigned char s_warm[1024];
+  constexpr int kLines = D / 64;  // 128-byte lines per fp16 row
+  for (int i = threadIdx.x; i < (te - tb) * kLines; i += nthreads) {
+    const int t = tb + i / kLines, part = i - (i / kLines) * kLines;
+    const size_t off = (size_t)t * kv_dim + 64 * part;
+    __builtin_amdgcn_global_load_lds((global_ptr)(kbase + off), (lds_ptr)s_warm, 16, 0, 0);
+    __builtin_amdgcn_global_load_lds((global_ptr)(vbase + off), (lds_ptr)s_warm, 16, 0, 0);
+  }
+  __builtin_amdgcn_s_waitcnt(0);
+}
+
 // The split kernel's body.  PFR: the launch also carries the prefetch
 // workgroups of pl (attn_decode_pf_kernel); launches without them take the
 // smaller argument block of attn_decode_kernel.  FUSED: one unsplit group
@@ -538,42 +580,10 @@ __device__ __forceinline__ void attn_decode_body(const DecodeArgs& a, const PfLa
 #pragma unroll
     for (int j = 0; j < PF; ++j)
       load_tile<D>(buf[j], kbase, vbase, kv_dim, tw + j * kStride, tclamp, lane, col, grp);
-    // The projections take microseconds: meanwhile the group's other cached
-    // rows come into this XCD's L2 (one 16-byte load per 128-byte line of each
-    // K and V row, straight into a scratch LDS buffer), so the tiles after the
-    // first are read from the L2.  Waited for here: the waves only wait next.
-    {
-      typedef __attribute__((address_space(3))) void* lds_ptr;
-      typedef __attribute__((address_space(1))) void* global_ptr;
-      __shared__ __align__(16) unsigned char s_warm[1024];
-      constexpr int kLines = D / 64;  // 128-byte lines per fp16 row
-      for (int i = tid; i < (te - tb) * kLines; i += kThreads) {
-        const int t = tb + i / kLines, part = i - (i / kLines) * kLines;
-        const size_t off = (size_t)t * kv_dim + 64 * part;
-        __builtin_amdgcn_global_load_lds((global_ptr)(kbase + off), (lds_ptr)s_warm, 16, 0, 0);
-        __builtin_amdgcn_global_load_lds((global_ptr)(vbase + off), (lds_ptr)s_warm, 16, 0, 0);
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-    }
+    fuse_warm_rows<D>(kbase, vbase, kv_dim, tb, te, kThreads);
     if (tid == 0) {
-      // the producers of this group's rows of q, k and v
-      const int g = kvh;
-      const int want = fuse_span(g * fw.group_rows[0], (g + 1) * fw.group_rows[0], fw.wg_rows[0]) +
-                       fuse_span(g * fw.group_rows[1], (g + 1) * fw.group_rows[1], fw.wg_rows[1]) +
-                       fuse_span(g * fw.group_rows[2], (g + 1) * fw.group_rows[2], fw.wg_rows[2]);
-      unsigned* c = fw.ctr + g * kFuseCtrPitch;
-      // They are all dispatched eventually (this launch's attention
-      // workgroups come first and take one slot each), so the wait ends; the
-      // poll count only bounds it outright.  The poll is an atomic, read
-      // where the counts are kept.
-      for (int it = 0; it < (1 << 22); ++it) {
-        if (__hip_atomic_fetch_add(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) >=
-            (unsigned)want)
-          break;
-        __builtin_amdgcn_s_sleep(2);
-      }
-      // every producer has counted in: zero it for the next launch
-      __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      fuse_wait(fw, kvh);
+      fuse_reset(fw, kvh);  // this group's only waiter
     }
     __syncthreads();
     load_q_raw<D, QKN, true>(a, li, kvh, G, h0, nh, col, grp, qr);
@@ -730,6 +740,306 @@ __device__ __forceinline__ void attn_decode_body(const DecodeArgs& a, const PfLa
       M = Mc;
     }
     out_base[(size_t)h * D + d] = O * (1.0f / L);
+  }
+}
+
+
+// ---- stream-K decode with the merge inside the kernel --------------------
+//
+// The groups' cached rows, in 16-row blocks, are flattened group-major and
+// cut into sk_W equal ranges, one per workgroup (about one per CU), so every
+// CU streams the same number of bytes whatever the shape.  A range covers
+// the end of one group and the start of the next at most a few times; for
+// each group segment the workgroup's 4 waves take its 32-row tiles in turn
+// with two tiles of loads in flight per wave (a paced stream: the memory
+// queues stay short, so q and the first tiles arrive early), merge through
+// LDS as the split kernel does, and then either write the output (the only
+// producer of the group) or store a partial and count themselves in.  The
+// last producer of a group to arrive merges its partials and writes the
+// output, so one launch does everything.  Partials that cross XCDs, whose L2
+// caches are not coherent with each other, are stored and loaded with
+// device-scope cache policy (sc1: written through, read past the L2); when
+// every producer of a group runs on one XCD (sk_wx > 0 places the ranges so,
+// see the launch) they go through that XCD's L2 instead (sc0: past the CU's
+// L1 only).  Either way the stores complete before the arrival counter is
+// bumped, the counter is an atomic at device scope, and the merging
+// workgroup resets it to zero for the next launch.
+
+// The T blocks are cut into W ranges of q or q + 1 blocks (q = T / W,
+// r = T % W: the first r ranges take q + 1): range w starts at w*q + min(w,
+// r).  All in 32-bit integers (the host checks T fits): 64-bit division
+// would cost the prologue about a thousand instructions.
+__device__ __forceinline__ int sk_start(int w, int q, int r) { return w * q + min(w, r); }
+__device__ __forceinline__ int sk_owner(int t, const DecodeArgs& a) {
+  const int big = a.sk_r * (a.sk_q + 1);
+  return t < big ? (int)fdiv(t, a.fd_q1) : a.sk_r + (int)fdiv(t - big, a.fd_q);
+}
+
+constexpr int kSkAux = 16;   // buffer cache policy: sc1 (device scope)
+constexpr int kSkLocal = 1;  // sc0: past the CU's L1, served by the XCD's L2
+// Arrival counters sit one 128-byte line apart: the producers of different
+// groups arrive at once, and atomics on one line queue behind each other
+// (one Llama-3.2 layer, 8 groups of 32 producers: 161 us per token with the
+// counters a line apart, 191 us with them 4 bytes apart).
+constexpr int kSkCtrPitch = 32;
+
+// The last producer's merge of a group's np partials (slots slot0..): POL is
+// the cache policy the producers stored them with.
+template <int D, int POL>
+__device__ __forceinline__ void sk_merge_partials(const DecodeArgs& a,
+                                                  __amdgpu_buffer_rsrc_t prs, int slot0, int np,
+                                                  int h, int d, float* dst) {
+  constexpr int PS = D + 4;
+  float M = kNegBig, L = 0.f;
+  float4_t O = float4_t{0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < np; j0 += 8) {
+    float4_t ml[8], oj[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int off = ((slot0 + min(j0 + j, np - 1)) * a.nhm + h) * PS;
+      ml[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, (off + D) * 4, 0, POL);
+      oj[j] = __builtin_amdgcn_raw_buffer_load_b128(prs, (off + d) * 4, 0, POL);
+    }
+    float Mc = M;
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      if (j0 + j < np) Mc = fmaxf(Mc, ml[j][0]);
+    const float r = fast_exp2(M - Mc);
+    L *= r;
+    O *= r;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (j0 + j < np) {
+        const float wt = fast_exp2(ml[j][0] - Mc);
+        L = __builtin_fmaf(ml[j][1], wt, L);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) O[c] = __builtin_fmaf(oj[j][c], wt, O[c]);
+      }
+    }
+    M = Mc;
+  }
+  const float inv = 1.0f / L;
+  *reinterpret_cast<float4_t*>(dst) = O * inv;
+}
+
+template <int D>
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t sk_rsrc(const DecodeArgs& a) {
+  return __builtin_amdgcn_make_buffer_rsrc(a.sk_part, 0, (int)a.sk_part_bytes, 0x00020000);
+}
+
+// The stream-K kernel's body; PFR as for attn_decode_body.
+template <int D, bool QKN, int kSkPF, bool PFR>
+__device__ __forceinline__ void attn_decode_sk_body(const DecodeArgs& a, const PfLaunch& pl) {
+  constexpr int kWaves = 4;
+  constexpr int kThreads = 64 * kWaves;
+  constexpr int ND = D / 32;
+  constexpr int NO = D / 16;
+  constexpr int VP = D + 16;
+  constexpr int PS = D + 4;  // floats per (slot, head) of a partial: o[D], m, l, pad
+  constexpr int kVtileHalves = kWaves * kTile * VP;
+  constexpr int kCombFloats = kWaves * 16 * (D + 2);
+  constexpr int kSmemBytes =
+      (kVtileHalves * 2 > kCombFloats * 4) ? kVtileHalves * 2 : kCombFloats * 4;
+  __shared__ __align__(16) unsigned char smem[kSmemBytes];
+  __shared__ float s_knew[D], s_vnew[D], s_mnew[16];
+  __shared__ int s_last;
+
+#define PLH_SK_ARGS(a)                                                                           \
+  "s"(a.q), "s"(a.k), "s"(a.v), "s"(a.kc), "s"(a.vc), "s"(a.cos_t), "s"(a.sin_t), "s"(a.out),   \
+      "s"(a.layer0), "s"(a.n_heads), "s"(a.n_kv_heads), "s"(a.max_seq_len), "s"(a.pos),        \
+      "s"(a.rope_type), "s"(a.n_hblk), "s"(a.nhm), "s"(a.score_scale), "s"(a.sk_q),             \
+      "s"(a.sk_r), "s"(a.sk_nbk), "s"(a.sk_maxp), "s"(a.sk_part), "s"(a.sk_part_bytes),         \
+      "s"(a.sk_ctr), "s"(a.k_rows), "s"(a.v_rows), "s"(a.qn), "s"(a.kn), "s"(a.norm_eps),       \
+      "s"(a.G), "s"(a.fd_hblk.m), "s"(a.fd_hblk.sh), "s"(a.fd_kvh.m), "s"(a.fd_kvh.sh),         \
+      "s"(a.fd_nbk.m), "s"(a.fd_nbk.sh), "s"(a.fd_q.m), "s"(a.fd_q.sh), "s"(a.fd_q1.m),         \
+      "s"(a.fd_q1.sh), "s"(a.sk_wx), "s"(a.fd_wx.m), "s"(a.fd_wx.sh), "s"(a.sk_k),              \
+      "s"(a.sk_kshift)
+  if constexpr (PFR) {
+    // the prefetch split from the same batch of argument loads
+    PLH_ARGS_NOW(PLH_SK_ARGS(a), "s"(pl.n_main));
+    static_assert(kSmemBytes >= kPfLdsBytes, "prefetch workgroups use the kernel's LDS");
+    if (l2_prefetch_role(pl.plan, pl.n_main, kWaves, smem)) return;
+  } else {
+    PLH_ARGS_NOW(PLH_SK_ARGS(a));
+  }
+#undef PLH_SK_ARGS
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 15, grp = lane >> 4;
+  // sk_wx > 0: ranges x*wx .. x*wx + wx - 1 run on XCD x (workgroup ids x,
+  // x + 8, ...: the dispatcher deals workgroups to the XCDs in turn), so
+  // most groups' producers share one L2
+  const int w = a.sk_wx ? (int)(blockIdx.x & 7) * a.sk_wx + (int)(blockIdx.x >> 3)
+                        : (int)blockIdx.x;
+  int b0, b1;
+  if (a.sk_k) {
+    // range j of group g: blocks [j * nbk / k, (j + 1) * nbk / k) of the group
+    const int g = w >> a.sk_kshift, j = w & (a.sk_k - 1);
+    b0 = g * a.sk_nbk + ((j * a.sk_nbk) >> a.sk_kshift);
+    b1 = g * a.sk_nbk + (((j + 1) * a.sk_nbk) >> a.sk_kshift);
+  } else {
+    b0 = sk_start(w, a.sk_q, a.sk_r);
+    b1 = sk_start(w + 1, a.sk_q, a.sk_r);
+  }
+  const int G = a.G;
+  const int kv_dim = a.n_kv_heads * D;
+  const int pos = a.pos;
+  const int q_dim = a.n_heads * D;
+  const __amdgpu_buffer_rsrc_t prs = sk_rsrc<D>(a);
+
+  for (int s0 = b0; s0 < b1;) {
+    const int group = (int)fdiv(s0, a.fd_nbk);
+    const int gb = group * a.sk_nbk;
+    const int s1 = min(b1, gb + a.sk_nbk);
+    const int gh = (int)fdiv(group, a.fd_hblk);  // group / n_hblk
+    const int hblk = group - gh * a.n_hblk;
+    const int li = (int)fdiv(gh, a.fd_kvh);
+    const int kvh = gh - li * a.n_kv_heads;
+    const int layer = a.layer0 + li;
+    const int h0 = hblk * 16;
+    const int nh = min(16, G - h0);
+    const int tb = (s0 - gb) * 16;
+    const int te = min((s1 - gb) * 16, pos);  // cached rows [tb, te); row pos is new
+    const bool owner = s1 == gb + a.sk_nbk;   // covers the group's last block
+
+    const int tlast = te - 1;
+    const size_t row0 = (size_t)layer * a.max_seq_len;
+    const uint16_t* kbase = a.kc + row0 * kv_dim + (size_t)kvh * D;
+    const uint16_t* vbase = a.vc + row0 * kv_dim + (size_t)kvh * D;
+    constexpr int kStride = kWaves * kTile;
+    const int tw = tb + wave * kTile;
+    const bool new_row = owner && wave == 0;
+
+    QRaw<D> qr;
+    load_q_raw<D, QKN>(a, li, kvh, G, h0, nh, col, grp, qr);
+    RowRaw<D> rr;
+    load_row_raw<D, QKN>(a, li, kvh, lane, rr);
+
+    const bool has_rows = te > tb;
+    const int tclamp = has_rows ? tlast : 0;
+    Tile<D> buf[kSkPF];
+#pragma unroll
+    for (int j = 0; j < kSkPF; ++j)
+      load_tile<D>(buf[j], kbase, vbase, kv_dim, tw + j * kStride, tclamp, lane, col, grp);
+
+    half8_t qhi[ND], qlo[ND];
+    __builtin_amdgcn_sched_barrier(0);
+    const float qup = split_q<D, QKN>(a, col < nh, grp, qr, qhi, qlo);
+    if (new_row)
+      append_new_row<D, QKN>(a, li, kvh, row0, lane, col, grp, qr, rr, s_knew, s_vnew, s_mnew);
+
+    _Float16* vt = reinterpret_cast<_Float16*>(smem) + wave * (kTile * VP);
+    const float sscale = a.score_scale * qup;
+    float m = kNegBig;
+    float4_t lsum = float4_t{0.f, 0.f, 0.f, 0.f};
+    half8_t ones;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ones[j] = (_Float16)1.0f;
+    float4_t o[NO];
+#pragma unroll
+    for (int ob = 0; ob < NO; ++ob) o[ob] = float4_t{0.f, 0.f, 0.f, 0.f};
+
+    if (has_rows) {
+      for (int base = tw; base < te; base += kSkPF * kStride) {
+#pragma unroll
+        for (int j = 0; j < kSkPF; ++j) {
+          const int t0 = base + j * kStride;
+          if (t0 < te)
+            process_tile<D>(buf[j], qhi, qlo, vt, t0, tlast, lane, col, grp, sscale, ones, m,
+                            lsum, o);
+          load_tile<D>(buf[j], kbase, vbase, kv_dim, t0 + kSkPF * kStride, tclamp, lane, col,
+                       grp);
+        }
+      }
+    }
+    const float l = lsum[0];
+
+    __syncthreads();  // V tiles are dead; the LDS now holds the combine slots
+    float* cm = reinterpret_cast<float*>(smem);
+    float* cl = cm + kWaves * 16;
+    float* co = cl + kWaves * 16;
+    if (grp == 0) {
+      cm[wave * 16 + col] = m;
+      cl[wave * 16 + col] = l;
+    }
+#pragma unroll
+    for (int ob = 0; ob < NO; ++ob)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) co[(wave * 16 + col) * D + 16 * ob + 4 * grp + r] = o[ob][r];
+    __syncthreads();
+
+    // producers of this group: the workgroups owning its first and last block
+    const int p0 = a.sk_k ? group << a.sk_kshift : sk_owner(gb, a);
+    const int np = a.sk_k ? a.sk_k : sk_owner(gb + a.sk_nbk - 1, a) - p0 + 1;
+    // all producers on one XCD: partials and the count stay in its L2
+    const bool local = a.sk_wx && fdiv(p0, a.fd_wx) == fdiv(p0 + np - 1, a.fd_wx);
+
+    // ---- merge the waves (and the new row); one float4 of d per thread -----
+    float* out_base = a.out + (size_t)li * q_dim + (size_t)(kvh * G + h0) * D;
+    const int slot0 = group * a.sk_maxp;
+    for (int idx = tid; idx < nh * (D / 4); idx += kThreads) {
+      const int h = idx / (D / 4), d = 4 * (idx - h * (D / 4));
+      float M = kNegBig;
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) M = fmaxf(M, cm[ww * 16 + h]);
+      if (owner) M = fmaxf(M, s_mnew[h]);
+      float L = 0.f;
+      float4_t O = float4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ww = 0; ww < kWaves; ++ww) {
+        const float wt = fast_exp2(cm[ww * 16 + h] - M);
+        L = __builtin_fmaf(cl[ww * 16 + h], wt, L);
+        const float4_t x = *reinterpret_cast<const float4_t*>(co + (ww * 16 + h) * D + d);
+#pragma unroll
+        for (int c = 0; c < 4; ++c) O[c] = __builtin_fmaf(x[c], wt, O[c]);
+      }
+      if (owner) {
+        const float wt = fast_exp2(s_mnew[h] - M);
+        L += wt;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) O[c] = __builtin_fmaf(s_vnew[d + c], wt, O[c]);
+      }
+      if (np == 1) {
+        const float inv = 1.0f / L;
+        *reinterpret_cast<float4_t*>(out_base + (size_t)h * D + d) = O * inv;
+      } else {
+        const int off = ((slot0 + (w - p0)) * a.nhm + h) * PS;
+        const float4_t ml = float4_t{M, L, 0.f, 0.f};
+        if (local) {
+          __builtin_amdgcn_raw_buffer_store_b128(O, prs, (off + d) * 4, 0, kSkLocal);
+          if (d == 0) __builtin_amdgcn_raw_buffer_store_b128(ml, prs, (off + D) * 4, 0, kSkLocal);
+        } else {
+          __builtin_amdgcn_raw_buffer_store_b128(O, prs, (off + d) * 4, 0, kSkAux);
+          if (d == 0) __builtin_amdgcn_raw_buffer_store_b128(ml, prs, (off + D) * 4, 0, kSkAux);
+        }
+      }
+    }
+
+    if (np > 1) {
+      // every partial store has reached memory before the count goes up
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+      // the count is a device-scope atomic on either path
+      unsigned* ctr = a.sk_ctr + group * kSkCtrPitch;
+      if (tid == 0)
+        s_last = __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 (unsigned)(np - 1);
+      __syncthreads();
+      if (s_last) {
+        if (tid == 0) __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        for (int idx = tid; idx < nh * (D / 4); idx += kThreads) {
+          const int h = idx / (D / 4), d = 4 * (idx - h * (D / 4));
+          float* dst = out_base + (size_t)h * D + d;
+          if (local)
+            sk_merge_partials<D, kSkLocal>(a, prs, slot0, np, h, d, dst);
+          else
+            sk_merge_partials<D, kSkAux>(a, prs, slot0, np, h, d, dst);
+        }
+      }
+    }
+    s0 = s1;
+    __syncthreads();  // the LDS is reused by the next segment
   }
 }
 
