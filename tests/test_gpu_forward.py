@@ -409,9 +409,15 @@ def test_forward_weight_prefetch_changes_nothing(gpu, cfg):
 
 # head_dim 128 without QK-norm: the fused q/k/v + attention launch's other shape
 PF_LLAMA128 = dict(PF_LLAMA, n_heads=4, n_kv_heads=2, head_dim=128)
+# Qwen's rope pairing and q/k/v biases without QK-norm; one q head per kv head;
+# 16 q heads per kv head (the most one head block takes)
+PF_QWENROPE = dict(PF_LLAMA, rope_type=1, rope_base=1e6, biases=True)
+PF_G1 = dict(PF_LLAMA, n_heads=4, n_kv_heads=4, head_dim=64, n_embd=256)
+PF_G16 = dict(PF_LLAMA, n_heads=16, n_kv_heads=1, head_dim=64, n_embd=1024)
 
 
-@pytest.mark.parametrize("cfg", [PF_LLAMA, PF_LLAMA128], ids=["hd64", "hd128"])
+@pytest.mark.parametrize("cfg", [PF_LLAMA, PF_LLAMA128, PF_QWENROPE, PF_G1, PF_G16],
+                         ids=["hd64", "hd128", "qwen_rope_bias", "g1", "g16"])
 def test_forward_fused_qkv_attention_changes_nothing(gpu, cfg):
     """Tuning key 17: q, k, v and the attention in one launch (the attention
     workgroups wait on per-group counts of the GEMV workgroups that stored
