@@ -339,9 +339,10 @@ int forward_token(const plh_model* m, int token, int pos, void* workspace, float
                                         m->key_cache, m->val_cache, m->rope_cos, m->rope_sin,
                                         a.att, fd, &fctr);
     if (!fuse && gemv_multi_launch(qkv, 3)) return -1;
-    // The attention launch leaves most CUs idle: its spare workgroups bring
-    // the o-projection's, the gate/up pair's and the down projection's
-    // weights into the L2 of the XCDs whose GEMV workgroups will read them.
+    // The attention launch (or the fused one) leaves most CUs idle: extra
+    // workgroups bring the o-projection's, the gate/up pair's and the down
+    // projection's weights into the L2 of the XCDs whose GEMV workgroups will
+    // read them.
     PfPlan& pf = ctx().pf_next;
     pf.n = 0;
     if (g_fwd_prefetch >= 0) {
