@@ -60,6 +60,23 @@ int plh_memcpy_dtoh_async(void *dst, const void *src, size_t bytes);
 /* plh_memcpy2d_dtoh queued the same way, without waiting. */
 int plh_memcpy2d_dtoh_async(void *dst, size_t dpitch, const void *src, size_t spitch,
                             size_t width, size_t height);
+/* Up to four strided copies as ONE kernel launch on the library stream,
+ * without waiting: copy i moves `height` rows of `width` bytes from `src`
+ * (rows `spitch` bytes apart) to `dst` (rows `dpitch` apart).  Either side
+ * may be device memory or pinned host memory from plh_host_alloc (the kernel
+ * reads and writes it over PCIe), so a host collecting several results after
+ * a pass pays one launch rather than one DMA command per copy.  Copies must
+ * not overlap each other; rows of a copy must not overlap (pitch >= width).
+ * Returns -1 (plh_last_error) for n outside 1..4, a null pointer with a
+ * non-empty copy, or a pitch below the width; empty copies are skipped. */
+typedef struct {
+    void *dst;
+    size_t dpitch;
+    const void *src;
+    size_t spitch;
+    size_t width, height;
+} plh_copy2d;
+int plh_copy2d_batch_async(const plh_copy2d *copies, int n);
 
 /* ---- timing on the library stream (hipEvents) -------------------------- */
 void *plh_event_create(void);

@@ -76,6 +76,7 @@ _SIGS = {
     "plh_memcpy_htod_async": (_i, [_vp, _vp, _sz]),
     "plh_memcpy_dtoh_async": (_i, [_vp, _vp, _sz]),
     "plh_memcpy2d_dtoh_async": (_i, [_vp, _sz, _vp, _sz, _sz, _sz]),
+    "plh_copy2d_batch_async": (_i, [_vp, _i]),
     # events
     "plh_event_create": (_vp, []),
     "plh_event_record": (_i, [_vp]),

@@ -64,6 +64,36 @@ int ensure_workspace(size_t bytes) {
 
 using namespace plh;
 
+namespace {
+
+// One copy of plh_copy2d_batch_async in units of the launch's unit type.
+struct Copy2D {
+  const uint8_t* src;
+  uint8_t* dst;
+  uint64_t spitch, dpitch;
+  uint32_t row_units, units;  // units per row, units in all (< 2^31)
+};
+
+struct Copy2DBatch {
+  Copy2D c[4];
+};
+
+// blockIdx.y picks the copy (the same for the whole workgroup); the x
+// workgroups stride over its units.  Stores to pinned host memory go out over
+// PCIe and are visible to the host once the stream has been synchronised.
+template <typename U>
+__global__ __launch_bounds__(256) void copy2d_batch_kernel(Copy2DBatch b) {
+  const Copy2D& c = b.c[blockIdx.y];
+  const uint32_t stride = gridDim.x * 256u;
+  for (uint32_t u = blockIdx.x * 256u + threadIdx.x; u < c.units; u += stride) {
+    const uint32_t row = u / c.row_units, col = u - row * c.row_units;
+    *reinterpret_cast<U*>(c.dst + row * c.dpitch + (uint64_t)col * sizeof(U)) =
+        *reinterpret_cast<const U*>(c.src + row * c.spitch + (uint64_t)col * sizeof(U));
+  }
+}
+
+}  // namespace
+
 extern "C" {
 
 const char* plh_last_error(void) { return g_err; }
@@ -202,6 +232,63 @@ int plh_memcpy2d_dtoh_async(void* dst, size_t dpitch, const void* src, size_t sp
   return check_hip(hipMemcpy2DAsync(dst, dpitch, src, spitch, width, height,
                                     hipMemcpyDeviceToHost, g_ctx.stream),
                    "dtoh 2d async");
+}
+
+int plh_copy2d_batch_async(const plh_copy2d* copies, int n) {
+  if (!g_ctx.stream) {
+    set_error("plh_copy2d_batch_async: library not initialised");
+    return -1;
+  }
+  if (!copies || n < 1 || n > 4) {
+    set_error("plh_copy2d_batch_async: %d copies (1..4 taken)", copies ? n : 0);
+    return -1;
+  }
+  const plh_copy2d* live[4];
+  int m = 0;
+  uintptr_t bits = 0;  // every address, width and used pitch: their common alignment
+  for (int i = 0; i < n; ++i) {
+    const plh_copy2d& c = copies[i];
+    if (c.width == 0 || c.height == 0) continue;
+    if (!c.dst || !c.src) {
+      set_error("plh_copy2d_batch_async: copy %d has a null pointer", i);
+      return -1;
+    }
+    if (c.dpitch < c.width || c.spitch < c.width) {
+      set_error("plh_copy2d_batch_async: copy %d has a pitch below its width", i);
+      return -1;
+    }
+    if (c.width > (1ull << 31) || c.height > (1ull << 31)) {
+      set_error("plh_copy2d_batch_async: copy %d is too large", i);
+      return -1;
+    }
+    bits |= (uintptr_t)c.dst | (uintptr_t)c.src | c.width;
+    if (c.height > 1) bits |= c.dpitch | c.spitch;
+    live[m++] = &c;
+  }
+  if (m == 0) return 0;
+  const size_t unit = (bits & 15) == 0 ? 16 : (bits & 3) == 0 ? 4 : 1;
+  Copy2DBatch b{};
+  uint32_t blocks = 1;
+  for (int i = 0; i < m; ++i) {
+    const size_t units = live[i]->width / unit * live[i]->height;
+    if (units >= (1ull << 31)) {
+      set_error("plh_copy2d_batch_async: copy of %zu units of %zu bytes is too large", units,
+                unit);
+      return -1;
+    }
+    b.c[i] = Copy2D{(const uint8_t*)live[i]->src, (uint8_t*)live[i]->dst, live[i]->spitch,
+                    live[i]->dpitch, (uint32_t)(live[i]->width / unit), (uint32_t)units};
+    const size_t need = (units + 255) / 256;
+    if (need > blocks) blocks = need > 512 ? 512 : (uint32_t)need;
+  }
+  const dim3 grid(blocks, (unsigned)m);
+  if (unit == 16)
+    hipLaunchKernelGGL(copy2d_batch_kernel<uint4>, grid, dim3(256), 0, g_ctx.stream, b);
+  else if (unit == 4)
+    hipLaunchKernelGGL(copy2d_batch_kernel<uint32_t>, grid, dim3(256), 0, g_ctx.stream, b);
+  else
+    hipLaunchKernelGGL(copy2d_batch_kernel<uint8_t>, grid, dim3(256), 0, g_ctx.stream, b);
+  return check_hip(hipGetLastError(), "copy2d_batch_kernel");
 }
 
 int plh_memcpy_dtod(void* dst, const void* src, size_t bytes) {

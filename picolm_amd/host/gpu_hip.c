@@ -701,9 +701,9 @@ static float *forward_stage(int n) {
 }
 
 /* After plh_forward(_prefill) has written the logits into h_fwd: x and the
- * rows of positions pos0..pos0+n-1 of every layer queued into h_fwd (one
- * strided copy per cache), one synchronisation, then the host state and
- * caches filled from the staging. */
+ * rows of positions pos0..pos0+n-1 of every layer into h_fwd by one copy
+ * kernel (x, then one strided copy per cache), one synchronisation, then the
+ * host state and caches filled from the staging. */
 static int forward_done(model_t *m, int pos0, int n) {
     const model_config_t *c = &m->config;
     const size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
@@ -713,10 +713,12 @@ static int forward_done(model_t *m, int pos0, int n) {
     const size_t lb = (size_t)c->vocab_size * sizeof(float), xb = (size_t)c->n_embd * sizeof(float);
     const size_t rb = width * (size_t)gs.n_layers;
     unsigned char *hx = gs.h_fwd + lb, *hk = hx + xb, *hv = hk + rb;
-    if (plh_memcpy_dtoh_async(hx, gs.d_x, xb) ||
-        plh_memcpy2d_dtoh_async(hk, width, gs.d_key + off, pitch, width, (size_t)gs.n_layers) ||
-        plh_memcpy2d_dtoh_async(hv, width, gs.d_val + off, pitch, width, (size_t)gs.n_layers) ||
-        plh_synchronize()) {
+    const plh_copy2d back[3] = {
+        {hx, xb, gs.d_x, xb, xb, 1},
+        {hk, width, gs.d_key + off, pitch, width, (size_t)gs.n_layers},
+        {hv, width, gs.d_val + off, pitch, width, (size_t)gs.n_layers},
+    };
+    if (plh_copy2d_batch_async(back, 3) || plh_synchronize()) {
         backend_lost("copy back");
         return -1;
     }
