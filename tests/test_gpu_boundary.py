@@ -105,6 +105,8 @@ CASES = [
     ((2, 32, 32, 128, 300, 0), 1e4, 90, 4),    # Llama-2 MHA
     ((2, 16, 2, 64, 128, 1), 1e6, 60, 3),      # QWEN rotation
     ((2, 8, 2, 96, 300, 0), 1e4, 90, 3),       # head_dim 96 (generic kernels)
+    # 17 MB of out and rows back per prefill call: the DMA copies, not the copy kernel
+    ((1, 32, 32, 128, 600, 0), 1e4, 520, 2),   # Llama-2 MHA, long prompt
 ]
 
 
