@@ -45,6 +45,10 @@ int plh_memcpy_dtod(void *dst, const void *src, size_t bytes);
  * (blocking): the per-layer rows of one position in one call. */
 int plh_memcpy2d_dtoh(void *dst, size_t dpitch, const void *src, size_t spitch,
                       size_t width, size_t height);
+/* plh_memcpy2d_dtoh in the other direction (host rows to device rows),
+ * blocking: every layer's rows of a cache in one call. */
+int plh_memcpy2d_htod(void *dst, size_t dpitch, const void *src, size_t spitch, size_t width,
+                      size_t height);
 int plh_memset(void *dst, int value, size_t bytes);
 int plh_synchronize(void);
 /* Pinned (page-locked) host memory, for staging copies that the DMA engines

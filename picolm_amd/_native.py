@@ -69,6 +69,7 @@ _SIGS = {
     "plh_memcpy_dtoh": (_i, [_vp, _vp, _sz]),
     "plh_memcpy_dtod": (_i, [_vp, _vp, _sz]),
     "plh_memcpy2d_dtoh": (_i, [_vp, _sz, _vp, _sz, _sz, _sz]),
+    "plh_memcpy2d_htod": (_i, [_vp, _sz, _vp, _sz, _sz, _sz]),
     "plh_memset": (_i, [_vp, _i, _sz]),
     "plh_synchronize": (_i, []),
     "plh_host_alloc": (_vp, [_sz]),

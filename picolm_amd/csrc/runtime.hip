@@ -201,6 +201,16 @@ int plh_memcpy2d_dtoh(void* dst, size_t dpitch, const void* src, size_t spitch, 
   return check_hip(hipStreamSynchronize(g_ctx.stream), "dtoh 2d sync");
 }
 
+int plh_memcpy2d_htod(void* dst, size_t dpitch, const void* src, size_t spitch, size_t width,
+                      size_t height) {
+  if (height == 0 || width == 0) return 0;
+  if (check_hip(hipMemcpy2DAsync(dst, dpitch, src, spitch, width, height, hipMemcpyHostToDevice,
+                                 g_ctx.stream),
+                "htod 2d"))
+    return -1;
+  return check_hip(hipStreamSynchronize(g_ctx.stream), "htod 2d sync");
+}
+
 void* plh_host_alloc(size_t bytes) {
   void* p = nullptr;
   if (check_hip(hipHostMalloc(&p, bytes ? bytes : 1, hipHostMallocDefault), "hipHostMalloc"))

@@ -667,28 +667,27 @@ int gpu_try_attention_prefill(model_t *m, int layer, int start_pos, int n_tokens
     return 0;
 }
 
-/* Rows 0..n_pos-1 of the layers the device handles (l < gpu_layers).  The
- * other layers' rows exist only in the host cache (their CPU block appends
- * them there), so they are neither overwritten by a download nor needed on
- * the device. */
+/* Rows 0..n_pos-1 of the layers the device handles (l < gpu_layers), one
+ * strided copy per cache (host and device caches share the layout
+ * [layer][max_seq_len][kv_dim]).  The other layers' rows exist only in the
+ * host cache (their CPU block appends them there), so they are neither
+ * overwritten by a download nor needed on the device. */
 static int kv_copy(const model_t *m, int n_pos, int to_host) {
     if (!gpu_available() || !same_shape(m) || n_pos < 0 || n_pos > gs.max_seq_len) return -1;
-    size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
-    size_t bytes = (size_t)n_pos * kv_dim * sizeof(uint16_t);
-    for (int l = 0; l < gs.n_layers && l < gs.gpu_layers; l++) {
-        size_t off = (size_t)l * gs.max_seq_len * kv_dim;
-        int rc;
-        if (to_host) {
-            rc = plh_memcpy_dtoh(m->state.key_cache + off, gs.d_key + off, bytes) ||
-                 plh_memcpy_dtoh(m->state.val_cache + off, gs.d_val + off, bytes);
-        } else {
-            rc = plh_memcpy_htod(gs.d_key + off, m->state.key_cache + off, bytes) ||
-                 plh_memcpy_htod(gs.d_val + off, m->state.val_cache + off, bytes);
-        }
-        if (rc) {
-            backend_lost(to_host ? "kv download" : "kv upload");
-            return -1;
-        }
+    const size_t kv_dim = (size_t)gs.n_kv_heads * gs.head_dim;
+    const size_t width = (size_t)n_pos * kv_dim * sizeof(uint16_t);
+    const size_t pitch = (size_t)gs.max_seq_len * kv_dim * sizeof(uint16_t);
+    const size_t layers = (size_t)(gs.gpu_layers < gs.n_layers ? gs.gpu_layers : gs.n_layers);
+    int rc;
+    if (to_host)
+        rc = plh_memcpy2d_dtoh(m->state.key_cache, pitch, gs.d_key, pitch, width, layers) ||
+             plh_memcpy2d_dtoh(m->state.val_cache, pitch, gs.d_val, pitch, width, layers);
+    else
+        rc = plh_memcpy2d_htod(gs.d_key, pitch, m->state.key_cache, pitch, width, layers) ||
+             plh_memcpy2d_htod(gs.d_val, pitch, m->state.val_cache, pitch, width, layers);
+    if (rc) {
+        backend_lost(to_host ? "kv download" : "kv upload");
+        return -1;
     }
     return 0;
 }

@@ -12,7 +12,9 @@
  * Usage: bench_forward L n_embd n_ffn n_heads n_kv_heads vocab max_seq pos reps prompt
  * Decode: one untimed token at `pos`, then `reps` timed tokens at pos+1...
  * Prefill: one untimed `prompt`-token prefill at position 0, then `reps`
- * timed ones.  Prints one JSON line of medians and means in microseconds.
+ * timed ones.  KV: gpu_kv_download then gpu_kv_upload of every layer's rows
+ * 0..pos+reps-1 (one untimed pair, then `reps` timed).  Prints one JSON line
+ * of medians and means in microseconds.
  */
 #include <stdint.h>
 #include <stdio.h>
@@ -156,11 +158,38 @@ int main(int argc, char **argv) {
         }
         if (r >= 0) pre[r] = now_us() - t0;
     }
+    /* kvcache_save / kvcache_load coherence (model.c:1146-1259): every layer's
+     * rows 0..kv_pos-1 down into the host caches and back up */
+    const int kv_pos = pos + reps;
+    double *kvd = malloc((size_t)reps * sizeof(double));
+    double *kvu = malloc((size_t)reps * sizeof(double));
+    if (!kvd || !kvu) return 1;
+    for (int r = -1; r < reps; r++) {
+        double t0 = now_us();
+        if (gpu_kv_download(&m, kv_pos) != 0) {
+            fprintf(stderr, "gpu_kv_download failed\n");
+            return 1;
+        }
+        double t1 = now_us();
+        if (gpu_kv_upload(&m, kv_pos) != 0) {
+            fprintf(stderr, "gpu_kv_upload failed\n");
+            return 1;
+        }
+        double t2 = now_us();
+        if (r >= 0) {
+            kvd[r] = t1 - t0;
+            kvu[r] = t2 - t1;
+        }
+    }
     printf("{\"hook\": \"gpu_try_forward\", \"pos\": %d, \"prompt\": %d, \"reps\": %d, ", pos + 1,
            prompt, reps);
     summary("decode", dec, reps);
     printf(", ");
     summary("prefill", pre, reps);
+    printf(", \"kv_pos\": %d, ", kv_pos);
+    summary("kv_download", kvd, reps);
+    printf(", ");
+    summary("kv_upload", kvu, reps);
     printf("}\n");
     gpu_shutdown();
     return 0;
