@@ -44,8 +44,9 @@ Method (device):
     q/k/v in, host output and cache rows back over PCIe) -- the latency
     picolm's own call sites would see; never the headline value; with it
     matmul_hook, gpu_try_matmul for every projection of one TinyLlama token
-    (tests/c/bench_matmul), and forward_hook, gpu_try_forward and
-    gpu_try_forward_prefill of a TinyLlama-shaped model (tests/c/bench_forward).
+    (tests/c/bench_matmul), and forward_hook, gpu_try_forward,
+    gpu_try_forward_prefill, gpu_kv_download and gpu_kv_upload of a
+    TinyLlama-shaped model (tests/c/bench_forward).
 Method (CPU baseline, kind "reference"): picolm's own attention code, i.e.
 its model_forward_ex / model_forward_prefill compiled from its sources into
 oracle/_ref, on the host, median of 5 runs after 1 warm-up, over a bounded
@@ -969,8 +970,10 @@ def matmul_hook_latency(reps=10):
 def forward_hook_latency(reps=10):
     """gpu_try_forward (a decode token at position 257) and
     gpu_try_forward_prefill (a 128-token prompt) of a TinyLlama-shaped
-    Q4_K_M model, logits, x and cache rows back in host memory, from
-    tests/c/bench_forward; None if not built."""
+    Q4_K_M model, logits, x and cache rows back in host memory, then
+    gpu_kv_download / gpu_kv_upload of every layer's rows up to kv_pos
+    (kvcache_save / kvcache_load coherence), from tests/c/bench_forward;
+    None if not built."""
     exe = os.path.join(ROOT, "tests", "c", "bench_forward")
     if not os.path.exists(exe):
         return None
